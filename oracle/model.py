@@ -1,0 +1,351 @@
+"""ORACLE (test infrastructure only): one sequence's forward path on the CPU.
+
+A restatement of the reference engine (miracle_reasoning/model.py) over the
+C kernels in oracle/kernels.c, numpy arrays standing in for device buffers.
+Host control (MoE routing, block top-k, latent compaction bookkeeping) is the
+same numpy float32 arithmetic the reference performs on its host.
+
+Pinned by: golden per-token logits, greedy streams, chosen experts / active
+widths, chosen blocks and latent-cache metadata, written by
+tests/golden/make_golden.py from the reference's own model.py for micro
+configurations of all six families (tests/test_oracle_model.py), and by the
+reference's invariants (decode == prefill bit-exact, ring lengths, relay count,
+latent rows, loop caches; tests/test_inference.py:42-69 of the reference).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import kernels as K
+from .config import OracleConfig, inverse_frequencies, weight_shapes
+
+
+class _Ring:
+    """Circular KV buffer: slot of the next row is count % capacity (model.py:15-33)."""
+
+    def __init__(self, capacity, width):
+        self.k = np.zeros((capacity, width), np.float32)
+        self.v = np.zeros((capacity, width), np.float32)
+        self.capacity, self.count = capacity, 0
+
+    def push(self, key, value):
+        slot = self.count % self.capacity
+        self.k[slot] = key.reshape(-1)
+        self.v[slot] = value.reshape(-1)
+        self.count += 1
+
+    @property
+    def length(self):
+        return min(self.count, self.capacity)
+
+    @property
+    def start(self):
+        return (self.count - self.length) % self.capacity
+
+
+def _widen(array):
+    """Weights are held as FP32 or as BF16 bits (uint16); 1-D tensors are widened."""
+    if array.dtype == np.uint16:
+        return (array.astype(np.uint32) << 16).view(np.float32)
+    return np.asarray(array, np.float32)
+
+
+class OracleModel:
+    """Same call surface as the reference engine: prefill / decode / generate / reset.
+
+    ``weights`` maps canonical names to FP32 arrays or BF16 bit arrays (uint16).
+    ``trace`` (optional list) receives per-step routing and block-selection
+    records for parity checks of discrete decisions.
+    """
+
+    def __init__(self, config, weights, context_length=None, trace=None):
+        cfg = config if isinstance(config, OracleConfig) else OracleConfig.from_bundle(config)
+        self.cfg = cfg
+        self.ctx = context_length if context_length is not None else min(2048, cfg.max_positions)
+        if not 0 < self.ctx <= cfg.max_positions:
+            raise ValueError("context_length out of range")
+        self.w = {}
+        for name, shape in weight_shapes(cfg).items():
+            a = weights[name]
+            a = np.ascontiguousarray(a if getattr(a, "dtype", None) == np.uint16 else np.asarray(a, np.float32))
+            if tuple(a.shape) != shape:
+                raise ValueError(f"{name}: expected {shape}, got {a.shape}")
+            self.w[name] = _widen(a) if len(shape) == 1 else a
+        self.freq = inverse_frequencies(cfg)
+        self.trace = trace
+        self.reset()
+
+    # ---------------------------------------------------------------- helpers
+    def reset(self):
+        self.position = 0
+        self.failed = False
+        self.layers = [dict() for _ in range(self.cfg.layers)]
+
+    def _rms(self, x, name, width=None, eps=None):
+        c = self.cfg
+        return K.rms(x, self.w[name] if name else None, width or c.hidden_size,
+                     c.norm_eps if eps is None else eps)
+
+    def _rope(self, x, positions, heads):
+        return K.rope(x, self.freq, positions, heads, self.cfg.head_dim, self.cfg.split_half)
+
+    def _mlp(self, x, root):
+        g = K.linear(x, self.w[root + "gate"])
+        u = K.linear(x, self.w[root + "up"])
+        return K.linear(K.swiglu(g, u), self.w[root + "down"])
+
+    # ------------------------------------------------ GQA (1.5 / 1.6 / 1.7 / lite)
+    def _gqa(self, x, layer, state, pos):
+        c, p = self.cfg, f"layers.{layer}."
+        kvh = c.kv_heads_of(layer)
+        q = K.linear(x, self.w[p + "q"])
+        k = K.linear(x, self.w[p + "k"])
+        v = K.linear(x, self.w[p + "v"])
+        if c.qk_norm:
+            q = self._rms(q, p + "q_norm", c.head_dim)
+            k = self._rms(k, p + "k_norm", c.head_dim)
+        q = self._rope(q, pos, c.query_heads)
+        k = self._rope(k, pos, kvh)
+        ring = state.get("ring")
+        if ring is None:
+            ring = state["ring"] = _Ring(min(c.window_of(layer) or self.ctx, self.ctx), kvh * c.head_dim)
+        ring.push(k, v)
+        relay = state.get("relay")
+        attended = K.attention(q, ring.k, ring.v, c.query_heads, kvh, c.head_dim, ring.start, ring.length,
+                               relay["k"] if relay else None, relay["v"] if relay else None,
+                               relay["count"] if relay else 0)
+        if c.family == "flashnano-1.6":
+            self._cbr(x, layer, state, kvh)
+        return K.linear(attended, self.w[p + "o"])
+
+    def _cbr(self, x, layer, state, kvh):
+        """Chunk pooling into relay keys (model.py:118-144)."""
+        c, p = self.cfg, f"layers.{layer}."
+        chunk, slots, h = c.cbr_chunk_size, c.cbr_slots, c.hidden_size
+        if "pending" not in state:
+            state["pending"] = np.zeros((min(chunk, self.ctx), h), np.float32)
+        row = self.position % chunk
+        state["pending"][row] = x.reshape(-1)
+        if row != chunk - 1:
+            return
+        queries = K.rms(self.w[p + "cbr"], None, h, c.cbr_norm_eps)
+        probs = K.softmax(K.pool_scores(state["pending"], queries, chunk, slots, h))
+        pooled, anchors = K.pool_mix(state["pending"], probs, chunk, slots, h, self.position + 1 - chunk)
+        key = K.linear(pooled, self.w[p + "k"])
+        value = K.linear(pooled, self.w[p + "v"])
+        key = self._rope(self._rms(key, p + "k_norm", c.head_dim), anchors, kvh)
+        relay = state.get("relay")
+        if relay is None:
+            cap = (self.ctx // chunk) * slots
+            width = kvh * c.head_dim
+            relay = state["relay"] = {"k": np.zeros((cap, width), np.float32),
+                                      "v": np.zeros((cap, width), np.float32), "count": 0}
+        n = relay["count"]
+        relay["k"][n:n + slots] = key
+        relay["v"][n:n + slots] = value
+        relay["count"] = n + slots
+
+    # ------------------------------------------------------- flashlighting-2.0
+    def _lighting(self, x, layer, state, pos):
+        """Latent attention with memory compaction (model.py:146-190)."""
+        c, p = self.cfg, f"layers.{layer}."
+        q = self._rope(self._rms(K.linear(x, self.w[p + "q"]), p + "q_norm", c.head_dim), pos, c.query_heads)
+        latent = self._rms(K.linear(x, self.w[p + "latent"]), p + "latent_norm", c.latent_dim)
+        old = state.get("latent")
+        rows = latent if old is None else np.concatenate([old, latent])
+        n1 = rows.shape[0]
+        positions = state.get("positions", []) + [self.position]
+        counts = state.get("counts", []) + [1.0]
+        key_pos = np.asarray(positions, np.float32)
+        key = self._rope(self._rms(K.linear(rows, self.w[p + "k"]), p + "k_norm", c.head_dim), key_pos, c.kv_heads)
+        value = K.linear(rows, self.w[p + "v"])
+        s = K.scores(q, key, None, c.query_heads, c.kv_heads, c.head_dim, n1, 0, n1, 0)
+        K.latent_mask(s, key_pos, c.query_heads, n1, state.get("memory_size", 0), self.position - c.window + 1)
+        attended = K.mix(K.softmax(s), value, None, c.query_heads, c.kv_heads, c.head_dim, n1, 0, n1, 0)
+        overflow = max(0, n1 - c.window)
+        if c.memory_slots == 0 and overflow:
+            rows, positions, counts, memory = rows[overflow:], positions[overflow:], counts[overflow:], 0
+        elif overflow > c.memory_slots:
+            a, b = np.float32(counts[0]), np.float32(counts[1])
+            merged = K.merge_rows(rows[:2], c.latent_dim, float(a), float(b))
+            rows = np.concatenate([merged[None, :], rows[2:]])
+            centre = np.float32(np.float32(positions[0]) * a + np.float32(positions[1]) * b) / np.float32(a + b)
+            positions = [int(np.rint(centre))] + positions[2:]
+            counts = [float(a + b)] + counts[2:]
+            memory = c.memory_slots
+        else:
+            memory = overflow
+        state.update(latent=np.ascontiguousarray(rows), positions=positions, counts=counts, memory_size=memory)
+        return K.linear(attended, self.w[p + "o"])
+
+    # -------------------------------------------------------- heavy-medium-2.0
+    def _heavy_attention(self, x, layer, state, pos):
+        """Window + block-mean sparse attention (model.py:192-229)."""
+        c, p = self.cfg, f"layers.{layer}."
+        d, H, kvh = c.head_dim, c.query_heads, c.kv_heads
+        width = kvh * d
+        q = K.rms(K.linear(x, self.w[p + "q"]), None, d, 1e-6)
+        kv = K.linear(K.linear(x, self.w[p + "latent"]), self.w[p + "kv_up"])
+        key, value = kv[:, :width], kv[:, width:]
+        q = self._rope(q, pos, H)
+        key = self._rope(K.rms(key, None, d, 1e-6), pos, kvh)
+        ring = state.get("ring")
+        if ring is None:
+            ring = state["ring"] = _Ring(self.ctx, width)
+        ring.push(key, value)
+        count = ring.count
+        length = min(c.window, count)
+        start = count - length
+        lc = c.source["long_context"]
+        block = lc["global_block_size"]
+        blocks = (count + block - 1) // block
+        mk = K.block_means(ring.k, count, width, block)
+        mv = K.block_means(ring.v, count, width, block)
+        s = K.scores(q, ring.k, mk, H, kvh, d, ring.capacity, start, length, blocks)
+        ends = np.minimum((np.arange(blocks) + 1) * block - 1, self.position)
+        slope = np.float32(lc.get("alibi_slope_scale", 0.015) / math.sqrt(d))
+        s[:, length:] -= slope * np.log1p((self.position - ends).astype(np.float32))
+        keep = min(lc["global_slots"], blocks)
+        order = np.argsort(-s[:, length:], axis=1, kind="stable")
+        for h in range(H):
+            s[h, length + order[h, keep:]] = -np.inf
+        if self.trace is not None:
+            self.trace.append(("blocks", layer, self.position, [sorted(order[h, :keep].tolist()) for h in range(H)]))
+        attended = K.mix(K.softmax(s), ring.v, mv, H, kvh, d, ring.capacity, start, length, blocks)
+        return K.linear(attended, self.w[p + "o"])
+
+    def _moe(self, x, layer):
+        """Grouped adaptive routing + experts + shared experts (model.py:231-255)."""
+        c, p, s = self.cfg, f"layers.{layer}.", self.cfg.source
+        E, G = s["routed_experts"], s["router_groups"]
+        coarse = K.linear(x, self.w[p + "router.coarse.weight"])[0]
+        fine = K.linear(x, self.w[p + "router.fine.weight"])[0]
+        coarse = coarse + (self.w[p + "router.coarse.bias"] + self.w[p + "router.group_bias"])
+        fine = fine + (self.w[p + "router.fine.bias"] + self.w[p + "router.expert_bias"])
+        size = -(-E // G)
+        group_of = np.minimum(np.arange(E) // size, G - 1)
+        logits = (fine + coarse[group_of]) / np.float32(max(s.get("router_temperature", 1.0), 1e-4))
+        probs = K.softmax(logits.reshape(1, -1))[0]
+        kmax, kmin = s["router_top_k_max"], s["router_top_k_min"]
+        chosen = np.argsort(-probs, kind="stable")[:kmax]
+        weights = probs[chosen].copy()
+        confidence = weights[0] - weights[min(kmax - 1, 1)]
+        entropy = -(probs * np.log(np.maximum(probs, np.float32(1e-9)))).sum()
+        spread = np.rint((np.float32(1) - confidence) * np.float32(2)
+                         + entropy / max(np.float32(np.log(E)), np.float32(1)))
+        active = int(np.clip(kmin + spread, kmin, kmax))
+        weights[active:] = 0
+        weights /= max(weights.sum(), np.float32(1e-9))
+        if self.trace is not None:
+            self.trace.append(("experts", layer, self.position, chosen[:active].tolist(), active))
+        out = np.zeros_like(x)
+        for e, wgt in zip(chosen[:active], weights[:active]):
+            out = K.axpy(out, self._mlp(x, p + f"experts.{e}."), float(wgt))
+        for e in range(s["shared_experts"]):
+            out = K.axpy(out, self._mlp(x, p + f"shared.{e}."), c.residual_scale / max(s["shared_experts"], 1))
+        return out
+
+    # --------------------------------------------------------------- one token
+    def step(self, token):
+        """One token through every layer; returns the final-normed hidden row."""
+        c = self.cfg
+        hidden = _widen(np.asarray(self.w["embed"][token:token + 1]))
+        pos = np.asarray([self.position], np.float32)
+        rs = c.residual_scale
+        for layer, state in enumerate(self.layers):
+            p = f"layers.{layer}."
+            if c.family == "heavy-medium-2.0":
+                loops = state.setdefault("loops", [dict() for _ in range(c.inner_loop_steps)])
+                scale = rs / math.sqrt(c.inner_loop_steps)
+                for inner in loops:
+                    hidden = K.axpy(hidden, self._heavy_attention(self._rms(hidden, p + "a_norm"), layer, inner, pos),
+                                    scale)
+                    hidden = K.axpy(hidden, self._moe(self._rms(hidden, p + "f_norm"), layer), scale)
+            elif c.family == "flashlighting-2.0":
+                x = self._rms(hidden, p + "a_norm")
+                attended = self._lighting(x, layer, state, pos)
+                ag = float(self.w[p + "attention_gate"][0])
+                fg = float(self.w[p + "ffn_gate"][0])
+                branch = K.axpy(np.zeros_like(hidden), attended, ag)
+                branch = K.axpy(branch, self._mlp(x, p + "ffn."), fg)
+                hidden = K.axpy(hidden, branch, rs)
+            else:
+                hidden = K.axpy(hidden, self._gqa(self._rms(hidden, p + "a_norm"), layer, state, pos), rs)
+                hidden = K.axpy(hidden, self._mlp(self._rms(hidden, p + "f_norm"), p + "ffn."), rs)
+        self.position += 1
+        return self._rms(hidden, "norm")
+
+    def head(self, hidden):
+        return K.linear(hidden, self.w["embed" if self.cfg.tie_embeddings else "output"])[0]
+
+    # ------------------------------------------------------------- public API
+    def _ids(self, ids):
+        a = np.asarray(ids)
+        if a.ndim != 1 or a.size == 0 or a.dtype.kind not in "iu":
+            raise ValueError("input_ids must be a non-empty 1D integer sequence")
+        if np.any(a < 0) or np.any(a >= self.cfg.vocab_size):
+            raise ValueError("input token is outside the vocabulary")
+        return a
+
+    def prefill(self, ids, return_all=False):
+        toks = self._ids(ids)
+        if self.failed:
+            raise RuntimeError("A previous device operation failed; call reset() before reusing this model")
+        if self.position + len(toks) > self.ctx:
+            raise ValueError("input would exceed context_length; reset or allocate a larger context")
+        rows = []
+        try:
+            for i, t in enumerate(toks):
+                hidden = self.step(int(t))
+                if return_all or i == len(toks) - 1:
+                    rows.append(self.head(hidden))
+        except Exception:
+            self.failed = True
+            raise
+        return np.stack(rows) if return_all else rows[0]
+
+    def decode(self, token):
+        return self.prefill([token])
+
+    def generate(self, ids, max_new_tokens=32, temperature=0.0, top_k=0, top_p=1.0, seed=17, eos_token_id=None):
+        """Greedy or seeded sampling with the reference's numpy stream (model.py:318-357)."""
+        toks = self._ids(ids)
+        if type(max_new_tokens) is not int or max_new_tokens < 0:
+            raise ValueError("max_new_tokens must be a non-negative integer")
+        if not math.isfinite(temperature) or temperature < 0:
+            raise ValueError("temperature must be finite and non-negative")
+        if type(top_k) is not int or top_k < 0 or not math.isfinite(top_p) or not 0 < top_p <= 1:
+            raise ValueError("top_k must be non-negative and top_p must be in (0,1]")
+        eos = self.cfg.eos_token_id if eos_token_id is None else eos_token_id
+        if type(eos) is not int or not 0 <= eos < self.cfg.vocab_size:
+            raise ValueError("eos_token_id is outside vocabulary")
+        if len(toks) + max(0, max_new_tokens - 1) > self.ctx:
+            raise ValueError("prompt plus requested generation exceeds context_length")
+        self.reset()
+        if max_new_tokens == 0:
+            return []
+        rng = np.random.default_rng(seed)
+        out = []
+        logits = self.prefill(toks)
+        for i in range(max_new_tokens):
+            if not np.all(np.isfinite(logits)):
+                raise FloatingPointError("non-finite output logits")
+            if temperature == 0:
+                tok = int(np.argmax(logits))
+            else:
+                order = np.argsort(-logits, kind="stable")
+                if top_k:
+                    order = order[:top_k]
+                z = logits[order].astype(np.float64) / temperature
+                pr = np.exp(z - z.max())
+                pr /= pr.sum()
+                cut = min(len(order), int(np.searchsorted(np.cumsum(pr), top_p)) + 1)
+                order, pr = order[:cut], pr[:cut]
+                tok = int(rng.choice(order, p=pr / pr.sum()))
+            out.append(tok)
+            if tok == eos or i + 1 == max_new_tokens:
+                break
+            logits = self.decode(tok)
+        return out

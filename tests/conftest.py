@@ -1,0 +1,28 @@
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for path in (ROOT, ROOT / "miraclereasoning-cpu_amd"):
+    if str(path) not in sys.path:
+        sys.path.insert(0, str(path))
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def golden_dir():
+    return GOLDEN
+
+
+@pytest.fixture(scope="session")
+def backend():
+    """One HIPBackend for the whole GPU session (the reference's tests share one
+    OpenCL backend the same way, tests/conftest.py:8-17)."""
+    from miracle_hip import HIPBackend
+    return HIPBackend()
