@@ -1,0 +1,141 @@
+// Internal helpers shared by the library's translation units (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "miracle_hip.h"
+
+namespace mr {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+
+#define MR_HIP(expr, what)                                                                        \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return ::mr::fail(MR_ERR_HIP, std::string(what) + " failed (HIP error " +             \
+                                              std::to_string((int)e_) + ": " + hipGetErrorString(e_) + ")"); \
+    } while (0)
+
+#define MR_REQUIRE(cond, msg)                                                                     \
+    do {                                                                                          \
+        if (!(cond)) return ::mr::fail(MR_ERR_INVALID, msg);                                     \
+    } while (0)
+
+#define MR_TRY(call)                                                                              \
+    do {                                                                                          \
+        int rc_ = (call);                                                                         \
+        if (rc_ != MR_OK) return rc_;                                                             \
+    } while (0)
+
+// Launch-error check after a kernel launch.
+#define MR_LAUNCHED(what) MR_HIP(hipGetLastError(), what)
+
+}  // namespace mr
+
+// The context: one device, one stream, a caching allocator.
+struct mr_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int64_t max_alloc = 0;
+    bool fail_next = false;
+    // size -> free device blocks (all blocks of one size class)
+    std::unordered_map<size_t, std::vector<void *>> free_blocks;
+    std::unordered_map<void *, size_t> live;   // block -> size class
+};
+
+namespace mr {
+
+int ctx_alloc(mr_ctx *ctx, size_t bytes, void **ptr);
+void ctx_release(mr_ctx *ctx, void *ptr);
+
+// ---------------------------------------------------------------- device helpers
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Sum within aligned groups of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Block-wide sum for blockDim.x == nthreads (multiple of 64, <= 1024); uses `scratch`
+// of at least nthreads/64 floats; all threads receive the total.
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < waves; ++w) t += scratch[w];
+    return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float *scratch) {
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int w = 0; w < waves; ++w) t = fmaxf(t, scratch[w]);
+    return t;
+}
+
+// RoPE of one pair at an FP32 angle pos*freq (kernels.cl:38-43).  cos/sin are
+// taken in double and rounded once, which is within half an ulp of the exact
+// value for every angle the models reach.
+__device__ __forceinline__ void rope_pair(float &u, float &v, float pos, float freq) {
+    float a = pos * freq;
+    double ad = (double)a;
+    float c = (float)cos(ad), s = (float)sin(ad);
+    float nu = u * c - v * s;
+    float nv = u * s + v * c;
+    u = nu;
+    v = nv;
+}
+
+// Element j of a weight row of the given storage dtype, widened to FP32.
+template <int DT>
+__device__ __forceinline__ float load_w(const void *w, int64_t i) {
+    if constexpr (DT == MR_F32) return ((const float *)w)[i];
+    else if constexpr (DT == MR_BF16) return bf16_to_f32(((const uint16_t *)w)[i]);
+    else return f16_to_f32(((const uint16_t *)w)[i]);
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- shared launches
+// y[rows, n] = x[rows, k] . W[n, k]^T with FP32 accumulation; dispatches a GEMV
+// (rows == 1) or a tiled GEMM.  Used by the op-level ABI and by the engine.
+int launch_linear(hipStream_t s, const float *x, const void *w, int dtype, float *y, int rows, int n, int k);
+
+}  // namespace mr

@@ -1,0 +1,79 @@
+// Step-level engine internals: model weights, sequence state and step launchers.
+#pragma once
+
+#include <array>
+#include <vector>
+
+#include "attention.h"
+#include "linear.h"
+
+namespace mr {
+
+struct Weight {
+    void *ptr = nullptr;
+    int dtype = MR_F32;
+    int64_t rows = 0, cols = 0;
+    bool owned = true;
+    explicit operator bool() const { return ptr != nullptr; }
+    const float *f() const { return (const float *)ptr; }
+};
+
+struct Mlp {
+    Weight gate, up, down;
+};
+
+struct Layer {
+    bool global = false;
+    int kv_heads = 0;
+    int capacity = 0;          // ring rows
+    Weight a_norm, f_norm, qkv, q_norm, k_norm, o;
+    Mlp ffn;
+    Weight cbr;                // flashnano-1.6 learned queries [slots, h]
+    float *cbr_queries = nullptr;  // RMS-normalized queries (fixed per model)
+    // flashlighting-2.0
+    Weight latent, latent_norm, k_up, v_up, attention_gate, ffn_gate;
+    // heavy-medium-2.0
+    Weight kv_up, router_coarse, router_coarse_bias, router_fine, router_fine_bias, group_bias, expert_bias;
+    std::vector<Mlp> experts, shared;
+    // caches
+    float *ring_k = nullptr, *ring_v = nullptr;        // [capacity, kv_heads*dim] (per inner loop for heavy)
+    float *relay_k = nullptr, *relay_v = nullptr;      // flashnano-1.6 relay
+    int relay_capacity = 0;
+    float *pending = nullptr;                          // flashnano-1.6 chunk rows
+    int splits = 0, split_len = 0;                     // attention plan
+};
+
+enum StepKind { STEP_PLAIN = 0, STEP_LOGITS = 1, STEP_GREEDY = 2, STEP_KINDS = 3 };
+
+}  // namespace mr
+
+struct mr_model {
+    mr_ctx *ctx = nullptr;
+    mr_model_desc d{};
+    std::vector<mr::Layer> layers;
+    mr::Weight embed, output, norm;
+    float *freq = nullptr;
+    bool finalized = false;
+    int position = 0;            // host mirror of *pos_dev
+    // device state (one allocation, see engine.hip)
+    void *state = nullptr;
+    int *pos_dev = nullptr;      // position of the next token
+    int *done_dev = nullptr;     // 0 run; 1 greedy loop hit EOS; 2 non-finite logits
+    int *ids_dev = nullptr;      // [context+1] token per position
+    int *gen_dev = nullptr;      // [context+1] generated tokens; gen_dev[-1] is at count_dev
+    int *count_dev = nullptr;    // number of generated tokens
+    int *eos_dev = nullptr;      // EOS id for the greedy loop (-1 none)
+    int *cbr_skip = nullptr;     // flashnano-1.6: non-zero = no chunk completes this step
+    float *hidden = nullptr, *xnorm = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float *part = nullptr;
+    unsigned *counters = nullptr;
+    float *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;
+    // graphs of one decode step, by StepKind
+    bool use_graph = true;
+    std::array<hipGraphExec_t, mr::STEP_KINDS> exec{};
+    std::array<int, mr::STEP_KINDS> eager_runs{};
+};
+
+namespace mr {
+int record_step(mr_model *m, int kind);   // enqueue one step's kernels on the context stream
+}

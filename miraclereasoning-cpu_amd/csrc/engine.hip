@@ -1,0 +1,779 @@
+// Step-level engine: MiracleModel._step + LM head (model.py:257-308) for one
+// sequence, with weights and caches resident in HBM.
+//
+// One token step of a GQA family (flashnano-1.5/1.6/1.7, flashlite-2.0) is five
+// fused kernels per layer:
+//   1. RMSNorm(hidden, a_norm) -> [Wq;Wk;Wv] GEMV           (model.py:281, 98-99)
+//   2. Q/K RMSNorm + RoPE + ring write + split-key attention (model.py:100-113)
+//   3. Wo GEMV + residual                                    (model.py:116, 282)
+//   4. RMSNorm(hidden, f_norm) -> gate/up GEMV + SwiGLU      (model.py:87-89, 283)
+//   5. Wdown GEMV + residual                                 (model.py:283)
+// plus, for flashnano-1.6, the chunk-end CBR pooling into the relay
+// (model.py:118-144).  The position, the token ids and the greedy-loop state
+// live in device memory, so one step is a fixed launch sequence that is
+// captured once in a hipGraph and replayed for every token.
+#include <cmath>
+#include <cstring>
+
+#include "engine.h"
+
+using namespace mr;
+
+namespace mr {
+namespace {
+
+bool is_gqa(int family) {
+    return family == MR_FAMILY_FLASHNANO_15 || family == MR_FAMILY_FLASHNANO_16 ||
+           family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
+}
+
+int dtype_bytes(int dt) { return dt == MR_F32 ? 4 : 2; }
+
+__device__ __forceinline__ float widen_any(const void *p, int dt, int64_t i) {
+    if (dt == MR_F32) return ((const float *)p)[i];
+    uint32_t b = ((const uint16_t *)p)[i];
+    return dt == MR_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+}
+
+// hidden = embed[ids[pos]] widened (model.py:259).
+__global__ void k_embed(const void *table, int dt, const int *ids, const int *pos, const int *done, float *hidden,
+                        int h) {
+    if (*done) return;
+    int tok = ids[*pos];
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < h; j += gridDim.x * blockDim.x)
+        hidden[j] = widen_any(table, dt, (int64_t)tok * h + j);
+}
+
+__global__ void k_advance(int *pos, const int *done) {
+    if (!*done) *pos += 1;
+}
+
+// Greedy token choice over logits (np.argmax: first maximum), the finiteness
+// check of model.py:339-342, then optional position advance, token append and
+// EOS stop.
+__global__ void __launch_bounds__(1024) k_argmax(const float *logits, int n, int *pos, int *done, int *ids,
+                                                 int *gen, int *count, const int *eos, int advance) {
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    __shared__ int bad;
+    if (*done) return;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    float best = -INFINITY;
+    int idx = n;
+    bool nonfinite = false;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = logits[i];
+        if (!isfinite(v)) nonfinite = true;
+        if (v > best || (v == best && i < idx)) {
+            best = v;
+            idx = i;
+        }
+    }
+    if (nonfinite) atomicOr(&bad, 1);
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            float ov = bv[threadIdx.x + s];
+            int oi = bi[threadIdx.x + s];
+            if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
+                bv[threadIdx.x] = ov;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        int p = *pos;
+        if (advance) *pos = ++p;
+        if (bad) {
+            *done = 2;
+            return;
+        }
+        int tok = bi[0];
+        ids[p] = tok;
+        gen[*count] = tok;
+        *count += 1;
+        if (tok == *eos) *done = 1;
+    }
+}
+
+// ---- flashnano-1.6 CBR (model.py:118-144) -----------------------------------
+// Stores this step's normalized input in the pending chunk; at a chunk end pools
+// it into `slots` rows with learned queries (kernels.cl:110-130).  Block m pools
+// slot m.
+__global__ void __launch_bounds__(256) k_cbr_pool(const float *xnorm, float *pending, const float *queries,
+                                                  float *pooled, float *anchors, int *skip_flag, const int *pos_p,
+                                                  const int *done, int chunk, int h) {
+    extern __shared__ float sp[];   // [chunk] probabilities, then reduction scratch
+    float *red = sp + chunk;
+    const int pos = *pos_p;
+    const bool skip = *done || (pos % chunk != chunk - 1);
+    if (blockIdx.x == 0) {
+        if (threadIdx.x == 0) *skip_flag = skip ? 1 : 0;
+        if (!*done)
+            for (int j = threadIdx.x; j < h; j += blockDim.x) pending[(int64_t)(pos % chunk) * h + j] = xnorm[j];
+    }
+    if (skip) return;
+    const int m = blockIdx.x;
+    const float *q = queries + (int64_t)m * h;
+    auto row = [&](int t) -> const float * { return t == chunk - 1 ? xnorm : pending + (int64_t)t * h; };
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int t = wave; t < chunk; t += blockDim.x / 64) {
+        const float *u = row(t);
+        float acc = 0.0f;
+        for (int j = lane; j < h; j += 64) acc = fmaf(u[j], q[j], acc);
+        acc = wave_sum(acc);
+        if (lane == 0) sp[t] = acc / sqrtf((float)h);
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) mx = fmaxf(mx, sp[t]);
+    mx = block_max(mx, red);
+    float den = 0.0f;
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) den += expf(sp[t] - mx);
+    den = block_sum(den, red);
+    __syncthreads();
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) sp[t] = expf(sp[t] - mx) / den;
+    __syncthreads();
+    const int start_position = pos + 1 - chunk;
+    for (int j = threadIdx.x; j < h; j += blockDim.x) {
+        float v = 0.0f;
+        for (int t = 0; t < chunk; ++t) v = fmaf(sp[t], row(t)[j], v);
+        pooled[(int64_t)m * h + j] = v;
+    }
+    if (threadIdx.x == 0) {
+        float ps = 0.0f;
+        for (int t = 0; t < chunk; ++t) ps = fmaf(sp[t], (float)(start_position + t), ps);
+        anchors[m] = rintf(ps);
+    }
+}
+
+// Pooled rows through Wk and Wv (model.py:135): one wave per output value.
+__global__ void __launch_bounds__(256) k_cbr_project(const float *pooled, const void *wkv, int dt, float *out,
+                                                     const int *skip_flag, int kvw2, int h) {
+    if (*skip_flag) return;
+    const int m = blockIdx.y, lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= kvw2) return;
+    const float *x = pooled + (int64_t)m * h;
+    float acc = 0.0f;
+    for (int j = lane; j < h; j += 64) acc = fmaf(widen_any(wkv, dt, (int64_t)o * h + j), x[j], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) out[(int64_t)m * kvw2 + o] = acc;
+}
+
+// K-norm + RoPE at the pooled anchors, then relay append (model.py:136-144).
+__global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float *anchors, const float *k_gain,
+                                                    float eps, const float *freq, int split_half, float *relay_k,
+                                                    float *relay_v, const int *skip_flag, const int *pos_p,
+                                                    int chunk, int slots, int kv_heads, int d) {
+    extern __shared__ float kr[];
+    if (*skip_flag) return;
+    const int m = blockIdx.x, kvw = kv_heads * d;
+    const float *src = kv + (int64_t)m * 2 * kvw;
+    for (int j = threadIdx.x; j < kvw; j += blockDim.x) kr[j] = src[j];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int hh = wave; hh < kv_heads; hh += blockDim.x / 64) {
+        float *row = kr + hh * d;
+        float ss = 0.0f;
+        for (int j = lane; j < d; j += 64) ss = fmaf(row[j], row[j], ss);
+        ss = wave_sum(ss);
+        float scale = 1.0f / sqrtf(ss / (float)d + eps);
+        for (int j = lane; j < d; j += 64) row[j] = row[j] * scale * k_gain[j];
+    }
+    __syncthreads();
+    const int half = d / 2;
+    for (int i = threadIdx.x; i < kv_heads * half; i += blockDim.x) {
+        int hh = i / half, p = i % half;
+        float *row = kr + hh * d;
+        int j = split_half ? p : 2 * p, k = split_half ? p + half : 2 * p + 1;
+        float u = row[j], v = row[k];
+        rope_pair(u, v, anchors[m], freq[p]);
+        row[j] = u;
+        row[k] = v;
+    }
+    __syncthreads();
+    const int64_t dst = ((int64_t)(*pos_p / chunk) * slots + m) * kvw;
+    for (int j = threadIdx.x; j < kvw; j += blockDim.x) {
+        relay_k[dst + j] = kr[j];
+        relay_v[dst + j] = src[kvw + j];
+    }
+}
+
+// Non-affine RMSNorm of the learned CBR queries, once per model (model.py:126-127).
+__global__ void __launch_bounds__(256) k_rows_rms(const void *x, int dt, float *y, int width, float eps) {
+    __shared__ float red[4];
+    const int64_t base = (int64_t)blockIdx.x * width;
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) {
+        float v = widen_any(x, dt, base + j);
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, red);
+    float scale = 1.0f / sqrtf(ss / (float)width + eps);
+    for (int j = threadIdx.x; j < width; j += blockDim.x) y[base + j] = widen_any(x, dt, base + j) * scale;
+}
+
+// ------------------------------------------------------------------ host helpers
+int device_alloc(mr_model *m, size_t bytes, void **p) {
+    MR_HIP(hipMalloc(p, bytes ? bytes : 16), "allocate model buffer");
+    (void)m;
+    return MR_OK;
+}
+
+struct Expect {
+    int64_t rows, cols;
+};
+
+int expected_shape(const mr_model *m, int kind, int layer, Expect *e) {
+    const mr_model_desc &d = m->d;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * d.head_dim;
+    int kvh = layer >= 0 ? m->layers[layer].kv_heads : d.kv_heads;
+    int kvw = kvh * hd;
+    int inner = d.latent_dim ? d.latent_dim : h;
+    switch (kind) {
+        case MR_W_EMBED: case MR_W_OUTPUT: *e = {d.vocab_size, h}; return MR_OK;
+        case MR_W_NORM: case MR_W_A_NORM: case MR_W_F_NORM: *e = {h, 1}; return MR_OK;
+        case MR_W_Q: *e = {qd, h}; return MR_OK;
+        case MR_W_K: case MR_W_V: *e = {kvw, inner}; return MR_OK;
+        case MR_W_O: *e = {h, qd}; return MR_OK;
+        case MR_W_Q_NORM: case MR_W_K_NORM: *e = {hd, 1}; return MR_OK;
+        case MR_W_GATE: case MR_W_UP: case MR_W_SHARED_GATE: case MR_W_SHARED_UP: *e = {d.ffn_dim, h}; return MR_OK;
+        case MR_W_DOWN: case MR_W_SHARED_DOWN: *e = {h, d.ffn_dim}; return MR_OK;
+        case MR_W_LATENT: *e = {d.latent_dim, h}; return MR_OK;
+        case MR_W_LATENT_NORM: *e = {d.latent_dim, 1}; return MR_OK;
+        case MR_W_KV_UP: *e = {2 * kvw, d.latent_dim}; return MR_OK;
+        case MR_W_ATTENTION_GATE: case MR_W_FFN_GATE: *e = {1, 1}; return MR_OK;
+        case MR_W_CBR: *e = {d.cbr_slots, h}; return MR_OK;
+        case MR_W_ROUTER_COARSE: *e = {d.router_groups, h}; return MR_OK;
+        case MR_W_ROUTER_FINE: *e = {d.routed_experts, h}; return MR_OK;
+        case MR_W_ROUTER_COARSE_BIAS: case MR_W_ROUTER_GROUP_BIAS: *e = {d.router_groups, 1}; return MR_OK;
+        case MR_W_ROUTER_FINE_BIAS: case MR_W_ROUTER_EXPERT_BIAS: *e = {d.routed_experts, 1}; return MR_OK;
+    }
+    return fail(MR_ERR_INVALID, "unknown weight kind " + std::to_string(kind));
+}
+
+bool is_vector_kind(int kind) {
+    switch (kind) {
+        case MR_W_NORM: case MR_W_A_NORM: case MR_W_F_NORM: case MR_W_Q_NORM: case MR_W_K_NORM:
+        case MR_W_LATENT_NORM: case MR_W_ATTENTION_GATE: case MR_W_FFN_GATE: case MR_W_ROUTER_COARSE_BIAS:
+        case MR_W_ROUTER_FINE_BIAS: case MR_W_ROUTER_GROUP_BIAS: case MR_W_ROUTER_EXPERT_BIAS:
+            return true;
+    }
+    return false;
+}
+
+int upload_into(mr_model *m, Weight &w, const void *host, int dtype, int64_t rows, int64_t cols) {
+    size_t bytes = (size_t)rows * cols * dtype_bytes(dtype);
+    if (!w.ptr) MR_TRY(device_alloc(m, bytes, &w.ptr));
+    w.dtype = dtype;
+    w.rows = rows;
+    w.cols = cols;
+    MR_HIP(hipMemcpy(w.ptr, host, bytes, hipMemcpyHostToDevice), "upload weight");
+    return MR_OK;
+}
+
+Weight *weight_slot(mr_model *m, int kind, int layer, int expert) {
+    if (layer < 0) {
+        switch (kind) {
+            case MR_W_EMBED: return &m->embed;
+            case MR_W_OUTPUT: return &m->output;
+            case MR_W_NORM: return &m->norm;
+        }
+        return nullptr;
+    }
+    Layer &L = m->layers[layer];
+    const bool heavy = m->d.family == MR_FAMILY_HEAVY_MEDIUM_20;
+    switch (kind) {
+        case MR_W_A_NORM: return &L.a_norm;
+        case MR_W_F_NORM: return &L.f_norm;
+        case MR_W_O: return &L.o;
+        case MR_W_Q_NORM: return &L.q_norm;
+        case MR_W_K_NORM: return &L.k_norm;
+        case MR_W_LATENT: return &L.latent;
+        case MR_W_LATENT_NORM: return &L.latent_norm;
+        case MR_W_KV_UP: return &L.kv_up;
+        case MR_W_ATTENTION_GATE: return &L.attention_gate;
+        case MR_W_FFN_GATE: return &L.ffn_gate;
+        case MR_W_CBR: return &L.cbr;
+        case MR_W_ROUTER_COARSE: return &L.router_coarse;
+        case MR_W_ROUTER_COARSE_BIAS: return &L.router_coarse_bias;
+        case MR_W_ROUTER_FINE: return &L.router_fine;
+        case MR_W_ROUTER_FINE_BIAS: return &L.router_fine_bias;
+        case MR_W_ROUTER_GROUP_BIAS: return &L.group_bias;
+        case MR_W_ROUTER_EXPERT_BIAS: return &L.expert_bias;
+        case MR_W_GATE: case MR_W_UP: case MR_W_DOWN: {
+            Mlp *mlp = &L.ffn;
+            if (heavy) {
+                if (expert < 0 || expert >= (int)L.experts.size()) return nullptr;
+                mlp = &L.experts[expert];
+            }
+            return kind == MR_W_GATE ? &mlp->gate : kind == MR_W_UP ? &mlp->up : &mlp->down;
+        }
+        case MR_W_SHARED_GATE: case MR_W_SHARED_UP: case MR_W_SHARED_DOWN: {
+            if (expert < 0 || expert >= (int)L.shared.size()) return nullptr;
+            Mlp &mlp = L.shared[expert];
+            return kind == MR_W_SHARED_GATE ? &mlp.gate : kind == MR_W_SHARED_UP ? &mlp.up : &mlp.down;
+        }
+    }
+    return nullptr;
+}
+
+void free_weight(Weight &w) {
+    if (w.ptr && w.owned) hipFree(w.ptr);
+    w.ptr = nullptr;
+}
+
+// Launch the kernels of one token step on the context stream.
+int record_gqa_layer(mr_model *m, Layer &L, int li) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    const int dt = L.qkv.dtype;
+    // 1. RMSNorm -> fused Q/K/V projection.
+    GemvArgs g;
+    g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
+    g.n = qd + 2 * kvw; g.k = h; g.y = m->qkv; g.done = m->done_dev;
+    if (d.family == MR_FAMILY_FLASHNANO_16) g.x_out = m->xnorm;
+    MR_TRY(launch_gemv(s, dt, PRO_RMS, EPI_STORE, g));
+    // 2. Q/K norm + RoPE + ring write + attention.
+    AttnStepArgs a;
+    a.q = m->qkv; a.k_new = m->qkv + qd; a.v_new = m->qkv + qd + kvw;
+    if (d.qk_norm) { a.q_gain = L.q_norm.f(); a.k_gain = L.k_norm.f(); }
+    a.eps = d.norm_eps; a.freq = m->freq; a.split_half = d.split_half_rope;
+    a.pos = m->pos_dev; a.done = m->done_dev;
+    a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.capacity = L.capacity;
+    if (d.family == MR_FAMILY_FLASHNANO_16) {
+        a.extra_k = L.relay_k; a.extra_v = L.relay_v;
+        a.extra_chunk = d.cbr_chunk_size; a.extra_slots = d.cbr_slots;
+    }
+    a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.dim = hd;
+    a.part = m->part; a.counters = m->counters; a.out = m->attn;
+    a.splits = L.splits; a.split_len = L.split_len;
+    MR_TRY(launch_attention_step(s, a));
+    // flashnano-1.6: chunk pooling into the relay, after this step's attention.
+    if (d.family == MR_FAMILY_FLASHNANO_16) {
+        const int chunk = d.cbr_chunk_size, slots = d.cbr_slots;
+        size_t lds = (size_t)(chunk + 8) * sizeof(float);
+        k_cbr_pool<<<slots, 256, lds, s>>>(m->xnorm, L.pending, L.cbr_queries, m->cbr_pooled, m->cbr_anchor,
+                                            m->cbr_skip, m->pos_dev, m->done_dev, chunk, h);
+        MR_LAUNCHED("enqueue cbr pool");
+        const void *wkv = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(dt);
+        k_cbr_project<<<dim3(ceil_div(2 * kvw, 4), slots), 256, 0, s>>>(m->cbr_pooled, wkv, dt, m->cbr_kv,
+                                                                         m->cbr_skip, 2 * kvw, h);
+        MR_LAUNCHED("enqueue cbr project");
+        k_cbr_finish<<<slots, 256, (size_t)kvw * sizeof(float), s>>>(
+            m->cbr_kv, m->cbr_anchor, L.k_norm.f(), d.norm_eps, m->freq, d.split_half_rope, L.relay_k, L.relay_v,
+            m->cbr_skip, m->pos_dev, chunk, slots, L.kv_heads, hd);
+        MR_LAUNCHED("enqueue cbr finish");
+    }
+    // 3. o projection + residual.
+    GemvArgs o;
+    o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->hidden; o.scale = d.residual_scale;
+    o.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_RESIDUAL, o));
+    // 4. RMSNorm -> gate/up + SwiGLU.
+    GemvArgs gu;
+    gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->hidden; gu.gain = L.f_norm.f(); gu.eps = d.norm_eps;
+    gu.n = d.ffn_dim; gu.k = h; gu.y = m->act; gu.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_RMS, EPI_SWIGLU, gu));
+    // 5. down projection + residual.
+    GemvArgs dn;
+    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden; dn.scale = d.residual_scale;
+    dn.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_RESIDUAL, dn));
+    (void)li;
+    return MR_OK;
+}
+
+int record_head(mr_model *m, int kind) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    if (kind == STEP_PLAIN) {
+        k_advance<<<1, 1, 0, s>>>(m->pos_dev, m->done_dev);
+        MR_LAUNCHED("enqueue advance");
+        return MR_OK;
+    }
+    const Weight &head = d.tie_embeddings ? m->embed : m->output;
+    GemvArgs g;
+    g.w = head.ptr; g.x = m->hidden; g.gain = m->norm.f(); g.eps = d.norm_eps;
+    g.n = d.vocab_size; g.k = d.hidden_size; g.y = m->logits; g.done = m->done_dev;
+    MR_TRY(launch_gemv(s, head.dtype, PRO_RMS, EPI_STORE, g));
+    if (kind == STEP_LOGITS) {
+        k_advance<<<1, 1, 0, s>>>(m->pos_dev, m->done_dev);
+        MR_LAUNCHED("enqueue advance");
+    } else {
+        k_argmax<<<1, 1024, 0, s>>>(m->logits, d.vocab_size, m->pos_dev, m->done_dev, m->ids_dev, m->gen_dev,
+                                    m->count_dev, m->eos_dev, 1);
+        MR_LAUNCHED("enqueue argmax");
+    }
+    return MR_OK;
+}
+
+}  // namespace
+
+int record_step(mr_model *m, int kind) {
+    hipStream_t s = m->ctx->stream;
+    const mr_model_desc &d = m->d;
+    k_embed<<<ceil_div(d.hidden_size, 256), 256, 0, s>>>(m->embed.ptr, m->embed.dtype, m->ids_dev, m->pos_dev,
+                                                         m->done_dev, m->hidden, d.hidden_size);
+    MR_LAUNCHED("enqueue embed");
+    for (int li = 0; li < d.layers; ++li) MR_TRY(record_gqa_layer(m, m->layers[li], li));
+    return record_head(m, kind);
+}
+
+namespace {
+
+int run_step(mr_model *m, int kind) {
+    hipStream_t s = m->ctx->stream;
+    if (!m->use_graph) return record_step(m, kind);
+    if (!m->exec[kind]) {
+        // The first run of each step kind is eager (it also checks every launch
+        // configuration); the second captures the same sequence.
+        if (m->eager_runs[kind] == 0) {
+            m->eager_runs[kind] = 1;
+            return record_step(m, kind);
+        }
+        hipGraph_t graph = nullptr;
+        MR_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin step capture");
+        int rc = record_step(m, kind);
+        hipError_t e = hipStreamEndCapture(s, &graph);
+        if (rc != MR_OK) {
+            if (graph) hipGraphDestroy(graph);
+            return rc;
+        }
+        MR_HIP(e, "end step capture");
+        hipError_t ie = hipGraphInstantiate(&m->exec[kind], graph, nullptr, nullptr, 0);
+        hipGraphDestroy(graph);
+        MR_HIP(ie, "instantiate step graph");
+    }
+    MR_HIP(hipGraphLaunch(m->exec[kind], s), "launch step graph");
+    return MR_OK;
+}
+
+int check_ctx(mr_model *m, const char *what) {
+    MR_REQUIRE(m, std::string(what) + ": null model");
+    if (m->ctx->fail_next) {
+        m->ctx->fail_next = false;
+        return fail(MR_ERR_INJECTED, std::string(what) + ": injected failure");
+    }
+    if (!m->finalized) return fail(MR_ERR_STATE, std::string(what) + ": model not finalized");
+    MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    return MR_OK;
+}
+
+void destroy_graphs(mr_model *m) {
+    for (auto &e : m->exec)
+        if (e) {
+            hipGraphExecDestroy(e);
+            e = nullptr;
+        }
+    m->eager_runs.fill(0);
+}
+
+}  // namespace
+}  // namespace mr
+
+extern "C" {
+
+int mr_model_create(mr_ctx *ctx, const mr_model_desc *desc, mr_model **out) {
+    MR_REQUIRE(ctx && desc && out, "mr_model_create: null argument");
+    const mr_model_desc &d = *desc;
+    MR_REQUIRE(d.family >= 0 && d.family <= MR_FAMILY_HEAVY_MEDIUM_20, "unsupported family");
+    MR_REQUIRE(d.vocab_size > 0 && d.hidden_size > 0 && d.layers > 0 && d.layers <= 128 && d.query_heads > 0 &&
+                   d.kv_heads > 0 && d.head_dim > 0 && d.head_dim % 2 == 0 && d.ffn_dim > 0 &&
+                   d.context_length > 0 && d.query_heads % d.kv_heads == 0,
+               "invalid model geometry");
+    if (!is_gqa(d.family))
+        return fail(MR_ERR_INVALID, "this library build runs the GQA families (flashnano-1.5/1.6/1.7, "
+                                    "flashlite-2.0) only");
+    if (d.family == MR_FAMILY_FLASHNANO_16)
+        MR_REQUIRE(d.cbr_chunk_size > 0 && d.cbr_slots > 0, "FlashNano 1.6 requires CBR chunk size and slots");
+    mr_model *m = new mr_model();
+    m->ctx = ctx;
+    m->d = d;
+    m->layers.resize(d.layers);
+    for (int i = 0; i < d.layers; ++i) {
+        Layer &L = m->layers[i];
+        uint64_t bit = i < 64 ? (d.global_layer_mask_lo >> i) & 1 : (d.global_layer_mask_hi >> (i - 64)) & 1;
+        L.global = bit != 0;
+        L.kv_heads = L.global && d.global_kv_heads ? d.global_kv_heads : d.kv_heads;
+        // model.py:105 capacity = min(window or ctx, ctx)
+        int win = L.global ? 0 : d.window;
+        L.capacity = win > 0 ? std::min(win, d.context_length) : d.context_length;
+        MR_REQUIRE(d.query_heads % L.kv_heads == 0, "query heads must divide into KV groups");
+    }
+    *out = m;
+    return MR_OK;
+}
+
+int mr_model_destroy(mr_model *m) {
+    if (!m) return MR_OK;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    destroy_graphs(m);
+    free_weight(m->embed);
+    free_weight(m->output);
+    free_weight(m->norm);
+    for (Layer &L : m->layers) {
+        for (Weight *w : {&L.a_norm, &L.f_norm, &L.qkv, &L.q_norm, &L.k_norm, &L.o, &L.ffn.gate, &L.ffn.up,
+                          &L.ffn.down, &L.cbr, &L.latent, &L.latent_norm, &L.k_up, &L.v_up, &L.attention_gate,
+                          &L.ffn_gate, &L.kv_up, &L.router_coarse, &L.router_coarse_bias, &L.router_fine,
+                          &L.router_fine_bias, &L.group_bias, &L.expert_bias})
+            free_weight(*w);
+        for (Mlp &e : L.experts) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
+        for (Mlp &e : L.shared) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
+        for (float *p : {L.ring_k, L.ring_v, L.relay_k, L.relay_v, L.pending, L.cbr_queries})
+            if (p) hipFree(p);
+    }
+    if (m->freq) hipFree(m->freq);
+    if (m->state) hipFree(m->state);
+    delete m;
+    return MR_OK;
+}
+
+int mr_model_set_weight(mr_model *m, int kind, int layer, int expert, const void *host, int dtype, int64_t rows,
+                        int64_t cols) {
+    MR_REQUIRE(m && host, "set_weight: null argument");
+    MR_REQUIRE(dtype == MR_F32 || dtype == MR_BF16 || dtype == MR_F16, "set_weight: unknown dtype");
+    MR_REQUIRE(layer >= -1 && layer < m->d.layers, "set_weight: layer out of range");
+    MR_REQUIRE(!m->finalized, "set_weight: model already finalized");
+    MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    Expect e;
+    MR_TRY(expected_shape(m, kind, layer, &e));
+    if (rows != e.rows || cols != e.cols)
+        return fail(MR_ERR_INVALID, "weight kind " + std::to_string(kind) + " layer " + std::to_string(layer) +
+                                        ": expected (" + std::to_string(e.rows) + ", " + std::to_string(e.cols) +
+                                        "), got (" + std::to_string(rows) + ", " + std::to_string(cols) + ")");
+    if (is_vector_kind(kind)) MR_REQUIRE(dtype == MR_F32, "set_weight: 1-D tensors must be float32");
+    const bool model_level = kind == MR_W_EMBED || kind == MR_W_OUTPUT || kind == MR_W_NORM;
+    MR_REQUIRE(model_level == (layer < 0), "set_weight: layer index does not match weight kind");
+    if (is_gqa(m->d.family) && (kind == MR_W_Q || kind == MR_W_K || kind == MR_W_V)) {
+        // Pack [Wq; Wk; Wv] so one GEMV produces the whole projection.
+        Layer &L = m->layers[layer];
+        const int64_t h = m->d.hidden_size, qd = (int64_t)m->d.query_heads * m->d.head_dim;
+        const int64_t kvw = (int64_t)L.kv_heads * m->d.head_dim;
+        const int64_t total = qd + 2 * kvw;
+        if (!L.qkv.ptr) {
+            MR_TRY(device_alloc(m, (size_t)total * h * dtype_bytes(dtype), &L.qkv.ptr));
+            L.qkv.dtype = dtype;
+            L.qkv.rows = 0;
+            L.qkv.cols = h;
+        }
+        MR_REQUIRE(L.qkv.dtype == dtype, "set_weight: q, k and v must share one dtype");
+        int64_t row0 = kind == MR_W_Q ? 0 : kind == MR_W_K ? qd : qd + kvw;
+        char *dst = (char *)L.qkv.ptr + (size_t)row0 * h * dtype_bytes(dtype);
+        MR_HIP(hipMemcpy(dst, host, (size_t)rows * cols * dtype_bytes(dtype), hipMemcpyHostToDevice),
+               "upload weight");
+        L.qkv.rows |= kind == MR_W_Q ? 1 : kind == MR_W_K ? 2 : 4;   // presence bits until finalize
+        return MR_OK;
+    }
+    Weight *slot = weight_slot(m, kind, layer, expert);
+    MR_REQUIRE(slot, "set_weight: weight kind not used by this family or expert index out of range");
+    if (slot->ptr && slot->dtype != dtype) free_weight(*slot);
+    return upload_into(m, *slot, host, dtype, rows, cols);
+}
+
+int mr_model_set_rope(mr_model *m, const float *inv_freq, int count) {
+    MR_REQUIRE(m && inv_freq && count == m->d.head_dim / 2, "set_rope: expected head_dim/2 frequencies");
+    MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    if (!m->freq) MR_TRY(device_alloc(m, count * sizeof(float), (void **)&m->freq));
+    MR_HIP(hipMemcpy(m->freq, inv_freq, count * sizeof(float), hipMemcpyHostToDevice), "upload rope table");
+    return MR_OK;
+}
+
+int mr_model_finalize(mr_model *m) {
+    MR_REQUIRE(m, "finalize: null model");
+    if (m->finalized) return MR_OK;
+    MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    const mr_model_desc &d = m->d;
+    auto need = [&](const Weight &w, const char *name, int layer) -> int {
+        if (!w.ptr)
+            return fail(MR_ERR_STATE, std::string("missing weight ") + name +
+                                          (layer >= 0 ? " in layer " + std::to_string(layer) : std::string()));
+        return MR_OK;
+    };
+    MR_TRY(need(m->embed, "embed", -1));
+    MR_TRY(need(m->norm, "norm", -1));
+    if (!d.tie_embeddings) MR_TRY(need(m->output, "output", -1));
+    MR_REQUIRE(m->freq, "finalize: RoPE table not set");
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd;
+    int max_kvw = 0, max_kvh = 0;
+    size_t max_part = 0;
+    for (int i = 0; i < d.layers; ++i) {
+        Layer &L = m->layers[i];
+        MR_TRY(need(L.a_norm, "a_norm", i));
+        MR_TRY(need(L.f_norm, "f_norm", i));
+        MR_TRY(need(L.o, "o", i));
+        if (L.qkv.rows != 7) return fail(MR_ERR_STATE, "missing q/k/v weight in layer " + std::to_string(i));
+        L.qkv.rows = qd + 2 * (int64_t)L.kv_heads * hd;
+        if (d.qk_norm) {
+            MR_TRY(need(L.q_norm, "q_norm", i));
+            MR_TRY(need(L.k_norm, "k_norm", i));
+        }
+        MR_TRY(need(L.ffn.gate, "ffn.gate", i));
+        MR_TRY(need(L.ffn.up, "ffn.up", i));
+        MR_TRY(need(L.ffn.down, "ffn.down", i));
+        MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
+        const int kvw = L.kv_heads * hd;
+        max_kvw = std::max(max_kvw, kvw);
+        max_kvh = std::max(max_kvh, L.kv_heads);
+        size_t ring = (size_t)L.capacity * kvw * sizeof(float);
+        MR_TRY(device_alloc(m, ring, (void **)&L.ring_k));
+        MR_TRY(device_alloc(m, ring, (void **)&L.ring_v));
+        MR_HIP(hipMemset(L.ring_k, 0, ring), "clear ring");
+        MR_HIP(hipMemset(L.ring_v, 0, ring), "clear ring");
+        int extra_max = 0;
+        if (d.family == MR_FAMILY_FLASHNANO_16) {
+            MR_TRY(need(L.cbr, "cbr", i));
+            L.relay_capacity = (d.context_length / d.cbr_chunk_size) * d.cbr_slots;
+            extra_max = L.relay_capacity;
+            size_t relay = (size_t)std::max(L.relay_capacity, 1) * kvw * sizeof(float);
+            MR_TRY(device_alloc(m, relay, (void **)&L.relay_k));
+            MR_TRY(device_alloc(m, relay, (void **)&L.relay_v));
+            int prow = std::min(d.cbr_chunk_size, d.context_length);
+            MR_TRY(device_alloc(m, (size_t)prow * h * sizeof(float), (void **)&L.pending));
+            MR_TRY(device_alloc(m, (size_t)d.cbr_slots * h * sizeof(float), (void **)&L.cbr_queries));
+            k_rows_rms<<<d.cbr_slots, 256, 0, m->ctx->stream>>>(L.cbr.ptr, L.cbr.dtype, L.cbr_queries, h,
+                                                                d.cbr_norm_eps);
+            MR_LAUNCHED("normalize cbr queries");
+        }
+        attention_plan(L.capacity + extra_max, L.kv_heads, &L.splits, &L.split_len);
+        max_part = std::max(max_part, attention_part_floats(d.query_heads, L.kv_heads, hd, L.splits));
+    }
+    // One allocation for all per-sequence scalars and activation vectors.
+    const int ctxn = d.context_length + 2;
+    const int slots = std::max(d.cbr_slots, 1);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t at = off;
+        off += (bytes + 255) / 256 * 256;
+        return at;
+    };
+    size_t o_ints = take(8 * sizeof(int));
+    size_t o_ids = take((size_t)ctxn * sizeof(int));
+    size_t o_gen = take((size_t)ctxn * sizeof(int));
+    size_t o_hidden = take((size_t)h * sizeof(float));
+    size_t o_xnorm = take((size_t)h * sizeof(float));
+    size_t o_qkv = take((size_t)(qd + 2 * max_kvw) * sizeof(float));
+    size_t o_attn = take((size_t)qd * sizeof(float));
+    size_t o_act = take((size_t)d.ffn_dim * sizeof(float));
+    size_t o_logits = take((size_t)d.vocab_size * sizeof(float));
+    size_t o_part = take(max_part * sizeof(float));
+    size_t o_cnt = take((size_t)std::max(max_kvh, 1) * sizeof(unsigned));
+    size_t o_pool = take((size_t)slots * h * sizeof(float));
+    size_t o_anchor = take((size_t)slots * sizeof(float));
+    size_t o_cbrkv = take((size_t)slots * 2 * max_kvw * sizeof(float));
+    MR_TRY(device_alloc(m, off, &m->state));
+    MR_HIP(hipMemset(m->state, 0, off), "clear model state");
+    char *base = (char *)m->state;
+    int *ints = (int *)(base + o_ints);
+    m->pos_dev = ints + 0;
+    m->done_dev = ints + 1;
+    m->count_dev = ints + 2;
+    m->eos_dev = ints + 3;
+    m->cbr_skip = ints + 4;
+    m->ids_dev = (int *)(base + o_ids);
+    m->gen_dev = (int *)(base + o_gen);
+    m->hidden = (float *)(base + o_hidden);
+    m->xnorm = (float *)(base + o_xnorm);
+    m->qkv = (float *)(base + o_qkv);
+    m->attn = (float *)(base + o_attn);
+    m->act = (float *)(base + o_act);
+    m->logits = (float *)(base + o_logits);
+    m->part = (float *)(base + o_part);
+    m->counters = (unsigned *)(base + o_cnt);
+    m->cbr_pooled = (float *)(base + o_pool);
+    m->cbr_anchor = (float *)(base + o_anchor);
+    m->cbr_kv = (float *)(base + o_cbrkv);
+    MR_HIP(hipDeviceSynchronize(), "finalize model");
+    m->finalized = true;
+    m->position = 0;
+    return MR_OK;
+}
+
+int mr_model_reset(mr_model *m) {
+    MR_REQUIRE(m, "reset: null model");
+    if (!m->finalized) return MR_OK;
+    MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    // Caches are overwritten before they are read (ring rows by position, the
+    // relay by chunk), so a reset only rewinds the position.
+    MR_HIP(hipMemsetAsync(m->pos_dev, 0, 4 * sizeof(int), m->ctx->stream), "reset position");
+    MR_HIP(hipStreamSynchronize(m->ctx->stream), "reset");
+    m->position = 0;
+    return MR_OK;
+}
+
+int mr_model_position(mr_model *m, int *position) {
+    MR_REQUIRE(m && position, "position: null argument");
+    *position = m->position;
+    return MR_OK;
+}
+
+int mr_model_use_graph(mr_model *m, int enable) {
+    MR_REQUIRE(m, "use_graph: null model");
+    m->use_graph = enable != 0;
+    if (!m->use_graph) destroy_graphs(m);
+    return MR_OK;
+}
+
+int mr_model_forward(mr_model *m, const int32_t *ids, int n, int flags, float *logits) {
+    MR_TRY(check_ctx(m, "forward"));
+    MR_REQUIRE(ids && n > 0, "forward: input_ids must be a non-empty 1D integer sequence");
+    const mr_model_desc &d = m->d;
+    for (int i = 0; i < n; ++i)
+        MR_REQUIRE(ids[i] >= 0 && ids[i] < d.vocab_size, "forward: input token is outside the vocabulary");
+    if (m->position + n > d.context_length)
+        return fail(MR_ERR_INVALID, "input would exceed context_length; reset or allocate a larger context");
+    if (flags & MR_FWD_BATCHED)
+        return fail(MR_ERR_INVALID, "forward: batched prefill is not available in this build");
+    hipStream_t s = m->ctx->stream;
+    MR_HIP(hipMemcpyAsync(m->ids_dev + m->position, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s),
+           "upload token ids");
+    MR_HIP(hipMemsetAsync(m->done_dev, 0, sizeof(int), s), "clear stop flag");
+    const bool all = (flags & MR_FWD_RETURN_ALL) != 0;
+    for (int i = 0; i < n; ++i) {
+        const bool want = all || i == n - 1;
+        MR_TRY(run_step(m, want ? STEP_LOGITS : STEP_PLAIN));
+        if (want && logits) {
+            float *dst = logits + (all ? (size_t)i * d.vocab_size : 0);
+            MR_HIP(hipMemcpyAsync(dst, m->logits, (size_t)d.vocab_size * sizeof(float), hipMemcpyDeviceToHost, s),
+                   "read logits");
+        }
+    }
+    MR_HIP(hipStreamSynchronize(s), "forward");
+    m->position += n;
+    return MR_OK;
+}
+
+int mr_model_generate_greedy(mr_model *m, int max_new, int eos, int32_t *tokens, int *produced) {
+    MR_TRY(check_ctx(m, "generate"));
+    MR_REQUIRE(tokens && produced && max_new >= 1, "generate: bad arguments");
+    MR_REQUIRE(m->position >= 1, "generate: call forward first");
+    MR_REQUIRE(m->position + max_new - 1 <= m->d.context_length, "generate: exceeds context_length");
+    hipStream_t s = m->ctx->stream;
+    int init[3] = {0, 0, eos};   // done, count, eos
+    MR_HIP(hipMemcpyAsync(m->done_dev, init, sizeof(init), hipMemcpyHostToDevice, s), "arm greedy loop");
+    // Choice from the logits of the last forward, without a step.
+    k_argmax<<<1, 1024, 0, s>>>(m->logits, m->d.vocab_size, m->pos_dev, m->done_dev, m->ids_dev, m->gen_dev,
+                                m->count_dev, m->eos_dev, 0);
+    MR_LAUNCHED("enqueue argmax");
+    for (int i = 1; i < max_new; ++i) MR_TRY(run_step(m, STEP_GREEDY));
+    int host[3];
+    MR_HIP(hipMemcpyAsync(host, m->done_dev, sizeof(host), hipMemcpyDeviceToHost, s), "read greedy state");
+    MR_HIP(hipStreamSynchronize(s), "generate");
+    int count = host[1];
+    MR_HIP(hipMemcpy(tokens, m->gen_dev, (size_t)count * sizeof(int), hipMemcpyDeviceToHost), "read tokens");
+    int pos = 0;
+    MR_HIP(hipMemcpy(&pos, m->pos_dev, sizeof(int), hipMemcpyDeviceToHost), "read position");
+    m->position = pos;
+    *produced = count;
+    if (host[0] == 2) return fail(MR_ERR_NONFINITE, "non-finite output logits");
+    return MR_OK;
+}
+
+}  // extern "C"

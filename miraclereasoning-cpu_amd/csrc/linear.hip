@@ -1,0 +1,302 @@
+// GEMV (decode) and small GEMM (op-level) projection kernels.
+//
+// GEMV layout: the weight matrix stays in its stored dtype, row-major [n, k]
+// (the reference's [out, in] layout, weights.py:211-245).  The input vector is
+// staged in LDS as FP32 (after an optional RMSNorm prologue computed by every
+// workgroup from the same values, so all workgroups see identical x).  A group
+// of `lpr` lanes owns R output rows; each lane streams 16-byte weight vectors
+// (8 BF16/F16 or 4 FP32 values) at a stride of lpr vectors, widens them in
+// registers and accumulates with FMA in FP32, then the group reduces by lane
+// shuffles.  HBM traffic is the weight bytes once plus the vector from L2.
+#include "linear.h"
+
+namespace mr {
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / kWave;
+
+template <int DT>
+struct Vec16;
+template <>
+struct Vec16<MR_F32> {
+    static constexpr int E = 4;
+    __device__ static void widen(const u32x4 &v, float *o) {
+        o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y);
+        o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+    }
+};
+template <>
+struct Vec16<MR_BF16> {
+    static constexpr int E = 8;
+    __device__ static void widen(const u32x4 &v, float *o) {
+        o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+        o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xffff0000u);
+        o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xffff0000u);
+    }
+};
+template <>
+struct Vec16<MR_F16> {
+    static constexpr int E = 8;
+    __device__ static void widen(const u32x4 &v, float *o) {
+        o[0] = f16_to_f32(v.x & 0xffffu); o[1] = f16_to_f32(v.x >> 16);
+        o[2] = f16_to_f32(v.y & 0xffffu); o[3] = f16_to_f32(v.y >> 16);
+        o[4] = f16_to_f32(v.z & 0xffffu); o[5] = f16_to_f32(v.z >> 16);
+        o[6] = f16_to_f32(v.w & 0xffffu); o[7] = f16_to_f32(v.w >> 16);
+    }
+};
+
+template <int DT>
+__device__ __forceinline__ u32x4 load16(const void *base, int64_t elem) {
+    constexpr int bytes = DT == MR_F32 ? 4 : 2;
+    return __builtin_nontemporal_load((const u32x4 *)((const char *)base + elem * bytes));
+}
+
+// Stage x into LDS, applying the RMSNorm prologue (kernels.cl:19-28 arithmetic:
+// scale = 1/sqrt(sum/k + eps), x * scale * gain).
+template <int PRO>
+__device__ __forceinline__ void stage_x(const GemvArgs &a, float *xs, float *red) {
+    const int tid = threadIdx.x;
+    for (int j = tid; j < a.k; j += blockDim.x) xs[j] = a.x[j];
+    if constexpr (PRO == PRO_RMS) {
+        float ss = 0.0f;
+        for (int j = tid; j < a.k; j += blockDim.x) {
+            float v = xs[j];
+            ss = fmaf(v, v, ss);
+        }
+        ss = block_sum(ss, red);
+        float scale = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+        for (int j = tid; j < a.k; j += blockDim.x) {
+            float v = xs[j] * scale * (a.gain ? a.gain[j] : 1.0f);
+            xs[j] = v;
+            if (a.x_out && blockIdx.x == 0) a.x_out[j] = v;
+        }
+    }
+    __syncthreads();
+}
+
+template <int EPI>
+__device__ __forceinline__ void finish_row(const GemvArgs &a, int row, float acc, float acc2) {
+    if constexpr (EPI == EPI_STORE) {
+        a.y[row] = acc;
+    } else if constexpr (EPI == EPI_RESIDUAL) {
+        // hidden + scale * projected, each product rounded (kernels.cl:52-56)
+        a.y[row] = a.y[row] + a.scale * acc;
+    } else if constexpr (EPI == EPI_SCALE_ADD) {
+        a.y[row] = a.y[row] + (*a.scale_ptr) * acc;
+    } else {
+        // SwiGLU (kernels.cl:46-50): (g / (1 + exp(-g))) * u
+        a.y[row] = (acc / (1.0f + expf(-acc))) * acc2;
+    }
+}
+
+template <int DT, int R, int PRO, int EPI>
+__global__ void __launch_bounds__(kGemvThreads) k_gemv_vec(GemvArgs a, int lpr) {
+    extern __shared__ float smem[];
+    if (a.done && *a.done) return;
+    float *xs = smem;
+    float *red = smem + ((a.k + 3) & ~3);
+    stage_x<PRO>(a, xs, red);
+
+    using V = Vec16<DT>;
+    constexpr int E = V::E;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (lpr - 1), slot = lane / lpr;
+    const int slots = kWave / lpr;
+    const int row0 = ((blockIdx.x * kGemvWaves + wave) * slots + slot) * R;
+    const int nvec = a.k / E;
+    const int64_t k = a.k;
+
+    int rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.n - 1);
+
+    float acc[R], acc2[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.0f;
+
+#pragma unroll 2
+    for (int v = sub; v < nvec; v += lpr) {
+        u32x4 wv[R], uv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wv[r] = load16<DT>(a.w, rows[r] * k + (int64_t)v * E);
+            if constexpr (EPI == EPI_SWIGLU) uv[r] = load16<DT>(a.w2, rows[r] * k + (int64_t)v * E);
+        }
+        float xv[E];
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            float4 t = *(const float4 *)(xs + v * E + e);
+            xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float wf[E];
+            V::widen(wv[r], wf);
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[r] = fmaf(wf[e], xv[e], acc[r]);
+            if constexpr (EPI == EPI_SWIGLU) {
+                V::widen(uv[r], wf);
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc2[r] = fmaf(wf[e], xv[e], acc2[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        acc[r] = group_sum(acc[r], lpr);
+        if constexpr (EPI == EPI_SWIGLU) acc2[r] = group_sum(acc2[r], lpr);
+    }
+    if (sub == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < a.n) finish_row<EPI>(a, row0 + r, acc[r], acc2[r]);
+    }
+}
+
+// Any k, any alignment: one wave per row, lanes stride over elements.
+template <int DT, int PRO, int EPI>
+__global__ void __launch_bounds__(kGemvThreads) k_gemv_scalar(GemvArgs a) {
+    extern __shared__ float smem[];
+    if (a.done && *a.done) return;
+    float *xs = smem;
+    float *red = smem + ((a.k + 3) & ~3);
+    stage_x<PRO>(a, xs, red);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kGemvWaves + wave;
+    if (row >= a.n) return;
+    float acc = 0.0f, acc2 = 0.0f;
+    for (int j = lane; j < a.k; j += kWave) {
+        acc = fmaf(load_w<DT>(a.w, (int64_t)row * a.k + j), xs[j], acc);
+        if constexpr (EPI == EPI_SWIGLU) acc2 = fmaf(load_w<DT>(a.w2, (int64_t)row * a.k + j), xs[j], acc2);
+    }
+    acc = wave_sum(acc);
+    if constexpr (EPI == EPI_SWIGLU) acc2 = wave_sum(acc2);
+    if (lane == 0) finish_row<EPI>(a, row, acc, acc2);
+}
+
+template <int DT, int PRO, int EPI>
+int launch_gemv_t(hipStream_t s, const GemvArgs &a) {
+    constexpr int E = Vec16<DT>::E;
+    const int bytes = DT == MR_F32 ? 4 : 2;
+    size_t lds = (size_t)(((a.k + 3) & ~3) + kGemvWaves) * sizeof(float);
+    bool aligned = (a.k % E) == 0 && ((uintptr_t)a.w % 16) == 0 &&
+                   (EPI != EPI_SWIGLU || ((uintptr_t)a.w2 % 16) == 0) && ((int64_t)a.k * bytes) % 16 == 0;
+    if (aligned) {
+        int nvec = a.k / E;
+        int lpr = 1;
+        while (lpr * 2 <= nvec && lpr < kWave) lpr *= 2;
+        const int slots = kWave / lpr;
+        if (a.n >= 16384) {
+            constexpr int R = 4;
+            int grid = ceil_div(a.n, kGemvWaves * slots * R);
+            k_gemv_vec<DT, R, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
+        } else {
+            constexpr int R = 2;
+            int grid = ceil_div(a.n, kGemvWaves * slots * R);
+            k_gemv_vec<DT, R, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
+        }
+    } else {
+        int grid = ceil_div(a.n, kGemvWaves);
+        k_gemv_scalar<DT, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a);
+    }
+    MR_LAUNCHED("gemv launch");
+    return MR_OK;
+}
+
+template <int DT>
+int launch_gemv_dt(hipStream_t s, int pro, int epi, const GemvArgs &a) {
+    if (pro == PRO_COPY) {
+        switch (epi) {
+            case EPI_STORE: return launch_gemv_t<DT, PRO_COPY, EPI_STORE>(s, a);
+            case EPI_RESIDUAL: return launch_gemv_t<DT, PRO_COPY, EPI_RESIDUAL>(s, a);
+            case EPI_SWIGLU: return launch_gemv_t<DT, PRO_COPY, EPI_SWIGLU>(s, a);
+            case EPI_SCALE_ADD: return launch_gemv_t<DT, PRO_COPY, EPI_SCALE_ADD>(s, a);
+        }
+    } else {
+        switch (epi) {
+            case EPI_STORE: return launch_gemv_t<DT, PRO_RMS, EPI_STORE>(s, a);
+            case EPI_RESIDUAL: return launch_gemv_t<DT, PRO_RMS, EPI_RESIDUAL>(s, a);
+            case EPI_SWIGLU: return launch_gemv_t<DT, PRO_RMS, EPI_SWIGLU>(s, a);
+            case EPI_SCALE_ADD: return launch_gemv_t<DT, PRO_RMS, EPI_SCALE_ADD>(s, a);
+        }
+    }
+    return fail(MR_ERR_INVALID, "gemv: bad prologue/epilogue");
+}
+
+// ------------------------------------------------------------------ small GEMM
+// 64x64 output tile per 256-thread block, 16-wide k slices through LDS, 4x4
+// outputs per thread, FP32 FMA.  For op-level calls with a handful of rows.
+template <int DT>
+__global__ void __launch_bounds__(256) k_gemm_small(const float *x, const void *w, float *y, int rows, int n,
+                                                    int k) {
+    __shared__ float xs[16][65];
+    __shared__ float ws[16][65];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    float acc[4][4] = {};
+    for (int kk = 0; kk < k; kk += 16) {
+        for (int i = threadIdx.x; i < 64 * 16; i += 256) {
+            int rr = i / 16, cc = i % 16;
+            int gr = r0 + rr, gk = kk + cc;
+            xs[cc][rr] = (gr < rows && gk < k) ? x[(int64_t)gr * k + gk] : 0.0f;
+            int gn = c0 + rr;
+            ws[cc][rr] = (gn < n && gk < k) ? load_w<DT>(w, (int64_t)gn * k + gk) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            float xv[4], wv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { xv[i] = xs[c][ty * 4 + i]; wv[i] = ws[c][tx * 4 + i]; }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int gr = r0 + ty * 4 + i, gn = c0 + tx * 4 + j;
+            if (gr < rows && gn < n) y[(int64_t)gr * n + gn] = acc[i][j];
+        }
+}
+
+}  // namespace
+
+int launch_gemv(hipStream_t s, int dtype, int pro, int epi, const GemvArgs &a) {
+    if (a.n <= 0 || a.k <= 0) return fail(MR_ERR_INVALID, "gemv: empty shape");
+    switch (dtype) {
+        case MR_F32: return launch_gemv_dt<MR_F32>(s, pro, epi, a);
+        case MR_BF16: return launch_gemv_dt<MR_BF16>(s, pro, epi, a);
+        case MR_F16: return launch_gemv_dt<MR_F16>(s, pro, epi, a);
+    }
+    return fail(MR_ERR_INVALID, "gemv: unknown weight dtype");
+}
+
+int launch_linear(hipStream_t s, const float *x, const void *w, int dtype, float *y, int rows, int n, int k) {
+    if (rows <= 0 || n <= 0 || k <= 0) return fail(MR_ERR_INVALID, "linear: empty shape");
+    if (rows == 1) {
+        GemvArgs a;
+        a.w = w; a.x = x; a.y = y; a.n = n; a.k = k;
+        return launch_gemv(s, dtype, PRO_COPY, EPI_STORE, a);
+    }
+    dim3 grid(ceil_div(n, 64), ceil_div(rows, 64));
+    switch (dtype) {
+        case MR_F32: k_gemm_small<MR_F32><<<grid, 256, 0, s>>>(x, w, y, rows, n, k); break;
+        case MR_BF16: k_gemm_small<MR_BF16><<<grid, 256, 0, s>>>(x, w, y, rows, n, k); break;
+        case MR_F16: k_gemm_small<MR_F16><<<grid, 256, 0, s>>>(x, w, y, rows, n, k); break;
+        default: return fail(MR_ERR_INVALID, "linear: unknown weight dtype");
+    }
+    MR_LAUNCHED("linear launch");
+    return MR_OK;
+}
+
+}  // namespace mr

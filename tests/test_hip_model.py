@@ -1,0 +1,124 @@
+"""MiracleModel on the GPU against the reference's golden fixtures and the oracle.
+
+Tolerances (the contract's): per-token logits within atol 2e-5 / rtol 2e-4 on
+the micro and tiny configurations, rtol 1e-3 (atol 1e-4) on the larger ones;
+greedy and seeded-sampling token streams identical; the reference's invariants
+(decode == prefill bit for bit, context overflow rejected without advancing,
+bad inputs rejected before any step) exact.
+"""
+import json
+
+import numpy as np
+import pytest
+
+from miracle_hip import MiracleModel, ModelConfig, presets, synthetic
+from oracle.model import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+GQA = ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
+
+
+def _variants():
+    from conftest import GOLDEN
+    names = sorted(p.stem[len("micro_"):] for p in GOLDEN.glob("micro_*.npz"))
+    return [n for n in names if n.rsplit("-untied", 1)[0] in GQA]
+
+
+def _micro(golden_dir, name):
+    z = np.load(golden_dir / f"micro_{name}.npz")
+    bundle = json.loads(str(z["bundle"]))
+    return z, ModelConfig.from_dict(bundle), synthetic.micro_weights(bundle)
+
+
+@pytest.mark.parametrize("variant", _variants())
+def test_micro_matches_reference(backend, golden_dir, variant):
+    z, cfg, weights = _micro(golden_dir, variant)
+    print("case", variant, flush=True)
+    model = MiracleModel(cfg, weights, backend=backend, context_length=32)
+    ids = z["ids"]
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), z["logits"], atol=2e-5, rtol=2e-4)
+    model.reset()
+    chunked = np.concatenate([model.prefill(ids[:5], return_all=True), model.prefill(ids[5:], return_all=True)])
+    np.testing.assert_allclose(chunked, z["chunked"], atol=2e-5, rtol=2e-4)
+    assert model.generate(list(ids[:4]), max_new_tokens=8) == z["greedy"].tolist()
+    assert model.generate([1, 3], max_new_tokens=4, temperature=0.8, top_k=5, top_p=0.9, seed=7) == \
+        z["sampled"].tolist()
+
+
+def test_cache_reset_bounds_and_decode_equals_prefill(backend):
+    # reference tests/test_inference.py:52-69
+    bundle = presets.micro("flashnano-1.5")
+    model = MiracleModel(ModelConfig.from_dict(bundle), synthetic.micro_weights(bundle), backend=backend,
+                         context_length=12)
+    ids = [1, 3, 5, 8, 2, 9, 11, 10, 9, 7, 6, 4]
+    whole = model.prefill(ids, return_all=True)
+    with pytest.raises(ValueError, match="context_length"):
+        model.decode(1)
+    assert model.position == 12
+    model.reset()
+    np.testing.assert_array_equal(np.stack([model.decode(i) for i in ids]), whole)
+    model.reset()
+    for bad in ([32], [-1], [1.5], [[1]], [], [True]):
+        with pytest.raises(ValueError):
+            model.prefill(bad)
+        assert model.position == 0
+
+
+def test_generation_is_repeatable_and_validates_before_reset(backend):
+    # reference tests/test_inference.py:87-99
+    bundle = presets.micro("flashnano-1.5")
+    model = MiracleModel(ModelConfig.from_dict(bundle), synthetic.micro_weights(bundle), backend=backend,
+                         context_length=12)
+    a = model.generate([1, 3], max_new_tokens=4, temperature=.8, top_k=5, top_p=.9, seed=7)
+    assert a == model.generate([1, 3], max_new_tokens=4, temperature=.8, top_k=5, top_p=.9, seed=7)
+    position = model.position
+    for kwargs in ({"max_new_tokens": -1}, {"max_new_tokens": 12}, {"temperature": float("nan")}, {"top_p": 0}):
+        with pytest.raises(ValueError):
+            model.generate([1, 3], **kwargs)
+        assert model.position == position
+    greedy = model.generate([1], max_new_tokens=1)[0]
+    assert model.generate([1], max_new_tokens=4, eos_token_id=greedy) == [greedy]
+    assert model.position == 1
+    assert model.generate([1], max_new_tokens=0) == []
+
+
+def test_failed_step_poisons_until_reset(backend):
+    bundle = presets.micro("flashnano-1.7")
+    model = MiracleModel(ModelConfig.from_dict(bundle), synthetic.micro_weights(bundle), backend=backend,
+                         context_length=16)
+    model.prefill([1, 2])
+    backend.fail_next()
+    with pytest.raises(RuntimeError):
+        model.decode(3)
+    with pytest.raises(RuntimeError, match="reset"):
+        model.decode(3)
+    model.reset()
+    model.prefill([1, 2])
+
+
+def test_workload_tiny_matches_reference(backend, golden_dir):
+    z = np.load(golden_dir / "workload_flashnano-1.5-tiny.npz")
+    wl = presets.workload("flashnano-1.5-tiny")
+    cfg = ModelConfig.from_dict(wl["config"])
+    model = MiracleModel(cfg, synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"]), backend=backend,
+                         context_length=wl["context"])
+    np.testing.assert_allclose(model.prefill(z["prompt"]), z["last_logits"], atol=2e-5, rtol=2e-4)
+    assert model.generate(list(z["prompt"]), max_new_tokens=16) == z["greedy"].tolist()
+
+
+@pytest.mark.parametrize("name,prompt,steps", [("flashnano-1.5-mid", 40, 6), ("flashnano-1.7", 12, 4)])
+def test_workload_geometry_matches_oracle(backend, name, prompt, steps):
+    """Full-size geometry (BF16 weights as drawn for the workload) on a short
+    prompt: logits of every step and the greedy stream against the oracle."""
+    wl = presets.workload(name)
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
+    print("case", name, flush=True)
+    model = MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"])
+    got = model.prefill(ids, return_all=True)[-steps:]
+    ref = OracleModel(wl["config"], {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=wl["context"])
+    want = ref.prefill(ids, return_all=True)[-steps:]
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
+    assert model.generate(list(ids), max_new_tokens=steps) == ref.generate(list(ids), max_new_tokens=steps)

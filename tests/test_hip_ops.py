@@ -1,0 +1,190 @@
+"""HIPBackend op surface on the GPU: the reference's closed-form kernel tests
+(tests/test_opencl.py:19-80 of the reference) and every op against the oracle's
+C restatement on seeded inputs.
+
+Tolerances: elementwise ops with the same formula agree to 1-2 ulp (rtol 1e-6);
+dot products (linear, scores, mix, pool) sum in a different order on the GPU
+(lanes + shuffles + FMA) and agree to rtol 1e-5 / atol 1e-6 at these sizes.
+"""
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def test_primitives_with_non_aligned_shapes(backend):
+    b = backend
+    rng = np.random.default_rng(9)
+    x = rng.normal(size=(3, 19)).astype(np.float32)
+    w = rng.normal(size=(7, 19)).astype(np.float32)
+    np.testing.assert_allclose(b.read(b.linear(b.upload(x), b.upload(w))), x @ w.T, atol=4e-6)
+    scales = rng.normal(size=19).astype(np.float32)
+    expected = x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + 1e-6) * scales
+    np.testing.assert_allclose(b.read(b.norm(b.upload(x), b.upload(scales), 19, 1e-6)), expected, atol=1e-6)
+    logits = np.array([[1000, 1001, -1000], [-1000, -1001, -1002]], np.float32)
+    e = np.exp(logits - logits.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(b.read(b.softmax(b.upload(logits))), e / e.sum(axis=1, keepdims=True), atol=1e-7)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_rope_layouts(backend, split):
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(2, 3, 6)).astype(np.float32)
+    pos = np.array([7, 29], np.float32)
+    freq = np.array([1, .1, .01], np.float32)
+    ang = pos[:, None, None] * freq[None, None, :]
+    a, c = (x[..., :3], x[..., 3:]) if split else (x[..., ::2], x[..., 1::2])
+    u, v = a * np.cos(ang) - c * np.sin(ang), a * np.sin(ang) + c * np.cos(ang)
+    want = np.concatenate([u, v], axis=-1) if split else np.stack([u, v], axis=-1).reshape(2, 3, 6)
+    got = backend.rotate(backend.upload(x.reshape(2, 18)), backend.upload(freq), backend.upload(pos), 3, 6, split)
+    np.testing.assert_allclose(backend.read(got).reshape(x.shape), want, atol=3e-6)
+
+
+def test_attention_group_mapping_ring_and_relays(backend):
+    b, rng = backend, np.random.default_rng(6)
+    q = rng.normal(size=(4, 6)).astype(np.float32)
+    k, v = [rng.normal(size=(5, 2, 6)).astype(np.float32) for _ in range(2)]
+    rk, rv = [rng.normal(size=(3, 2, 6)).astype(np.float32) for _ in range(2)]
+    keys, values = np.concatenate([k[[3, 4, 0, 1]], rk]), np.concatenate([v[[3, 4, 0, 1]], rv])
+    want = []
+    for h in range(4):
+        logits = keys[:, h // 2] @ q[h] / np.sqrt(6)
+        p = np.exp(logits - logits.max())
+        want.append((p / p.sum()) @ values[:, h // 2])
+    got = b.attention(b.upload(q.reshape(1, -1)), b.upload(k.reshape(5, -1)), b.upload(v.reshape(5, -1)),
+                      heads=4, kv_heads=2, dim=6, start=3, length=4,
+                      extra_keys=b.upload(rk.reshape(3, -1)), extra_values=b.upload(rv.reshape(3, -1)),
+                      extra_length=3)
+    np.testing.assert_allclose(b.read(got).reshape(4, 6), want, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,out,inner,dtype", [
+    (1, 2048, 2048, "bf16"), (1, 5632, 2048, "bf16"), (1, 2048, 5632, "bf16"), (1, 32000, 2048, "bf16"),
+    (1, 1000, 256, "bf16"), (1, 37, 19, "f32"), (1, 300, 64, "f32"), (1, 24, 12, "bf16"), (4, 70, 33, "f32"),
+    (3, 129, 256, "bf16"), (1, 64, 1024, "f16")])
+def test_linear_matches_oracle(backend, rows, out, inner, dtype):
+    from miracle_hip.weights import BF16Array, bf16_bits
+    rng = np.random.default_rng(rows * 7 + out)
+    x = rng.normal(size=(rows, inner)).astype(np.float32)
+    w32 = (rng.normal(size=(out, inner)) * 0.02).astype(np.float32)
+    if dtype == "bf16":
+        bits = bf16_bits(w32)
+        wt = backend.upload_weight(BF16Array(bits))
+        want = K.linear(x, bits)
+    elif dtype == "f16":
+        w16 = w32.astype(np.float16)
+        wt = backend.upload_weight(w16)
+        want = K.linear(x, w16.astype(np.float32))
+    else:
+        wt = backend.upload(w32)
+        want = K.linear(x, w32)
+    got = backend.read(backend.linear(backend.upload(x), wt))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_elementwise_ops_match_oracle(backend):
+    b, rng = backend, np.random.default_rng(11)
+    x = rng.normal(size=(5, 64)).astype(np.float32)
+    g = rng.normal(size=64).astype(np.float32)
+    np.testing.assert_allclose(b.read(b.norm(b.upload(x), b.upload(g), 64, 1e-5)), K.rms(x, g, 64, 1e-5),
+                               rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(b.read(b.norm(b.upload(x), None, 16, 1e-6)), K.rms(x, None, 16, 1e-6),
+                               rtol=2e-6, atol=1e-7)
+    u = rng.normal(size=(5, 64)).astype(np.float32)
+    np.testing.assert_allclose(b.read(b.swiglu(b.upload(x), b.upload(u))), K.swiglu(x, u), rtol=2e-6, atol=1e-7)
+    np.testing.assert_array_equal(b.read(b.add(b.upload(x), b.upload(u), 0.37)), K.axpy(x, u, 0.37))
+    big = (rng.normal(size=(3, 4099)) * 30).astype(np.float32)
+    np.testing.assert_allclose(b.read(b.softmax(b.upload(big))), K.softmax(big), rtol=1e-5, atol=1e-9)
+
+
+def test_rope_large_positions_match_oracle(backend):
+    rng = np.random.default_rng(12)
+    x = rng.normal(size=(3, 4 * 128)).astype(np.float32)
+    pos = np.array([0, 4095, 8191], np.float32)
+    from miracle_hip import ModelConfig, presets
+    freq = ModelConfig.from_dict(presets.workload("flashnano-1.7")["config"]).inverse_frequencies()
+    for split in (0, 1):
+        got = backend.read(backend.rotate(backend.upload(x), backend.upload(freq), backend.upload(pos), 4, 128, split))
+        np.testing.assert_allclose(got, K.rope(x, freq, pos, 4, 128, split), rtol=1e-6, atol=1e-6)
+
+
+def test_scores_softmax_mix_latent_mask_match_oracle(backend):
+    b, rng = backend, np.random.default_rng(13)
+    heads, kvh, d, cap, start, length, extra = 8, 2, 32, 40, 33, 37, 5
+    q = rng.normal(size=(1, heads * d)).astype(np.float32)
+    k = rng.normal(size=(cap, kvh * d)).astype(np.float32)
+    v = rng.normal(size=(cap, kvh * d)).astype(np.float32)
+    ek = rng.normal(size=(extra, kvh * d)).astype(np.float32)
+    ev = rng.normal(size=(extra, kvh * d)).astype(np.float32)
+    total = length + extra
+    s = b.empty((heads, total))
+    b.run("scores", (total, heads), b.upload(q), b.upload(k), b.upload(ek), s, heads, kvh, d, cap, start, length,
+          extra)
+    want_s = K.scores(q, k, ek, heads, kvh, d, cap, start, length, extra)
+    np.testing.assert_allclose(b.read(s), want_s, rtol=1e-5, atol=1e-5)
+    p = b.softmax(s)
+    got = b.read(b.mix(p, b.upload(v), heads, kvh, d, start, length, b.upload(ev), extra))
+    want = K.mix(K.softmax(want_s), v, ev, heads, kvh, d, cap, start, length, extra)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    fused = b.read(b.attention(b.upload(q), b.upload(k), b.upload(v), heads=heads, kv_heads=kvh, dim=d, start=start,
+                               length=length, extra_keys=b.upload(ek), extra_values=b.upload(ev), extra_length=extra))
+    np.testing.assert_allclose(fused, want, rtol=1e-5, atol=1e-5)
+    positions = np.arange(total, dtype=np.float32)
+    sm = b.upload(want_s)
+    b.run("latent_mask", (total, heads), sm, b.upload(positions), heads, total, 3, 20)
+    np.testing.assert_array_equal(b.read(sm), K.latent_mask(want_s.copy(), positions, heads, total, 3, 20))
+
+
+@pytest.mark.parametrize("length", [1, 100, 1023, 1024, 4097, 8192])
+def test_fused_attention_long_windows(backend, length):
+    """Split-key attention at decode shapes of the 1.7 workload (d 128, 16/4 and
+    16/8 heads), including a wrapped ring and the full 8192 global window."""
+    b, rng = backend, np.random.default_rng(length)
+    heads, d = 16, 128
+    kvh = 8 if length > 1024 else 4
+    cap = max(length, 1024)
+    start = (cap - 7) % cap if length < cap else 0
+    q = rng.normal(size=(1, heads * d)).astype(np.float32)
+    k = rng.normal(size=(cap, kvh * d)).astype(np.float32)
+    v = rng.normal(size=(cap, kvh * d)).astype(np.float32)
+    got = b.read(b.attention(b.upload(q), b.upload(k), b.upload(v), heads=heads, kv_heads=kvh, dim=d, start=start,
+                             length=length))
+    want = K.attention(q, k, v, heads, kvh, d, start, length)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_pool_merge_block_means_match_oracle(backend):
+    b, rng = backend, np.random.default_rng(14)
+    u = rng.normal(size=(6, 48)).astype(np.float32)
+    q = rng.normal(size=(3, 48)).astype(np.float32)
+    s = b.empty((3, 6))
+    b.run("pool_scores", (6, 3), b.upload(u), b.upload(q), s, 6, 3, 48)
+    want_s = K.pool_scores(u, q, 6, 3, 48)
+    np.testing.assert_allclose(b.read(s), want_s, rtol=1e-5, atol=1e-6)
+    p = K.softmax(want_s)
+    z, anchors = b.empty((3, 48)), b.empty((3,))
+    b.run("pool_mix", (48, 3), b.upload(u), b.upload(p), z, anchors, 6, 3, 48, 100)
+    want_z, want_a = K.pool_mix(u, p, 6, 3, 48, 100)
+    np.testing.assert_allclose(b.read(z), want_z, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(b.read(anchors), want_a)
+    y = b.empty((48,))
+    b.run("merge_rows", (48,), b.upload(u[:2]), y, 48, 3.0, 5.0)
+    np.testing.assert_allclose(b.read(y), K.merge_rows(u[:2], 48, 3.0, 5.0), rtol=1e-6)
+    rows = rng.normal(size=(131, 24)).astype(np.float32)
+    bm = b.empty((3, 24))
+    b.run("block_means", (24, 3), b.upload(rows), bm, 131, 24, 64)
+    np.testing.assert_allclose(b.read(bm), K.block_means(rows, 131, 24, 64), rtol=1e-6, atol=1e-7)
+
+
+def test_copy_bounds_and_ownership(backend):
+    b = backend
+    src = b.upload(np.arange(10, dtype=np.float32))
+    dst = b.empty((6,))
+    b.copy(src, dst, source_offset=4, count=6)
+    np.testing.assert_array_equal(b.read(dst), np.arange(4, 10, dtype=np.float32))
+    with pytest.raises(ValueError, match="out of bounds"):
+        b.copy(src, dst, source_offset=3, count=7, target_offset=1)
+    with pytest.raises(ValueError):
+        b.empty((0, 3))
