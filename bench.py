@@ -1,0 +1,187 @@
+#!/usr/bin/env python3
+"""flashnano-1.7 on one MI355X: bs=1 greedy decode tokens/s (+ fraction of the HBM
+roofline) and prefill tokens/s.
+
+Workload (seed 2, BF16 random-init weights, synthetic prompt ids): 24 layers,
+every 4th global, local ring window 1024, hidden 2048, 16 Q heads x d128,
+4 local / 8 global KV heads, split-half RoPE theta 5e5, FFN 5632, vocab 32000,
+context 8192.  A 4096-token prompt is prefilled, then K greedy decode steps run
+on device (a step = one token through all 24 layers + LM head + argmax; only
+the token id crosses to the host).  Default K = 511 = the decode passes of a
+512-token generation, positions 4096..4606.
+
+Prints one JSON line.  `value` is decode tokens/s with weights and KV cache
+resident in HBM.  `roofline` is for the dominant kernel (the fused
+RMSNorm + gate/up GEMV + SwiGLU, 46.1 MB of BF16 weights per launch), timed live
+with HIP events; `cpu_baseline` times the oracle (a C restatement of the
+reference's OpenCL kernels, FP32 weights resident, the reference's token loop)
+on this host's cores for a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "miraclereasoning-cpu_amd"))
+
+import numpy as np  # noqa: E402
+
+from miracle_hip import ModelConfig, presets, synthetic  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+WORKLOAD = "flashnano-1.7"
+METRIC = "bs=1 decode tok/s + % of HBM roofline; prefill tok/s (flashnano-1.7)"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_bytes(cfg, dtype_bytes=2):
+    """Stored bytes of every tensor read by one decode step (norm gains are FP32)."""
+    from miracle_hip.weights import expected_shapes
+    total = 0
+    for name, shape in expected_shapes(cfg).items():
+        n = int(np.prod(shape))
+        total += n * (4 if len(shape) == 1 else dtype_bytes)
+    return total
+
+
+def decode_bytes(cfg, context, position):
+    """Algorithmic HBM bytes of one decode step at `position` (0-based):
+    every projection weight once, the LM head, one embedding row, the KV rows
+    the attention reads (FP32), the new K/V rows written, and the logits."""
+    h, d, V = cfg.hidden_size, cfg.head_dim, cfg.vocab_size
+    head = V * h * 2
+    embed_row = h * 2
+    body = weight_bytes(cfg) - V * h * 2 * (1 if cfg.tie_embeddings else 2)   # layers + final norm
+    kv = 0
+    for layer in range(cfg.layers):
+        kvw = cfg.layer_kv_heads(layer) * d
+        cap = min(cfg.layer_window(layer) or context, context)
+        kv += 2 * min(position + 1, cap) * kvw * 4 + 2 * kvw * 4
+    return body + head + embed_row + kv + V * 4
+
+
+def gate_up_bytes(cfg):
+    """Algorithmic bytes of one fused RMSNorm + gate/up GEMV + SwiGLU launch."""
+    h, f = cfg.hidden_size, cfg.ffn_dim
+    return 2 * f * h * 2 + h * 4 + h * 4 + f * 4   # weights + hidden + gain + activations out
+
+
+def cpu_baseline(wl, weights, budget_s):
+    """Oracle token steps on the host (FP32 weights resident, all affine cores)."""
+    from oracle import kernels as K
+    from oracle.model import OracleModel
+    widened = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
+    model = OracleModel(wl["config"], widened, context_length=wl["context"])
+    ids = synthetic.prompt_ids(wl["config"]["vocab_size"], 256, wl["seed"])
+    model.step(int(ids[0]))          # first touch of every page of the weights
+    n, t0 = 0, time.perf_counter()
+    while n < 255 and (n < 4 or time.perf_counter() - t0 < budget_s):
+        model.step(int(ids[n + 1]))
+        n += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(n / elapsed, 3), "unit": "tok/s", "cores": K.threads(), "kind": "port",
+            "sample": f"{n} token steps (positions 1..{n}) of {WORKLOAD} through the oracle's C restatement of "
+                      f"the reference kernels, FP32 weights resident, the reference's token-by-token loop; "
+                      f"{elapsed:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=511, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode steps before timing")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt length (default: the workload's 4096)")
+    ap.add_argument("--prefill-mode", choices=("exact", "batched"), default="exact")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-baseline budget; 0 skips it")
+    ap.add_argument("--kernel-reps", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch step kernels eagerly instead of replaying the captured step graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no multi-GPU "
+              "sharding: bs=1 decode of one sequence runs on one GPU).", file=sys.stderr)
+        return 2
+
+    from miracle_hip import HIPBackend, MiracleModel
+
+    wl = presets.workload(WORKLOAD)
+    cfg = ModelConfig.from_dict(wl["config"])
+    prompt_len = args.prompt or wl["prompt"]
+    if prompt_len + args.warmup + args.steps > wl["context"]:
+        raise SystemExit("prompt + warmup + steps exceed the context")
+    log("generating synthetic weights")
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    prompt = synthetic.prompt_ids(cfg.vocab_size, prompt_len, wl["seed"])
+    backend = HIPBackend()
+    log(f"device {backend.device.name} {backend.device.arch}, {backend.device.compute_units} CUs")
+    model = MiracleModel(cfg, weights, backend=backend, context_length=wl["context"],
+                         prefill_mode=args.prefill_mode)
+    eng = model.engine
+    if args.no_graph:
+        eng.use_graph(False)
+
+    # Prefill: the whole prompt, logits of the last token.
+    log(f"prefill {prompt_len} tokens ({args.prefill_mode})")
+    model.prefill(prompt[:8])        # first launches + graph capture outside the timed region
+    model.reset()
+    t0 = time.perf_counter()
+    model.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {prompt_len / prefill_s:.1f} tok/s")
+
+    # Warm-up decode steps (captures the greedy step graph), then a fresh sequence.
+    eng.generate_greedy(args.warmup + 1, -1)
+    model.reset()
+    model.prefill(prompt)
+    backend.finish()
+    t0 = time.perf_counter()
+    tokens = eng.generate_greedy(args.steps + 1, -1)      # 1 choice from prefill + `steps` decode steps
+    decode_s = time.perf_counter() - t0
+    assert len(tokens) == args.steps + 1
+    tok_s = args.steps / decode_s
+    positions = range(prompt_len, prompt_len + args.steps)
+    avg_bytes = float(np.mean([decode_bytes(cfg, wl["context"], p) for p in positions]))
+    log(f"decode {tok_s:.1f} tok/s, {avg_bytes * tok_s / 1e9:.1f} GB/s algorithmic")
+
+    # Per-kernel device time (HIP events), each kernel launched for every layer in turn.
+    kernels = {k: eng.time_kernel(k, args.kernel_reps) for k in ("qkv", "attention", "o", "gate_up", "down", "head")}
+    gu_ms = kernels["gate_up"]
+    gu_gbs = gate_up_bytes(cfg) / (gu_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(1e3 * decode_s / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": WORKLOAD, "weights": "bf16 random-init seed 2", "prompt": prompt_len,
+                   "decode_positions": [prompt_len, prompt_len + args.steps - 1], "context": wl["context"],
+                   "prefill_mode": args.prefill_mode, "step_graph": not args.no_graph},
+        "decode_hbm": {"algorithmic_bytes_per_token": int(avg_bytes),
+                       "achieved_gbs": round(avg_bytes * tok_s / 1e9, 1),
+                       "peak_gbs": HBM_PEAK_GBS, "frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
+        "prefill": {"tok_s": round(prompt_len / prefill_s, 1), "seconds": round(prefill_s, 4),
+                    "mode": args.prefill_mode},
+        "roofline": {"kernel": "gemv gate/up + SwiGLU (RMSNorm prologue)", "bound": "hbm",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": gate_up_bytes(cfg), "avg_ms": round(gu_ms, 5)},
+        "kernels_ms": {k: round(v, 5) for k, v in kernels.items()},
+        "greedy_head": tokens[:8],
+    }
+    if args.cpu_seconds > 0:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(wl, weights, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

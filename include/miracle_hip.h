@@ -192,6 +192,18 @@ MR_API int mr_model_generate_greedy(mr_model *model, int max_new, int eos, int32
  * enable = 0 launches kernels eagerly instead. */
 MR_API int mr_model_use_graph(mr_model *model, int enable);
 
+/* Measurement: average device time of one launch of a step kernel, taken with
+ * HIP events on the context stream.  `which` is an MR_KERNEL_* id; the kernel is
+ * launched for every layer in turn (so a repeat never finds the previous
+ * layer's weights in cache), `reps` times over, at the current position.  The
+ * position and every cached key/value row the next step reads are left as they
+ * were; the scratch activations and the last logits are not (call
+ * mr_model_forward again before mr_model_generate_greedy).  No counterpart in
+ * the reference (it has no timers); used by bench.py. */
+enum { MR_KERNEL_QKV = 0, MR_KERNEL_ATTENTION = 1, MR_KERNEL_O = 2, MR_KERNEL_GATE_UP = 3, MR_KERNEL_DOWN = 4,
+       MR_KERNEL_HEAD = 5 };
+MR_API int mr_model_time_kernel(mr_model *model, int which, int reps, float *avg_ms);
+
 /* Test hook: make the next model call on this context fail with
  * MR_ERR_INJECTED (the reference's failed-device-operation path,
  * model.py:298-311).  Not a counterpart of any reference function. */

@@ -1,16 +1,20 @@
 // Split-key attention for one query token.
 //
 // Grid: (splits, kv_heads).  Workgroup (split, kh) owns the G = heads/kv_heads
-// query heads that share KV head kh (kernels.cl:66 mapping) and the logical keys
-// [split*split_len, (split+1)*split_len) of the order [ring window, extra rows]
-// (kernels.cl:67-68).  It scores those keys (dot / sqrt(dim), kernels.cl:72),
-// takes a local max m and l = sum exp(s - m), accumulates o = sum exp(s - m) v,
-// and writes (m, l, o).  The last workgroup of each KV head to finish (a device
-// counter) merges the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s,
-// the same softmax-weighted value sum as kernels.cl:75-107 up to rounding.
+// query heads that share KV head kh (kernels.cl:66 mapping) and a contiguous
+// range of the logical keys [ring window, extra rows] (kernels.cl:67-68).  It
+// scores them (dot / sqrt(dim), kernels.cl:72), keeps a running max m and
+// l = sum exp(s - m), accumulates o = sum exp(s - m) v, and writes (m, l, o).
+// The last workgroup of each KV head to finish (a device counter) merges the
+// splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s -- the softmax-
+// weighted value sum of kernels.cl:75-107, up to rounding.
 //
-// Key rows are read once from HBM by a group of lanes per key (16-byte loads
-// when dim % 4 == 0); value rows are read once, coalesced across the dim.
+// Fast path (head dim 32/64/128): keys and values stream through LDS in 16 KB
+// tiles (4096 floats = 4096/dim keys), each thread loading 4 float4 of K and 4
+// of V per tile, coalesced along the row; the next tile is prefetched into
+// registers while the current one is consumed.  The split length follows the
+// current window, so every workgroup of the fixed grid has work.  Other head
+// dims take a plain per-element path (micro models only).
 #include "attention.h"
 
 namespace mr {
@@ -18,10 +22,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-
-struct Geo {
-    int start, length, extra, total, pos;
-};
+constexpr int kTileFloats = 4096;
+constexpr int kMaxG = 16;
 
 struct KernelArgs {
     AttnStepArgs s;       // engine fields (mode 1)
@@ -30,34 +32,12 @@ struct KernelArgs {
     const float *ring_k_ro, *ring_v_ro;
 };
 
-template <int VEC>
-__device__ __forceinline__ float dot_part(const float *q, const float *k, int sub, int lpk, int nv) {
-    float acc = 0.0f;
-    if constexpr (VEC == 4) {
-        for (int v = sub; v < nv; v += lpk) {
-            float4 a = *(const float4 *)(q + 4 * v);
-            float4 b = *(const float4 *)(k + 4 * v);
-            acc = fmaf(a.x, b.x, acc);
-            acc = fmaf(a.y, b.y, acc);
-            acc = fmaf(a.z, b.z, acc);
-            acc = fmaf(a.w, b.w, acc);
-        }
-    } else {
-        for (int v = sub; v < nv; v += lpk) acc = fmaf(q[v], k[v], acc);
-    }
-    return acc;
-}
+struct Geo {
+    int pos, start, length, extra, total;
+};
 
-template <int VEC>
-__global__ void __launch_bounds__(kThreads) k_attn_split(KernelArgs ka) {
-    extern __shared__ float lds[];
+__device__ __forceinline__ Geo geometry(const KernelArgs &ka) {
     const AttnStepArgs &a = ka.s;
-    if (ka.mode == 1 && a.done && *a.done) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kh = blockIdx.y, split = blockIdx.x;
-    const int d = a.dim, G = a.heads / a.kv_heads, kvw = a.kv_heads * d;
-    const int split_len = a.split_len;
-
     Geo g;
     if (ka.mode == 1) {
         g.pos = *a.pos;
@@ -72,151 +52,367 @@ __global__ void __launch_bounds__(kThreads) k_attn_split(KernelArgs ka) {
         g.extra = ka.extra_length;
     }
     g.total = g.length + g.extra;
-    const int t0 = split * split_len;
-    const int t1 = min(t0 + split_len, g.total);
+    return g;
+}
 
-    float *qs = lds;                       // [G*d]
-    float *kn = qs + G * d;                // [d]
-    float *vn = kn + d;                    // [d]
-    float *sc = vn + d;                    // [G*split_len]
-    float *stat = sc + G * split_len;      // [2*G]
-    float *red = stat + 2 * G;             // [kWaves]
-    int *flag = (int *)(red + kWaves);
-
+// Engine mode: normalize (optional) and rotate the G queries and the new key in
+// LDS, then store the new key/value in the ring slot of this position (by the
+// split that holds the newest key).  Ends with a barrier.
+__device__ void prepare(const KernelArgs &ka, const Geo &g, int kh, int G, int d, float *qs, float *kn, float *vn,
+                        int t0, int t1) {
+    const AttnStepArgs &a = ka.s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *q_src = a.q + (int64_t)kh * G * d;
     for (int i = tid; i < G * d; i += kThreads) qs[i] = q_src[i];
-    if (ka.mode == 1) {
-        for (int j = tid; j < d; j += kThreads) {
-            kn[j] = a.k_new[kh * d + j];
-            vn[j] = a.v_new[kh * d + j];
-        }
+    if (ka.mode != 1) {
         __syncthreads();
-        // Per-head RMSNorm of the G queries and the key (kernels.cl:19-28, width = dim).
-        if (a.q_gain) {
-            for (int r = wave; r < G + 1; r += kWaves) {
-                float *row = r < G ? qs + r * d : kn;
-                const float *gain = r < G ? a.q_gain : a.k_gain;
-                float ss = 0.0f;
-                for (int j = lane; j < d; j += kWave) ss = fmaf(row[j], row[j], ss);
-                ss = wave_sum(ss);
-                float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
-                for (int j = lane; j < d; j += kWave) row[j] = row[j] * scale * gain[j];
-            }
-            __syncthreads();
-        }
-        // RoPE at this position (kernels.cl:30-44).
-        const int half = d / 2;
-        const float fpos = (float)g.pos;
-        for (int i = tid; i < (G + 1) * half; i += kThreads) {
-            int r = i / half, p = i % half;
-            float *row = r < G ? qs + r * d : kn;
-            int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
-            float u = row[j], v = row[k];
-            rope_pair(u, v, fpos, a.freq[p]);
-            row[j] = u;
-            row[k] = v;
-        }
-        __syncthreads();
-        // The split holding the newest key stores it in the ring slot of this position.
-        const int newest = g.length - 1;
-        if (t0 <= newest && newest < t1) {
-            int64_t slot = (int64_t)(g.pos % a.capacity) * kvw + (int64_t)kh * d;
-            for (int j = tid; j < d; j += kThreads) {
-                a.ring_k[slot + j] = kn[j];
-                a.ring_v[slot + j] = vn[j];
-            }
-        }
+        return;
+    }
+    for (int j = tid; j < d; j += kThreads) {
+        kn[j] = a.k_new[kh * d + j];
+        vn[j] = a.v_new[kh * d + j];
     }
     __syncthreads();
+    if (a.q_gain) {   // per-head RMSNorm, width = dim (kernels.cl:19-28)
+        for (int r = wave; r < G + 1; r += kWaves) {
+            float *row = r < G ? qs + r * d : kn;
+            const float *gain = r < G ? a.q_gain : a.k_gain;
+            float ss = 0.0f;
+            for (int j = lane; j < d; j += kWave) ss = fmaf(row[j], row[j], ss);
+            ss = wave_sum(ss);
+            float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
+            for (int j = lane; j < d; j += kWave) row[j] = row[j] * scale * gain[j];
+        }
+        __syncthreads();
+    }
+    const int half = d / 2;   // RoPE at this position (kernels.cl:30-44)
+    const float fpos = (float)g.pos;
+    for (int i = tid; i < (G + 1) * half; i += kThreads) {
+        int r = i / half, p = i % half;
+        float *row = r < G ? qs + r * d : kn;
+        int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
+        float u = row[j], v = row[k];
+        rope_pair(u, v, fpos, a.freq[p]);
+        row[j] = u;
+        row[k] = v;
+    }
+    __syncthreads();
+    const int newest = g.length - 1;
+    if (t0 <= newest && newest < t1) {
+        const int kvw = a.kv_heads * d;
+        int64_t slot = (int64_t)(g.pos % a.capacity) * kvw + (int64_t)kh * d;
+        for (int j = tid; j < d; j += kThreads) {
+            a.ring_k[slot + j] = kn[j];
+            a.ring_v[slot + j] = vn[j];
+        }
+    }
+}
+
+// Merge the splits of KV head kh (run by the last workgroup to finish).
+template <int D>
+__device__ void combine(const AttnStepArgs &a, int kh, int G, int active, float *lds) {
+    const int tid = threadIdx.x;
+    const float *base = a.part + (int64_t)kh * a.splits * G * (D + 2);
+    float *w = lds;                      // [active][G] split maxima, then weights e^(m_s - M)
+    float *lv = w + active * G;          // [active][G] split sums
+    float *L = lv + active * G;          // [G]
+    float *red = L + G;                  // [SG][G*D] partial sums
+    for (int i = tid; i < active * G; i += kThreads) {
+        w[i] = base[(int64_t)i * (D + 2)];
+        lv[i] = base[(int64_t)i * (D + 2) + 1];
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < active; ++s) M = fmaxf(M, w[s * G + tid]);
+        float sum = 0.0f;
+        for (int s = 0; s < active; ++s) {
+            float l = lv[s * G + tid];
+            float e = l == 0.0f ? 0.0f : expf(w[s * G + tid] - M);
+            w[s * G + tid] = e;
+            sum = fmaf(e, l, sum);
+        }
+        L[tid] = sum;
+    }
+    __syncthreads();
+    // Thread (sg, j4): float4 column j4 of every head, splits sg, sg+8, ...
+    constexpr int C4 = D / 4;
+    constexpr int SG = kThreads / C4;
+    const int j4 = tid % C4, sg = tid / C4;
+    for (int gh = 0; gh < G; ++gh) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int s = sg; s < active; s += SG) {
+            const float4 o = *(const float4 *)(base + (int64_t)(s * G + gh) * (D + 2) + 2 + 4 * j4);
+            const float e = w[s * G + gh];
+            acc.x = fmaf(e, o.x, acc.x);
+            acc.y = fmaf(e, o.y, acc.y);
+            acc.z = fmaf(e, o.z, acc.z);
+            acc.w = fmaf(e, o.w, acc.w);
+        }
+        *(float4 *)(red + (sg * G + gh) * D + 4 * j4) = acc;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * D; i += kThreads) {
+        int gh = i / D, j = i % D;
+        float sum = 0.0f;
+        for (int q = 0; q < SG; ++q) sum += red[(q * G + gh) * D + j];
+        a.out[(int64_t)(kh * G + gh) * D + j] = sum / L[gh];
+    }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kThreads) k_attn_tiled(KernelArgs ka) {
+    extern __shared__ float lds[];
+    const AttnStepArgs &a = ka.s;
+    if (ka.mode == 1 && a.done && *a.done) return;
+    constexpr int T = kTileFloats / D;          // keys per tile
+    constexpr int C4 = D / 4;                   // float4 per row
+    constexpr int LPK = C4 < 16 ? C4 : 16;      // lanes per key in the score pass
+    constexpr int VPL = C4 / LPK;               // float4 per lane per key
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kh = blockIdx.y, split = blockIdx.x;
+    const int G = a.heads / a.kv_heads, kvw = a.kv_heads * D;
+
+    const Geo g = geometry(ka);
+    int split_len = (g.total + a.splits - 1) / a.splits;
+    split_len = (split_len + T - 1) / T * T;
+    const int t0 = min(split * split_len, g.total);
+    const int t1 = min(t0 + split_len, g.total);
+
+    float *Ks = lds;                           // [T][D]
+    float *Vs = Ks + T * D;                    // [T][D]
+    float *qs = Vs + T * D;                    // [G][D]
+    float *kn = qs + G * D;                    // [D]
+    float *vn = kn + D;                        // [D]
+    float *sc = vn + D;                        // [G][T]
+    float *st = sc + G * T;                    // [G] running max, [G] running sum, [G] rescale
+    int *flag = (int *)(st + 3 * kMaxG);
+
+    prepare(ka, g, kh, G, D, qs, kn, vn, t0, t1);
+    if (tid < G) {
+        st[tid] = -INFINITY;
+        st[kMaxG + tid] = 0.0f;
+    }
 
     const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
     const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
-    const int newest_from_lds = ka.mode == 1 ? g.length - 1 : -1;
-    auto key_row = [&](int t) -> const float * {
-        if (t == newest_from_lds) return kn;
-        if (t < g.length) return rk + (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * d;
-        return a.extra_k + (int64_t)(t - g.length) * kvw + (int64_t)kh * d;
+    const int newest = ka.mode == 1 ? g.length - 1 : -1;
+
+    // Output ownership in the PV pass: thread -> column j, heads gs, gs+GS, ...
+    constexpr int GS = kThreads / D > 0 ? kThreads / D : 1;
+    const int pj = tid % D, pg = tid / D;
+    float acc[kMaxG / GS > 0 ? kMaxG / GS : 1];
+    const int nacc = (G + GS - 1) / GS;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(acc) / sizeof(float)); ++i) acc[i] = 0.0f;
+
+    // Tile loader: float4 index f = tid + 256*i -> (row f / C4, column f % C4).
+    float4 pk[4], pv[4];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int f = tid + kThreads * i, r = f / C4, c = f % C4;
+            int t = c0 + r;
+            if (t < t1 && t != newest) {
+                const float *kr, *vr;
+                if (t < g.length) {
+                    int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D;
+                    kr = rk + off;
+                    vr = rv + off;
+                } else {
+                    int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D;
+                    kr = a.extra_k + off;
+                    vr = a.extra_v + off;
+                }
+                pk[i] = *(const float4 *)(kr + 4 * c);
+                pv[i] = *(const float4 *)(vr + 4 * c);
+            }
+        }
     };
-    auto value_row = [&](int t) -> const float * {
-        if (t == newest_from_lds) return vn;
-        if (t < g.length) return rv + (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * d;
-        return a.extra_v + (int64_t)(t - g.length) * kvw + (int64_t)kh * d;
+    auto stash = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int f = tid + kThreads * i, r = f / C4, c = f % C4;
+            int t = c0 + r;
+            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
+            if (t == newest) {
+                kk = *(const float4 *)(kn + 4 * c);
+                vv = *(const float4 *)(vn + 4 * c);
+            } else if (t < t1) {
+                kk = pk[i];
+                vv = pv[i];
+            }
+            *(float4 *)(Ks + r * D + 4 * c) = kk;
+            *(float4 *)(Vs + r * D + 4 * c) = vv;
+        }
     };
 
-    // Scores: lpk lanes per key.
-    const int nv = d / VEC;
-    int lpk = 1;
-    while (lpk * 2 <= nv && lpk < 16) lpk *= 2;
-    const int sub = lane & (lpk - 1), kslot = lane / lpk, kper_wave = kWave / lpk;
-    const float inv_norm = sqrtf((float)d);
-    for (int base = t0 + wave * kper_wave; base < t1; base += kWaves * kper_wave) {
-        int t = base + kslot;
-        bool ok = t < t1;
-        const float *kr = key_row(ok ? t : t0);
-        for (int gh = 0; gh < G; ++gh) {
-            float part = dot_part<VEC>(qs + gh * d, kr, sub, lpk, nv);
-            part = group_sum(part, lpk);
-            if (ok && sub == 0) sc[gh * split_len + (t - t0)] = part / inv_norm;
+    const float inv_norm = sqrtf((float)D);
+    if (t0 < t1) fetch(t0);
+    for (int c0 = t0; c0 < t1; c0 += T) {
+        const int n = min(T, t1 - c0);
+        stash(c0);
+        __syncthreads();
+        if (c0 + T < t1) fetch(c0 + T);   // in flight while this tile is consumed
+        // Scores: LPK lanes per key.
+        {
+            const int sub = lane % LPK, ks = lane / LPK;
+            constexpr int KPW = kWave / LPK;
+            for (int r0 = wave * KPW; r0 < n; r0 += kWaves * KPW) {
+                int r = r0 + ks;
+                const float *kr = Ks + min(r, T - 1) * D;
+                float4 kv[VPL];
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) kv[v] = *(const float4 *)(kr + 4 * (sub + LPK * v));
+                for (int gh = 0; gh < G; ++gh) {
+                    float part = 0.0f;
+#pragma unroll
+                    for (int v = 0; v < VPL; ++v) {
+                        float4 q4 = *(const float4 *)(qs + gh * D + 4 * (sub + LPK * v));
+                        part = fmaf(q4.x, kv[v].x, part);
+                        part = fmaf(q4.y, kv[v].y, part);
+                        part = fmaf(q4.z, kv[v].z, part);
+                        part = fmaf(q4.w, kv[v].w, part);
+                    }
+                    part = group_sum(part, LPK);
+                    if (sub == 0 && r < n) sc[gh * T + r] = part / inv_norm;
+                }
+            }
+        }
+        __syncthreads();
+        // Online softmax statistics per head (one wave per head).
+        for (int gh = wave; gh < G; gh += kWaves) {
+            float mx = -INFINITY;
+            for (int r = lane; r < n; r += kWave) mx = fmaxf(mx, sc[gh * T + r]);
+            mx = wave_max(mx);
+            const float m_old = st[gh];
+            const float m_new = fmaxf(m_old, mx);
+            const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+            float sum = 0.0f;
+            for (int r = lane; r < n; r += kWave) {
+                float p = expf(sc[gh * T + r] - m_new);
+                sc[gh * T + r] = p;
+                sum += p;
+            }
+            sum = wave_sum(sum);
+            if (lane == 0) {
+                st[gh] = m_new;
+                st[kMaxG + gh] = st[kMaxG + gh] * alpha + sum;
+                st[2 * kMaxG + gh] = alpha;
+            }
+        }
+        __syncthreads();
+        // Weighted values.
+        for (int i = 0; i < nacc; ++i) {
+            int gh = pg + GS * i;
+            if (gh < G) {
+                float v = acc[i] * st[2 * kMaxG + gh];
+                const float *p = sc + gh * T;
+                for (int r = 0; r < n; ++r) v = fmaf(p[r], Vs[r * D + pj], v);
+                acc[i] = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    // Partial (m, l, o) of this split.
+    float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
+    if (t0 < t1) {
+        for (int i = 0; i < nacc; ++i) {
+            int gh = pg + GS * i;
+            if (gh < G) part[gh * (D + 2) + 2 + pj] = acc[i];
+        }
+        if (tid < G) {
+            part[tid * (D + 2)] = st[tid];
+            part[tid * (D + 2) + 1] = st[kMaxG + tid];
         }
     }
-    __syncthreads();
-
-    // Local softmax statistics per head.
-    const int n = max(t1 - t0, 0);
-    for (int gh = wave; gh < G; gh += kWaves) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += kWave) m = fmaxf(m, sc[gh * split_len + i]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int i = lane; i < n; i += kWave) {
-            float p = expf(sc[gh * split_len + i] - m);
-            sc[gh * split_len + i] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            stat[2 * gh] = m;
-            stat[2 * gh + 1] = l;
-        }
-    }
-    __syncthreads();
-
-    // Weighted values.
-    float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (d + 2);
-    for (int idx = tid; idx < G * d; idx += kThreads) {
-        int gh = idx / d, j = idx % d;
-        float acc = 0.0f;
-        const float *p = sc + gh * split_len;
-        for (int i = 0; i < n; ++i) acc = fmaf(p[i], value_row(t0 + i)[j], acc);
-        part[gh * (d + 2) + 2 + j] = acc;
-    }
-    if (tid < G) {
-        part[tid * (d + 2)] = n ? stat[2 * tid] : -INFINITY;
-        part[tid * (d + 2) + 1] = n ? stat[2 * tid + 1] : 0.0f;
-    }
-
-    // Last workgroup of this KV head merges all splits.
     __threadfence();
     __syncthreads();
-    if (tid == 0) {
-        unsigned prev = atomicAdd(&a.counters[kh], 1u);
-        *flag = prev == (unsigned)(a.splits - 1);
+    if (tid == 0) *flag = atomicAdd(&a.counters[kh], 1u) == (unsigned)(a.splits - 1);
+    __syncthreads();
+    const bool last = *flag;
+    __syncthreads();   // the combine reuses this LDS
+    if (!last) return;
+    __threadfence();
+    const int active = (g.total + split_len - 1) / split_len;
+    combine<D>(a, kh, G, active, lds);
+    if (tid == 0) a.counters[kh] = 0u;
+}
+
+// ---------------------------------------------------------------- generic path
+// Any head dim (micro models, op-level tests with dim 6): per-element loops.
+__global__ void __launch_bounds__(kThreads) k_attn_generic(KernelArgs ka) {
+    extern __shared__ float lds[];
+    const AttnStepArgs &a = ka.s;
+    if (ka.mode == 1 && a.done && *a.done) return;
+    const int tid = threadIdx.x;
+    const int kh = blockIdx.y, split = blockIdx.x;
+    const int d = a.dim, G = a.heads / a.kv_heads, kvw = a.kv_heads * d;
+    const Geo g = geometry(ka);
+    int split_len = (g.total + a.splits - 1) / a.splits;
+    const int t0 = min(split * split_len, g.total);
+    const int t1 = min(t0 + split_len, g.total);
+    const int cap_len = a.split_len;   // LDS score rows sized for the plan's maximum
+    float *qs = lds, *kn = qs + G * d, *vn = kn + d, *sc = vn + d;
+    int *flag = (int *)(sc + G * cap_len);
+    prepare(ka, g, kh, G, d, qs, kn, vn, t0, t1);
+    const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
+    const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
+    const int newest = ka.mode == 1 ? g.length - 1 : -1;
+    auto row = [&](const float *ring, const float *extra, const float *fresh, int t) -> const float * {
+        if (t == newest) return fresh;
+        if (t < g.length) return ring + (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * d;
+        return extra + (int64_t)(t - g.length) * kvw + (int64_t)kh * d;
+    };
+    const int n = t1 - t0;
+    for (int i = tid; i < G * n; i += kThreads) {
+        int gh = i / n, r = i % n;
+        const float *kr = row(rk, a.extra_k, kn, t0 + r);
+        float v = 0.0f;
+        for (int j = 0; j < d; ++j) v = fmaf(qs[gh * d + j], kr[j], v);
+        sc[gh * cap_len + r] = v / sqrtf((float)d);
     }
+    __syncthreads();
+    float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (d + 2);
+    if (tid < G && n > 0) {
+        float m = -INFINITY;
+        for (int r = 0; r < n; ++r) m = fmaxf(m, sc[tid * cap_len + r]);
+        float l = 0.0f;
+        for (int r = 0; r < n; ++r) {
+            float p = expf(sc[tid * cap_len + r] - m);
+            sc[tid * cap_len + r] = p;
+            l += p;
+        }
+        part[tid * (d + 2)] = m;
+        part[tid * (d + 2) + 1] = l;
+    }
+    __syncthreads();
+    if (n > 0)
+        for (int i = tid; i < G * d; i += kThreads) {
+            int gh = i / d, j = i % d;
+            float acc = 0.0f;
+            for (int r = 0; r < n; ++r) acc = fmaf(sc[gh * cap_len + r], row(rv, a.extra_v, vn, t0 + r)[j], acc);
+            part[gh * (d + 2) + 2 + j] = acc;
+        }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) *flag = atomicAdd(&a.counters[kh], 1u) == (unsigned)(a.splits - 1);
     __syncthreads();
     if (!*flag) return;
     __threadfence();
+    const int active = split_len ? (g.total + split_len - 1) / split_len : 0;
     const float *base = a.part + (int64_t)kh * a.splits * G * (d + 2);
-    for (int idx = tid; idx < G * d; idx += kThreads) {
-        int gh = idx / d, j = idx % d;
+    for (int i = tid; i < G * d; i += kThreads) {
+        int gh = i / d, j = i % d;
         float M = -INFINITY;
-        for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[(s * G + gh) * (d + 2)]);
+        for (int s = 0; s < active; ++s) M = fmaxf(M, base[(s * G + gh) * (d + 2)]);
         float L = 0.0f, O = 0.0f;
-        for (int s = 0; s < a.splits; ++s) {
+        for (int s = 0; s < active; ++s) {
             const float *ps = base + (s * G + gh) * (d + 2);
-            float l = ps[1];
-            if (l == 0.0f) continue;
             float w = expf(ps[0] - M);
-            L = fmaf(w, l, L);
+            L = fmaf(w, ps[1], L);
             O = fmaf(w, ps[2 + j], O);
         }
         a.out[(int64_t)(kh * G + gh) * d + j] = O / L;
@@ -224,33 +420,47 @@ __global__ void __launch_bounds__(kThreads) k_attn_split(KernelArgs ka) {
     if (tid == 0) a.counters[kh] = 0u;
 }
 
-size_t lds_bytes(int G, int d, int split_len) {
-    return (size_t)(G * d + 2 * d + G * split_len + 2 * G + kWaves + 4) * sizeof(float);
+bool tiled_dim(int d) { return d == 32 || d == 64 || d == 128; }
+
+size_t lds_tiled(int G, int d, int splits) {
+    const int T = kTileFloats / d;
+    size_t main = (size_t)(2 * T * d + G * d + 2 * d + G * T + 3 * kMaxG + 4);
+    size_t comb = (size_t)(2 * splits * G + G + (kThreads / (d / 4)) * G * d);
+    return std::max(main, comb) * sizeof(float);
 }
+
+size_t lds_generic(int G, int d, int split_len) { return (size_t)(G * d + 2 * d + G * split_len + 4) * sizeof(float); }
 
 int launch(hipStream_t s, const KernelArgs &ka) {
     const AttnStepArgs &a = ka.s;
-    int G = a.heads / a.kv_heads;
+    const int G = a.heads / a.kv_heads;
     dim3 grid(a.splits, a.kv_heads);
-    size_t lds = lds_bytes(G, a.dim, a.split_len);
-    if (lds > 160 * 1024) return fail(MR_ERR_INVALID, "attention: workgroup LDS need above 160 KiB");
-    if (a.dim % 4 == 0)
-        k_attn_split<4><<<grid, kThreads, lds, s>>>(ka);
-    else
-        k_attn_split<1><<<grid, kThreads, lds, s>>>(ka);
+    if (tiled_dim(a.dim) && G <= kMaxG) {
+        size_t lds = lds_tiled(G, a.dim, a.splits);
+        if (lds > 64 * 1024) return fail(MR_ERR_INVALID, "attention: workgroup LDS need above 64 KiB");
+        switch (a.dim) {
+            case 32: k_attn_tiled<32><<<grid, kThreads, lds, s>>>(ka); break;
+            case 64: k_attn_tiled<64><<<grid, kThreads, lds, s>>>(ka); break;
+            default: k_attn_tiled<128><<<grid, kThreads, lds, s>>>(ka); break;
+        }
+    } else {
+        size_t lds = lds_generic(G, a.dim, a.split_len);
+        if (lds > 64 * 1024) return fail(MR_ERR_INVALID, "attention: workgroup LDS need above 64 KiB");
+        k_attn_generic<<<grid, kThreads, lds, s>>>(ka);
+    }
     MR_LAUNCHED("enqueue attention");
     return MR_OK;
 }
 
 }  // namespace
 
-void attention_plan(int max_total, int kv_heads, int *splits, int *split_len) {
-    // Aim for ~512 workgroups over the KV heads, at least 16 keys per split.
+void attention_plan(int max_total, int kv_heads, int dim, int *splits, int *split_len) {
+    // One tile of keys per split at the full window, at most ~512 workgroups.
+    const int T = tiled_dim(dim) ? kTileFloats / dim : 64;
     int want = std::max(1, 512 / std::max(kv_heads, 1));
-    int len = std::max(16, ceil_div(max_total, want));
-    len = (len + 15) / 16 * 16;
-    *split_len = len;
-    *splits = std::max(1, ceil_div(max_total, len));
+    int n = std::max(1, std::min(want, ceil_div(max_total, T)));
+    *splits = n;
+    *split_len = ceil_div(max_total, n);   // upper bound of the per-split key count
 }
 
 size_t attention_part_floats(int heads, int kv_heads, int dim, int splits) {
@@ -279,7 +489,7 @@ int launch_attention_op(mr_ctx *ctx, const AttnProblem &p) {
     a.dim = p.dim;
     a.capacity = p.capacity;
     a.out = p.out;
-    attention_plan(total, p.kv_heads, &a.splits, &a.split_len);
+    attention_plan(total, p.kv_heads, p.dim, &a.splits, &a.split_len);
     ka.mode = 0;
     ka.start = p.start;
     ka.length = p.length;

@@ -328,66 +328,88 @@ void free_weight(Weight &w) {
     w.ptr = nullptr;
 }
 
-// Launch the kernels of one token step on the context stream.
-int record_gqa_layer(mr_model *m, Layer &L, int li) {
+// The five fused kernels of one GQA layer (plus the flashnano-1.6 CBR kernels,
+// timed together with attention).
+int launch_gqa_part(mr_model *m, Layer &L, int part) {
     const mr_model_desc &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
-    const int dt = L.qkv.dtype;
-    // 1. RMSNorm -> fused Q/K/V projection.
-    GemvArgs g;
-    g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
-    g.n = qd + 2 * kvw; g.k = h; g.y = m->qkv; g.done = m->done_dev;
-    if (d.family == MR_FAMILY_FLASHNANO_16) g.x_out = m->xnorm;
-    MR_TRY(launch_gemv(s, dt, PRO_RMS, EPI_STORE, g));
-    // 2. Q/K norm + RoPE + ring write + attention.
-    AttnStepArgs a;
-    a.q = m->qkv; a.k_new = m->qkv + qd; a.v_new = m->qkv + qd + kvw;
-    if (d.qk_norm) { a.q_gain = L.q_norm.f(); a.k_gain = L.k_norm.f(); }
-    a.eps = d.norm_eps; a.freq = m->freq; a.split_half = d.split_half_rope;
-    a.pos = m->pos_dev; a.done = m->done_dev;
-    a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.capacity = L.capacity;
-    if (d.family == MR_FAMILY_FLASHNANO_16) {
-        a.extra_k = L.relay_k; a.extra_v = L.relay_v;
-        a.extra_chunk = d.cbr_chunk_size; a.extra_slots = d.cbr_slots;
+    switch (part) {
+        case MR_KERNEL_QKV: {   // RMSNorm -> fused Q/K/V projection
+            GemvArgs g;
+            g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
+            g.n = qd + 2 * kvw; g.k = h; g.y = m->qkv; g.done = m->done_dev;
+            if (d.family == MR_FAMILY_FLASHNANO_16) g.x_out = m->xnorm;
+            return launch_gemv(s, L.qkv.dtype, PRO_RMS, EPI_STORE, g);
+        }
+        case MR_KERNEL_ATTENTION: {   // Q/K norm + RoPE + ring write + attention
+            AttnStepArgs a;
+            a.q = m->qkv; a.k_new = m->qkv + qd; a.v_new = m->qkv + qd + kvw;
+            if (d.qk_norm) { a.q_gain = L.q_norm.f(); a.k_gain = L.k_norm.f(); }
+            a.eps = d.norm_eps; a.freq = m->freq; a.split_half = d.split_half_rope;
+            a.pos = m->pos_dev; a.done = m->done_dev;
+            a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.capacity = L.capacity;
+            if (d.family == MR_FAMILY_FLASHNANO_16) {
+                a.extra_k = L.relay_k; a.extra_v = L.relay_v;
+                a.extra_chunk = d.cbr_chunk_size; a.extra_slots = d.cbr_slots;
+            }
+            a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.dim = hd;
+            a.part = m->part; a.counters = m->counters; a.out = m->attn;
+            a.splits = L.splits; a.split_len = L.split_len;
+            MR_TRY(launch_attention_step(s, a));
+            if (d.family != MR_FAMILY_FLASHNANO_16) return MR_OK;
+            // flashnano-1.6: chunk pooling into the relay, after this step's attention.
+            const int chunk = d.cbr_chunk_size, slots = d.cbr_slots;
+            const int dt = L.qkv.dtype;
+            size_t lds = (size_t)(chunk + 8) * sizeof(float);
+            k_cbr_pool<<<slots, 256, lds, s>>>(m->xnorm, L.pending, L.cbr_queries, m->cbr_pooled, m->cbr_anchor,
+                                                m->cbr_skip, m->pos_dev, m->done_dev, chunk, h);
+            MR_LAUNCHED("enqueue cbr pool");
+            const void *wkv = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(dt);
+            k_cbr_project<<<dim3(ceil_div(2 * kvw, 4), slots), 256, 0, s>>>(m->cbr_pooled, wkv, dt, m->cbr_kv,
+                                                                             m->cbr_skip, 2 * kvw, h);
+            MR_LAUNCHED("enqueue cbr project");
+            k_cbr_finish<<<slots, 256, (size_t)kvw * sizeof(float), s>>>(
+                m->cbr_kv, m->cbr_anchor, L.k_norm.f(), d.norm_eps, m->freq, d.split_half_rope, L.relay_k,
+                L.relay_v, m->cbr_skip, m->pos_dev, chunk, slots, L.kv_heads, hd);
+            MR_LAUNCHED("enqueue cbr finish");
+            return MR_OK;
+        }
+        case MR_KERNEL_O: {   // o projection + residual
+            GemvArgs o;
+            o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->hidden; o.scale = d.residual_scale;
+            o.done = m->done_dev;
+            return launch_gemv(s, L.o.dtype, PRO_COPY, EPI_RESIDUAL, o);
+        }
+        case MR_KERNEL_GATE_UP: {   // RMSNorm -> gate/up + SwiGLU
+            GemvArgs gu;
+            gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->hidden; gu.gain = L.f_norm.f();
+            gu.eps = d.norm_eps; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act; gu.done = m->done_dev;
+            return launch_gemv(s, L.ffn.gate.dtype, PRO_RMS, EPI_SWIGLU, gu);
+        }
+        case MR_KERNEL_DOWN: {   // down projection + residual
+            GemvArgs dn;
+            dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden;
+            dn.scale = d.residual_scale; dn.done = m->done_dev;
+            return launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_RESIDUAL, dn);
+        }
     }
-    a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.dim = hd;
-    a.part = m->part; a.counters = m->counters; a.out = m->attn;
-    a.splits = L.splits; a.split_len = L.split_len;
-    MR_TRY(launch_attention_step(s, a));
-    // flashnano-1.6: chunk pooling into the relay, after this step's attention.
-    if (d.family == MR_FAMILY_FLASHNANO_16) {
-        const int chunk = d.cbr_chunk_size, slots = d.cbr_slots;
-        size_t lds = (size_t)(chunk + 8) * sizeof(float);
-        k_cbr_pool<<<slots, 256, lds, s>>>(m->xnorm, L.pending, L.cbr_queries, m->cbr_pooled, m->cbr_anchor,
-                                            m->cbr_skip, m->pos_dev, m->done_dev, chunk, h);
-        MR_LAUNCHED("enqueue cbr pool");
-        const void *wkv = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(dt);
-        k_cbr_project<<<dim3(ceil_div(2 * kvw, 4), slots), 256, 0, s>>>(m->cbr_pooled, wkv, dt, m->cbr_kv,
-                                                                         m->cbr_skip, 2 * kvw, h);
-        MR_LAUNCHED("enqueue cbr project");
-        k_cbr_finish<<<slots, 256, (size_t)kvw * sizeof(float), s>>>(
-            m->cbr_kv, m->cbr_anchor, L.k_norm.f(), d.norm_eps, m->freq, d.split_half_rope, L.relay_k, L.relay_v,
-            m->cbr_skip, m->pos_dev, chunk, slots, L.kv_heads, hd);
-        MR_LAUNCHED("enqueue cbr finish");
-    }
-    // 3. o projection + residual.
-    GemvArgs o;
-    o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->hidden; o.scale = d.residual_scale;
-    o.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_RESIDUAL, o));
-    // 4. RMSNorm -> gate/up + SwiGLU.
-    GemvArgs gu;
-    gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->hidden; gu.gain = L.f_norm.f(); gu.eps = d.norm_eps;
-    gu.n = d.ffn_dim; gu.k = h; gu.y = m->act; gu.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_RMS, EPI_SWIGLU, gu));
-    // 5. down projection + residual.
-    GemvArgs dn;
-    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden; dn.scale = d.residual_scale;
-    dn.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_RESIDUAL, dn));
-    (void)li;
+    return fail(MR_ERR_INVALID, "unknown layer kernel");
+}
+
+int record_gqa_layer(mr_model *m, Layer &L) {
+    for (int part : {MR_KERNEL_QKV, MR_KERNEL_ATTENTION, MR_KERNEL_O, MR_KERNEL_GATE_UP, MR_KERNEL_DOWN})
+        MR_TRY(launch_gqa_part(m, L, part));
     return MR_OK;
+}
+
+int launch_lm_head(mr_model *m) {
+    const mr_model_desc &d = m->d;
+    const Weight &head = d.tie_embeddings ? m->embed : m->output;
+    GemvArgs g;
+    g.w = head.ptr; g.x = m->hidden; g.gain = m->norm.f(); g.eps = d.norm_eps;
+    g.n = d.vocab_size; g.k = d.hidden_size; g.y = m->logits; g.done = m->done_dev;
+    return launch_gemv(m->ctx->stream, head.dtype, PRO_RMS, EPI_STORE, g);
 }
 
 int record_head(mr_model *m, int kind) {
@@ -398,11 +420,7 @@ int record_head(mr_model *m, int kind) {
         MR_LAUNCHED("enqueue advance");
         return MR_OK;
     }
-    const Weight &head = d.tie_embeddings ? m->embed : m->output;
-    GemvArgs g;
-    g.w = head.ptr; g.x = m->hidden; g.gain = m->norm.f(); g.eps = d.norm_eps;
-    g.n = d.vocab_size; g.k = d.hidden_size; g.y = m->logits; g.done = m->done_dev;
-    MR_TRY(launch_gemv(s, head.dtype, PRO_RMS, EPI_STORE, g));
+    MR_TRY(launch_lm_head(m));
     if (kind == STEP_LOGITS) {
         k_advance<<<1, 1, 0, s>>>(m->pos_dev, m->done_dev);
         MR_LAUNCHED("enqueue advance");
@@ -422,7 +440,7 @@ int record_step(mr_model *m, int kind) {
     k_embed<<<ceil_div(d.hidden_size, 256), 256, 0, s>>>(m->embed.ptr, m->embed.dtype, m->ids_dev, m->pos_dev,
                                                          m->done_dev, m->hidden, d.hidden_size);
     MR_LAUNCHED("enqueue embed");
-    for (int li = 0; li < d.layers; ++li) MR_TRY(record_gqa_layer(m, m->layers[li], li));
+    for (int li = 0; li < d.layers; ++li) MR_TRY(record_gqa_layer(m, m->layers[li]));
     return record_head(m, kind);
 }
 
@@ -642,7 +660,7 @@ int mr_model_finalize(mr_model *m) {
                                                                 d.cbr_norm_eps);
             MR_LAUNCHED("normalize cbr queries");
         }
-        attention_plan(L.capacity + extra_max, L.kv_heads, &L.splits, &L.split_len);
+        attention_plan(L.capacity + extra_max, L.kv_heads, hd, &L.splits, &L.split_len);
         max_part = std::max(max_part, attention_part_floats(d.query_heads, L.kv_heads, hd, L.splits));
     }
     // One allocation for all per-sequence scalars and activation vectors.
@@ -773,6 +791,40 @@ int mr_model_generate_greedy(mr_model *m, int max_new, int eos, int32_t *tokens,
     m->position = pos;
     *produced = count;
     if (host[0] == 2) return fail(MR_ERR_NONFINITE, "non-finite output logits");
+    return MR_OK;
+}
+
+int mr_model_time_kernel(mr_model *m, int which, int reps, float *avg_ms) {
+    MR_TRY(check_ctx(m, "time_kernel"));
+    MR_REQUIRE(avg_ms && reps >= 1 && which >= MR_KERNEL_QKV && which <= MR_KERNEL_HEAD, "time_kernel: bad arguments");
+    hipStream_t s = m->ctx->stream;
+    hipEvent_t e0, e1;
+    MR_HIP(hipEventCreate(&e0), "create event");
+    MR_HIP(hipEventCreate(&e1), "create event");
+    MR_HIP(hipMemsetAsync(m->done_dev, 0, sizeof(int), s), "clear stop flag");
+    int launches = 0, rc = MR_OK;
+    hipEventRecord(e0, s);
+    for (int r = 0; r < reps && rc == MR_OK; ++r) {
+        if (which == MR_KERNEL_HEAD) {
+            rc = launch_lm_head(m);
+            ++launches;
+            continue;
+        }
+        for (Layer &L : m->layers) {
+            rc = launch_gqa_part(m, L, which);
+            if (rc != MR_OK) break;
+            ++launches;
+        }
+    }
+    hipEventRecord(e1, s);
+    hipError_t e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc != MR_OK) return rc;
+    MR_HIP(e, "time kernel");
+    *avg_ms = ms / (float)std::max(launches, 1);
     return MR_OK;
 }
 

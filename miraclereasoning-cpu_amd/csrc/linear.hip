@@ -94,67 +94,82 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int row, float acc
     }
 }
 
-template <int DT, int R, int PRO, int EPI>
+template <int DT, int R, int U, int PRO, int EPI>
 __global__ void __launch_bounds__(kGemvThreads) k_gemv_vec(GemvArgs a, int lpr) {
     extern __shared__ float smem[];
     if (a.done && *a.done) return;
-    float *xs = smem;
-    float *red = smem + ((a.k + 3) & ~3);
-    stage_x<PRO>(a, xs, red);
-
     using V = Vec16<DT>;
     constexpr int E = V::E;
+    constexpr int M = EPI == EPI_SWIGLU ? 2 : 1;   // matrices read per row
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane & (lpr - 1), slot = lane / lpr;
     const int slots = kWave / lpr;
     const int row0 = ((blockIdx.x * kGemvWaves + wave) * slots + slot) * R;
     const int nvec = a.k / E;
     const int64_t k = a.k;
+    int64_t rowoff[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rowoff[r] = (int64_t)min(row0 + r, a.n - 1) * k;
 
-    int rows[R];
+    // Weight vectors of one batch: U vectors per row per matrix, lane-strided.
+    u32x4 wv[U][R][M];
+    auto issue = [&](int b) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.n - 1);
-
-    float acc[R], acc2[R];
+        for (int u = 0; u < U; ++u) {
+            const int v = sub + (b * U + u) * lpr;
+            if (v < nvec) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.0f;
-
-#pragma unroll 2
-    for (int v = sub; v < nvec; v += lpr) {
-        u32x4 wv[R], uv[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            wv[r] = load16<DT>(a.w, rows[r] * k + (int64_t)v * E);
-            if constexpr (EPI == EPI_SWIGLU) uv[r] = load16<DT>(a.w2, rows[r] * k + (int64_t)v * E);
-        }
-        float xv[E];
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            float4 t = *(const float4 *)(xs + v * E + e);
-            xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float wf[E];
-            V::widen(wv[r], wf);
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[r] = fmaf(wf[e], xv[e], acc[r]);
-            if constexpr (EPI == EPI_SWIGLU) {
-                V::widen(uv[r], wf);
-#pragma unroll
-                for (int e = 0; e < E; ++e) acc2[r] = fmaf(wf[e], xv[e], acc2[r]);
+                for (int r = 0; r < R; ++r) {
+                    wv[u][r][0] = load16<DT>(a.w, rowoff[r] + (int64_t)v * E);
+                    if constexpr (M == 2) wv[u][r][1] = load16<DT>(a.w2, rowoff[r] + (int64_t)v * E);
+                }
             }
         }
+    };
+    // The first batch is in flight while the prologue stages x.
+    issue(0);
+    float *xs = smem;
+    float *red = smem + ((a.k + 3) & ~3);
+    stage_x<PRO>(a, xs, red);
+
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+    for (int b = 0;; ++b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int v = sub + (b * U + u) * lpr;
+            if (v < nvec) {
+                float xv[E];
+#pragma unroll
+                for (int e = 0; e < E; e += 4) {
+                    float4 t = *(const float4 *)(xs + v * E + e);
+                    xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float wf[E];
+                        V::widen(wv[u][r][m], wf);
+#pragma unroll
+                        for (int e = 0; e < E; ++e) acc[r][m] = fmaf(wf[e], xv[e], acc[r][m]);
+                    }
+            }
+        }
+        if (sub + (b + 1) * U * lpr >= nvec) break;
+        issue(b + 1);
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        acc[r] = group_sum(acc[r], lpr);
-        if constexpr (EPI == EPI_SWIGLU) acc2[r] = group_sum(acc2[r], lpr);
-    }
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r][m] = group_sum(acc[r][m], lpr);
     if (sub == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (row0 + r < a.n) finish_row<EPI>(a, row0 + r, acc[r], acc2[r]);
+            if (row0 + r < a.n) finish_row<EPI>(a, row0 + r, acc[r][0], acc[r][M - 1]);
     }
 }
 
@@ -191,15 +206,15 @@ int launch_gemv_t(hipStream_t s, const GemvArgs &a) {
         int lpr = 1;
         while (lpr * 2 <= nvec && lpr < kWave) lpr *= 2;
         const int slots = kWave / lpr;
-        if (a.n >= 16384) {
-            constexpr int R = 4;
-            int grid = ceil_div(a.n, kGemvWaves * slots * R);
-            k_gemv_vec<DT, R, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
-        } else {
-            constexpr int R = 2;
-            int grid = ceil_div(a.n, kGemvWaves * slots * R);
-            k_gemv_vec<DT, R, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
-        }
+        const int per_lane = ceil_div(nvec, lpr);   // vectors per lane per row
+        constexpr int R = EPI == EPI_SWIGLU ? 1 : 2;
+        int grid = ceil_div(a.n, kGemvWaves * slots * R);
+        if (per_lane <= 2)
+            k_gemv_vec<DT, R, 2, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
+        else if (per_lane <= 4)
+            k_gemv_vec<DT, R, 4, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
+        else
+            k_gemv_vec<DT, R, 6, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a, lpr);
     } else {
         int grid = ceil_div(a.n, kGemvWaves);
         k_gemv_scalar<DT, PRO, EPI><<<grid, kGemvThreads, lds, s>>>(a);

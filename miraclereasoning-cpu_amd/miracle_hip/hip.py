@@ -89,6 +89,7 @@ _SIGNATURES = {
     "mr_model_forward": [_P, _P, _i, _i, _P],
     "mr_model_generate_greedy": [_P, _i, _i, _P, C.POINTER(C.c_int)],
     "mr_model_use_graph": [_P, _i],
+    "mr_model_time_kernel": [_P, _i, _i, C.POINTER(C.c_float)],
     "mr_debug_fail_next": [_P],
 }
 

@@ -118,6 +118,19 @@ class Engine:
         _check(code, "generate")
         return [int(t) for t in tokens[:produced.value]]
 
+    KERNELS = {"qkv": 0, "attention": 1, "o": 2, "gate_up": 3, "down": 4, "head": 5}
+
+    def time_kernel(self, which, reps=3):
+        """Average device milliseconds of one launch of a step kernel (HIP events)."""
+        ms = C.c_float()
+        _check(self.lib.mr_model_time_kernel(self.handle, self.KERNELS[which], reps, C.byref(ms)), "time kernel")
+        return ms.value
+
+    def position(self):
+        pos = C.c_int()
+        _check(self.lib.mr_model_position(self.handle, C.byref(pos)), "position")
+        return pos.value
+
     def use_graph(self, enable):
         _check(self.lib.mr_model_use_graph(self.handle, int(bool(enable))), "use_graph")
 
@@ -239,9 +252,7 @@ class MiracleModel:
                 self._failed = True
                 raise
             finally:
-                pos = C.c_int()
-                self.engine.lib.mr_model_position(self.engine.handle, C.byref(pos))
-                self.position = pos.value
+                self.position = self.engine.position()
             return generated
         rng, generated = np.random.default_rng(seed), []
         logits = self.prefill(tokens)

@@ -1,12 +1,15 @@
 """Seeded random-init weights and prompts for the named workloads.
 
 The stream is frozen: every fixture and measurement depends on it.
-  * ``np.random.default_rng(seed)`` walks ``expected_shapes(config)`` in its
-    insertion order (the order the reference's own tests use,
+  * tensors are numbered i = 0, 1, ... in ``expected_shapes(config)`` insertion
+    order (the order the reference's own tests use,
     tests/test_inference.py:19-21);
-  * a 2-D tensor draws ``standard_normal(shape, float32) * std`` with std 0.02,
+  * a 2-D tensor, flattened row-major, is cut into chunks of 2**22 values;
+    chunk c draws ``standard_normal(float32)`` from
+    ``Generator(PCG64(SeedSequence([seed, i, c])))`` and is scaled by std 0.02,
     except heavy-medium router matrices, std 1/sqrt(hidden) so router logits on
-    an RMS-normalised input are about N(0, 1);
+    an RMS-normalised input are about N(0, 1).  Chunks are independent, so they
+    are drawn in parallel and the values do not depend on the thread count;
   * 1-D tensors are ones (norm gains, residual gates), except heavy-medium
     router biases, zeros;
   * BF16 workloads round the FP32 draws to BF16 (nearest-even) and store bits;
@@ -18,12 +21,15 @@ The stream is frozen: every fixture and measurement depends on it.
 from __future__ import annotations
 
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
 from .config import ModelConfig
 from .weights import BF16Array, bf16_bits, expected_shapes
 
+_CHUNK = 1 << 22
 _ROUTER_BIAS = ("router.coarse.bias", "router.fine.bias", "router.group_bias", "router.expert_bias")
 
 
@@ -36,18 +42,29 @@ def synthetic_weights(config, seed, dtype="bf16", std=0.02):
     cfg = _as_config(config)
     if dtype not in ("f32", "bf16"):
         raise ValueError("dtype must be f32 or bf16")
-    rng = np.random.default_rng(seed)
     router_std = np.float32(1.0 / math.sqrt(cfg.hidden_size))
-    out = {}
-    for name, shape in expected_shapes(cfg).items():
+    out, jobs = {}, []
+    for index, (name, shape) in enumerate(expected_shapes(cfg).items()):
         if len(shape) == 2:
             scale = router_std if ".router." in name else np.float32(std)
-            a = rng.standard_normal(shape, dtype=np.float32)
-            a *= scale
-            out[name] = BF16Array(bf16_bits(a)) if dtype == "bf16" else a
+            target = np.empty(shape, np.uint16 if dtype == "bf16" else np.float32)
+            out[name] = BF16Array(target) if dtype == "bf16" else target
+            flat = target.reshape(-1)
+            jobs += [(flat, index, c, scale) for c in range(-(-flat.size // _CHUNK))]
         else:
             fill = 0.0 if name.endswith(_ROUTER_BIAS) else 1.0
             out[name] = np.full(shape, fill, np.float32)
+
+    def draw(job):
+        flat, index, c, scale = job
+        g = np.random.Generator(np.random.PCG64(np.random.SeedSequence([seed, index, c])))
+        begin = c * _CHUNK
+        values = g.standard_normal(min(_CHUNK, flat.size - begin), dtype=np.float32)
+        values *= scale
+        flat[begin:begin + values.size] = bf16_bits(values) if flat.dtype == np.uint16 else values
+
+    with ThreadPoolExecutor(max(1, min(16, len(os.sched_getaffinity(0))))) as pool:
+        list(pool.map(draw, jobs))
     return out
 
 
