@@ -188,9 +188,27 @@ MR_API int mr_model_forward(mr_model *model, const int32_t *ids, int n, int flag
  * logits were not all finite (tokens before it are still written). */
 MR_API int mr_model_generate_greedy(mr_model *model, int max_new, int eos, int32_t *tokens, int *produced);
 
-/* Capture the decode step in a hipGraph (on by default after the first step);
- * enable = 0 launches kernels eagerly instead. */
-MR_API int mr_model_use_graph(mr_model *model, int enable);
+/* How a token step runs.  MR_STEP_PERSISTENT (default): one cooperative
+ * kernel per step walks the whole layer stack (used when every phase fits it;
+ * otherwise the model runs MR_STEP_GRAPH).  MR_STEP_GRAPH: five fused kernels
+ * per layer, replayed from a captured hipGraph.  MR_STEP_EAGER: the same
+ * kernels launched one by one (for profilers). */
+enum { MR_STEP_PERSISTENT = 0, MR_STEP_GRAPH = 1, MR_STEP_EAGER = 2 };
+MR_API int mr_model_set_step_mode(mr_model *model, int mode);
+/* The mode steps actually run in (a persistent request may fall back). */
+MR_API int mr_model_get_step_mode(mr_model *model, int *mode);
+/* Phase timeline of the persistent step kernel (diagnostics; no counterpart in
+ * the reference).  Runs one greedy decode step at the current position with
+ * timestamps (100 MHz device wall clock) written per phase and workgroup:
+ * out[(phase * grid + wg) * 3 + {0: phase start, 1: barrier arrival,
+ * 2: barrier release}].  `capacity` is the number of uint64 in `out`;
+ * *phases and *grid receive the program size.  The step advances the sequence
+ * like any decode step. */
+MR_API int mr_model_trace_step(mr_model *model, uint64_t *out, int64_t capacity, int *phases, int *grid);
+
+/* Device milliseconds of the last mr_model_generate_greedy call (HIP events
+ * around its decode steps). */
+MR_API int mr_model_last_decode_ms(mr_model *model, float *ms);
 
 /* Measurement: average device time of one launch of a step kernel, taken with
  * HIP events on the context stream.  `which` is an MR_KERNEL_* id; the kernel is

@@ -27,7 +27,7 @@ struct AttnStepArgs {
     const float *q_gain = nullptr;     // per-head RMSNorm gains (null: no Q/K norm)
     const float *k_gain = nullptr;
     float eps = 0.0f;
-    const float *freq = nullptr;       // [dim/2]
+    const float *rope = nullptr;       // [positions][dim/2][2] cos, sin of pos * inv_freq
     int split_half = 0;
     const int *pos = nullptr;          // device position of this token
     const int *done = nullptr;

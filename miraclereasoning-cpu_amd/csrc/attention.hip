@@ -1,343 +1,40 @@
-// Split-key attention for one query token.
+// Split-key attention for one query token: the standalone kernels.
 //
-// Grid: (splits, kv_heads).  Workgroup (split, kh) owns the G = heads/kv_heads
-// query heads that share KV head kh (kernels.cl:66 mapping) and a contiguous
-// range of the logical keys [ring window, extra rows] (kernels.cl:67-68).  It
-// scores them (dot / sqrt(dim), kernels.cl:72), keeps a running max m and
-// l = sum exp(s - m), accumulates o = sum exp(s - m) v, and writes (m, l, o).
-// The last workgroup of each KV head to finish (a device counter) merges the
-// splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s -- the softmax-
-// weighted value sum of kernels.cl:75-107, up to rounding.
-//
-// Fast path (head dim 32/64/128): keys and values stream through LDS in 16 KB
-// tiles (4096 floats = 4096/dim keys), each thread loading 4 float4 of K and 4
-// of V per tile, coalesced along the row; the next tile is prefetched into
-// registers while the current one is consumed.  The split length follows the
-// current window, so every workgroup of the fixed grid has work.  Other head
-// dims take a plain per-element path (micro models only).
-#include "attention.h"
+// Grid: (splits, kv_heads).  Each workgroup runs one (split, kh) unit
+// (attention_tile.h); the last workgroup of each KV head to finish (a device
+// counter) merges that head's splits.  Head dims 32/64/128 take the tiled
+// unit; other head dims (micro models, op-level calls with dim 6) take a plain
+// per-element path.
+#include "attention_tile.h"
 
 namespace mr {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kTileFloats = 4096;
-constexpr int kMaxG = 16;
-
-struct KernelArgs {
-    AttnStepArgs s;       // engine fields (mode 1)
-    int mode;             // 0 = op-level, 1 = engine step
-    int start, length, extra_length;   // mode 0 geometry
-    const float *ring_k_ro, *ring_v_ro;
-};
-
-struct Geo {
-    int pos, start, length, extra, total;
-};
-
-__device__ __forceinline__ Geo geometry(const KernelArgs &ka) {
-    const AttnStepArgs &a = ka.s;
-    Geo g;
-    if (ka.mode == 1) {
-        g.pos = *a.pos;
-        int count = g.pos + 1;
-        g.length = min(count, a.capacity);
-        g.start = (count - g.length) % a.capacity;
-        g.extra = a.extra_chunk ? (g.pos / a.extra_chunk) * a.extra_slots : 0;
-    } else {
-        g.pos = 0;
-        g.start = ka.start;
-        g.length = ka.length;
-        g.extra = ka.extra_length;
-    }
-    g.total = g.length + g.extra;
-    return g;
-}
-
-// Engine mode: normalize (optional) and rotate the G queries and the new key in
-// LDS, then store the new key/value in the ring slot of this position (by the
-// split that holds the newest key).  Ends with a barrier.
-__device__ void prepare(const KernelArgs &ka, const Geo &g, int kh, int G, int d, float *qs, float *kn, float *vn,
-                        int t0, int t1) {
-    const AttnStepArgs &a = ka.s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float *q_src = a.q + (int64_t)kh * G * d;
-    for (int i = tid; i < G * d; i += kThreads) qs[i] = q_src[i];
-    if (ka.mode != 1) {
-        __syncthreads();
-        return;
-    }
-    for (int j = tid; j < d; j += kThreads) {
-        kn[j] = a.k_new[kh * d + j];
-        vn[j] = a.v_new[kh * d + j];
-    }
-    __syncthreads();
-    if (a.q_gain) {   // per-head RMSNorm, width = dim (kernels.cl:19-28)
-        for (int r = wave; r < G + 1; r += kWaves) {
-            float *row = r < G ? qs + r * d : kn;
-            const float *gain = r < G ? a.q_gain : a.k_gain;
-            float ss = 0.0f;
-            for (int j = lane; j < d; j += kWave) ss = fmaf(row[j], row[j], ss);
-            ss = wave_sum(ss);
-            float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
-            for (int j = lane; j < d; j += kWave) row[j] = row[j] * scale * gain[j];
-        }
-        __syncthreads();
-    }
-    const int half = d / 2;   // RoPE at this position (kernels.cl:30-44)
-    const float fpos = (float)g.pos;
-    for (int i = tid; i < (G + 1) * half; i += kThreads) {
-        int r = i / half, p = i % half;
-        float *row = r < G ? qs + r * d : kn;
-        int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
-        float u = row[j], v = row[k];
-        rope_pair(u, v, fpos, a.freq[p]);
-        row[j] = u;
-        row[k] = v;
-    }
-    __syncthreads();
-    const int newest = g.length - 1;
-    if (t0 <= newest && newest < t1) {
-        const int kvw = a.kv_heads * d;
-        int64_t slot = (int64_t)(g.pos % a.capacity) * kvw + (int64_t)kh * d;
-        for (int j = tid; j < d; j += kThreads) {
-            a.ring_k[slot + j] = kn[j];
-            a.ring_v[slot + j] = vn[j];
-        }
-    }
-}
-
-// Merge the splits of KV head kh (run by the last workgroup to finish).
-template <int D>
-__device__ void combine(const AttnStepArgs &a, int kh, int G, int active, float *lds) {
-    const int tid = threadIdx.x;
-    const float *base = a.part + (int64_t)kh * a.splits * G * (D + 2);
-    float *w = lds;                      // [active][G] split maxima, then weights e^(m_s - M)
-    float *lv = w + active * G;          // [active][G] split sums
-    float *L = lv + active * G;          // [G]
-    float *red = L + G;                  // [SG][G*D] partial sums
-    for (int i = tid; i < active * G; i += kThreads) {
-        w[i] = base[(int64_t)i * (D + 2)];
-        lv[i] = base[(int64_t)i * (D + 2) + 1];
-    }
-    __syncthreads();
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s = 0; s < active; ++s) M = fmaxf(M, w[s * G + tid]);
-        float sum = 0.0f;
-        for (int s = 0; s < active; ++s) {
-            float l = lv[s * G + tid];
-            float e = l == 0.0f ? 0.0f : expf(w[s * G + tid] - M);
-            w[s * G + tid] = e;
-            sum = fmaf(e, l, sum);
-        }
-        L[tid] = sum;
-    }
-    __syncthreads();
-    // Thread (sg, j4): float4 column j4 of every head, splits sg, sg+8, ...
-    constexpr int C4 = D / 4;
-    constexpr int SG = kThreads / C4;
-    const int j4 = tid % C4, sg = tid / C4;
-    for (int gh = 0; gh < G; ++gh) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-        for (int s = sg; s < active; s += SG) {
-            const float4 o = *(const float4 *)(base + (int64_t)(s * G + gh) * (D + 2) + 2 + 4 * j4);
-            const float e = w[s * G + gh];
-            acc.x = fmaf(e, o.x, acc.x);
-            acc.y = fmaf(e, o.y, acc.y);
-            acc.z = fmaf(e, o.z, acc.z);
-            acc.w = fmaf(e, o.w, acc.w);
-        }
-        *(float4 *)(red + (sg * G + gh) * D + 4 * j4) = acc;
-    }
-    __syncthreads();
-    for (int i = tid; i < G * D; i += kThreads) {
-        int gh = i / D, j = i % D;
-        float sum = 0.0f;
-        for (int q = 0; q < SG; ++q) sum += red[(q * G + gh) * D + j];
-        a.out[(int64_t)(kh * G + gh) * D + j] = sum / L[gh];
-    }
-}
+using namespace att;
+using KernelArgs = att::Args;
 
 template <int D>
 __global__ void __launch_bounds__(kThreads) k_attn_tiled(KernelArgs ka) {
     extern __shared__ float lds[];
     const AttnStepArgs &a = ka.s;
     if (ka.mode == 1 && a.done && *a.done) return;
-    constexpr int T = kTileFloats / D;          // keys per tile
-    constexpr int C4 = D / 4;                   // float4 per row
-    constexpr int LPK = C4 < 16 ? C4 : 16;      // lanes per key in the score pass
-    constexpr int VPL = C4 / LPK;               // float4 per lane per key
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int kh = blockIdx.y, split = blockIdx.x;
-    const int G = a.heads / a.kv_heads, kvw = a.kv_heads * D;
-
-    const Geo g = geometry(ka);
-    int split_len = (g.total + a.splits - 1) / a.splits;
-    split_len = (split_len + T - 1) / T * T;
-    const int t0 = min(split * split_len, g.total);
-    const int t1 = min(t0 + split_len, g.total);
-
-    float *Ks = lds;                           // [T][D]
-    float *Vs = Ks + T * D;                    // [T][D]
-    float *qs = Vs + T * D;                    // [G][D]
-    float *kn = qs + G * D;                    // [D]
-    float *vn = kn + D;                        // [D]
-    float *sc = vn + D;                        // [G][T]
-    float *st = sc + G * T;                    // [G] running max, [G] running sum, [G] rescale
-    int *flag = (int *)(st + 3 * kMaxG);
-
-    prepare(ka, g, kh, G, D, qs, kn, vn, t0, t1);
-    if (tid < G) {
-        st[tid] = -INFINITY;
-        st[kMaxG + tid] = 0.0f;
-    }
-
-    const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
-    const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
-    const int newest = ka.mode == 1 ? g.length - 1 : -1;
-
-    // Output ownership in the PV pass: thread -> column j, heads gs, gs+GS, ...
-    constexpr int GS = kThreads / D > 0 ? kThreads / D : 1;
-    const int pj = tid % D, pg = tid / D;
-    float acc[kMaxG / GS > 0 ? kMaxG / GS : 1];
-    const int nacc = (G + GS - 1) / GS;
-#pragma unroll
-    for (int i = 0; i < (int)(sizeof(acc) / sizeof(float)); ++i) acc[i] = 0.0f;
-
-    // Tile loader: float4 index f = tid + 256*i -> (row f / C4, column f % C4).
-    float4 pk[4], pv[4];
-    auto fetch = [&](int c0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int f = tid + kThreads * i, r = f / C4, c = f % C4;
-            int t = c0 + r;
-            if (t < t1 && t != newest) {
-                const float *kr, *vr;
-                if (t < g.length) {
-                    int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D;
-                    kr = rk + off;
-                    vr = rv + off;
-                } else {
-                    int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D;
-                    kr = a.extra_k + off;
-                    vr = a.extra_v + off;
-                }
-                pk[i] = *(const float4 *)(kr + 4 * c);
-                pv[i] = *(const float4 *)(vr + 4 * c);
-            }
-        }
-    };
-    auto stash = [&](int c0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int f = tid + kThreads * i, r = f / C4, c = f % C4;
-            int t = c0 + r;
-            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-            if (t == newest) {
-                kk = *(const float4 *)(kn + 4 * c);
-                vv = *(const float4 *)(vn + 4 * c);
-            } else if (t < t1) {
-                kk = pk[i];
-                vv = pv[i];
-            }
-            *(float4 *)(Ks + r * D + 4 * c) = kk;
-            *(float4 *)(Vs + r * D + 4 * c) = vv;
-        }
-    };
-
-    const float inv_norm = sqrtf((float)D);
-    if (t0 < t1) fetch(t0);
-    for (int c0 = t0; c0 < t1; c0 += T) {
-        const int n = min(T, t1 - c0);
-        stash(c0);
-        __syncthreads();
-        if (c0 + T < t1) fetch(c0 + T);   // in flight while this tile is consumed
-        // Scores: LPK lanes per key.
-        {
-            const int sub = lane % LPK, ks = lane / LPK;
-            constexpr int KPW = kWave / LPK;
-            for (int r0 = wave * KPW; r0 < n; r0 += kWaves * KPW) {
-                int r = r0 + ks;
-                const float *kr = Ks + min(r, T - 1) * D;
-                float4 kv[VPL];
-#pragma unroll
-                for (int v = 0; v < VPL; ++v) kv[v] = *(const float4 *)(kr + 4 * (sub + LPK * v));
-                for (int gh = 0; gh < G; ++gh) {
-                    float part = 0.0f;
-#pragma unroll
-                    for (int v = 0; v < VPL; ++v) {
-                        float4 q4 = *(const float4 *)(qs + gh * D + 4 * (sub + LPK * v));
-                        part = fmaf(q4.x, kv[v].x, part);
-                        part = fmaf(q4.y, kv[v].y, part);
-                        part = fmaf(q4.z, kv[v].z, part);
-                        part = fmaf(q4.w, kv[v].w, part);
-                    }
-                    part = group_sum(part, LPK);
-                    if (sub == 0 && r < n) sc[gh * T + r] = part / inv_norm;
-                }
-            }
-        }
-        __syncthreads();
-        // Online softmax statistics per head (one wave per head).
-        for (int gh = wave; gh < G; gh += kWaves) {
-            float mx = -INFINITY;
-            for (int r = lane; r < n; r += kWave) mx = fmaxf(mx, sc[gh * T + r]);
-            mx = wave_max(mx);
-            const float m_old = st[gh];
-            const float m_new = fmaxf(m_old, mx);
-            const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-            float sum = 0.0f;
-            for (int r = lane; r < n; r += kWave) {
-                float p = expf(sc[gh * T + r] - m_new);
-                sc[gh * T + r] = p;
-                sum += p;
-            }
-            sum = wave_sum(sum);
-            if (lane == 0) {
-                st[gh] = m_new;
-                st[kMaxG + gh] = st[kMaxG + gh] * alpha + sum;
-                st[2 * kMaxG + gh] = alpha;
-            }
-        }
-        __syncthreads();
-        // Weighted values.
-        for (int i = 0; i < nacc; ++i) {
-            int gh = pg + GS * i;
-            if (gh < G) {
-                float v = acc[i] * st[2 * kMaxG + gh];
-                const float *p = sc + gh * T;
-                for (int r = 0; r < n; ++r) v = fmaf(p[r], Vs[r * D + pj], v);
-                acc[i] = v;
-            }
-        }
-        __syncthreads();
-    }
-
-    // Partial (m, l, o) of this split.
-    float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
-    if (t0 < t1) {
-        for (int i = 0; i < nacc; ++i) {
-            int gh = pg + GS * i;
-            if (gh < G) part[gh * (D + 2) + 2 + pj] = acc[i];
-        }
-        if (tid < G) {
-            part[tid * (D + 2)] = st[tid];
-            part[tid * (D + 2) + 1] = st[kMaxG + tid];
-        }
-    }
+    const Geo g = geometry(ka, ka.mode == 1 ? *a.pos : 0);
+    attn_unit<D, false>(ka, g, kh, split, lds, Io{});
+    int *flag = (int *)(lds + unit_lds_floats<D>(a.heads / a.kv_heads) - 4);
     __threadfence();
     __syncthreads();
     if (tid == 0) *flag = atomicAdd(&a.counters[kh], 1u) == (unsigned)(a.splits - 1);
     __syncthreads();
     const bool last = *flag;
-    __syncthreads();   // the combine reuses this LDS
+    __syncthreads();   // the merge reuses this LDS
     if (!last) return;
     __threadfence();
+    int t0, t1, split_len;
+    split_range<D>(g, a.splits, 0, &t0, &t1, &split_len);
     const int active = (g.total + split_len - 1) / split_len;
-    combine<D>(a, kh, G, active, lds);
+    combine<D, false>(a, kh, active, lds, Io{});
     if (tid == 0) a.counters[kh] = 0u;
 }
 
@@ -350,14 +47,14 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(KernelArgs ka) {
     const int tid = threadIdx.x;
     const int kh = blockIdx.y, split = blockIdx.x;
     const int d = a.dim, G = a.heads / a.kv_heads, kvw = a.kv_heads * d;
-    const Geo g = geometry(ka);
+    const Geo g = geometry(ka, ka.mode == 1 ? *a.pos : 0);
     int split_len = (g.total + a.splits - 1) / a.splits;
     const int t0 = min(split * split_len, g.total);
     const int t1 = min(t0 + split_len, g.total);
     const int cap_len = a.split_len;   // LDS score rows sized for the plan's maximum
     float *qs = lds, *kn = qs + G * d, *vn = kn + d, *sc = vn + d;
     int *flag = (int *)(sc + G * cap_len);
-    prepare(ka, g, kh, G, d, qs, kn, vn, t0, t1);
+    prepare<false, kThreads>(ka, g, kh, G, d, qs, kn, vn, t0, t1, Io{});
     const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
     const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
     const int newest = ka.mode == 1 ? g.length - 1 : -1;
@@ -423,10 +120,13 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(KernelArgs ka) {
 bool tiled_dim(int d) { return d == 32 || d == 64 || d == 128; }
 
 size_t lds_tiled(int G, int d, int splits) {
-    const int T = kTileFloats / d;
-    size_t main = (size_t)(2 * T * d + G * d + 2 * d + G * T + 3 * kMaxG + 4);
-    size_t comb = (size_t)(2 * splits * G + G + (kThreads / (d / 4)) * G * d);
-    return std::max(main, comb) * sizeof(float);
+    int main = 0, comb = 0;
+    switch (d) {
+        case 32: main = unit_lds_floats<32>(G); comb = combine_lds_floats<32>(G, splits); break;
+        case 64: main = unit_lds_floats<64>(G); comb = combine_lds_floats<64>(G, splits); break;
+        default: main = unit_lds_floats<128>(G); comb = combine_lds_floats<128>(G, splits); break;
+    }
+    return (size_t)std::max(main, comb) * sizeof(float);
 }
 
 size_t lds_generic(int G, int d, int split_len) { return (size_t)(G * d + 2 * d + G * split_len + 4) * sizeof(float); }

@@ -1,0 +1,410 @@
+// Device code of the split-key attention unit, shared by the standalone
+// attention kernel (attention.hip) and the persistent step kernel (step.hip).
+//
+// A unit (split, kh) owns the G = heads/kv_heads query heads that share KV head
+// kh (kernels.cl:66 mapping) and a contiguous range of the logical keys
+// [ring window, extra rows] (kernels.cl:67-68).  It scores them (dot /
+// sqrt(dim), kernels.cl:72), keeps a running max m and l = sum exp(s - m),
+// accumulates o = sum exp(s - m) v, and writes (m, l, o).  Merging the units of
+// a head, out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, gives the
+// softmax-weighted value sum of kernels.cl:75-107 up to rounding.
+//
+// Keys and values stream through LDS in 16 KB tiles (4096 floats = 4096/dim
+// keys), each thread loading 4 float4 of K and 4 of V per tile, coalesced along
+// the row; the next tile is prefetched into registers while the current one is
+// consumed.  LL = true is the persistent kernel's mode: q/k/v arrive as
+// flag-in-data cells (ll.h) of this step, the partials are exchanged between
+// workgroups with agent-coherent accesses, and the merged output is written as
+// cells.
+#pragma once
+
+#include "attention.h"
+#include "ll.h"
+
+namespace mr {
+namespace att {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTileFloats = 4096;
+constexpr int kMaxG = 16;
+
+struct Args {
+    AttnStepArgs s;       // engine fields (mode 1)
+    int mode;             // 0 = op-level, 1 = engine step
+    int start, length, extra_length;   // mode 0 geometry
+    const float *ring_k_ro, *ring_v_ro;
+};
+
+struct Geo {
+    int pos, start, length, extra, total;
+};
+
+// LL-mode epochs: inputs (q/k/v cells) and output (merged cells); in that mode
+// AttnStepArgs' q, k_new, v_new and out point at uint64_t cells.
+struct Io {
+    unsigned ep_in, ep_out;
+    int *err;
+};
+
+template <bool COH>
+__device__ __forceinline__ float ld(const float *p) {
+    if constexpr (COH)
+        return __hip_atomic_load(gmem(const_cast<float *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *gmem(p);
+}
+
+template <bool COH>
+__device__ __forceinline__ void st(float *p, float v) {
+    if constexpr (COH) __hip_atomic_store(gmem(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *gmem(p) = v;
+}
+
+// Window geometry at position `pos` (engine) or from the arguments (op level).
+__device__ __forceinline__ Geo geometry(const Args &ka, int pos) {
+    const AttnStepArgs &a = ka.s;
+    Geo g;
+    if (ka.mode == 1) {
+        g.pos = pos;
+        int count = pos + 1;
+        g.length = min(count, a.capacity);
+        g.start = (count - g.length) % a.capacity;
+        g.extra = a.extra_chunk ? (pos / a.extra_chunk) * a.extra_slots : 0;
+    } else {
+        g.pos = 0;
+        g.start = ka.start;
+        g.length = ka.length;
+        g.extra = ka.extra_length;
+    }
+    g.total = g.length + g.extra;
+    return g;
+}
+
+// Engine mode: normalize (optional) and rotate the G queries and the new key in
+// LDS, then store the new key/value in the ring slot of this position (done by
+// the unit that holds the newest key).
+// Returns false (block-uniform) when an LL wait gave up.
+template <bool LL, int NT>
+__device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, int G, int d, float *qs, float *kn,
+                                        float *vn, int t0, int t1, const Io &io) {
+    const AttnStepArgs &a = ka.s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if constexpr (LL) {
+        ll::Wait w = ll::waiter(io.err);
+        const uint64_t *q_src = (const uint64_t *)a.q + (int64_t)kh * G * d;
+        for (int i = 2 * tid; i < G * d; i += 2 * NT) {
+            float2 v = ll::get2(q_src + i, io.ep_in, w);
+            qs[i] = v.x;
+            qs[i + 1] = v.y;
+        }
+        const uint64_t *k_src = (const uint64_t *)a.k_new + kh * d, *v_src = (const uint64_t *)a.v_new + kh * d;
+        for (int j = 2 * tid; j < 2 * d; j += 2 * NT) {
+            const bool isk = j < d;
+            const int c = isk ? j : j - d;
+            float2 v = ll::get2((isk ? k_src : v_src) + c, io.ep_in, w);
+            float *dst = isk ? kn : vn;
+            dst[c] = v.x;
+            dst[c + 1] = v.y;
+        }
+        if (!ll::all_ok(w)) return false;
+    } else {
+        const float *q_src = a.q + (int64_t)kh * G * d;
+        for (int i = tid; i < G * d; i += NT) qs[i] = *gmem(q_src + i);
+        if (ka.mode != 1) {
+            __syncthreads();
+            return true;
+        }
+        for (int j = tid; j < d; j += NT) {
+            kn[j] = *gmem(a.k_new + kh * d + j);
+            vn[j] = *gmem(a.v_new + kh * d + j);
+        }
+        __syncthreads();
+    }
+    if (a.q_gain) {   // per-head RMSNorm, width = dim (kernels.cl:19-28)
+        for (int r = wave; r < G + 1; r += (NT / kWave)) {
+            float *row = r < G ? qs + r * d : kn;
+            const float *gain = r < G ? a.q_gain : a.k_gain;
+            float ss = 0.0f;
+            for (int j = lane; j < d; j += kWave) ss = fmaf(row[j], row[j], ss);
+            ss = wave_sum(ss);
+            float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
+            for (int j = lane; j < d; j += kWave) row[j] = row[j] * scale * gmem(gain)[j];
+        }
+        __syncthreads();
+    }
+    const int half = d / 2;   // RoPE at this position (kernels.cl:30-44)
+    const float *cs = a.rope + (int64_t)g.pos * half * 2;
+    for (int i = tid; i < (G + 1) * half; i += NT) {
+        int r = i / half, p = i % half;
+        float *row = r < G ? qs + r * d : kn;
+        int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
+        float u = row[j], v = row[k];
+        rope_rotate(u, v, gmem(cs)[2 * p], gmem(cs)[2 * p + 1]);
+        row[j] = u;
+        row[k] = v;
+    }
+    __syncthreads();
+    const int newest = g.length - 1;
+    if (t0 <= newest && newest < t1) {
+        const int kvw = a.kv_heads * d;
+        int64_t slot = (int64_t)(g.pos % a.capacity) * kvw + (int64_t)kh * d;
+        for (int j = tid; j < d; j += NT) {
+            gmem(a.ring_k)[slot + j] = kn[j];
+            gmem(a.ring_v)[slot + j] = vn[j];
+        }
+    }
+    return true;
+}
+
+// Key range of `split` for the current total (the split length follows the
+// window so every split of the fixed grid has work).
+template <int D>
+__device__ __forceinline__ void split_range(const Geo &g, int splits, int split, int *t0, int *t1, int *len) {
+    constexpr int T = kTileFloats / D;
+    int split_len = (g.total + splits - 1) / splits;
+    split_len = (split_len + T - 1) / T * T;
+    *len = split_len;
+    *t0 = min(split * split_len, g.total);
+    *t1 = min(*t0 + split_len, g.total);
+}
+
+template <int D>
+__host__ __device__ constexpr int unit_lds_floats(int G) {
+    return 2 * (kTileFloats / D) * D + G * D + 2 * D + G * (kTileFloats / D) + 3 * kMaxG + 4;
+}
+
+// One (split, kh) unit: writes its partial (m, l, o) for the G heads.  Returns
+// false (block-uniform) when an LL wait gave up.
+template <int D, bool LL, int NT = kThreads>
+__device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, int split, float *lds, const Io &io) {
+    const AttnStepArgs &a = ka.s;
+    constexpr int T = kTileFloats / D;          // keys per tile
+    constexpr int C4 = D / 4;                   // float4 per row
+    constexpr int LPK = C4 < 16 ? C4 : 16;      // lanes per key in the score pass
+    constexpr int VPL = C4 / LPK;               // float4 per lane per key
+    constexpr int NWV = NT / kWave;
+    constexpr int FPT = kTileFloats / 4 / NT;   // float4 of K (and of V) per thread per tile
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.heads / a.kv_heads, kvw = a.kv_heads * D;
+    int t0, t1, split_len;
+    split_range<D>(g, a.splits, split, &t0, &t1, &split_len);
+
+    float *Ks = lds;                           // [T][D]
+    float *Vs = Ks + T * D;                    // [T][D]
+    float *qs = Vs + T * D;                    // [G][D]
+    float *kn = qs + G * D;                    // [D]
+    float *vn = kn + D;                        // [D]
+    float *sc = vn + D;                        // [G][T]
+    float *stt = sc + G * T;                   // [G] running max, [G] running sum, [G] rescale
+
+    const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
+    const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
+    const int newest = ka.mode == 1 ? g.length - 1 : -1;
+
+    // Output ownership in the PV pass: thread -> column j, heads pg, pg+GS, ...
+    constexpr int GS = NT / D > 0 ? NT / D : 1;
+    const int pj = tid % D, pg = tid / D;
+    constexpr int NACC = kMaxG / GS > 0 ? kMaxG / GS : 1;
+    float acc[NACC];
+    const int nacc = (G + GS - 1) / GS;
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) acc[i] = 0.0f;
+
+    // Tile loader: float4 index f = tid + 256*i -> (row f / C4, column f % C4).
+    float4 pk[FPT], pv[FPT];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) {
+            int f = tid + NT * i, r = f / C4, c = f % C4;
+            int t = c0 + r;
+            if (t < t1 && t != newest) {
+                const float *kr, *vr;
+                if (t < g.length) {
+                    int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D;
+                    kr = rk + off;
+                    vr = rv + off;
+                } else {
+                    int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D;
+                    kr = a.extra_k + off;
+                    vr = a.extra_v + off;
+                }
+                pk[i] = load_f4(kr + 4 * c);
+                pv[i] = load_f4(vr + 4 * c);
+            }
+        }
+    };
+    auto stash = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) {
+            int f = tid + NT * i, r = f / C4, c = f % C4;
+            int t = c0 + r;
+            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
+            if (t == newest) {
+                kk = *(const float4 *)(kn + 4 * c);
+                vv = *(const float4 *)(vn + 4 * c);
+            } else if (t < t1) {
+                kk = pk[i];
+                vv = pv[i];
+            }
+            *(float4 *)(Ks + r * D + 4 * c) = kk;
+            *(float4 *)(Vs + r * D + 4 * c) = vv;
+        }
+    };
+
+    const float inv_norm = sqrtf((float)D);
+    // The first tile holds keys of earlier steps only (the newest key comes
+    // from the prepared row), so it is in flight while the inputs are awaited.
+    if (t0 < t1) fetch(t0);
+    if (!prepare<LL, NT>(ka, g, kh, G, D, qs, kn, vn, t0, t1, io)) return false;
+    if (tid < G) {
+        stt[tid] = -INFINITY;
+        stt[kMaxG + tid] = 0.0f;
+    }
+    for (int c0 = t0; c0 < t1; c0 += T) {
+        const int n = min(T, t1 - c0);
+        stash(c0);
+        __syncthreads();
+        if (c0 + T < t1) fetch(c0 + T);   // in flight while this tile is consumed
+        {   // scores: LPK lanes per key
+            const int sub = lane % LPK, ks = lane / LPK;
+            constexpr int KPW = kWave / LPK;
+            for (int r0 = wave * KPW; r0 < n; r0 += NWV * KPW) {
+                int r = r0 + ks;
+                const float *kr = Ks + min(r, T - 1) * D;
+                float4 kv[VPL];
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) kv[v] = *(const float4 *)(kr + 4 * (sub + LPK * v));
+                for (int gh = 0; gh < G; ++gh) {
+                    float part = 0.0f;
+#pragma unroll
+                    for (int v = 0; v < VPL; ++v) {
+                        float4 q4 = *(const float4 *)(qs + gh * D + 4 * (sub + LPK * v));
+                        part = fmaf(q4.x, kv[v].x, part);
+                        part = fmaf(q4.y, kv[v].y, part);
+                        part = fmaf(q4.z, kv[v].z, part);
+                        part = fmaf(q4.w, kv[v].w, part);
+                    }
+                    part = group_sum(part, LPK);
+                    if (sub == 0 && r < n) sc[gh * T + r] = part / inv_norm;
+                }
+            }
+        }
+        __syncthreads();
+        // Online softmax statistics per head (one wave per head).
+        for (int gh = wave; gh < G; gh += NWV) {
+            float mx = -INFINITY;
+            for (int r = lane; r < n; r += kWave) mx = fmaxf(mx, sc[gh * T + r]);
+            mx = wave_max(mx);
+            const float m_old = stt[gh];
+            const float m_new = fmaxf(m_old, mx);
+            const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+            float sum = 0.0f;
+            for (int r = lane; r < n; r += kWave) {
+                float p = expf(sc[gh * T + r] - m_new);
+                sc[gh * T + r] = p;
+                sum += p;
+            }
+            sum = wave_sum(sum);
+            if (lane == 0) {
+                stt[gh] = m_new;
+                stt[kMaxG + gh] = stt[kMaxG + gh] * alpha + sum;
+                stt[2 * kMaxG + gh] = alpha;
+            }
+        }
+        __syncthreads();
+        // Weighted values.
+#pragma unroll
+        for (int i = 0; i < NACC; ++i) {
+            int gh = pg + GS * i;
+            if (i < nacc && gh < G) {
+                float v = acc[i] * stt[2 * kMaxG + gh];
+                const float *p = sc + gh * T;
+                for (int r = 0; r < n; ++r) v = fmaf(p[r], Vs[r * D + pj], v);
+                acc[i] = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    // Partial (m, l, o) of this split.
+    float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
+    if (t0 < t1) {
+#pragma unroll
+        for (int i = 0; i < NACC; ++i) {
+            int gh = pg + GS * i;
+            if (i < nacc && gh < G) st<LL>(part + gh * (D + 2) + 2 + pj, acc[i]);
+        }
+        if (tid < G) {
+            st<LL>(part + tid * (D + 2), stt[tid]);
+            st<LL>(part + tid * (D + 2) + 1, stt[kMaxG + tid]);
+        }
+    }
+    return true;
+}
+
+// Merge the `active` splits of KV head kh into out[(kh*G + g)*D + j].
+// LL = true: partials come from other workgroups of the same launch and the
+// output is written as cells of epoch io.ep_out.
+template <int D, bool LL, int NT = kThreads>
+__device__ __forceinline__ void combine(const AttnStepArgs &a, int kh, int active, float *lds, const Io &io) {
+    const int tid = threadIdx.x;
+    const int G = a.heads / a.kv_heads;
+    const float *base = a.part + (int64_t)kh * a.splits * G * (D + 2);
+    float *w = lds;                      // [active][G] split maxima, then weights e^(m_s - M)
+    float *lv = w + active * G;          // [active][G] split sums
+    float *L = lv + active * G;          // [G]
+    float *red = L + G;                  // [SG][G*D] partial sums
+    for (int i = tid; i < active * G; i += NT) {
+        w[i] = ld<LL>(base + (int64_t)i * (D + 2));
+        lv[i] = ld<LL>(base + (int64_t)i * (D + 2) + 1);
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < active; ++s) M = fmaxf(M, w[s * G + tid]);
+        float sum = 0.0f;
+        for (int s = 0; s < active; ++s) {
+            float l = lv[s * G + tid];
+            float e = l == 0.0f ? 0.0f : expf(w[s * G + tid] - M);
+            w[s * G + tid] = e;
+            sum = fmaf(e, l, sum);
+        }
+        L[tid] = sum;
+    }
+    __syncthreads();
+    // Thread (sg, j4): float4 column j4 of every head over splits sg, sg+SG, ...
+    constexpr int C4 = D / 4;
+    constexpr int SG = NT / C4;
+    const int j4 = tid % C4, sg = tid / C4;
+    for (int gh = 0; gh < G; ++gh) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int s = sg; s < active; s += SG) {
+            const float *src = base + (int64_t)(s * G + gh) * (D + 2) + 2 + 4 * j4;
+            const float4 o = LL ? load_f4_coherent(src) : load_f4(src);
+            const float e = w[s * G + gh];
+            acc.x = fmaf(e, o.x, acc.x);
+            acc.y = fmaf(e, o.y, acc.y);
+            acc.z = fmaf(e, o.z, acc.z);
+            acc.w = fmaf(e, o.w, acc.w);
+        }
+        *(float4 *)(red + (sg * G + gh) * D + 4 * j4) = acc;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * D; i += NT) {
+        int gh = i / D, j = i % D;
+        float sum = 0.0f;
+        for (int q = 0; q < SG; ++q) sum += red[(q * G + gh) * D + j];
+        const int64_t o = (int64_t)(kh * G + gh) * D + j;
+        if constexpr (LL) ll::put((uint64_t *)a.out + o, sum / L[gh], io.ep_out);
+        else *gmem(a.out + o) = sum / L[gh];
+    }
+}
+
+template <int D, int NT = kThreads>
+__host__ __device__ constexpr int combine_lds_floats(int G, int splits) {
+    return 2 * splits * G + G + (NT / (D / 4)) * G * D;
+}
+
+}  // namespace att
+}  // namespace mr

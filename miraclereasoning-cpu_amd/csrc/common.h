@@ -59,6 +59,36 @@ void ctx_release(mr_ctx *ctx, void *ptr);
 // ---------------------------------------------------------------- device helpers
 constexpr int kWave = 64;
 
+// Global-memory view of a pointer.  Pointers that a kernel reads out of memory
+// (rather than receives as arguments) have no known address space, and the
+// compiler then emits FLAT accesses, which wait on the LDS counter too and so
+// serialize prefetched loads; these casts keep them GLOBAL.
+#define MR_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const MR_GLOBAL T *gmem(const T *p) {
+    return (const MR_GLOBAL T *)p;
+}
+template <typename T>
+__device__ __forceinline__ MR_GLOBAL T *gmem(T *p) {
+    return (MR_GLOBAL T *)p;
+}
+
+// 16-byte load of four floats from global memory.
+__device__ __forceinline__ float4 load_f4(const float *p) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 v = *gmem((const f32x4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// 16-byte load that is coherent across the device's L2 caches (cache policy
+// SC1 = agent scope): for data another workgroup wrote during this kernel.
+__device__ __forceinline__ float4 load_f4_coherent(const float *p) {
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000);
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 0, 0, 16);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
@@ -116,6 +146,14 @@ __device__ __forceinline__ void rope_pair(float &u, float &v, float pos, float f
     float a = pos * freq;
     double ad = (double)a;
     float c = (float)cos(ad), s = (float)sin(ad);
+    float nu = u * c - v * s;
+    float nv = u * s + v * c;
+    u = nu;
+    v = nv;
+}
+
+// Rotation of one pair by a tabulated (cos, sin) (kernels.cl:43).
+__device__ __forceinline__ void rope_rotate(float &u, float &v, float c, float s) {
     float nu = u * c - v * s;
     float nv = u * s + v * c;
     u = nu;

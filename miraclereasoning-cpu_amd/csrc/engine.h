@@ -6,6 +6,7 @@
 
 #include "attention.h"
 #include "linear.h"
+#include "step.h"
 
 namespace mr {
 
@@ -43,8 +44,6 @@ struct Layer {
     int splits = 0, split_len = 0;                     // attention plan
 };
 
-enum StepKind { STEP_PLAIN = 0, STEP_LOGITS = 1, STEP_GREEDY = 2, STEP_KINDS = 3 };
-
 }  // namespace mr
 
 struct mr_model {
@@ -52,7 +51,8 @@ struct mr_model {
     mr_model_desc d{};
     std::vector<mr::Layer> layers;
     mr::Weight embed, output, norm;
-    float *freq = nullptr;
+    float *freq = nullptr;       // [head_dim/2] inverse frequencies
+    float *rope = nullptr;       // [context][head_dim/2][2] cos, sin per integer position
     bool finalized = false;
     int position = 0;            // host mirror of *pos_dev
     // device state (one allocation, see engine.hip)
@@ -68,8 +68,27 @@ struct mr_model {
     float *part = nullptr;
     unsigned *counters = nullptr;
     float *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;
-    // graphs of one decode step, by StepKind
-    bool use_graph = true;
+    // step execution: persistent kernel (when the model fits its phases) or
+    // per-layer kernels replayed from a hipGraph / launched eagerly
+    int mode = MR_STEP_PERSISTENT;
+    bool persistent_ok = false;
+    int grid = 0;                        // persistent workgroups (one per CU)
+    size_t step_lds = 0;
+    mr::Phase *prog_plain = nullptr, *prog_head = nullptr;
+    int n_plain = 0, n_head = 0;
+    // Persistent-kernel state, cleared on reset: flag-in-data activation cells
+    // (hidden, qkv, attn, act) and the counters (per layer and KV head merge
+    // counters, then the launch exit counter), each one allocation.
+    uint64_t *cells = nullptr;
+    size_t cell_count = 0;
+    uint64_t *c_hidden = nullptr, *c_qkv = nullptr, *c_attn = nullptr, *c_act = nullptr;
+    unsigned *sync = nullptr;
+    size_t sync_count = 0;
+    void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end
+    int *err = nullptr;                  // wait timeout flag
+    float *best_val = nullptr;
+    int *best_idx = nullptr, *bad = nullptr;
+    float last_ms = 0.0f;                // device time of the last greedy loop
     std::array<hipGraphExec_t, mr::STEP_KINDS> exec{};
     std::array<int, mr::STEP_KINDS> eager_runs{};
 };

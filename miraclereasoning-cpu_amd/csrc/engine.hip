@@ -167,7 +167,7 @@ __global__ void __launch_bounds__(256) k_cbr_project(const float *pooled, const 
 
 // K-norm + RoPE at the pooled anchors, then relay append (model.py:136-144).
 __global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float *anchors, const float *k_gain,
-                                                    float eps, const float *freq, int split_half, float *relay_k,
+                                                    float eps, const float *rope, int split_half, float *relay_k,
                                                     float *relay_v, const int *skip_flag, const int *pos_p,
                                                     int chunk, int slots, int kv_heads, int d) {
     extern __shared__ float kr[];
@@ -192,7 +192,9 @@ __global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float
         float *row = kr + hh * d;
         int j = split_half ? p : 2 * p, k = split_half ? p + half : 2 * p + 1;
         float u = row[j], v = row[k];
-        rope_pair(u, v, anchors[m], freq[p]);
+        // anchors are rounded positions inside the chunk, so they index the table
+        const float *cs = rope + (int64_t)anchors[m] * half * 2;
+        rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
         row[j] = u;
         row[k] = v;
     }
@@ -346,7 +348,7 @@ int launch_gqa_part(mr_model *m, Layer &L, int part) {
             AttnStepArgs a;
             a.q = m->qkv; a.k_new = m->qkv + qd; a.v_new = m->qkv + qd + kvw;
             if (d.qk_norm) { a.q_gain = L.q_norm.f(); a.k_gain = L.k_norm.f(); }
-            a.eps = d.norm_eps; a.freq = m->freq; a.split_half = d.split_half_rope;
+            a.eps = d.norm_eps; a.rope = m->rope; a.split_half = d.split_half_rope;
             a.pos = m->pos_dev; a.done = m->done_dev;
             a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.capacity = L.capacity;
             if (d.family == MR_FAMILY_FLASHNANO_16) {
@@ -370,7 +372,7 @@ int launch_gqa_part(mr_model *m, Layer &L, int part) {
                                                                              m->cbr_skip, 2 * kvw, h);
             MR_LAUNCHED("enqueue cbr project");
             k_cbr_finish<<<slots, 256, (size_t)kvw * sizeof(float), s>>>(
-                m->cbr_kv, m->cbr_anchor, L.k_norm.f(), d.norm_eps, m->freq, d.split_half_rope, L.relay_k,
+                m->cbr_kv, m->cbr_anchor, L.k_norm.f(), d.norm_eps, m->rope, d.split_half_rope, L.relay_k,
                 L.relay_v, m->cbr_skip, m->pos_dev, chunk, slots, L.kv_heads, hd);
             MR_LAUNCHED("enqueue cbr finish");
             return MR_OK;
@@ -446,9 +448,24 @@ int record_step(mr_model *m, int kind) {
 
 namespace {
 
+int run_persistent(mr_model *m, int kind, unsigned long long *trace = nullptr) {
+    StepArgs a;
+    a.trace = trace;
+    a.phases = kind == STEP_PLAIN ? m->prog_plain : m->prog_head;
+    a.nphases = kind == STEP_PLAIN ? m->n_plain : m->n_head;
+    a.stride = m->n_head;
+    a.kind = kind;
+    a.pos = m->pos_dev; a.done = m->done_dev; a.ids = m->ids_dev; a.gen = m->gen_dev; a.count = m->count_dev;
+    a.eos = m->eos_dev; a.err = m->err; a.exits = m->sync + m->sync_count - 1;
+    a.best_val = m->best_val; a.best_idx = m->best_idx; a.bad = m->bad;
+    a.embed = m->embed.ptr; a.embed_dtype = m->embed.dtype; a.dummy = m->dummy;
+    return launch_step(m->ctx->stream, a, m->grid, m->step_lds);
+}
+
 int run_step(mr_model *m, int kind) {
     hipStream_t s = m->ctx->stream;
-    if (!m->use_graph) return record_step(m, kind);
+    if (m->mode == MR_STEP_PERSISTENT && m->persistent_ok) return run_persistent(m, kind);
+    if (m->mode == MR_STEP_EAGER) return record_step(m, kind);
     if (!m->exec[kind]) {
         // The first run of each step kind is eager (it also checks every launch
         // configuration); the second captures the same sequence.
@@ -481,6 +498,163 @@ int check_ctx(mr_model *m, const char *what) {
     }
     if (!m->finalized) return fail(MR_ERR_STATE, std::string(what) + ": model not finalized");
     MR_HIP(hipSetDevice(m->ctx->device), "select device");
+    return MR_OK;
+}
+
+// A persistent step whose wait timed out leaves err set; report it.
+int check_step_error(mr_model *m) {
+    if (!m->persistent_ok) return MR_OK;
+    int err = 0;
+    MR_HIP(hipMemcpy(&err, m->err, sizeof(int), hipMemcpyDeviceToHost), "read step status");
+    if (err) return fail(MR_ERR_HIP, "persistent step kernel: a wait for another workgroup timed out");
+    return MR_OK;
+}
+
+// Phase program of one step for the persistent kernel (GQA families).  Each
+// read names the phase whose cells it expects: x_phase for the input,
+// res_phase for a residual's previous value.
+std::vector<Phase> build_program(mr_model *m, bool head) {
+    const mr_model_desc &d = m->d;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd;
+    std::vector<Phase> prog;
+    auto last = [&]() { return (int)prog.size() - 1; };
+    Phase e;
+    e.kind = PH_EMBED;
+    e.n = h;
+    e.y = m->c_hidden;
+    prog.push_back(e);
+    int hidden_at = last();
+    for (int li = 0; li < d.layers; ++li) {
+        Layer &L = m->layers[li];
+        const int kvw = L.kv_heads * hd;
+        Phase g;
+        g.kind = PH_GEMV; g.dtype = L.qkv.dtype; g.n = qd + 2 * kvw; g.k = h; g.pro = PRO_RMS; g.epi = EPI_STORE;
+        g.w = L.qkv.ptr; g.x = m->c_hidden; g.x_phase = hidden_at; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
+        g.y = m->c_qkv;
+        prog.push_back(g);
+        const int qkv_at = last();
+        Phase a;
+        a.kind = PH_ATTN;
+        a.x_phase = qkv_at;
+        a.merge = m->sync + (size_t)li * d.query_heads;   // kv_heads <= query_heads
+        AttnStepArgs &t = a.at.s;
+        t.q = (const float *)m->c_qkv;
+        t.k_new = (const float *)(m->c_qkv + qd);
+        t.v_new = (const float *)(m->c_qkv + qd + kvw);
+        if (d.qk_norm) { t.q_gain = L.q_norm.f(); t.k_gain = L.k_norm.f(); }
+        t.eps = d.norm_eps; t.rope = m->rope; t.split_half = d.split_half_rope;
+        t.ring_k = L.ring_k; t.ring_v = L.ring_v; t.capacity = L.capacity;
+        t.heads = d.query_heads; t.kv_heads = L.kv_heads; t.dim = hd;
+        t.part = m->part; t.out = (float *)m->c_attn; t.splits = L.splits; t.split_len = L.split_len;
+        a.at.mode = 1;
+        a.at.ring_k_ro = L.ring_k; a.at.ring_v_ro = L.ring_v;
+        prog.push_back(a);
+        const int attn_at = last();
+        Phase o;
+        o.kind = PH_GEMV; o.dtype = L.o.dtype; o.n = h; o.k = qd; o.pro = PRO_COPY; o.epi = EPI_RESIDUAL;
+        o.w = L.o.ptr; o.x = m->c_attn; o.x_phase = attn_at; o.y = m->c_hidden; o.res_phase = hidden_at;
+        o.scale = d.residual_scale;
+        prog.push_back(o);
+        hidden_at = last();
+        Phase gu;
+        gu.kind = PH_GEMV; gu.dtype = L.ffn.gate.dtype; gu.n = d.ffn_dim; gu.k = h; gu.pro = PRO_RMS;
+        gu.epi = EPI_SWIGLU; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->c_hidden; gu.x_phase = hidden_at;
+        gu.gain = L.f_norm.f(); gu.eps = d.norm_eps; gu.y = m->c_act;
+        prog.push_back(gu);
+        const int act_at = last();
+        Phase dn;
+        dn.kind = PH_GEMV; dn.dtype = L.ffn.down.dtype; dn.n = h; dn.k = d.ffn_dim; dn.pro = PRO_COPY;
+        dn.epi = EPI_RESIDUAL; dn.w = L.ffn.down.ptr; dn.x = m->c_act; dn.x_phase = act_at; dn.y = m->c_hidden;
+        dn.res_phase = hidden_at; dn.scale = d.residual_scale;
+        prog.push_back(dn);
+        hidden_at = last();
+    }
+    if (head) {
+        const Weight &w = d.tie_embeddings ? m->embed : m->output;
+        Phase hp;
+        hp.kind = PH_HEAD; hp.dtype = w.dtype; hp.n = d.vocab_size; hp.k = h; hp.pro = PRO_RMS; hp.epi = EPI_STORE;
+        hp.w = w.ptr; hp.x = m->c_hidden; hp.x_phase = hidden_at; hp.gain = m->norm.f(); hp.eps = d.norm_eps;
+        hp.logits = m->logits;
+        prog.push_back(hp);
+    }
+    return prog;
+}
+
+// The persistent kernel covers GQA families whose head dim has a tiled
+// attention unit and whose matrices all take 16-byte row vectors.
+bool persistent_fits(mr_model *m) {
+    const mr_model_desc &d = m->d;
+    if (d.family == MR_FAMILY_FLASHNANO_16 || !is_gqa(d.family)) return false;
+    if (d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128) return false;
+    if (d.query_heads / d.kv_heads > 16) return false;
+    auto vec_ok = [](const Weight &w, int k) {
+        int e = w.dtype == MR_F32 ? 4 : 8;
+        return k % e == 0 && ((uintptr_t)w.ptr % 16) == 0;
+    };
+    const int h = d.hidden_size;
+    if (!vec_ok(d.tie_embeddings ? m->embed : m->output, h)) return false;
+    for (Layer &L : m->layers) {
+        if (d.query_heads / L.kv_heads > 16) return false;
+        if (!vec_ok(L.qkv, h) || !vec_ok(L.o, d.query_heads * d.head_dim) || !vec_ok(L.ffn.gate, h) ||
+            !vec_ok(L.ffn.up, h) || !vec_ok(L.ffn.down, d.ffn_dim))
+            return false;
+        if (L.ffn.gate.dtype != L.ffn.up.dtype) return false;
+    }
+    return true;
+}
+
+int setup_persistent(mr_model *m) {
+    m->persistent_ok = false;
+    if (!persistent_fits(m)) return MR_OK;
+    const mr_model_desc &d = m->d;
+    hipDeviceProp_t p;
+    MR_HIP(hipGetDeviceProperties(&p, m->ctx->device), "query device");
+    int coop = 0;
+    MR_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->ctx->device), "query device");
+    if (!coop) return MR_OK;
+    m->grid = p.multiProcessorCount;
+    if (m->grid < 8) return MR_OK;
+    // Epochs are position * stride + phase + 1 in 32 bits.
+    const int64_t stride = 2 + 5 * (int64_t)d.layers;
+    if ((int64_t)(d.context_length + 1) * stride >= (int64_t)UINT32_MAX) return MR_OK;
+    // Cells: hidden, qkv, attn, act, each region a multiple of two cells so
+    // every region starts 16-byte aligned.
+    int max_kvw = 0;
+    for (Layer &L : m->layers) max_kvw = std::max(max_kvw, L.kv_heads * d.head_dim);
+    auto even = [](size_t n) { return (n + 1) & ~(size_t)1; };
+    const size_t qd = (size_t)d.query_heads * d.head_dim;
+    const size_t n_hidden = even(d.hidden_size), n_qkv = even(qd + 2 * (size_t)max_kvw), n_attn = even(qd);
+    m->cell_count = n_hidden + n_qkv + n_attn + even(d.ffn_dim);
+    MR_TRY(device_alloc(m, m->cell_count * sizeof(uint64_t), (void **)&m->cells));
+    m->c_hidden = m->cells;
+    m->c_qkv = m->c_hidden + n_hidden;
+    m->c_attn = m->c_qkv + n_qkv;
+    m->c_act = m->c_attn + n_attn;
+    m->sync_count = (size_t)d.layers * d.query_heads + 1;
+    MR_TRY(device_alloc(m, m->sync_count * sizeof(unsigned), (void **)&m->sync));
+    MR_TRY(device_alloc(m, 256, &m->dummy));
+    MR_TRY(device_alloc(m, sizeof(int), (void **)&m->err));
+    MR_TRY(device_alloc(m, m->grid * sizeof(float), (void **)&m->best_val));
+    MR_TRY(device_alloc(m, m->grid * sizeof(int), (void **)&m->best_idx));
+    MR_TRY(device_alloc(m, m->grid * sizeof(int), (void **)&m->bad));
+    MR_HIP(hipMemset(m->cells, 0, m->cell_count * sizeof(uint64_t)), "clear step cells");
+    MR_HIP(hipMemset(m->sync, 0, m->sync_count * sizeof(unsigned)), "clear step counters");
+    MR_HIP(hipMemset(m->dummy, 0, 256), "clear step dummy");
+    MR_HIP(hipMemset(m->err, 0, sizeof(int)), "clear step status");
+
+    std::vector<Phase> plain = build_program(m, false), head = build_program(m, true);
+    if ((int64_t)head.size() != stride) return fail(MR_ERR_INVALID, "step program: unexpected phase count");
+    m->step_lds = std::max(step_lds_bytes(plain, m->grid), step_lds_bytes(head, m->grid));
+    if (m->step_lds > 64 * 1024) return MR_OK;
+    m->n_plain = (int)plain.size();
+    m->n_head = (int)head.size();
+    MR_TRY(device_alloc(m, plain.size() * sizeof(Phase), (void **)&m->prog_plain));
+    MR_TRY(device_alloc(m, head.size() * sizeof(Phase), (void **)&m->prog_head));
+    MR_HIP(hipMemcpy(m->prog_plain, plain.data(), plain.size() * sizeof(Phase), hipMemcpyHostToDevice),
+           "upload step program");
+    MR_HIP(hipMemcpy(m->prog_head, head.data(), head.size() * sizeof(Phase), hipMemcpyHostToDevice),
+           "upload step program");
+    m->persistent_ok = true;
     return MR_OK;
 }
 
@@ -549,7 +723,11 @@ int mr_model_destroy(mr_model *m) {
             if (p) hipFree(p);
     }
     if (m->freq) hipFree(m->freq);
+    if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
+    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, m->dummy,
+                    (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
+        if (p) hipFree(p);
     delete m;
     return MR_OK;
 }
@@ -601,6 +779,19 @@ int mr_model_set_rope(mr_model *m, const float *inv_freq, int count) {
     MR_HIP(hipSetDevice(m->ctx->device), "select device");
     if (!m->freq) MR_TRY(device_alloc(m, count * sizeof(float), (void **)&m->freq));
     MR_HIP(hipMemcpy(m->freq, inv_freq, count * sizeof(float), hipMemcpyHostToDevice), "upload rope table");
+    // cos/sin of every integer position: the angle is the FP32 product pos*freq
+    // (kernels.cl:38), its cosine and sine are taken in double and rounded once.
+    const int ctxn = m->d.context_length;
+    std::vector<float> table((size_t)ctxn * count * 2);
+    for (int pos = 0; pos < ctxn; ++pos)
+        for (int p = 0; p < count; ++p) {
+            float a = (float)pos * inv_freq[p];
+            table[((size_t)pos * count + p) * 2] = (float)std::cos((double)a);
+            table[((size_t)pos * count + p) * 2 + 1] = (float)std::sin((double)a);
+        }
+    if (!m->rope) MR_TRY(device_alloc(m, table.size() * sizeof(float), (void **)&m->rope));
+    MR_HIP(hipMemcpy(m->rope, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
+           "upload rope table");
     return MR_OK;
 }
 
@@ -709,6 +900,7 @@ int mr_model_finalize(mr_model *m) {
     m->cbr_anchor = (float *)(base + o_anchor);
     m->cbr_kv = (float *)(base + o_cbrkv);
     MR_HIP(hipDeviceSynchronize(), "finalize model");
+    MR_TRY(setup_persistent(m));
     m->finalized = true;
     m->position = 0;
     return MR_OK;
@@ -721,6 +913,11 @@ int mr_model_reset(mr_model *m) {
     // Caches are overwritten before they are read (ring rows by position, the
     // relay by chunk), so a reset only rewinds the position.
     MR_HIP(hipMemsetAsync(m->pos_dev, 0, 4 * sizeof(int), m->ctx->stream), "reset position");
+    if (m->persistent_ok) {   // epochs restart with the position
+        MR_HIP(hipMemsetAsync(m->cells, 0, m->cell_count * sizeof(uint64_t), m->ctx->stream), "reset step cells");
+        MR_HIP(hipMemsetAsync(m->sync, 0, m->sync_count * sizeof(unsigned), m->ctx->stream), "reset step counters");
+        MR_HIP(hipMemsetAsync(m->err, 0, sizeof(int), m->ctx->stream), "reset step status");
+    }
     MR_HIP(hipStreamSynchronize(m->ctx->stream), "reset");
     m->position = 0;
     return MR_OK;
@@ -732,10 +929,23 @@ int mr_model_position(mr_model *m, int *position) {
     return MR_OK;
 }
 
-int mr_model_use_graph(mr_model *m, int enable) {
-    MR_REQUIRE(m, "use_graph: null model");
-    m->use_graph = enable != 0;
-    if (!m->use_graph) destroy_graphs(m);
+int mr_model_set_step_mode(mr_model *m, int mode) {
+    MR_REQUIRE(m, "set_step_mode: null model");
+    MR_REQUIRE(mode >= MR_STEP_PERSISTENT && mode <= MR_STEP_EAGER, "set_step_mode: unknown mode");
+    m->mode = mode;
+    if (mode != MR_STEP_GRAPH) destroy_graphs(m);
+    return MR_OK;
+}
+
+int mr_model_get_step_mode(mr_model *m, int *mode) {
+    MR_REQUIRE(m && mode, "get_step_mode: null argument");
+    *mode = m->mode == MR_STEP_PERSISTENT && !m->persistent_ok ? MR_STEP_GRAPH : m->mode;
+    return MR_OK;
+}
+
+int mr_model_last_decode_ms(mr_model *m, float *ms) {
+    MR_REQUIRE(m && ms, "last_decode_ms: null argument");
+    *ms = m->last_ms;
     return MR_OK;
 }
 
@@ -764,6 +974,7 @@ int mr_model_forward(mr_model *m, const int32_t *ids, int n, int flags, float *l
         }
     }
     MR_HIP(hipStreamSynchronize(s), "forward");
+    MR_TRY(check_step_error(m));
     m->position += n;
     return MR_OK;
 }
@@ -780,10 +991,24 @@ int mr_model_generate_greedy(mr_model *m, int max_new, int eos, int32_t *tokens,
     k_argmax<<<1, 1024, 0, s>>>(m->logits, m->d.vocab_size, m->pos_dev, m->done_dev, m->ids_dev, m->gen_dev,
                                 m->count_dev, m->eos_dev, 0);
     MR_LAUNCHED("enqueue argmax");
-    for (int i = 1; i < max_new; ++i) MR_TRY(run_step(m, STEP_GREEDY));
+    hipEvent_t e0, e1;
+    MR_HIP(hipEventCreate(&e0), "create event");
+    MR_HIP(hipEventCreate(&e1), "create event");
+    hipEventRecord(e0, s);
+    int rc = MR_OK;
+    for (int i = 1; i < max_new && rc == MR_OK; ++i) rc = run_step(m, STEP_GREEDY);
+    hipEventRecord(e1, s);
     int host[3];
-    MR_HIP(hipMemcpyAsync(host, m->done_dev, sizeof(host), hipMemcpyDeviceToHost, s), "read greedy state");
-    MR_HIP(hipStreamSynchronize(s), "generate");
+    hipError_t ce = hipMemcpyAsync(host, m->done_dev, sizeof(host), hipMemcpyDeviceToHost, s);
+    hipError_t se = hipStreamSynchronize(s);
+    float ms = 0.0f;
+    if (se == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess) m->last_ms = ms;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc != MR_OK) return rc;
+    MR_HIP(ce, "read greedy state");
+    MR_HIP(se, "generate");
+    MR_TRY(check_step_error(m));
     int count = host[1];
     MR_HIP(hipMemcpy(tokens, m->gen_dev, (size_t)count * sizeof(int), hipMemcpyDeviceToHost), "read tokens");
     int pos = 0;
@@ -825,6 +1050,33 @@ int mr_model_time_kernel(mr_model *m, int which, int reps, float *avg_ms) {
     if (rc != MR_OK) return rc;
     MR_HIP(e, "time kernel");
     *avg_ms = ms / (float)std::max(launches, 1);
+    return MR_OK;
+}
+
+int mr_model_trace_step(mr_model *m, uint64_t *out, int64_t capacity, int *phases, int *grid) {
+    MR_TRY(check_ctx(m, "trace_step"));
+    MR_REQUIRE(out && phases && grid, "trace_step: null argument");
+    if (!m->persistent_ok || m->mode != MR_STEP_PERSISTENT)
+        return fail(MR_ERR_STATE, "trace_step: the model does not run the persistent step kernel");
+    MR_REQUIRE(m->position >= 1 && m->position < m->d.context_length, "trace_step: call forward first");
+    const size_t n = (size_t)m->n_head * m->grid * 3;
+    MR_REQUIRE((int64_t)n <= capacity, "trace_step: output too small");
+    *phases = m->n_head;
+    *grid = m->grid;
+    unsigned long long *buf = nullptr;
+    MR_TRY(device_alloc(m, n * sizeof(unsigned long long), (void **)&buf));
+    hipStream_t s = m->ctx->stream;
+    hipMemsetAsync(buf, 0, n * sizeof(unsigned long long), s);
+    int init[3] = {0, 0, -1};   // done, count, eos
+    hipMemcpyAsync(m->done_dev, init, sizeof(init), hipMemcpyHostToDevice, s);
+    int rc = run_persistent(m, STEP_GREEDY, buf);
+    hipError_t e = hipStreamSynchronize(s);
+    if (rc == MR_OK && e == hipSuccess) e = hipMemcpy(out, buf, n * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    hipFree(buf);
+    MR_TRY(rc);
+    MR_HIP(e, "trace step");
+    MR_TRY(check_step_error(m));
+    m->position += 1;
     return MR_OK;
 }
 

@@ -1,0 +1,62 @@
+// Persistent step kernel: one cooperative launch runs a whole token step as a
+// program of phases whose workgroups exchange activations as flag-in-data
+// cells (ll.h) instead of meeting at grid barriers.
+#pragma once
+
+#include <vector>
+
+#include "attention_tile.h"
+#include "linear.h"
+
+namespace mr {
+
+enum PhaseKind : int { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN = 2, PH_HEAD = 3 };
+
+// What a step does after the last layer: nothing (prompt token), LM head
+// (logits for the host), or LM head + greedy choice on device.
+enum StepKind { STEP_PLAIN = 0, STEP_LOGITS = 1, STEP_GREEDY = 2, STEP_KINDS = 3 };
+
+// One phase of the step program (device memory, built once per model).  Cell
+// buffers (uint64_t) hold flag-in-data activations; a read of x expects the
+// epoch of phase x_phase, a residual read of y the epoch of phase res_phase.
+struct Phase {
+    int kind = PH_GEMV;
+    // PH_EMBED: y[j] = embedding row of the position's token, j < n
+    // PH_GEMV / PH_HEAD: y = epilogue(W . prologue(x)), rows split over workgroups
+    int dtype = MR_BF16, n = 0, k = 0, pro = PRO_COPY, epi = EPI_STORE;
+    int x_phase = -1, res_phase = -1;
+    const void *w = nullptr, *w2 = nullptr;
+    const uint64_t *x = nullptr;
+    const float *gain = nullptr;
+    float eps = 0.0f, scale = 1.0f;
+    uint64_t *y = nullptr;
+    float *logits = nullptr;       // PH_HEAD: plain logits for the host
+    // PH_ATTN: at.s.q / k_new / v_new / out point at cells; x_phase = Q/K/V phase
+    unsigned *merge = nullptr;     // [kv_heads] last-arriver counters of this layer
+    att::Args at{};
+};
+
+// Per-launch arguments (all pointers into the model's device state).
+struct StepArgs {
+    const Phase *phases = nullptr;
+    int nphases = 0;
+    int stride = 0;                     // epochs per position (>= phases of any program)
+    int kind = 0;                       // StepKind
+    int *pos = nullptr, *done = nullptr, *ids = nullptr, *gen = nullptr, *count = nullptr;
+    const int *eos = nullptr;
+    int *err = nullptr;                 // 1 = a wait timed out
+    unsigned *exits = nullptr;          // workgroups that left this launch (last one finishes)
+    float *best_val = nullptr;          // [grid] per-workgroup argmax partials
+    int *best_idx = nullptr, *bad = nullptr;
+    const void *embed = nullptr;
+    int embed_dtype = MR_F32;
+    const void *dummy = nullptr;        // 16 readable bytes: target of loads past a matrix's end
+    unsigned long long *trace = nullptr;   // optional [nphases][grid][3]: entry, inputs ready, exit
+};
+
+constexpr int kStepThreads = 512;
+
+size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
+int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds);
+
+}  // namespace mr

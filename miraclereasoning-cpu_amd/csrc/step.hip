@@ -1,0 +1,451 @@
+// Persistent step kernel.
+//
+// One cooperative launch of one workgroup per CU runs a whole token step: the
+// host builds, once per model, a program of phases (embedding row; per layer:
+// Q/K/V GEMV, attention units with the split merge, O GEMV + residual, gate/up
+// GEMV + SwiGLU, down GEMV + residual; LM head + greedy choice) and every
+// workgroup walks it.
+//
+// Why one kernel: at bs = 1 a step streams 2.3-2.6 GB through ~120 dependent
+// phases of 8-50 MB.  Separate launches pay a launch gap and a ramp-up each;
+// here a workgroup issues the weight loads of its share of a phase (weights
+// never depend on activations) before it waits for that phase's input, so the
+// weights are in flight while the previous phase finishes elsewhere.
+//
+// No grid barriers: activations travel as flag-in-data cells (ll.h), and a
+// workgroup waits only for the cells it reads.  The split merge of a KV head is
+// done by the last of its attention units to finish (a counter per layer and
+// head), and the step's closing work (greedy choice, position) by the last
+// workgroup to leave the launch.  Every wait is bounded (ll.h).
+//
+// Reuse of a cell buffer within a step is ordered by the data dependencies
+// themselves: a phase that rewrites a buffer consumes, directly or through the
+// phases between, the outputs of every workgroup that read the previous
+// contents, and those reads precede the reader's own outputs.
+#include "step.h"
+
+namespace mr {
+namespace {
+
+using namespace att;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int NT = kStepThreads;
+constexpr int NW = NT / kWave;
+
+// Program descriptors are read through the constant address space: uniform
+// loads from it become scalar loads, made where a field is used.
+#define MR_CONST __attribute__((address_space(4)))
+
+__device__ __forceinline__ unsigned epoch(const StepArgs &s, int pos, int phase) {
+    return (unsigned)pos * (unsigned)s.stride + (unsigned)phase + 1u;
+}
+
+__device__ __forceinline__ float ldc(const float *p) {
+    return __hip_atomic_load(gmem(const_cast<float *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stc(float *p, float v) {
+    __hip_atomic_store(gmem(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ldci(const int *p) {
+    return __hip_atomic_load(gmem(const_cast<int *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stci(int *p, int v) {
+    __hip_atomic_store(gmem(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void stamp(unsigned long long *tr, int i) {
+    if (tr && threadIdx.x == 0) tr[i] = wall_clock64();
+}
+
+// ------------------------------------------------------------------ GEMV phase
+// Rows [r0, r1) of each workgroup, in groups of `slots` rows (lpr lanes per
+// row) dealt round-robin to the waves.  A job is kVC 16-byte vectors per lane
+// of one row group of one matrix; a wave keeps kDepth jobs in flight, and the
+// first kDepth are issued before the phase's input is awaited.  Loads past a
+// matrix's end read a 16-byte dummy so every job issues the same number of
+// loads and the compiler's waits stay exact.
+constexpr int kVC = 4;
+constexpr int kDepth = 6;
+
+struct GemvGeo {
+    int r0, r1;      // rows of this workgroup
+    int nvec;        // 16-byte vectors per row
+    int lpr, slots;  // lanes per row, rows per job
+    int cpr;         // jobs per row and matrix
+    int groups;      // row groups of this wave
+    int jobs;        // jobs of this wave
+    int64_t rowbytes;
+};
+
+template <int M>
+__device__ __forceinline__ GemvGeo gemv_geo(const Phase &ph) {
+    GemvGeo g;
+    const int eb = ph.dtype == MR_F32 ? 4 : 2;
+    g.rowbytes = (int64_t)ph.k * eb;
+    g.nvec = ph.k / (16 / eb);
+    g.lpr = 1;
+    while (g.lpr * 2 <= g.nvec && g.lpr < kWave) g.lpr *= 2;
+    g.slots = kWave / g.lpr;
+    const int vpl = (g.nvec + g.lpr - 1) / g.lpr;
+    g.cpr = (vpl + kVC - 1) / kVC;
+    const int rpw = (ph.n + gridDim.x - 1) / gridDim.x;
+    g.r0 = min((int)blockIdx.x * rpw, ph.n);
+    g.r1 = min(g.r0 + rpw, ph.n);
+    const int ngroups = (g.r1 - g.r0 + g.slots - 1) / g.slots;
+    const int wave = threadIdx.x >> 6;
+    g.groups = ngroups > wave ? (ngroups - wave + NW - 1) / NW : 0;
+    g.jobs = g.groups * M * g.cpr;
+    return g;
+}
+
+struct Cursor {
+    int j, m, c;   // row group of the wave, matrix, chunk
+};
+
+template <int M>
+__device__ __forceinline__ void advance(Cursor &u, int cpr) {
+    if (++u.c == cpr) {
+        u.c = 0;
+        if (++u.m == M) {
+            u.m = 0;
+            ++u.j;
+        }
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void issue(u32x4 (&b)[kVC], const Cursor &u, const Phase &ph, const GemvGeo &g,
+                                      const void *dummy) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (g.lpr - 1), slot = lane / g.lpr;
+    const int row = g.r0 + (wave + NW * u.j) * g.slots + slot;
+    const bool live = u.j < g.groups && row < g.r1;
+    const char *base = (const char *)(M == 2 && u.m ? ph.w2 : ph.w) + (int64_t)row * g.rowbytes;
+#pragma unroll
+    for (int i = 0; i < kVC; ++i) {
+        const int v = sub + (u.c * kVC + i) * g.lpr;
+        const char *p = live && v < g.nvec ? base + (int64_t)v * 16 : (const char *)dummy;
+        b[i] = __builtin_nontemporal_load(gmem((const u32x4 *)p));
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void widen16(const u32x4 &v, float *o) {
+    if constexpr (DT == MR_F32) {
+        o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y);
+        o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+    } else if constexpr (DT == MR_BF16) {
+        o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+        o[4] = __uint_as_float(v.z << 16); o[5] = __uint_as_float(v.z & 0xffff0000u);
+        o[6] = __uint_as_float(v.w << 16); o[7] = __uint_as_float(v.w & 0xffff0000u);
+    } else {
+        o[0] = f16_to_f32(v.x & 0xffffu); o[1] = f16_to_f32(v.x >> 16);
+        o[2] = f16_to_f32(v.y & 0xffffu); o[3] = f16_to_f32(v.y >> 16);
+        o[4] = f16_to_f32(v.z & 0xffffu); o[5] = f16_to_f32(v.z >> 16);
+        o[6] = f16_to_f32(v.w & 0xffffu); o[7] = f16_to_f32(v.w >> 16);
+    }
+}
+
+template <int DT, int M>
+__device__ __forceinline__ void consume(const u32x4 (&b)[kVC], const Cursor &u, const GemvGeo &g, const float *xs,
+                                        float (&acc)[M]) {
+    constexpr int E = DT == MR_F32 ? 4 : 8;
+    const int sub = (threadIdx.x & 63) & (g.lpr - 1);
+    float a = M == 2 && u.m ? acc[M - 1] : acc[0];
+#pragma unroll
+    for (int i = 0; i < kVC; ++i) {
+        const int v = sub + (u.c * kVC + i) * g.lpr;
+        if (v < g.nvec) {
+            float xv[E], wf[E];
+#pragma unroll
+            for (int e = 0; e < E; e += 4) {
+                const float4 t = *(const float4 *)(xs + v * E + e);
+                xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
+            }
+            widen16<DT>(b[i], wf);
+#pragma unroll
+            for (int e = 0; e < E; ++e) a = fmaf(wf[e], xv[e], a);
+        }
+    }
+    if (M == 2 && u.m) acc[M - 1] = a;
+    else acc[0] = a;
+}
+
+// Greedy choice bookkeeping of the LM head phase (per lane).
+struct Best {
+    float v;
+    int i;
+    int bad;
+};
+
+__device__ __forceinline__ void best_merge(Best &a, float v, int i) {
+    if (v > a.v || (v == a.v && i < a.i)) {
+        a.v = v;
+        a.i = i;
+    }
+}
+
+// Stage the phase input (cells of epoch ep_x) in LDS with the RMSNorm prologue
+// of kernels.cl:19-28 when asked, and the residual inputs of this workgroup's
+// rows (cells of epoch ep_res).  False when a wait gave up.
+__device__ __forceinline__ bool stage_input(const Phase &ph, const GemvGeo &g, const StepArgs &s, unsigned ep_x,
+                                            unsigned ep_res, float *xs, float *res, float *red) {
+    const int tid = threadIdx.x;
+    ll::Wait w = ll::waiter(s.err);
+    const int k2 = ph.k / 2;
+    for (int i = tid; i < k2; i += NT) {
+        const float2 v = ll::get2(ph.x + 2 * i, ep_x, w);
+        xs[2 * i] = v.x;
+        xs[2 * i + 1] = v.y;
+    }
+    if ((ph.k & 1) && tid == 0) xs[ph.k - 1] = ll::get(ph.x + ph.k - 1, ep_x, w);
+    if (ph.epi == EPI_RESIDUAL)
+        for (int r = g.r0 + tid; r < g.r1; r += NT) res[r - g.r0] = ll::get(ph.y + r, ep_res, w);
+    if (!ll::all_ok(w)) return false;
+    if (ph.pro == PRO_RMS) {
+        float ss = 0.0f;
+        for (int j = tid; j < ph.k; j += NT) ss = fmaf(xs[j], xs[j], ss);
+        ss = block_sum(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)ph.k + ph.eps);
+        __syncthreads();
+        for (int j = tid; j < ph.k; j += NT) xs[j] = xs[j] * scale * (ph.gain ? gmem(ph.gain)[j] : 1.0f);
+        __syncthreads();
+    }
+    return true;
+}
+
+template <int DT, int M, bool HEAD>
+__device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
+                                           unsigned ep_y, float *lds, unsigned long long *tr) {
+    const GemvGeo g = gemv_geo<M>(ph);
+    u32x4 buf[kDepth][kVC];
+    Cursor is{0, 0, 0};
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        issue<M>(buf[d], is, ph, g, s.dummy);
+        advance<M>(is, g.cpr);
+    }
+    float *xs = lds;
+    float *res = xs + ((ph.k + 3) & ~3);
+    float *red = res + ((g.r1 - g.r0 + 3) & ~3);
+    if (g.r0 < g.r1 && !stage_input(ph, g, s, ep_x, ep_res, xs, res, red)) return false;
+    stamp(tr, 1);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (g.lpr - 1), slot = lane / g.lpr;
+    Best best{-INFINITY, 0x7fffffff, 0};
+    float acc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+    Cursor cs{0, 0, 0};
+    for (int t0 = 0; t0 < g.jobs; t0 += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            if (t0 + d < g.jobs) {
+                consume<DT, M>(buf[d], cs, g, xs, acc);
+                if (cs.c == g.cpr - 1 && cs.m == M - 1) {   // row group complete
+                    const float a0 = group_sum(acc[0], g.lpr);
+                    const float a1 = M == 2 ? group_sum(acc[M - 1], g.lpr) : a0;
+                    const int row = g.r0 + (wave + NW * cs.j) * g.slots + slot;
+                    if (sub == 0 && row < g.r1) {
+                        float out;
+                        if (M == 2) out = (a0 / (1.0f + expf(-a0))) * a1;   // SwiGLU (kernels.cl:46-50)
+                        else if (ph.epi == EPI_RESIDUAL) out = res[row - g.r0] + ph.scale * a0;
+                        else out = a0;
+                        if (HEAD) {
+                            gmem(ph.logits)[row] = out;
+                            if (!isfinite(out)) best.bad = 1;
+                            best_merge(best, out, row);
+                        } else {
+                            ll::put(ph.y + row, out, ep_y);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+                }
+                advance<M>(cs, g.cpr);
+            }
+            issue<M>(buf[d], is, ph, g, s.dummy);
+            advance<M>(is, g.cpr);
+        }
+    }
+    if (HEAD) {   // per-workgroup greedy partial
+        __shared__ float bv[NW];
+        __shared__ int bi[NW], bb[NW];
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best.v, off);
+            const int oi = __shfl_xor(best.i, off);
+            best.bad |= __shfl_xor(best.bad, off);
+            best_merge(best, ov, oi);
+        }
+        if (lane == 0) {
+            bv[wave] = best.v;
+            bi[wave] = best.i;
+            bb[wave] = best.bad;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            Best w{bv[0], bi[0], bb[0]};
+            for (int i = 1; i < NW; ++i) {
+                w.bad |= bb[i];
+                best_merge(w, bv[i], bi[i]);
+            }
+            stc(s.best_val + blockIdx.x, w.v);
+            stci(s.best_idx + blockIdx.x, w.i);
+            stci(s.bad + blockIdx.x, w.bad);
+        }
+    }
+    __syncthreads();   // LDS is reused by the next phase
+    return true;
+}
+
+template <bool HEAD>
+__device__ __forceinline__ bool gemv_dispatch(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
+                                              unsigned ep_y, float *lds, unsigned long long *tr) {
+    const int dt = ph.dtype;
+    if (!HEAD && ph.epi == EPI_SWIGLU) {
+        if (dt == MR_BF16) return gemv_phase<MR_BF16, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+        if (dt == MR_F32) return gemv_phase<MR_F32, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+        return gemv_phase<MR_F16, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+    }
+    if (dt == MR_BF16) return gemv_phase<MR_BF16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+    if (dt == MR_F32) return gemv_phase<MR_F32, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+    return gemv_phase<MR_F16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+}
+
+// ------------------------------------------------------------------ other phases
+__device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_y) {
+    const int h = ph.n;
+    const int rpw = (h + gridDim.x - 1) / gridDim.x;
+    const int j0 = blockIdx.x * rpw, j1 = min(j0 + rpw, h);
+    const int tok = gmem(s.ids)[pos];
+    for (int j = j0 + threadIdx.x; j < j1; j += NT) {
+        const int64_t i = (int64_t)tok * h + j;
+        float v;
+        if (s.embed_dtype == MR_F32) v = gmem((const float *)s.embed)[i];
+        else if (s.embed_dtype == MR_BF16) v = bf16_to_f32(gmem((const uint16_t *)s.embed)[i]);
+        else v = f16_to_f32(gmem((const uint16_t *)s.embed)[i]);
+        ll::put(ph.y + j, v, ep_y);
+    }
+}
+
+// Attention units (kv head, split) dealt round-robin to the workgroups; the
+// last unit of a head to finish merges the head's splits (kernels.cl:58-107).
+template <int D>
+__device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
+                                           unsigned ep_out, float *lds) {
+    __shared__ int last;
+    const AttnStepArgs &a = ph.at.s;
+    const Geo g = geometry(ph.at, pos);
+    const Io io{ep_in, ep_out, s.err};
+    const int splits = a.splits, units = a.kv_heads * splits;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const int kh = u / splits;
+        if (!attn_unit<D, true, NT>(ph.at, g, kh, u % splits, lds, io)) return false;
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's partial stores have reached the coherence point
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(gmem(ph.merge + kh), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (unsigned)(splits - 1);
+        __syncthreads();
+        if (last) {
+            int t0, t1, split_len;
+            split_range<D>(g, splits, 0, &t0, &t1, &split_len);
+            combine<D, true, NT>(a, kh, (g.total + split_len - 1) / split_len, lds, io);
+            if (threadIdx.x == 0)
+                __hip_atomic_store(gmem(ph.merge + kh), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+    }
+    return true;
+}
+
+__global__ void __launch_bounds__(NT) k_step(StepArgs s) {
+    extern __shared__ float lds[];
+    __shared__ int last;
+    if (ldci(s.done) || ldci(s.err)) return;
+    const int pos = *s.pos;
+    const MR_CONST Phase *prog = (const MR_CONST Phase *)s.phases;
+    for (int p = 0; p < s.nphases; ++p) {
+        const Phase &ph = *(const Phase *)(prog + p);
+        unsigned long long *tr = s.trace ? s.trace + ((size_t)p * gridDim.x + blockIdx.x) * 3 : nullptr;
+        stamp(tr, 0);
+        const unsigned ep_y = epoch(s, pos, p);
+        const unsigned ep_x = epoch(s, pos, ph.x_phase), ep_res = epoch(s, pos, ph.res_phase);
+        bool ok = true;
+        switch (ph.kind) {
+            case PH_EMBED:
+                embed_phase(ph, s, pos, ep_y);
+                stamp(tr, 1);
+                break;
+            case PH_GEMV: ok = gemv_dispatch<false>(ph, s, ep_x, ep_res, ep_y, lds, tr); break;
+            case PH_HEAD: ok = gemv_dispatch<true>(ph, s, ep_x, ep_res, ep_y, lds, tr); break;
+            case PH_ATTN:
+                stamp(tr, 1);
+                if (ph.at.s.dim == 128) ok = attn_phase<128>(ph, s, pos, ep_x, ep_y, lds);
+                else if (ph.at.s.dim == 64) ok = attn_phase<64>(ph, s, pos, ep_x, ep_y, lds);
+                else ok = attn_phase<32>(ph, s, pos, ep_x, ep_y, lds);
+                break;
+        }
+        if (!ok) return;
+        stamp(tr, 2);
+    }
+    // The last workgroup to leave finishes the step: greedy choice, EOS, position.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(gmem(s.exits), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    __syncthreads();
+    if (!last || threadIdx.x != 0) return;
+    __hip_atomic_store(gmem(s.exits), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int next = pos + 1;
+    *s.pos = next;
+    if (s.kind == STEP_GREEDY) {
+        Best w{-INFINITY, 0x7fffffff, 0};
+        for (int i = 0; i < (int)gridDim.x; ++i) {
+            w.bad |= ldci(s.bad + i);
+            best_merge(w, ldc(s.best_val + i), ldci(s.best_idx + i));
+        }
+        if (w.bad) {
+            *s.done = 2;
+        } else {
+            s.ids[next] = w.i;
+            s.gen[*s.count] = w.i;
+            *s.count += 1;
+            if (w.i == *s.eos) *s.done = 1;
+        }
+    }
+}
+
+}  // namespace
+
+size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
+    size_t need = 0;
+    for (const Phase &ph : program) {
+        size_t f = 0;
+        if (ph.kind == PH_GEMV || ph.kind == PH_HEAD) {
+            const int rpw = (ph.n + grid - 1) / grid;
+            f = ((ph.k + 3) & ~3) + ((rpw + 3) & ~3) + NW;
+        }
+        if (ph.kind == PH_ATTN) {
+            const int G = ph.at.s.heads / ph.at.s.kv_heads, d = ph.at.s.dim, sp = ph.at.s.splits;
+            if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_lds_floats<128, NT>(G, sp));
+            else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_lds_floats<64, NT>(G, sp));
+            else f = std::max(unit_lds_floats<32>(G), combine_lds_floats<32, NT>(G, sp));
+        }
+        need = std::max(need, f * sizeof(float));
+    }
+    return need;
+}
+
+int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds) {
+    StepArgs copy = a;
+    void *args[] = {&copy};
+    MR_HIP(hipLaunchCooperativeKernel((const void *)k_step, dim3(grid), dim3(NT), args, (unsigned)lds, s),
+           "launch step kernel");
+    return MR_OK;
+}
+
+}  // namespace mr

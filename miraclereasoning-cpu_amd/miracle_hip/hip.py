@@ -88,7 +88,10 @@ _SIGNATURES = {
     "mr_model_position": [_P, C.POINTER(C.c_int)],
     "mr_model_forward": [_P, _P, _i, _i, _P],
     "mr_model_generate_greedy": [_P, _i, _i, _P, C.POINTER(C.c_int)],
-    "mr_model_use_graph": [_P, _i],
+    "mr_model_set_step_mode": [_P, _i],
+    "mr_model_get_step_mode": [_P, C.POINTER(C.c_int)],
+    "mr_model_last_decode_ms": [_P, C.POINTER(C.c_float)],
+    "mr_model_trace_step": [_P, _P, C.c_int64, C.POINTER(C.c_int), C.POINTER(C.c_int)],
     "mr_model_time_kernel": [_P, _i, _i, C.POINTER(C.c_float)],
     "mr_debug_fail_next": [_P],
 }

@@ -131,8 +131,35 @@ class Engine:
         _check(self.lib.mr_model_position(self.handle, C.byref(pos)), "position")
         return pos.value
 
-    def use_graph(self, enable):
-        _check(self.lib.mr_model_use_graph(self.handle, int(bool(enable))), "use_graph")
+    STEP_MODES = {"persistent": 0, "graph": 1, "eager": 2}
+
+    def set_step_mode(self, mode):
+        """"persistent" (one kernel per token step), "graph" (per-layer kernels
+        replayed from a hipGraph) or "eager" (per-layer kernels, no graph)."""
+        _check(self.lib.mr_model_set_step_mode(self.handle, self.STEP_MODES[mode]), "set_step_mode")
+
+    def step_mode(self):
+        mode = C.c_int()
+        _check(self.lib.mr_model_get_step_mode(self.handle, C.byref(mode)), "get_step_mode")
+        return {v: k for k, v in self.STEP_MODES.items()}[mode.value]
+
+    def trace_step(self):
+        """Per-phase, per-workgroup timestamps (µs, relative to the step start) of
+        one persistent greedy decode step: array [phases, grid, 3] of (phase
+        entry, inputs ready, phase exit); NaN where a workgroup had no work."""
+        cap = 4 * 1024 * 1024
+        buf = np.zeros(cap, np.uint64)
+        phases, grid = C.c_int(), C.c_int()
+        _check(self.lib.mr_model_trace_step(self.handle, buf.ctypes.data, cap, C.byref(phases), C.byref(grid)),
+               "trace step")
+        t = buf[:phases.value * grid.value * 3].reshape(phases.value, grid.value, 3).astype(np.int64)
+        t0 = t[0, :, 0].min()
+        return np.where(t > 0, (t - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
+
+    def last_decode_ms(self):
+        ms = C.c_float()
+        _check(self.lib.mr_model_last_decode_ms(self.handle, C.byref(ms)), "last_decode_ms")
+        return ms.value
 
 
 class MiracleModel:

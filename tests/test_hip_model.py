@@ -107,18 +107,49 @@ def test_workload_tiny_matches_reference(backend, golden_dir):
     assert model.generate(list(z["prompt"]), max_new_tokens=16) == z["greedy"].tolist()
 
 
-@pytest.mark.parametrize("name,prompt,steps", [("flashnano-1.5-mid", 40, 6), ("flashnano-1.7", 12, 4)])
-def test_workload_geometry_matches_oracle(backend, name, prompt, steps):
-    """Full-size geometry (BF16 weights as drawn for the workload) on a short
-    prompt: logits of every step and the greedy stream against the oracle."""
-    wl = presets.workload(name)
-    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
-    ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
-    print("case", name, flush=True)
+_WORKLOAD_CACHE = {}
+
+
+def _workload(name, prompt):
+    """Weights, prompt and oracle results for a workload geometry (cached)."""
+    if name not in _WORKLOAD_CACHE:
+        wl = presets.workload(name)
+        weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+        ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
+        ref = OracleModel(wl["config"], {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                          context_length=wl["context"])
+        want = ref.prefill(ids, return_all=True)
+        stream = ref.generate(list(ids), max_new_tokens=6)
+        _WORKLOAD_CACHE[name] = (wl, weights, ids, want, stream)
+    return _WORKLOAD_CACHE[name]
+
+
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("name,prompt", [("flashnano-1.5-tiny", 70), ("flashnano-1.5-mid", 40), ("flashnano-1.7", 12)])
+def test_workload_geometry_matches_oracle(backend, name, prompt, mode):
+    """Full-size geometry (weights as drawn for the workload) on a short prompt:
+    logits of every prompt token and a greedy stream against the oracle, for
+    both step implementations.  The tiny prompt (70 tokens) wraps its 64-key
+    local ring."""
+    wl, weights, ids, want, stream = _workload(name, prompt)
+    print("case", name, mode, flush=True)
     model = MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"])
-    got = model.prefill(ids, return_all=True)[-steps:]
-    ref = OracleModel(wl["config"], {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
-                      context_length=wl["context"])
-    want = ref.prefill(ids, return_all=True)[-steps:]
-    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
-    assert model.generate(list(ids), max_new_tokens=steps) == ref.generate(list(ids), max_new_tokens=steps)
+    model.engine.set_step_mode(mode)
+    assert model.engine.step_mode() == mode
+    tol = dict(atol=2e-5, rtol=2e-4) if wl["dtype"] == "f32" else dict(rtol=1e-3, atol=1e-4)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, **tol)
+    assert model.generate(list(ids), max_new_tokens=6) == stream
+
+
+def test_persistent_decode_equals_prefill(backend):
+    """The exact-mode invariant (decode == prefill, bit for bit) on the
+    persistent path, which reduces across workgroups in a fixed order."""
+    wl = presets.workload("flashnano-1.5-tiny")
+    model = MiracleModel(ModelConfig.from_dict(wl["config"]),
+                         synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"]), backend=backend,
+                         context_length=128)
+    assert model.engine.step_mode() == "persistent"
+    ids = synthetic.prompt_ids(4096, 20, 5)
+    whole = model.prefill(ids, return_all=True)
+    model.reset()
+    np.testing.assert_array_equal(np.stack([model.decode(int(i)) for i in ids]), whole)
