@@ -41,10 +41,13 @@ struct Geo {
 };
 
 // LL-mode epochs: inputs (q/k/v cells) and output (merged cells); in that mode
-// AttnStepArgs' q, k_new, v_new and out point at uint64_t cells.
+// AttnStepArgs' q, k_new, v_new and out point at uint64_t cells.  The inputs'
+// producers report progress in ready[0..nready) (ll.h progress words).
 struct Io {
     unsigned ep_in, ep_out;
     int *err;
+    const unsigned *ready;
+    int nready;
 };
 
 template <bool COH>
@@ -91,17 +94,22 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if constexpr (LL) {
         ll::Wait w = ll::waiter(io.err);
-        const uint64_t *q_src = (const uint64_t *)a.q + (int64_t)kh * G * d;
+        ll::wait_words(io.ready, io.nready, io.ep_in, tid, w);
+        if (!ll::all_ok(w)) return false;
+        // Cell indices relative to q (the Q/K/V cells are one buffer).
+        const uint64_t *cells = (const uint64_t *)a.q;
+        const int q0 = kh * G * d;
+        const int k0 = (int)((const uint64_t *)a.k_new - cells) + kh * d;
+        const int v0 = (int)((const uint64_t *)a.v_new - cells) + kh * d;
         for (int i = 2 * tid; i < G * d; i += 2 * NT) {
-            float2 v = ll::get2(q_src + i, io.ep_in, w);
+            float2 v = ll::get2(cells, q0 + i, io.ep_in, w);
             qs[i] = v.x;
             qs[i + 1] = v.y;
         }
-        const uint64_t *k_src = (const uint64_t *)a.k_new + kh * d, *v_src = (const uint64_t *)a.v_new + kh * d;
         for (int j = 2 * tid; j < 2 * d; j += 2 * NT) {
             const bool isk = j < d;
             const int c = isk ? j : j - d;
-            float2 v = ll::get2((isk ? k_src : v_src) + c, io.ep_in, w);
+            float2 v = ll::get2(cells, (isk ? k0 : v0) + c, io.ep_in, w);
             float *dst = isk ? kn : vn;
             dst[c] = v.x;
             dst[c + 1] = v.y;
@@ -380,8 +388,8 @@ __device__ __forceinline__ void combine(const AttnStepArgs &a, int kh, int activ
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
         for (int s = sg; s < active; s += SG) {
-            const float *src = base + (int64_t)(s * G + gh) * (D + 2) + 2 + 4 * j4;
-            const float4 o = LL ? load_f4_coherent(src) : load_f4(src);
+            const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
+            const float4 o = LL ? load_f4_coherent(base, off) : load_f4(base + off);
             const float e = w[s * G + gh];
             acc.x = fmaf(e, o.x, acc.x);
             acc.y = fmaf(e, o.y, acc.y);

@@ -80,12 +80,14 @@ __device__ __forceinline__ float4 load_f4(const float *p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// 16-byte load that is coherent across the device's L2 caches (cache policy
-// SC1 = agent scope): for data another workgroup wrote during this kernel.
-__device__ __forceinline__ float4 load_f4_coherent(const float *p) {
-    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000);
+// 16-byte load of base[i .. i+4) that is coherent across the device's L2
+// caches (cache policy SC1 = agent scope): for data another workgroup wrote
+// during this kernel.  `base` must be the same for the whole wave (it becomes
+// a buffer resource, which lives in scalar registers); i varies per lane.
+__device__ __forceinline__ float4 load_f4_coherent(const float *base, int i) {
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
     typedef float f32x4 __attribute__((ext_vector_type(4)));
-    f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 0, 0, 16);
+    f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, i * 4, 0, 16);
     return make_float4(v.x, v.y, v.z, v.w);
 }
 

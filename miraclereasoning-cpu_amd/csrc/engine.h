@@ -84,6 +84,11 @@ struct mr_model {
     uint64_t *c_hidden = nullptr, *c_qkv = nullptr, *c_attn = nullptr, *c_act = nullptr;
     unsigned *sync = nullptr;
     size_t sync_count = 0;
+    // progress words: the stream waves' [grid * kStreamWaves], then the merged
+    // attention heads' [layers * query_heads]
+    unsigned *words = nullptr;
+    size_t word_count = 0;
+    int xbuf = 0;                        // floats of one GEMV input staging buffer
     void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end
     int *err = nullptr;                  // wait timeout flag
     float *best_val = nullptr;

@@ -458,7 +458,8 @@ int run_persistent(mr_model *m, int kind, unsigned long long *trace = nullptr) {
     a.pos = m->pos_dev; a.done = m->done_dev; a.ids = m->ids_dev; a.gen = m->gen_dev; a.count = m->count_dev;
     a.eos = m->eos_dev; a.err = m->err; a.exits = m->sync + m->sync_count - 1;
     a.best_val = m->best_val; a.best_idx = m->best_idx; a.bad = m->bad;
-    a.embed = m->embed.ptr; a.embed_dtype = m->embed.dtype; a.dummy = m->dummy;
+    a.embed = m->embed.ptr; a.embed_dtype = m->embed.dtype; a.dummy = m->dummy; a.xbuf = m->xbuf;
+    a.progress = m->words; a.nprogress = m->grid * kStreamWaves;
     return launch_step(m->ctx->stream, a, m->grid, m->step_lds);
 }
 
@@ -537,6 +538,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         a.kind = PH_ATTN;
         a.x_phase = qkv_at;
         a.merge = m->sync + (size_t)li * d.query_heads;   // kv_heads <= query_heads
+        a.heads_done = m->words + (size_t)m->grid * kStreamWaves + (size_t)li * d.query_heads;
         AttnStepArgs &t = a.at.s;
         t.q = (const float *)m->c_qkv;
         t.k_new = (const float *)(m->c_qkv + qd);
@@ -553,6 +555,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         Phase o;
         o.kind = PH_GEMV; o.dtype = L.o.dtype; o.n = h; o.k = qd; o.pro = PRO_COPY; o.epi = EPI_RESIDUAL;
         o.w = L.o.ptr; o.x = m->c_attn; o.x_phase = attn_at; o.y = m->c_hidden; o.res_phase = hidden_at;
+        o.ready = a.heads_done; o.nready = L.kv_heads;
         o.scale = d.residual_scale;
         prog.push_back(o);
         hidden_at = last();
@@ -632,6 +635,9 @@ int setup_persistent(mr_model *m) {
     m->c_act = m->c_attn + n_attn;
     m->sync_count = (size_t)d.layers * d.query_heads + 1;
     MR_TRY(device_alloc(m, m->sync_count * sizeof(unsigned), (void **)&m->sync));
+    m->word_count = (size_t)m->grid * kStreamWaves + (size_t)d.layers * d.query_heads;
+    MR_TRY(device_alloc(m, m->word_count * sizeof(unsigned), (void **)&m->words));
+    MR_HIP(hipMemset(m->words, 0, m->word_count * sizeof(unsigned)), "clear step progress");
     MR_TRY(device_alloc(m, 256, &m->dummy));
     MR_TRY(device_alloc(m, sizeof(int), (void **)&m->err));
     MR_TRY(device_alloc(m, m->grid * sizeof(float), (void **)&m->best_val));
@@ -644,6 +650,7 @@ int setup_persistent(mr_model *m) {
 
     std::vector<Phase> plain = build_program(m, false), head = build_program(m, true);
     if ((int64_t)head.size() != stride) return fail(MR_ERR_INVALID, "step program: unexpected phase count");
+    m->xbuf = std::max(step_xbuf_floats(plain, m->grid), step_xbuf_floats(head, m->grid));
     m->step_lds = std::max(step_lds_bytes(plain, m->grid), step_lds_bytes(head, m->grid));
     if (m->step_lds > 64 * 1024) return MR_OK;
     m->n_plain = (int)plain.size();
@@ -725,7 +732,7 @@ int mr_model_destroy(mr_model *m) {
     if (m->freq) hipFree(m->freq);
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
-    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, m->dummy,
+    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);
     delete m;
@@ -916,6 +923,7 @@ int mr_model_reset(mr_model *m) {
     if (m->persistent_ok) {   // epochs restart with the position
         MR_HIP(hipMemsetAsync(m->cells, 0, m->cell_count * sizeof(uint64_t), m->ctx->stream), "reset step cells");
         MR_HIP(hipMemsetAsync(m->sync, 0, m->sync_count * sizeof(unsigned), m->ctx->stream), "reset step counters");
+        MR_HIP(hipMemsetAsync(m->words, 0, m->word_count * sizeof(unsigned), m->ctx->stream), "reset step progress");
         MR_HIP(hipMemsetAsync(m->err, 0, sizeof(int), m->ctx->stream), "reset step status");
     }
     MR_HIP(hipStreamSynchronize(m->ctx->stream), "reset");

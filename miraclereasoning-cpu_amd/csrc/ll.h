@@ -35,12 +35,15 @@ __device__ __forceinline__ uint64_t peek(const uint64_t *p) {
     return __hip_atomic_load(gmem(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Two adjacent cells (16-byte aligned) with one agent-coherent load (cache
-// policy SC1); each 8-byte half is one cell as stored.
-__device__ __forceinline__ u64x2 peek2(const uint64_t *p) {
-    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000);
+// Cells base[i], base[i+1] (i even, base 16-byte aligned) with one
+// agent-coherent load (cache policy SC1); each 8-byte half is one cell as
+// stored.  `base` must be the same for the whole wave (it becomes a buffer
+// resource, which lives in scalar registers: a per-lane base would make the
+// compiler issue the load once per distinct lane value); i varies per lane.
+__device__ __forceinline__ u64x2 peek2(const uint64_t *base, int i) {
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 0, 0, 16);
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, i * 8, 0, 16);
     u64x2 r;
     r.x = ((uint64_t)v.y << 32) | v.x;
     r.y = ((uint64_t)v.w << 32) | v.z;
@@ -85,14 +88,82 @@ __device__ __forceinline__ float get(const uint64_t *p, unsigned ep, Wait &w) {
     return __uint_as_float((unsigned)c);
 }
 
-__device__ __forceinline__ float2 get2(const uint64_t *p, unsigned ep, Wait &w) {
-    u64x2 c = peek2(p);
-    while (((unsigned)(c.x >> 32) != ep || (unsigned)(c.y >> 32) != ep) && backoff(w)) c = peek2(p);
+__device__ __forceinline__ float2 get2(const uint64_t *base, int i, unsigned ep, Wait &w) {
+    u64x2 c = peek2(base, i);
+    while (((unsigned)(c.x >> 32) != ep || (unsigned)(c.y >> 32) != ep) && backoff(w)) c = peek2(base, i);
     return make_float2(__uint_as_float((unsigned)c.x), __uint_as_float((unsigned)c.y));
 }
 
 // Block-uniform result of the block's waits (all threads must call).
 __device__ __forceinline__ bool all_ok(const Wait &w) { return !__syncthreads_or(!w.ok); }
+
+// Read n cell pairs x[0..2n) into xs (FP32), lane `me` of `lanes` taking pairs
+// me, me+lanes, ...: B pairs per lane in flight per round, and the whole batch
+// is read again until every pair carries epoch ep.  Returns the lane's sum of
+// squares of what it read (for an RMSNorm prologue).
+template <int B>
+__device__ __forceinline__ float read_pairs(const uint64_t *x, int n, unsigned ep, float *xs, int me, int lanes,
+                                            Wait &w) {
+    float ss = 0.0f;
+    for (int base = me; base < n; base += lanes * B) {
+        u64x2 c[B];
+        bool ready;
+        do {
+#pragma unroll
+            for (int i = 0; i < B; ++i) c[i] = peek2(x, 2 * min(base + i * lanes, n - 1));
+            ready = true;
+#pragma unroll
+            for (int i = 0; i < B; ++i)
+                ready &= base + i * lanes >= n ||
+                         ((unsigned)(c[i].x >> 32) == ep && (unsigned)(c[i].y >> 32) == ep);
+        } while (!ready && backoff(w));
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int idx = base + i * lanes;
+            if (idx < n) {
+                const float a = __uint_as_float((unsigned)c[i].x), b = __uint_as_float((unsigned)c[i].y);
+                xs[2 * idx] = a;
+                xs[2 * idx + 1] = b;
+                ss = fmaf(a, a, ss);
+                ss = fmaf(b, b, ss);
+            }
+        }
+    }
+    return ss;
+}
+
+// Progress words: one 32-bit word per producer holds the epoch of the last
+// phase whose outputs it has stored.  Epochs only grow within a sequence, so
+// "word >= epoch" means the producer is done with that phase.  They are a
+// cheap hint that the cells are there; the cells' own epochs stay the check.
+__device__ __forceinline__ void mark(unsigned *p, unsigned ep) {
+    __hip_atomic_store(gmem(p), ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned word(const unsigned *p) {
+    return __hip_atomic_load(gmem(const_cast<unsigned *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until words[0..n) all reach ep.  Only the first wave of the caller
+// polls (lane `me` < 64 takes words me, me+64, ...; up to 16 each, all in
+// flight per round) and it pauses between rounds: every workgroup polls the
+// same few lines, so the poll rate is kept low.
+__device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigned ep, int me, Wait &w) {
+    constexpr int B = 16;
+    if (me >= kWave) return;
+    for (int base = me; base < n; base += kWave * B) {
+        bool ready;
+        do {
+            unsigned v[B];
+#pragma unroll
+            for (int i = 0; i < B; ++i) v[i] = word(words + min(base + i * kWave, n - 1));
+            ready = true;
+#pragma unroll
+            for (int i = 0; i < B; ++i) ready &= base + i * kWave >= n || v[i] >= ep;
+            if (!ready) __builtin_amdgcn_s_sleep(16);
+        } while (!ready && backoff(w));
+    }
+}
 
 }  // namespace ll
 }  // namespace mr

@@ -31,8 +31,13 @@ struct Phase {
     float eps = 0.0f, scale = 1.0f;
     uint64_t *y = nullptr;
     float *logits = nullptr;       // PH_HEAD: plain logits for the host
+    // Progress words of x's producers when they are not the stream waves
+    // (the O projection waits for the attention heads' words).
+    const unsigned *ready = nullptr;
+    int nready = 0;
     // PH_ATTN: at.s.q / k_new / v_new / out point at cells; x_phase = Q/K/V phase
     unsigned *merge = nullptr;     // [kv_heads] last-arriver counters of this layer
+    unsigned *heads_done = nullptr;   // [kv_heads] progress words of the merged heads
     att::Args at{};
 };
 
@@ -45,17 +50,26 @@ struct StepArgs {
     int *pos = nullptr, *done = nullptr, *ids = nullptr, *gen = nullptr, *count = nullptr;
     const int *eos = nullptr;
     int *err = nullptr;                 // 1 = a wait timed out
+    unsigned *progress = nullptr;       // [grid * kStreamWaves] progress words of the stream waves
+    int nprogress = 0;
     unsigned *exits = nullptr;          // workgroups that left this launch (last one finishes)
     float *best_val = nullptr;          // [grid] per-workgroup argmax partials
     int *best_idx = nullptr, *bad = nullptr;
     const void *embed = nullptr;
     int embed_dtype = MR_F32;
     const void *dummy = nullptr;        // 16 readable bytes: target of loads past a matrix's end
-    unsigned long long *trace = nullptr;   // optional [nphases][grid][3]: entry, inputs ready, exit
+    int xbuf = 0;                       // floats of one GEMV input staging buffer (two in LDS)
+    unsigned long long *trace = nullptr;   // optional [nphases][grid][3]: entry, inputs staged, outputs stored
 };
 
+// Waves 0..kControlWaves-1 of a workgroup wait for and stage phase inputs; the
+// other (stream) waves load weights, compute and store outputs.
 constexpr int kStepThreads = 512;
+constexpr int kControlWaves = 4;
+constexpr int kStreamWaves = kStepThreads / 64 - kControlWaves;
 
+// Floats of one GEMV input staging buffer, and the dynamic LDS of the kernel.
+int step_xbuf_floats(const std::vector<Phase> &program, int grid);
 size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds);
 

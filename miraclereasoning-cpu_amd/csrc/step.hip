@@ -59,21 +59,28 @@ __device__ __forceinline__ void stamp(unsigned long long *tr, int i) {
 
 // ------------------------------------------------------------------ GEMV phase
 // Rows [r0, r1) of each workgroup, in groups of `slots` rows (lpr lanes per
-// row) dealt round-robin to the waves.  A job is kVC 16-byte vectors per lane
-// of one row group of one matrix; a wave keeps kDepth jobs in flight, and the
-// first kDepth are issued before the phase's input is awaited.  Loads past a
-// matrix's end read a 16-byte dummy so every job issues the same number of
-// loads and the compiler's waits stay exact.
+// row) dealt round-robin to the stream waves.  A job is kVC 16-byte vectors per
+// lane of one row group of one matrix; a stream wave keeps kDepth jobs in
+// flight (96 KB per CU in all), and issues
+// its first kDepth before the phase's input is staged.  Loads past a matrix's
+// end read a 16-byte dummy so every job issues the same number of loads and
+// the compiler's waits stay exact.
+//
+// The control waves wait for the input's producers, read the input cells into
+// one of two LDS buffers (a phase's stream waves read one while the control
+// waves fill the other for the next phase) and take the RMSNorm sum.
+constexpr int NC = kControlWaves;
+constexpr int NS = kStreamWaves;
 constexpr int kVC = 4;
-constexpr int kDepth = 6;
+constexpr int kDepth = 6;   // jobs in flight per stream wave when a job is one matrix (M = 1)
 
 struct GemvGeo {
     int r0, r1;      // rows of this workgroup
     int nvec;        // 16-byte vectors per row
     int lpr, slots;  // lanes per row, rows per job
-    int cpr;         // jobs per row and matrix
-    int groups;      // row groups of this wave
-    int jobs;        // jobs of this wave
+    int cpr;         // jobs per row
+    int groups;      // row groups of this stream wave
+    int jobs;        // jobs of this stream wave
     int64_t rowbytes;
 };
 
@@ -92,40 +99,45 @@ __device__ __forceinline__ GemvGeo gemv_geo(const Phase &ph) {
     g.r0 = min((int)blockIdx.x * rpw, ph.n);
     g.r1 = min(g.r0 + rpw, ph.n);
     const int ngroups = (g.r1 - g.r0 + g.slots - 1) / g.slots;
-    const int wave = threadIdx.x >> 6;
-    g.groups = ngroups > wave ? (ngroups - wave + NW - 1) / NW : 0;
-    g.jobs = g.groups * M * g.cpr;
+    const int sw = (int)(threadIdx.x >> 6) - NC;
+    g.groups = sw >= 0 && ngroups > sw ? (ngroups - sw + NS - 1) / NS : 0;
+    g.jobs = g.groups * g.cpr;
     return g;
 }
 
+// A job: chunk c of row group j, for all M matrices (the gate and up rows of
+// SwiGLU travel together, so no job selects a matrix at run time).
 struct Cursor {
-    int j, m, c;   // row group of the wave, matrix, chunk
+    int j, c;
 };
 
-template <int M>
 __device__ __forceinline__ void advance(Cursor &u, int cpr) {
     if (++u.c == cpr) {
         u.c = 0;
-        if (++u.m == M) {
-            u.m = 0;
-            ++u.j;
-        }
+        ++u.j;
     }
 }
 
+__device__ __forceinline__ int job_row(const GemvGeo &g, int j) {
+    const int lane = threadIdx.x & 63, sw = (int)(threadIdx.x >> 6) - NC;
+    return g.r0 + (sw + NS * j) * g.slots + lane / g.lpr;
+}
+
 template <int M>
-__device__ __forceinline__ void issue(u32x4 (&b)[kVC], const Cursor &u, const Phase &ph, const GemvGeo &g,
-                                      const void *dummy) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & (g.lpr - 1), slot = lane / g.lpr;
-    const int row = g.r0 + (wave + NW * u.j) * g.slots + slot;
+__device__ __forceinline__ void issue(u32x4 (&b)[M][kVC], const Cursor &u, const char *w0, const char *w1,
+                                      const GemvGeo &g, const void *dummy) {
+    const int sub = (threadIdx.x & 63) & (g.lpr - 1);
+    const int row = job_row(g, u.j);
     const bool live = u.j < g.groups && row < g.r1;
-    const char *base = (const char *)(M == 2 && u.m ? ph.w2 : ph.w) + (int64_t)row * g.rowbytes;
 #pragma unroll
-    for (int i = 0; i < kVC; ++i) {
-        const int v = sub + (u.c * kVC + i) * g.lpr;
-        const char *p = live && v < g.nvec ? base + (int64_t)v * 16 : (const char *)dummy;
-        b[i] = __builtin_nontemporal_load(gmem((const u32x4 *)p));
+    for (int m = 0; m < M; ++m) {
+        const char *base = (m == 0 ? w0 : w1) + (int64_t)row * g.rowbytes;
+#pragma unroll
+        for (int i = 0; i < kVC; ++i) {
+            const int v = sub + (u.c * kVC + i) * g.lpr;
+            const char *p = live && v < g.nvec ? base + (int64_t)v * 16 : (const char *)dummy;
+            b[m][i] = __builtin_nontemporal_load(gmem((const u32x4 *)p));
+        }
     }
 }
 
@@ -148,28 +160,29 @@ __device__ __forceinline__ void widen16(const u32x4 &v, float *o) {
 }
 
 template <int DT, int M>
-__device__ __forceinline__ void consume(const u32x4 (&b)[kVC], const Cursor &u, const GemvGeo &g, const float *xs,
+__device__ __forceinline__ void consume(const u32x4 (&b)[M][kVC], const Cursor &u, const GemvGeo &g, const float *xs,
                                         float (&acc)[M]) {
     constexpr int E = DT == MR_F32 ? 4 : 8;
     const int sub = (threadIdx.x & 63) & (g.lpr - 1);
-    float a = M == 2 && u.m ? acc[M - 1] : acc[0];
 #pragma unroll
     for (int i = 0; i < kVC; ++i) {
         const int v = sub + (u.c * kVC + i) * g.lpr;
         if (v < g.nvec) {
-            float xv[E], wf[E];
+            float xv[E];
 #pragma unroll
             for (int e = 0; e < E; e += 4) {
                 const float4 t = *(const float4 *)(xs + v * E + e);
                 xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
             }
-            widen16<DT>(b[i], wf);
 #pragma unroll
-            for (int e = 0; e < E; ++e) a = fmaf(wf[e], xv[e], a);
+            for (int m = 0; m < M; ++m) {
+                float wf[E];
+                widen16<DT>(b[m][i], wf);
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[m] = fmaf(wf[e], xv[e], acc[m]);
+            }
         }
     }
-    if (M == 2 && u.m) acc[M - 1] = a;
-    else acc[0] = a;
 }
 
 // Greedy choice bookkeeping of the LM head phase (per lane).
@@ -186,89 +199,122 @@ __device__ __forceinline__ void best_merge(Best &a, float v, int i) {
     }
 }
 
-// Stage the phase input (cells of epoch ep_x) in LDS with the RMSNorm prologue
-// of kernels.cl:19-28 when asked, and the residual inputs of this workgroup's
-// rows (cells of epoch ep_res).  False when a wait gave up.
-__device__ __forceinline__ bool stage_input(const Phase &ph, const GemvGeo &g, const StepArgs &s, unsigned ep_x,
-                                            unsigned ep_res, float *xs, float *res, float *red) {
-    const int tid = threadIdx.x;
-    ll::Wait w = ll::waiter(s.err);
-    const int k2 = ph.k / 2;
-    for (int i = tid; i < k2; i += NT) {
-        const float2 v = ll::get2(ph.x + 2 * i, ep_x, w);
-        xs[2 * i] = v.x;
-        xs[2 * i + 1] = v.y;
+// Control waves: wait for the producers of the input (epoch ep_x), read it into
+// xs with its sum of squares per wave in red[], and read the residual inputs
+// of this workgroup's rows (epoch ep_res) into res[].
+__device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, const StepArgs &s, unsigned ep_x,
+                                            unsigned ep_res, float *xs, float *res, float *red, ll::Wait &w) {
+    const int me = threadIdx.x, lanes = NC * kWave;
+    // The first control wave waits for the producers, then releases the others
+    // through an LDS word (ep_x, or ~0 when its wait gave up).
+    __shared__ unsigned released;
+    if (me < kWave) {
+        if (ph.ready) ll::wait_words(ph.ready, ph.nready, ep_x, me, w);
+        else ll::wait_words(s.progress, s.nprogress, ep_x, me, w);
+        const bool ok = __all(w.ok);
+        if (me == 0) __hip_atomic_store(&released, ok ? ep_x : ~0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        unsigned r;
+        while ((r = __hip_atomic_load(&released, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) != ep_x && r != ~0u)
+            __builtin_amdgcn_s_sleep(1);
+        if (r == ~0u) w.ok = false;
     }
-    if ((ph.k & 1) && tid == 0) xs[ph.k - 1] = ll::get(ph.x + ph.k - 1, ep_x, w);
+    float ss = ll::read_pairs<12>(ph.x, ph.k / 2, ep_x, xs, me, lanes, w);
+    if ((ph.k & 1) && me == 0) {
+        const float v = ll::get(ph.x + ph.k - 1, ep_x, w);
+        xs[ph.k - 1] = v;
+        ss = fmaf(v, v, ss);
+    }
     if (ph.epi == EPI_RESIDUAL)
-        for (int r = g.r0 + tid; r < g.r1; r += NT) res[r - g.r0] = ll::get(ph.y + r, ep_res, w);
-    if (!ll::all_ok(w)) return false;
-    if (ph.pro == PRO_RMS) {
-        float ss = 0.0f;
-        for (int j = tid; j < ph.k; j += NT) ss = fmaf(xs[j], xs[j], ss);
-        ss = block_sum(ss, red);
-        const float scale = 1.0f / sqrtf(ss / (float)ph.k + ph.eps);
-        __syncthreads();
-        for (int j = tid; j < ph.k; j += NT) xs[j] = xs[j] * scale * (ph.gain ? gmem(ph.gain)[j] : 1.0f);
-        __syncthreads();
-    }
-    return true;
+        for (int r = g.r0 + me; r < g.r1; r += lanes) res[r - g.r0] = ll::get(ph.y + r, ep_res, w);
+    ss = wave_sum(ss);
+    if ((me & 63) == 0) red[me >> 6] = ss;
 }
 
 template <int DT, int M, bool HEAD>
 __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
-                                           unsigned ep_y, float *lds, unsigned long long *tr) {
+                                           unsigned ep_y, float *xs, unsigned long long *tr) {
     const GemvGeo g = gemv_geo<M>(ph);
-    u32x4 buf[kDepth][kVC];
-    Cursor is{0, 0, 0};
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        issue<M>(buf[d], is, ph, g, s.dummy);
-        advance<M>(is, g.cpr);
-    }
-    float *xs = lds;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool ctl = wave < NC;
     float *res = xs + ((ph.k + 3) & ~3);
     float *red = res + ((g.r1 - g.r0 + 3) & ~3);
-    if (g.r0 < g.r1 && !stage_input(ph, g, s, ep_x, ep_res, xs, res, red)) return false;
+    float *outs = red + ((NC + 3) & ~3);
+    const bool mine = g.r0 < g.r1;
+    constexpr int DEPTH = kDepth / M;
+    const char *w0 = (const char *)ph.w, *w1 = M == 2 ? (const char *)ph.w2 : w0;
+    u32x4 buf[DEPTH][M][kVC];
+    Cursor is{0, 0};
+    ll::Wait w = ll::waiter(s.err);
+    if (ctl) {
+        if (mine) stage_input(ph, g, s, ep_x, ep_res, xs, res, red, w);
+    } else {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            issue<M>(buf[d], is, w0, w1, g, s.dummy);
+            advance(is, g.cpr);
+        }
+    }
+    if (__syncthreads_or(!w.ok)) return false;
+    if (mine && ph.pro == PRO_RMS) {   // kernels.cl:19-28
+        float ss = red[0];
+#pragma unroll
+        for (int i = 1; i < NC; ++i) ss += red[i];
+        const float scale = 1.0f / sqrtf(ss / (float)ph.k + ph.eps);
+        for (int j = tid; j < ph.k; j += NT) xs[j] = xs[j] * scale * (ph.gain ? gmem(ph.gain)[j] : 1.0f);
+        __syncthreads();
+    }
     stamp(tr, 1);
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & (g.lpr - 1), slot = lane / g.lpr;
     Best best{-INFINITY, 0x7fffffff, 0};
-    float acc[M];
+    if (!ctl) {
+        const int sub = lane & (g.lpr - 1);
+        float acc[M];
 #pragma unroll
-    for (int i = 0; i < M; ++i) acc[i] = 0.0f;
-    Cursor cs{0, 0, 0};
-    for (int t0 = 0; t0 < g.jobs; t0 += kDepth) {
+        for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+        Cursor cs{0, 0};
+        for (int t0 = 0; t0 < g.jobs; t0 += DEPTH) {
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) {
-            if (t0 + d < g.jobs) {
-                consume<DT, M>(buf[d], cs, g, xs, acc);
-                if (cs.c == g.cpr - 1 && cs.m == M - 1) {   // row group complete
-                    const float a0 = group_sum(acc[0], g.lpr);
-                    const float a1 = M == 2 ? group_sum(acc[M - 1], g.lpr) : a0;
-                    const int row = g.r0 + (wave + NW * cs.j) * g.slots + slot;
-                    if (sub == 0 && row < g.r1) {
-                        float out;
-                        if (M == 2) out = (a0 / (1.0f + expf(-a0))) * a1;   // SwiGLU (kernels.cl:46-50)
-                        else if (ph.epi == EPI_RESIDUAL) out = res[row - g.r0] + ph.scale * a0;
-                        else out = a0;
-                        if (HEAD) {
-                            gmem(ph.logits)[row] = out;
-                            if (!isfinite(out)) best.bad = 1;
-                            best_merge(best, out, row);
-                        } else {
-                            ll::put(ph.y + row, out, ep_y);
+            for (int d = 0; d < DEPTH; ++d) {
+                if (t0 + d < g.jobs) {
+                    consume<DT, M>(buf[d], cs, g, xs, acc);
+                    if (cs.c == g.cpr - 1) {   // row group complete
+                        const float a0 = group_sum(acc[0], g.lpr);
+                        const float a1 = M == 2 ? group_sum(acc[M - 1], g.lpr) : a0;
+                        const int row = job_row(g, cs.j);
+                        if (sub == 0 && row < g.r1) {
+                            float out;
+                            if (M == 2) out = (a0 / (1.0f + expf(-a0))) * a1;   // SwiGLU (kernels.cl:46-50)
+                            else if (ph.epi == EPI_RESIDUAL) out = res[row - g.r0] + ph.scale * a0;
+                            else out = a0;
+                            if (HEAD) {
+                                gmem(ph.logits)[row] = out;
+                                if (!isfinite(out)) best.bad = 1;
+                                best_merge(best, out, row);
+                            } else {
+                                outs[row - g.r0] = out;
+                            }
                         }
-                    }
 #pragma unroll
-                    for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+                        for (int i = 0; i < M; ++i) acc[i] = 0.0f;
+                    }
+                    advance(cs, g.cpr);
                 }
-                advance<M>(cs, g.cpr);
+                issue<M>(buf[d], is, w0, w1, g, s.dummy);
+                advance(is, g.cpr);
             }
-            issue<M>(buf[d], is, ph, g, s.dummy);
-            advance<M>(is, g.cpr);
         }
+        // Output cells are stored after the loop: a store holds the wave's
+        // in-order memory counter until it is acknowledged, so stores inside
+        // the loop would stall the weight loads behind them.
+        if (!HEAD) {
+            for (int j = 0; j < g.groups; ++j) {
+                const int row = job_row(g, j);
+                if (sub == 0 && row < g.r1) ll::put(ph.y + row, outs[row - g.r0], ep_y);
+            }
+            if (lane == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
+        }
+        if (tr && tid == NC * kWave) tr[2] = wall_clock64();   // first stream wave done
     }
     if (HEAD) {   // per-workgroup greedy partial
         __shared__ float bv[NW];
@@ -285,42 +331,44 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
             bb[wave] = best.bad;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            Best w{bv[0], bi[0], bb[0]};
+        if (tid == 0) {
+            Best r{bv[0], bi[0], bb[0]};
             for (int i = 1; i < NW; ++i) {
-                w.bad |= bb[i];
-                best_merge(w, bv[i], bi[i]);
+                r.bad |= bb[i];
+                best_merge(r, bv[i], bi[i]);
             }
-            stc(s.best_val + blockIdx.x, w.v);
-            stci(s.best_idx + blockIdx.x, w.i);
-            stci(s.bad + blockIdx.x, w.bad);
+            stc(s.best_val + blockIdx.x, r.v);
+            stci(s.best_idx + blockIdx.x, r.i);
+            stci(s.bad + blockIdx.x, r.bad);
         }
     }
-    __syncthreads();   // LDS is reused by the next phase
     return true;
 }
 
 template <bool HEAD>
 __device__ __forceinline__ bool gemv_dispatch(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
-                                              unsigned ep_y, float *lds, unsigned long long *tr) {
+                                              unsigned ep_y, float *xs, unsigned long long *tr) {
     const int dt = ph.dtype;
     if (!HEAD && ph.epi == EPI_SWIGLU) {
-        if (dt == MR_BF16) return gemv_phase<MR_BF16, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
-        if (dt == MR_F32) return gemv_phase<MR_F32, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
-        return gemv_phase<MR_F16, 2, false>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+        if (dt == MR_BF16) return gemv_phase<MR_BF16, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+        if (dt == MR_F32) return gemv_phase<MR_F32, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+        return gemv_phase<MR_F16, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
     }
-    if (dt == MR_BF16) return gemv_phase<MR_BF16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
-    if (dt == MR_F32) return gemv_phase<MR_F32, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
-    return gemv_phase<MR_F16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, lds, tr);
+    if (dt == MR_BF16) return gemv_phase<MR_BF16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+    if (dt == MR_F32) return gemv_phase<MR_F32, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+    return gemv_phase<MR_F16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
 }
 
 // ------------------------------------------------------------------ other phases
+// Embedding row of the position's token (stream waves), as cells.
 __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_y) {
+    const int wave = threadIdx.x >> 6;
+    if (wave < NC) return;
     const int h = ph.n;
     const int rpw = (h + gridDim.x - 1) / gridDim.x;
     const int j0 = blockIdx.x * rpw, j1 = min(j0 + rpw, h);
     const int tok = gmem(s.ids)[pos];
-    for (int j = j0 + threadIdx.x; j < j1; j += NT) {
+    for (int j = j0 + (int)threadIdx.x - NC * kWave; j < j1; j += NS * kWave) {
         const int64_t i = (int64_t)tok * h + j;
         float v;
         if (s.embed_dtype == MR_F32) v = gmem((const float *)s.embed)[i];
@@ -328,18 +376,22 @@ __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, 
         else v = f16_to_f32(gmem((const uint16_t *)s.embed)[i]);
         ll::put(ph.y + j, v, ep_y);
     }
+    if ((threadIdx.x & 63) == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
 }
 
 // Attention units (kv head, split) dealt round-robin to the workgroups; the
-// last unit of a head to finish merges the head's splits (kernels.cl:58-107).
+// last unit of a head to finish merges the head's splits (kernels.cl:58-107)
+// and reports the head in its progress word.
 template <int D>
 __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
                                            unsigned ep_out, float *lds) {
     __shared__ int last;
     const AttnStepArgs &a = ph.at.s;
-    const Geo g = geometry(ph.at, pos);
-    const Io io{ep_in, ep_out, s.err};
     const int splits = a.splits, units = a.kv_heads * splits;
+    if ((int)blockIdx.x >= units) return true;
+    __syncthreads();   // the previous phase's readers of this LDS are done
+    const Geo g = geometry(ph.at, pos);
+    const Io io{ep_in, ep_out, s.err, s.progress, s.nprogress};
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const int kh = u / splits;
         if (!attn_unit<D, true, NT>(ph.at, g, kh, u % splits, lds, io)) return false;
@@ -353,8 +405,11 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
             int t0, t1, split_len;
             split_range<D>(g, splits, 0, &t0, &t1, &split_len);
             combine<D, true, NT>(a, kh, (g.total + split_len - 1) / split_len, lds, io);
-            if (threadIdx.x == 0)
+            __syncthreads();
+            if (threadIdx.x == 0) {
                 __hip_atomic_store(gmem(ph.merge + kh), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ll::mark(ph.heads_done + kh, ep_out);
+            }
         }
         __syncthreads();
     }
@@ -367,20 +422,28 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
     if (ldci(s.done) || ldci(s.err)) return;
     const int pos = *s.pos;
     const MR_CONST Phase *prog = (const MR_CONST Phase *)s.phases;
+    int gemvs = 0;   // GEMV phases so far: their inputs alternate between two LDS buffers
     for (int p = 0; p < s.nphases; ++p) {
         const Phase &ph = *(const Phase *)(prog + p);
         unsigned long long *tr = s.trace ? s.trace + ((size_t)p * gridDim.x + blockIdx.x) * 3 : nullptr;
         stamp(tr, 0);
         const unsigned ep_y = epoch(s, pos, p);
         const unsigned ep_x = epoch(s, pos, ph.x_phase), ep_res = epoch(s, pos, ph.res_phase);
+        float *xs = lds + (gemvs & 1) * s.xbuf;
         bool ok = true;
         switch (ph.kind) {
             case PH_EMBED:
                 embed_phase(ph, s, pos, ep_y);
                 stamp(tr, 1);
                 break;
-            case PH_GEMV: ok = gemv_dispatch<false>(ph, s, ep_x, ep_res, ep_y, lds, tr); break;
-            case PH_HEAD: ok = gemv_dispatch<true>(ph, s, ep_x, ep_res, ep_y, lds, tr); break;
+            case PH_GEMV:
+                ok = gemv_dispatch<false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+                ++gemvs;
+                break;
+            case PH_HEAD:
+                ok = gemv_dispatch<true>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+                ++gemvs;
+                break;
             case PH_ATTN:
                 stamp(tr, 1);
                 if (ph.at.s.dim == 128) ok = attn_phase<128>(ph, s, pos, ep_x, ep_y, lds);
@@ -389,7 +452,7 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
                 break;
         }
         if (!ok) return;
-        stamp(tr, 2);
+        if (ph.kind != PH_GEMV && ph.kind != PH_HEAD) stamp(tr, 2);
     }
     // The last workgroup to leave finishes the step: greedy choice, EOS, position.
     __builtin_amdgcn_s_waitcnt(0);
@@ -421,23 +484,28 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
 
 }  // namespace
 
-size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
-    size_t need = 0;
-    for (const Phase &ph : program) {
-        size_t f = 0;
+int step_xbuf_floats(const std::vector<Phase> &program, int grid) {
+    int need = 0;
+    for (const Phase &ph : program)
         if (ph.kind == PH_GEMV || ph.kind == PH_HEAD) {
             const int rpw = (ph.n + grid - 1) / grid;
-            f = ((ph.k + 3) & ~3) + ((rpw + 3) & ~3) + NW;
+            need = std::max(need, ((ph.k + 3) & ~3) + 2 * ((rpw + 3) & ~3) + ((NC + 3) & ~3));
         }
-        if (ph.kind == PH_ATTN) {
-            const int G = ph.at.s.heads / ph.at.s.kv_heads, d = ph.at.s.dim, sp = ph.at.s.splits;
-            if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_lds_floats<128, NT>(G, sp));
-            else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_lds_floats<64, NT>(G, sp));
-            else f = std::max(unit_lds_floats<32>(G), combine_lds_floats<32, NT>(G, sp));
-        }
-        need = std::max(need, f * sizeof(float));
+    return (need + 3) & ~3;
+}
+
+size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
+    size_t need = 2 * (size_t)step_xbuf_floats(program, grid);
+    for (const Phase &ph : program) {
+        if (ph.kind != PH_ATTN) continue;
+        const int G = ph.at.s.heads / ph.at.s.kv_heads, d = ph.at.s.dim, sp = ph.at.s.splits;
+        size_t f;
+        if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_lds_floats<128, NT>(G, sp));
+        else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_lds_floats<64, NT>(G, sp));
+        else f = std::max(unit_lds_floats<32>(G), combine_lds_floats<32, NT>(G, sp));
+        need = std::max(need, f);
     }
-    return need;
+    return need * sizeof(float);
 }
 
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds) {
