@@ -11,9 +11,11 @@ the token id crosses to the host).  Default K = 511 = the decode passes of a
 512-token generation, positions 4096..4606.
 
 Prints one JSON line.  `value` is decode tokens/s with weights and KV cache
-resident in HBM.  `roofline` is for the dominant kernel (the fused
-RMSNorm + gate/up GEMV + SwiGLU, 46.1 MB of BF16 weights per launch), timed live
-with HIP events; `cpu_baseline` times the oracle (a C restatement of the
+resident in HBM.  `roofline` is for the dominant kernel, timed live with HIP
+events: in the persistent step mode the step kernel itself (one launch = one
+token, algorithmic bytes B(P) averaged over the decode positions); in the graph
+and eager modes the fused RMSNorm + gate/up GEMV + SwiGLU (46.2 MB per launch).
+`cpu_baseline` times the oracle (a C restatement of the
 reference's OpenCL kernels, FP32 weights resident, the reference's token loop)
 on this host's cores for a bounded sample.
 """
@@ -102,6 +104,9 @@ def main():
     ap.add_argument("--prefill-mode", choices=("exact", "batched"), default="exact")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-baseline budget; 0 skips it")
     ap.add_argument("--kernel-reps", type=int, default=3)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="copy 256 MiB device to device once before decoding (the reference dispatch for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--step-mode", choices=("persistent", "graph", "eager"), default="persistent",
                     help="persistent: one cooperative kernel per token step; graph: five kernels per layer "
                          "replayed from a hipGraph; eager: the same kernels launched one by one")
@@ -139,6 +144,14 @@ def main():
     prefill_s = time.perf_counter() - t0
     log(f"prefill {prompt_len / prefill_s:.1f} tok/s")
 
+    if args.traffic_probe:
+        n = 64 * 1024 * 1024
+        src, dst = backend.empty((n,)), backend.empty((n,))
+        backend.copy(src, dst)
+        backend.finish()
+        del src, dst
+        log("traffic probe: copied 268435456 bytes device to device")
+
     # Warm-up decode steps (captures the greedy step graph), then a fresh sequence.
     eng.generate_greedy(args.warmup + 1, -1)
     model.reset()
@@ -159,10 +172,17 @@ def main():
     kernels = {k: eng.time_kernel(k, args.kernel_reps) for k in ("qkv", "attention", "o", "gate_up", "down", "head")}
     if step_mode == "persistent":
         # The dominant (and only) kernel of a decode step is the step kernel.
+        # HBM traffic per launch comes from the committed rocprofv3 counter
+        # summary of this kernel and workload (FETCH_SIZE + WRITE_SIZE, scaled
+        # by a copy of known size); it is not measured in this run.
         step_ms = device_ms / args.steps
+        traffic = None
+        tf = ROOT / "profiles" / "k_step_flashnano-1.7_traffic.json"
+        if tf.exists():
+            traffic = json.loads(tf.read_text()).get("traffic_bytes")
         roof = {"kernel": "persistent decode step (24 layers + LM head + greedy choice)", "bound": "hbm",
                 "achieved": round(avg_bytes / (step_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(avg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(avg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "algorithmic_bytes": int(avg_bytes), "avg_ms": round(step_ms, 5)}
     else:
         gu_ms = kernels["gate_up"]

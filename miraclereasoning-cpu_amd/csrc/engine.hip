@@ -612,9 +612,6 @@ int setup_persistent(mr_model *m) {
     const mr_model_desc &d = m->d;
     hipDeviceProp_t p;
     MR_HIP(hipGetDeviceProperties(&p, m->ctx->device), "query device");
-    int coop = 0;
-    MR_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->ctx->device), "query device");
-    if (!coop) return MR_OK;
     m->grid = p.multiProcessorCount;
     if (m->grid < 8) return MR_OK;
     // Epochs are position * stride + phase + 1 in 32 bits.
@@ -653,6 +650,9 @@ int setup_persistent(mr_model *m) {
     m->xbuf = std::max(step_xbuf_floats(plain, m->grid), step_xbuf_floats(head, m->grid));
     m->step_lds = std::max(step_lds_bytes(plain, m->grid), step_lds_bytes(head, m->grid));
     if (m->step_lds > 64 * 1024) return MR_OK;
+    int per_cu = 0;   // every workgroup must be resident at once (one per CU)
+    MR_TRY(step_blocks_per_cu(m->step_lds, &per_cu));
+    if (per_cu < 1) return MR_OK;
     m->n_plain = (int)plain.size();
     m->n_head = (int)head.size();
     MR_TRY(device_alloc(m, plain.size() * sizeof(Phase), (void **)&m->prog_plain));

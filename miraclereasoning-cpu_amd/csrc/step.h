@@ -1,4 +1,4 @@
-// Persistent step kernel: one cooperative launch runs a whole token step as a
+// Persistent step kernel: one launch (one workgroup per CU) runs a whole token step as a
 // program of phases whose workgroups exchange activations as flag-in-data
 // cells (ll.h) instead of meeting at grid barriers.
 #pragma once
@@ -71,6 +71,7 @@ constexpr int kStreamWaves = kStepThreads / 64 - kControlWaves;
 // Floats of one GEMV input staging buffer, and the dynamic LDS of the kernel.
 int step_xbuf_floats(const std::vector<Phase> &program, int grid);
 size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
+int step_blocks_per_cu(size_t lds, int *blocks);
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds);
 
 }  // namespace mr

@@ -1,6 +1,6 @@
 // Persistent step kernel.
 //
-// One cooperative launch of one workgroup per CU runs a whole token step: the
+// One launch of one workgroup per CU runs a whole token step: the
 // host builds, once per model, a program of phases (embedding row; per layer:
 // Q/K/V GEMV, attention units with the split merge, O GEMV + residual, gate/up
 // GEMV + SwiGLU, down GEMV + residual; LM head + greedy choice) and every
@@ -287,12 +287,10 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
                             if (M == 2) out = (a0 / (1.0f + expf(-a0))) * a1;   // SwiGLU (kernels.cl:46-50)
                             else if (ph.epi == EPI_RESIDUAL) out = res[row - g.r0] + ph.scale * a0;
                             else out = a0;
+                            outs[row - g.r0] = out;
                             if (HEAD) {
-                                gmem(ph.logits)[row] = out;
                                 if (!isfinite(out)) best.bad = 1;
                                 best_merge(best, out, row);
-                            } else {
-                                outs[row - g.r0] = out;
                             }
                         }
 #pragma unroll
@@ -307,13 +305,14 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
         // Output cells are stored after the loop: a store holds the wave's
         // in-order memory counter until it is acknowledged, so stores inside
         // the loop would stall the weight loads behind them.
-        if (!HEAD) {
-            for (int j = 0; j < g.groups; ++j) {
-                const int row = job_row(g, j);
-                if (sub == 0 && row < g.r1) ll::put(ph.y + row, outs[row - g.r0], ep_y);
+        for (int j = 0; j < g.groups; ++j) {
+            const int row = job_row(g, j);
+            if (sub == 0 && row < g.r1) {
+                if (HEAD) gmem(ph.logits)[row] = outs[row - g.r0];
+                else ll::put(ph.y + row, outs[row - g.r0], ep_y);
             }
-            if (lane == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
         }
+        if (!HEAD && lane == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
         if (tr && tid == NC * kWave) tr[2] = wall_clock64();   // first stream wave done
     }
     if (HEAD) {   // per-workgroup greedy partial
@@ -508,11 +507,19 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
     return need * sizeof(float);
 }
 
+int step_blocks_per_cu(size_t lds, int *blocks) {
+    MR_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)k_step, NT, lds),
+           "query step kernel occupancy");
+    return MR_OK;
+}
+
+// A plain launch of exactly one workgroup per CU: the kernel's registers fill
+// a CU, so the dispatcher places one workgroup on every CU at once (the setup
+// checks the occupancy).  Should a workgroup not start, the others' bounded
+// waits end the step with an error rather than hanging.
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds) {
-    StepArgs copy = a;
-    void *args[] = {&copy};
-    MR_HIP(hipLaunchCooperativeKernel((const void *)k_step, dim3(grid), dim3(NT), args, (unsigned)lds, s),
-           "launch step kernel");
+    k_step<<<grid, NT, lds, s>>>(a);
+    MR_LAUNCHED("launch step kernel");
     return MR_OK;
 }
 

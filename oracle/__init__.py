@@ -13,7 +13,6 @@ Layout:
                            decode and generate
   device.py                the reference backend's method surface over the C
                            kernels (used only to write golden fixtures)
-  synth.py                 the frozen synthetic weight / prompt generator
 
 Parity pinning (which check pins which function) is listed in each module's
 docstring.
