@@ -21,7 +21,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_tiled(KernelArgs ka) {
     const int tid = threadIdx.x;
     const int kh = blockIdx.y, split = blockIdx.x;
     const Geo g = geometry(ka, ka.mode == 1 ? *a.pos : 0);
-    attn_unit<D, false>(ka, g, kh, split, lds, Io{});
+    attn_unit<D, false>(ka, g, kh, split, lds, Io{0u, 0u, nullptr, nullptr, 0});
     int *flag = (int *)(lds + unit_lds_floats<D>(a.heads / a.kv_heads) - 4);
     __threadfence();
     __syncthreads();
@@ -34,7 +34,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_tiled(KernelArgs ka) {
     int t0, t1, split_len;
     split_range<D>(g, a.splits, 0, &t0, &t1, &split_len);
     const int active = (g.total + split_len - 1) / split_len;
-    combine<D, false>(a, kh, active, lds, Io{});
+    combine<D, false>(a, kh, active, lds, Io{0u, 0u, nullptr, nullptr, 0});
     if (tid == 0) a.counters[kh] = 0u;
 }
 
@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(KernelArgs ka) {
     const int cap_len = a.split_len;   // LDS score rows sized for the plan's maximum
     float *qs = lds, *kn = qs + G * d, *vn = kn + d, *sc = vn + d;
     int *flag = (int *)(sc + G * cap_len);
-    prepare<false, kThreads>(ka, g, kh, G, d, qs, kn, vn, t0, t1, Io{});
+    prepare<false, kThreads>(ka, g, kh, G, d, qs, kn, vn, t0, t1, Io{0u, 0u, nullptr, nullptr, 0});
     const float *rk = ka.mode == 1 ? a.ring_k : ka.ring_k_ro;
     const float *rv = ka.mode == 1 ? a.ring_v : ka.ring_v_ro;
     const int newest = ka.mode == 1 ? g.length - 1 : -1;

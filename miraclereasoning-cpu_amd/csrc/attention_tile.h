@@ -92,27 +92,37 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
                                         float *vn, int t0, int t1, const Io &io) {
     const AttnStepArgs &a = ka.s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = d / 2;
+    // Loads that do not depend on this step's values go out first: the RoPE
+    // row of this position (a thread rotates pairs p = tid % half only, as
+    // NT is a multiple of half) and the Q/K norm gains of its lanes.
+    float rc = 1.0f, rsn = 0.0f, gq[2] = {1.0f, 1.0f}, gk[2] = {1.0f, 1.0f};
+    if (ka.mode == 1) {
+        const float *cs = a.rope + ((int64_t)g.pos * half + tid % half) * 2;
+        rc = gmem(cs)[0];
+        rsn = gmem(cs)[1];
+        if (a.q_gain)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                if (lane + kWave * t < d) {
+                    gq[t] = gmem(a.q_gain)[lane + kWave * t];
+                    gk[t] = gmem(a.k_gain)[lane + kWave * t];
+                }
+    }
     if constexpr (LL) {
+        // Q/K/V cells of this head (indices relative to q: the cells are one
+        // buffer), each thread polling at most a few pairs.
         ll::Wait w = ll::waiter(io.err);
-        ll::wait_words(io.ready, io.nready, io.ep_in, tid, w);
-        if (!ll::all_ok(w)) return false;
-        // Cell indices relative to q (the Q/K/V cells are one buffer).
         const uint64_t *cells = (const uint64_t *)a.q;
         const int q0 = kh * G * d;
         const int k0 = (int)((const uint64_t *)a.k_new - cells) + kh * d;
         const int v0 = (int)((const uint64_t *)a.v_new - cells) + kh * d;
-        for (int i = 2 * tid; i < G * d; i += 2 * NT) {
-            float2 v = ll::get2(cells, q0 + i, io.ep_in, w);
-            qs[i] = v.x;
-            qs[i + 1] = v.y;
-        }
-        for (int j = 2 * tid; j < 2 * d; j += 2 * NT) {
-            const bool isk = j < d;
-            const int c = isk ? j : j - d;
-            float2 v = ll::get2(cells, (isk ? k0 : v0) + c, io.ep_in, w);
-            float *dst = isk ? kn : vn;
-            dst[c] = v.x;
-            dst[c + 1] = v.y;
+        for (int i = 2 * tid; i < G * d + 2 * d; i += 2 * NT) {
+            const int src = i < G * d ? q0 + i : (i < G * d + d ? k0 + i - G * d : v0 + i - G * d - d);
+            float *dst = i < G * d ? qs + i : (i < G * d + d ? kn + i - G * d : vn + i - G * d - d);
+            const float2 v = ll::get2(cells, src, io.ep_in, w);
+            dst[0] = v.x;
+            dst[1] = v.y;
         }
         if (!ll::all_ok(w)) return false;
     } else {
@@ -131,23 +141,23 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
     if (a.q_gain) {   // per-head RMSNorm, width = dim (kernels.cl:19-28)
         for (int r = wave; r < G + 1; r += (NT / kWave)) {
             float *row = r < G ? qs + r * d : kn;
-            const float *gain = r < G ? a.q_gain : a.k_gain;
             float ss = 0.0f;
             for (int j = lane; j < d; j += kWave) ss = fmaf(row[j], row[j], ss);
             ss = wave_sum(ss);
-            float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
-            for (int j = lane; j < d; j += kWave) row[j] = row[j] * scale * gmem(gain)[j];
+            const float scale = 1.0f / sqrtf(ss / (float)d + a.eps);
+            const float *gain = r < G ? a.q_gain : a.k_gain;
+            for (int j = lane, t = 0; j < d; j += kWave, ++t)
+                row[j] = row[j] * scale * (t < 2 ? (r < G ? gq[t] : gk[t]) : gmem(gain)[j]);
         }
         __syncthreads();
     }
-    const int half = d / 2;   // RoPE at this position (kernels.cl:30-44)
-    const float *cs = a.rope + (int64_t)g.pos * half * 2;
-    for (int i = tid; i < (G + 1) * half; i += NT) {
-        int r = i / half, p = i % half;
+    for (int i = tid; i < (G + 1) * half; i += NT) {   // RoPE at this position (kernels.cl:30-44)
+        const int r = i / half, p = i % half;
         float *row = r < G ? qs + r * d : kn;
-        int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
+        const int j = a.split_half ? p : 2 * p, k = a.split_half ? p + half : 2 * p + 1;
         float u = row[j], v = row[k];
-        rope_rotate(u, v, gmem(cs)[2 * p], gmem(cs)[2 * p + 1]);
+        if (NT % half == 0) rope_rotate(u, v, rc, rsn);
+        else rope_rotate(u, v, gmem(a.rope)[((int64_t)g.pos * half + p) * 2], gmem(a.rope)[((int64_t)g.pos * half + p) * 2 + 1]);
         row[j] = u;
         row[k] = v;
     }
@@ -342,7 +352,17 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
             int gh = pg + GS * i;
             if (i < nacc && gh < G) st<LL>(part + gh * (D + 2) + 2 + pj, acc[i]);
         }
-        if (tid < G) {
+        if constexpr (LL) {
+            // (m, l) are published as cells once every wave's o stores are
+            // acknowledged, so a merger that sees them can read o.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid < G) {
+                uint64_t *ml = a.part_ml + ((int64_t)(kh * a.splits + split) * G + tid) * 2;
+                ll::put(ml, stt[tid], io.ep_out);
+                ll::put(ml + 1, stt[kMaxG + tid], io.ep_out);
+            }
+        } else if (tid < G) {
             st<LL>(part + tid * (D + 2), stt[tid]);
             st<LL>(part + tid * (D + 2) + 1, stt[kMaxG + tid]);
         }
@@ -353,8 +373,9 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
 // Merge the `active` splits of KV head kh into out[(kh*G + g)*D + j].
 // LL = true: partials come from other workgroups of the same launch and the
 // output is written as cells of epoch io.ep_out.
+// Returns false (block-uniform) when an LL wait gave up.
 template <int D, bool LL, int NT = kThreads>
-__device__ __forceinline__ void combine(const AttnStepArgs &a, int kh, int active, float *lds, const Io &io) {
+__device__ __forceinline__ bool combine(const AttnStepArgs &a, int kh, int active, float *lds, const Io &io) {
     const int tid = threadIdx.x;
     const int G = a.heads / a.kv_heads;
     const float *base = a.part + (int64_t)kh * a.splits * G * (D + 2);
@@ -362,11 +383,22 @@ __device__ __forceinline__ void combine(const AttnStepArgs &a, int kh, int activ
     float *lv = w + active * G;          // [active][G] split sums
     float *L = lv + active * G;          // [G]
     float *red = L + G;                  // [SG][G*D] partial sums
-    for (int i = tid; i < active * G; i += NT) {
-        w[i] = ld<LL>(base + (int64_t)i * (D + 2));
-        lv[i] = ld<LL>(base + (int64_t)i * (D + 2) + 1);
+    if constexpr (LL) {
+        ll::Wait wt = ll::waiter(io.err);
+        const uint64_t *ml = a.part_ml + (int64_t)kh * a.splits * G * 2;
+        for (int i = tid; i < active * G; i += NT) {
+            const float2 v = ll::get2(ml, 2 * i, io.ep_out, wt);
+            w[i] = v.x;
+            lv[i] = v.y;
+        }
+        if (!ll::all_ok(wt)) return false;
+    } else {
+        for (int i = tid; i < active * G; i += NT) {
+            w[i] = ld<LL>(base + (int64_t)i * (D + 2));
+            lv[i] = ld<LL>(base + (int64_t)i * (D + 2) + 1);
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (tid < G) {
         float M = -INFINITY;
         for (int s = 0; s < active; ++s) M = fmaxf(M, w[s * G + tid]);
@@ -407,6 +439,7 @@ __device__ __forceinline__ void combine(const AttnStepArgs &a, int kh, int activ
         if constexpr (LL) ll::put((uint64_t *)a.out + o, sum / L[gh], io.ep_out);
         else *gmem(a.out + o) = sum / L[gh];
     }
+    return true;
 }
 
 template <int D, int NT = kThreads>

@@ -162,6 +162,15 @@ __device__ __forceinline__ void rope_rotate(float &u, float &v, float c, float s
     v = nv;
 }
 
+// Workgroup barrier that orders LDS accesses only: global loads still in
+// flight (weights prefetched into registers) stay in flight across it, where
+// __syncthreads would first wait for every one of them.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Element j of a weight row of the given storage dtype, widened to FP32.
 template <int DT>
 __device__ __forceinline__ float load_w(const void *w, int64_t i) {

@@ -77,8 +77,7 @@ struct mr_model {
     mr::Phase *prog_plain = nullptr, *prog_head = nullptr;
     int n_plain = 0, n_head = 0;
     // Persistent-kernel state, cleared on reset: flag-in-data activation cells
-    // (hidden, qkv, attn, act) and the counters (per layer and KV head merge
-    // counters, then the launch exit counter), each one allocation.
+    // (hidden, qkv, attn, act) and the launch exit counter.
     uint64_t *cells = nullptr;
     size_t cell_count = 0;
     uint64_t *c_hidden = nullptr, *c_qkv = nullptr, *c_attn = nullptr, *c_act = nullptr;
@@ -88,6 +87,8 @@ struct mr_model {
     // attention heads' [layers * query_heads]
     unsigned *words = nullptr;
     size_t word_count = 0;
+    uint64_t *part_ml = nullptr;         // attention (m, l) cells
+    size_t part_ml_count = 0;
     int xbuf = 0;                        // floats of one GEMV input staging buffer
     void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end
     int *err = nullptr;                  // wait timeout flag

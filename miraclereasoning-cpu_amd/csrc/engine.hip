@@ -537,7 +537,6 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         Phase a;
         a.kind = PH_ATTN;
         a.x_phase = qkv_at;
-        a.merge = m->sync + (size_t)li * d.query_heads;   // kv_heads <= query_heads
         a.heads_done = m->words + (size_t)m->grid * kStreamWaves + (size_t)li * d.query_heads;
         AttnStepArgs &t = a.at.s;
         t.q = (const float *)m->c_qkv;
@@ -548,6 +547,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         t.ring_k = L.ring_k; t.ring_v = L.ring_v; t.capacity = L.capacity;
         t.heads = d.query_heads; t.kv_heads = L.kv_heads; t.dim = hd;
         t.part = m->part; t.out = (float *)m->c_attn; t.splits = L.splits; t.split_len = L.split_len;
+        t.part_ml = m->part_ml;
         a.at.mode = 1;
         a.at.ring_k_ro = L.ring_k; a.at.ring_v_ro = L.ring_v;
         prog.push_back(a);
@@ -630,11 +630,16 @@ int setup_persistent(mr_model *m) {
     m->c_qkv = m->c_hidden + n_hidden;
     m->c_attn = m->c_qkv + n_qkv;
     m->c_act = m->c_attn + n_attn;
-    m->sync_count = (size_t)d.layers * d.query_heads + 1;
+    m->sync_count = 1;   // the launch exit counter
     MR_TRY(device_alloc(m, m->sync_count * sizeof(unsigned), (void **)&m->sync));
     m->word_count = (size_t)m->grid * kStreamWaves + (size_t)d.layers * d.query_heads;
     MR_TRY(device_alloc(m, m->word_count * sizeof(unsigned), (void **)&m->words));
     MR_HIP(hipMemset(m->words, 0, m->word_count * sizeof(unsigned)), "clear step progress");
+    m->part_ml_count = 0;
+    for (Layer &L : m->layers)
+        m->part_ml_count = std::max(m->part_ml_count, (size_t)d.query_heads * L.splits * 2);
+    MR_TRY(device_alloc(m, m->part_ml_count * sizeof(uint64_t), (void **)&m->part_ml));
+    MR_HIP(hipMemset(m->part_ml, 0, m->part_ml_count * sizeof(uint64_t)), "clear attention cells");
     MR_TRY(device_alloc(m, 256, &m->dummy));
     MR_TRY(device_alloc(m, sizeof(int), (void **)&m->err));
     MR_TRY(device_alloc(m, m->grid * sizeof(float), (void **)&m->best_val));
@@ -732,7 +737,7 @@ int mr_model_destroy(mr_model *m) {
     if (m->freq) hipFree(m->freq);
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
-    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, m->dummy,
+    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_ml, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);
     delete m;
@@ -924,6 +929,8 @@ int mr_model_reset(mr_model *m) {
         MR_HIP(hipMemsetAsync(m->cells, 0, m->cell_count * sizeof(uint64_t), m->ctx->stream), "reset step cells");
         MR_HIP(hipMemsetAsync(m->sync, 0, m->sync_count * sizeof(unsigned), m->ctx->stream), "reset step counters");
         MR_HIP(hipMemsetAsync(m->words, 0, m->word_count * sizeof(unsigned), m->ctx->stream), "reset step progress");
+        MR_HIP(hipMemsetAsync(m->part_ml, 0, m->part_ml_count * sizeof(uint64_t), m->ctx->stream),
+               "reset attention cells");
         MR_HIP(hipMemsetAsync(m->err, 0, sizeof(int), m->ctx->stream), "reset step status");
     }
     MR_HIP(hipStreamSynchronize(m->ctx->stream), "reset");

@@ -36,7 +36,6 @@ struct Phase {
     const unsigned *ready = nullptr;
     int nready = 0;
     // PH_ATTN: at.s.q / k_new / v_new / out point at cells; x_phase = Q/K/V phase
-    unsigned *merge = nullptr;     // [kv_heads] last-arriver counters of this layer
     unsigned *heads_done = nullptr;   // [kv_heads] progress words of the merged heads
     att::Args at{};
 };

@@ -61,7 +61,7 @@ __device__ __forceinline__ void stamp(unsigned long long *tr, int i) {
 // Rows [r0, r1) of each workgroup, in groups of `slots` rows (lpr lanes per
 // row) dealt round-robin to the stream waves.  A job is kVC 16-byte vectors per
 // lane of one row group of one matrix; a stream wave keeps kDepth jobs in
-// flight (96 KB per CU in all), and issues
+// flight (64 KB per CU in all), and issues
 // its first kDepth before the phase's input is staged.  Loads past a matrix's
 // end read a 16-byte dummy so every job issues the same number of loads and
 // the compiler's waits stay exact.
@@ -72,7 +72,7 @@ __device__ __forceinline__ void stamp(unsigned long long *tr, int i) {
 constexpr int NC = kControlWaves;
 constexpr int NS = kStreamWaves;
 constexpr int kVC = 4;
-constexpr int kDepth = 6;   // jobs in flight per stream wave when a job is one matrix (M = 1)
+constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
 
 struct GemvGeo {
     int r0, r1;      // rows of this workgroup
@@ -159,27 +159,35 @@ __device__ __forceinline__ void widen16(const u32x4 &v, float *o) {
     }
 }
 
-template <int DT, int M>
-__device__ __forceinline__ void consume(const u32x4 (&b)[M][kVC], const Cursor &u, const GemvGeo &g, const float *xs,
-                                        float (&acc)[M]) {
-    constexpr int E = DT == MR_F32 ? 4 : 8;
+// The input values of chunk c for this lane, from the staged input in LDS.
+template <int E>
+__device__ __forceinline__ void load_x(float (&xr)[kVC][E], const GemvGeo &g, const float *xs, int c) {
+    const int sub = (threadIdx.x & 63) & (g.lpr - 1);
+#pragma unroll
+    for (int i = 0; i < kVC; ++i) {
+        const int v = min(sub + (c * kVC + i) * g.lpr, g.nvec - 1);
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 t = *(const float4 *)(xs + v * E + e);
+            xr[i][e] = t.x; xr[i][e + 1] = t.y; xr[i][e + 2] = t.z; xr[i][e + 3] = t.w;
+        }
+    }
+}
+
+template <int DT, int M, int E>
+__device__ __forceinline__ void consume(const u32x4 (&b)[M][kVC], const Cursor &u, const GemvGeo &g,
+                                        const float (&xr)[kVC][E], float (&acc)[M]) {
     const int sub = (threadIdx.x & 63) & (g.lpr - 1);
 #pragma unroll
     for (int i = 0; i < kVC; ++i) {
         const int v = sub + (u.c * kVC + i) * g.lpr;
         if (v < g.nvec) {
-            float xv[E];
-#pragma unroll
-            for (int e = 0; e < E; e += 4) {
-                const float4 t = *(const float4 *)(xs + v * E + e);
-                xv[e] = t.x; xv[e + 1] = t.y; xv[e + 2] = t.z; xv[e + 3] = t.w;
-            }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 float wf[E];
                 widen16<DT>(b[m][i], wf);
 #pragma unroll
-                for (int e = 0; e < E; ++e) acc[m] = fmaf(wf[e], xv[e], acc[m]);
+                for (int e = 0; e < E; ++e) acc[m] = fmaf(wf[e], xr[i][e], acc[m]);
             }
         }
     }
@@ -200,8 +208,10 @@ __device__ __forceinline__ void best_merge(Best &a, float v, int i) {
 }
 
 // Control waves: wait for the producers of the input (epoch ep_x), read it into
-// xs with its sum of squares per wave in red[], and read the residual inputs
-// of this workgroup's rows (epoch ep_res) into res[].
+// xs, and read the residual inputs of this workgroup's rows (epoch ep_res) into
+// res.  With the RMSNorm prologue (kernels.cl:19-28) xs holds input x gain and
+// red[wave] the wave's sum of squares of the raw input: the 1/rms scale is
+// applied to the dot products, y = scale * W (x * gain).
 __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, const StepArgs &s, unsigned ep_x,
                                             unsigned ep_res, float *xs, float *res, float *red, ll::Wait &w) {
     const int me = threadIdx.x, lanes = NC * kWave;
@@ -219,10 +229,43 @@ __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, c
             __builtin_amdgcn_s_sleep(1);
         if (r == ~0u) w.ok = false;
     }
-    float ss = ll::read_pairs<12>(ph.x, ph.k / 2, ep_x, xs, me, lanes, w);
+    const float *gain = ph.pro == PRO_RMS ? ph.gain : nullptr;
+    const int n2 = ph.k / 2;
+    float ss = 0.0f;
+    constexpr int B = 8;
+    for (int base = me; base < n2; base += lanes * B) {
+        float2 gv[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int gi = 2 * min(base + i * lanes, n2 - 1);
+            gv[i] = gain ? make_float2(gmem(gain)[gi], gmem(gain)[gi + 1]) : make_float2(1.0f, 1.0f);
+        }
+        ll::u64x2 c[B];
+        bool ready;
+        do {
+#pragma unroll
+            for (int i = 0; i < B; ++i) c[i] = ll::peek2(ph.x, 2 * min(base + i * lanes, n2 - 1));
+            ready = true;
+#pragma unroll
+            for (int i = 0; i < B; ++i)
+                ready &= base + i * lanes >= n2 ||
+                         ((unsigned)(c[i].x >> 32) == ep_x && (unsigned)(c[i].y >> 32) == ep_x);
+        } while (!ready && ll::backoff(w));
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int idx = base + i * lanes;
+            if (idx < n2) {
+                const float a = __uint_as_float((unsigned)c[i].x), b = __uint_as_float((unsigned)c[i].y);
+                ss = fmaf(a, a, ss);
+                ss = fmaf(b, b, ss);
+                xs[2 * idx] = a * gv[i].x;
+                xs[2 * idx + 1] = b * gv[i].y;
+            }
+        }
+    }
     if ((ph.k & 1) && me == 0) {
         const float v = ll::get(ph.x + ph.k - 1, ep_x, w);
-        xs[ph.k - 1] = v;
+        xs[ph.k - 1] = v * (gain ? gmem(gain)[ph.k - 1] : 1.0f);
         ss = fmaf(v, v, ss);
     }
     if (ph.epi == EPI_RESIDUAL)
@@ -234,6 +277,8 @@ __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, c
 template <int DT, int M, bool HEAD>
 __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
                                            unsigned ep_y, float *xs, unsigned long long *tr) {
+    constexpr int E = DT == MR_F32 ? 4 : 8;
+    __shared__ unsigned status[NC];   // per control wave: ep_x, or ~0 when a wait gave up
     const GemvGeo g = gemv_geo<M>(ph);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool ctl = wave < NC;
@@ -245,9 +290,11 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
     const char *w0 = (const char *)ph.w, *w1 = M == 2 ? (const char *)ph.w2 : w0;
     u32x4 buf[DEPTH][M][kVC];
     Cursor is{0, 0};
-    ll::Wait w = ll::waiter(s.err);
     if (ctl) {
+        ll::Wait w = ll::waiter(s.err);
         if (mine) stage_input(ph, g, s, ep_x, ep_res, xs, res, red, w);
+        const bool ok = __all(w.ok);
+        if (lane == 0) status[wave] = ok ? ep_x : ~0u;
     } else {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
@@ -255,20 +302,24 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
             advance(is, g.cpr);
         }
     }
-    if (__syncthreads_or(!w.ok)) return false;
-    if (mine && ph.pro == PRO_RMS) {   // kernels.cl:19-28
+    lds_barrier();   // the weights stay in flight
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+        if (status[i] == ~0u) return false;
+    float scale = 1.0f;
+    if (mine && ph.pro == PRO_RMS) {
         float ss = red[0];
 #pragma unroll
         for (int i = 1; i < NC; ++i) ss += red[i];
-        const float scale = 1.0f / sqrtf(ss / (float)ph.k + ph.eps);
-        for (int j = tid; j < ph.k; j += NT) xs[j] = xs[j] * scale * (ph.gain ? gmem(ph.gain)[j] : 1.0f);
-        __syncthreads();
+        scale = 1.0f / sqrtf(ss / (float)ph.k + ph.eps);
     }
     stamp(tr, 1);
 
     Best best{-INFINITY, 0x7fffffff, 0};
     if (!ctl) {
         const int sub = lane & (g.lpr - 1);
+        float xr[kVC][E];
+        if (g.cpr == 1) load_x<E>(xr, g, xs, 0);   // one chunk per row: the lane's inputs stay in registers
         float acc[M];
 #pragma unroll
         for (int i = 0; i < M; ++i) acc[i] = 0.0f;
@@ -277,10 +328,11 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
                 if (t0 + d < g.jobs) {
-                    consume<DT, M>(buf[d], cs, g, xs, acc);
+                    if (g.cpr != 1) load_x<E>(xr, g, xs, cs.c);
+                    consume<DT, M, E>(buf[d], cs, g, xr, acc);
                     if (cs.c == g.cpr - 1) {   // row group complete
-                        const float a0 = group_sum(acc[0], g.lpr);
-                        const float a1 = M == 2 ? group_sum(acc[M - 1], g.lpr) : a0;
+                        const float a0 = scale * group_sum(acc[0], g.lpr);
+                        const float a1 = M == 2 ? scale * group_sum(acc[M - 1], g.lpr) : a0;
                         const int row = job_row(g, cs.j);
                         if (sub == 0 && row < g.r1) {
                             float out;
@@ -378,39 +430,32 @@ __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, 
     if ((threadIdx.x & 63) == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
 }
 
-// Attention units (kv head, split) dealt round-robin to the workgroups; the
-// last unit of a head to finish merges the head's splits (kernels.cl:58-107)
-// and reports the head in its progress word.
+// Attention units (kv head, split) dealt round-robin to the workgroups write
+// their partials; then the workgroup that held split 0 of a head merges the
+// head's splits (kernels.cl:58-107) and reports it in the head's progress
+// word.  Every unit runs before any merge waits, so a merge never waits on a
+// unit queued behind another merge.
 template <int D>
 __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
                                            unsigned ep_out, float *lds) {
-    __shared__ int last;
     const AttnStepArgs &a = ph.at.s;
     const int splits = a.splits, units = a.kv_heads * splits;
     if ((int)blockIdx.x >= units) return true;
     __syncthreads();   // the previous phase's readers of this LDS are done
     const Geo g = geometry(ph.at, pos);
-    const Io io{ep_in, ep_out, s.err, s.progress, s.nprogress};
+    const Io io{ep_in, ep_out, s.err, nullptr, 0};
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
-        const int kh = u / splits;
-        if (!attn_unit<D, true, NT>(ph.at, g, kh, u % splits, lds, io)) return false;
-        __builtin_amdgcn_s_waitcnt(0);   // this wave's partial stores have reached the coherence point
+        if (!attn_unit<D, true, NT>(ph.at, g, u / splits, u % splits, lds, io)) return false;
         __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(gmem(ph.merge + kh), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (unsigned)(splits - 1);
+    }
+    int t0, t1, split_len;
+    split_range<D>(g, splits, 0, &t0, &t1, &split_len);
+    const int active = (g.total + split_len - 1) / split_len;
+    for (int kh = 0; kh < a.kv_heads; ++kh) {
+        if ((kh * splits) % (int)gridDim.x != (int)blockIdx.x) continue;
+        if (!combine<D, true, NT>(a, kh, active, lds, io)) return false;
         __syncthreads();
-        if (last) {
-            int t0, t1, split_len;
-            split_range<D>(g, splits, 0, &t0, &t1, &split_len);
-            combine<D, true, NT>(a, kh, (g.total + split_len - 1) / split_len, lds, io);
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                __hip_atomic_store(gmem(ph.merge + kh), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ll::mark(ph.heads_done + kh, ep_out);
-            }
-        }
-        __syncthreads();
+        if (threadIdx.x == 0) ll::mark(ph.heads_done + kh, ep_out);
     }
     return true;
 }
