@@ -43,10 +43,10 @@ struct AttnStepArgs {
     int splits = 0, split_len = 0;
 };
 
-// Split geometry for at most `max_total` keys with kv_heads heads of `dim`.
-// The kernel divides the current key count over `splits`; `split_len` is the
-// upper bound of keys per split.
-void attention_plan(int max_total, int kv_heads, int dim, int *splits, int *split_len);
+// Split geometry for at most `max_total` keys with kv_heads heads of `dim`, at
+// most `max_units` (kv head, split) units.  The kernel divides the current key
+// count over `splits`; `split_len` is the upper bound of keys per split.
+void attention_plan(int max_total, int kv_heads, int dim, int max_units, int *splits, int *split_len);
 size_t attention_part_floats(int heads, int kv_heads, int dim, int splits);
 int launch_attention_step(hipStream_t s, const AttnStepArgs &a);
 

@@ -154,10 +154,10 @@ int launch(hipStream_t s, const KernelArgs &ka) {
 
 }  // namespace
 
-void attention_plan(int max_total, int kv_heads, int dim, int *splits, int *split_len) {
-    // One tile of keys per split at the full window, at most ~512 workgroups.
+void attention_plan(int max_total, int kv_heads, int dim, int max_units, int *splits, int *split_len) {
+    // One tile of keys per split at the full window, at most max_units units.
     const int T = tiled_dim(dim) ? kTileFloats / dim : 64;
-    int want = std::max(1, 512 / std::max(kv_heads, 1));
+    int want = std::max(1, max_units / std::max(kv_heads, 1));
     int n = std::max(1, std::min(want, ceil_div(max_total, T)));
     *splits = n;
     *split_len = ceil_div(max_total, n);   // upper bound of the per-split key count
@@ -189,7 +189,7 @@ int launch_attention_op(mr_ctx *ctx, const AttnProblem &p) {
     a.dim = p.dim;
     a.capacity = p.capacity;
     a.out = p.out;
-    attention_plan(total, p.kv_heads, p.dim, &a.splits, &a.split_len);
+    attention_plan(total, p.kv_heads, p.dim, 512, &a.splits, &a.split_len);
     ka.mode = 0;
     ka.start = p.start;
     ka.length = p.length;

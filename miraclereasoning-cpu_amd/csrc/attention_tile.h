@@ -12,7 +12,8 @@
 // Keys and values stream through LDS in 16 KB tiles (4096 floats = 4096/dim
 // keys), each thread loading 4 float4 of K and 4 of V per tile, coalesced along
 // the row; the next tile is prefetched into registers while the current one is
-// consumed.  LL = true is the persistent kernel's mode: q/k/v arrive as
+// consumed (the tile loop's barriers order LDS only, so the prefetch stays in
+// flight across them).  LL = true is the persistent kernel's mode: q/k/v arrive as
 // flag-in-data cells (ll.h) of this step, the partials are exchanged between
 // workgroups with agent-coherent accesses, and the merged output is written as
 // cells.
@@ -281,7 +282,7 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
     for (int c0 = t0; c0 < t1; c0 += T) {
         const int n = min(T, t1 - c0);
         stash(c0);
-        __syncthreads();
+        lds_barrier();
         if (c0 + T < t1) fetch(c0 + T);   // in flight while this tile is consumed
         {   // scores: LPK lanes per key
             const int sub = lane % LPK, ks = lane / LPK;
@@ -307,7 +308,7 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
         // Online softmax statistics per head (one wave per head).
         for (int gh = wave; gh < G; gh += NWV) {
             float mx = -INFINITY;
@@ -329,7 +330,7 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
                 stt[2 * kMaxG + gh] = alpha;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // Weighted values.
 #pragma unroll
         for (int i = 0; i < NACC; ++i) {
@@ -341,7 +342,7 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
                 acc[i] = v;
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // Partial (m, l, o) of this split.

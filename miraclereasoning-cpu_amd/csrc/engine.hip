@@ -812,6 +812,8 @@ int mr_model_finalize(mr_model *m) {
     if (m->finalized) return MR_OK;
     MR_HIP(hipSetDevice(m->ctx->device), "select device");
     const mr_model_desc &d = m->d;
+    int cus = 0;   // attention units per layer: at most one per CU
+    MR_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device), "query device");
     auto need = [&](const Weight &w, const char *name, int layer) -> int {
         if (!w.ptr)
             return fail(MR_ERR_STATE, std::string("missing weight ") + name +
@@ -863,7 +865,7 @@ int mr_model_finalize(mr_model *m) {
                                                                 d.cbr_norm_eps);
             MR_LAUNCHED("normalize cbr queries");
         }
-        attention_plan(L.capacity + extra_max, L.kv_heads, hd, &L.splits, &L.split_len);
+        attention_plan(L.capacity + extra_max, L.kv_heads, hd, cus, &L.splits, &L.split_len);
         max_part = std::max(max_part, attention_part_floats(d.query_heads, L.kv_heads, hd, L.splits));
     }
     // One allocation for all per-sequence scalars and activation vectors.
