@@ -37,7 +37,7 @@ struct AttnStepArgs {
     int extra_chunk = 0, extra_slots = 0;  // extra rows = (pos / chunk) * slots
     int heads = 0, kv_heads = 0, dim = 0;
     float *part = nullptr;             // [kv_heads, splits, G, dim + 2]
-    uint64_t *part_ml = nullptr;       // persistent kernel: (m, l) cells [kv_heads, splits, G, 2]
+    uint64_t *part_cells = nullptr;    // persistent kernel: the partials as cells [kv_heads, splits, G, dim + 2]
     unsigned *counters = nullptr;      // [kv_heads], zero between launches
     float *out = nullptr;              // [heads*dim]
     int splits = 0, split_len = 0;

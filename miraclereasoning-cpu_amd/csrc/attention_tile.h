@@ -338,6 +338,7 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
             if (i < nacc && gh < G) {
                 float v = acc[i] * stt[2 * kMaxG + gh];
                 const float *p = sc + gh * T;
+#pragma unroll 8
                 for (int r = 0; r < n; ++r) v = fmaf(p[r], Vs[r * D + pj], v);
                 acc[i] = v;
             }
@@ -345,7 +346,23 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
         lds_barrier();
     }
 
-    // Partial (m, l, o) of this split.
+    // Partial (m, l, o) of this split; in LL mode as cells of this phase's
+    // epoch (a merger reads them without any ordering between the stores).
+    if constexpr (LL) {
+        if (t0 < t1) {
+            uint64_t *part = a.part_cells + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
+#pragma unroll
+            for (int i = 0; i < NACC; ++i) {
+                int gh = pg + GS * i;
+                if (i < nacc && gh < G) ll::put(part + gh * (D + 2) + 2 + pj, acc[i], io.ep_out);
+            }
+            if (tid < G) {
+                ll::put(part + tid * (D + 2), stt[tid], io.ep_out);
+                ll::put(part + tid * (D + 2) + 1, stt[kMaxG + tid], io.ep_out);
+            }
+        }
+        return true;
+    }
     float *part = a.part + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
     if (t0 < t1) {
 #pragma unroll
@@ -353,22 +370,34 @@ __device__ __forceinline__ bool attn_unit(const Args &ka, const Geo &g, int kh, 
             int gh = pg + GS * i;
             if (i < nacc && gh < G) st<LL>(part + gh * (D + 2) + 2 + pj, acc[i]);
         }
-        if constexpr (LL) {
-            // (m, l) are published as cells once every wave's o stores are
-            // acknowledged, so a merger that sees them can read o.
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid < G) {
-                uint64_t *ml = a.part_ml + ((int64_t)(kh * a.splits + split) * G + tid) * 2;
-                ll::put(ml, stt[tid], io.ep_out);
-                ll::put(ml + 1, stt[kMaxG + tid], io.ep_out);
-            }
-        } else if (tid < G) {
+        if (tid < G) {
             st<LL>(part + tid * (D + 2), stt[tid]);
             st<LL>(part + tid * (D + 2) + 1, stt[kMaxG + tid]);
         }
     }
     return true;
+}
+
+// Split weights of a merge, one wave per head: M = max_s m_s, then
+// w_s = e^(m_s - M) (0 for a split without keys) and L = sum_s w_s l_s.
+template <int NT>
+__device__ __forceinline__ void merge_weights(float *w, const float *lv, float *L, int G, int active) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int gh = wave; gh < G; gh += NT / kWave) {
+        float mx = -INFINITY;
+        for (int s = lane; s < active; s += kWave) mx = fmaxf(mx, w[s * G + gh]);
+        const float M = wave_max(mx);
+        float sum = 0.0f;
+        for (int s = lane; s < active; s += kWave) {
+            const float l = lv[s * G + gh];
+            const float e = l == 0.0f ? 0.0f : expf(w[s * G + gh] - M);
+            w[s * G + gh] = e;
+            sum = fmaf(e, l, sum);
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) L[gh] = sum;
+    }
+    __syncthreads();
 }
 
 // Merge the `active` splits of KV head kh into out[(kh*G + g)*D + j].
@@ -384,35 +413,12 @@ __device__ __forceinline__ bool combine(const AttnStepArgs &a, int kh, int activ
     float *lv = w + active * G;          // [active][G] split sums
     float *L = lv + active * G;          // [G]
     float *red = L + G;                  // [SG][G*D] partial sums
-    if constexpr (LL) {
-        ll::Wait wt = ll::waiter(io.err);
-        const uint64_t *ml = a.part_ml + (int64_t)kh * a.splits * G * 2;
-        for (int i = tid; i < active * G; i += NT) {
-            const float2 v = ll::get2(ml, 2 * i, io.ep_out, wt);
-            w[i] = v.x;
-            lv[i] = v.y;
-        }
-        if (!ll::all_ok(wt)) return false;
-    } else {
-        for (int i = tid; i < active * G; i += NT) {
-            w[i] = ld<LL>(base + (int64_t)i * (D + 2));
-            lv[i] = ld<LL>(base + (int64_t)i * (D + 2) + 1);
-        }
-        __syncthreads();
-    }
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s = 0; s < active; ++s) M = fmaxf(M, w[s * G + tid]);
-        float sum = 0.0f;
-        for (int s = 0; s < active; ++s) {
-            float l = lv[s * G + tid];
-            float e = l == 0.0f ? 0.0f : expf(w[s * G + tid] - M);
-            w[s * G + tid] = e;
-            sum = fmaf(e, l, sum);
-        }
-        L[tid] = sum;
+    for (int i = tid; i < active * G; i += NT) {
+        w[i] = ld<LL>(base + (int64_t)i * (D + 2));
+        lv[i] = ld<LL>(base + (int64_t)i * (D + 2) + 1);
     }
     __syncthreads();
+    merge_weights<NT>(w, lv, L, G, active);
     // Thread (sg, j4): float4 column j4 of every head over splits sg, sg+SG, ...
     constexpr int C4 = D / 4;
     constexpr int SG = NT / C4;
@@ -422,7 +428,7 @@ __device__ __forceinline__ bool combine(const AttnStepArgs &a, int kh, int activ
 #pragma unroll 8
         for (int s = sg; s < active; s += SG) {
             const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
-            const float4 o = LL ? load_f4_coherent(base, off) : load_f4(base + off);
+            const float4 o = load_f4(base + off);
             const float e = w[s * G + gh];
             acc.x = fmaf(e, o.x, acc.x);
             acc.y = fmaf(e, o.y, acc.y);
@@ -446,6 +452,111 @@ __device__ __forceinline__ bool combine(const AttnStepArgs &a, int kh, int activ
 template <int D, int NT = kThreads>
 __host__ __device__ constexpr int combine_lds_floats(int G, int splits) {
     return 2 * splits * G + G + (NT / (D / 4)) * G * D;
+}
+
+// The persistent kernel's merge: the partials of the `active` splits of KV
+// head kh are cells of epoch io.ep_out.  Thread (gh, j4, sg) sums float4
+// column j4 of head gh over splits sg, sg + SG, ...; each thread issues its
+// o cells (up to kChunk float4 per round) together with one (m, l) pair and
+// polls until all carry the epoch, so a merge that starts after its splits
+// finished costs one round trip.  Writes out[(kh*G + g)*D + j] as cells.
+// Returns false (block-uniform) when a wait gave up.
+template <int D, int NT>
+__device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int active, float *lds, const Io &io) {
+    constexpr int C4 = D / 4;
+    constexpr int kChunk = 8;
+    const int tid = threadIdx.x;
+    const int G = a.heads / a.kv_heads;
+    const uint64_t *base = a.part_cells + (int64_t)kh * a.splits * G * (D + 2);
+    const int SG = max(1, NT / (G * C4));               // split groups per (gh, j4)
+    const bool owner = tid < G * C4 * SG;
+    const int gh = owner ? tid / (C4 * SG) : 0, j4 = tid % C4, sg = owner ? (tid / C4) % SG : 0;
+    float *w = lds;                      // [active][G] split maxima, then weights e^(m_s - M)
+    float *lv = w + active * G;          // [active][G] split sums
+    float *L = lv + active * G;          // [G]
+    float *red = L + G;                  // [SG][G*D] partial sums
+    ll::Wait wt = ll::waiter(io.err);
+    ll::u64x2 c[kChunk][2];
+    // Round 1: the first chunk of o and this thread's (m, l) pair.
+    {
+        const int i = tid < active * G ? tid : 0;
+        ll::u64x2 ml;
+        bool ready;
+        do {
+#pragma unroll
+            for (int q = 0; q < kChunk; ++q) {
+                const int s = min(sg + q * SG, active - 1);
+                const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
+                c[q][0] = ll::peek2(base, off);
+                c[q][1] = ll::peek2(base, off + 2);
+            }
+            ml = ll::peek2(base, i * (D + 2));
+            ready = (unsigned)(ml.x >> 32) == io.ep_out && (unsigned)(ml.y >> 32) == io.ep_out;
+#pragma unroll
+            for (int q = 0; q < kChunk; ++q)
+                ready &= !owner || sg + q * SG >= active ||
+                         ((unsigned)(c[q][0].x >> 32) == io.ep_out && (unsigned)(c[q][0].y >> 32) == io.ep_out &&
+                          (unsigned)(c[q][1].x >> 32) == io.ep_out && (unsigned)(c[q][1].y >> 32) == io.ep_out);
+        } while (!ready && ll::backoff(wt));
+        if (tid < active * G) {
+            w[tid] = __uint_as_float((unsigned)ml.x);
+            lv[tid] = __uint_as_float((unsigned)ml.y);
+        }
+    }
+    for (int i = tid + NT; i < active * G; i += NT) {   // more (m, l) pairs than threads
+        const float2 v = ll::get2(base, i * (D + 2), io.ep_out, wt);
+        w[i] = v.x;
+        lv[i] = v.y;
+    }
+    if (!ll::all_ok(wt)) return false;
+    merge_weights<NT>(w, lv, L, G, active);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < active; s0 += kChunk * SG) {
+        if (s0 > 0) {   // further chunks (more than kChunk splits per thread)
+            bool ready;
+            do {
+#pragma unroll
+                for (int q = 0; q < kChunk; ++q) {
+                    const int s = min(s0 + sg + q * SG, active - 1);
+                    const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
+                    c[q][0] = ll::peek2(base, off);
+                    c[q][1] = ll::peek2(base, off + 2);
+                }
+                ready = true;
+#pragma unroll
+                for (int q = 0; q < kChunk; ++q)
+                    ready &= !owner || s0 + sg + q * SG >= active ||
+                             ((unsigned)(c[q][0].x >> 32) == io.ep_out && (unsigned)(c[q][0].y >> 32) == io.ep_out &&
+                              (unsigned)(c[q][1].x >> 32) == io.ep_out && (unsigned)(c[q][1].y >> 32) == io.ep_out);
+            } while (!ready && ll::backoff(wt));
+        }
+#pragma unroll
+        for (int q = 0; q < kChunk; ++q) {
+            const int s = s0 + sg + q * SG;
+            if (owner && s < active) {
+                const float e = w[s * G + gh];
+                acc.x = fmaf(e, __uint_as_float((unsigned)c[q][0].x), acc.x);
+                acc.y = fmaf(e, __uint_as_float((unsigned)c[q][0].y), acc.y);
+                acc.z = fmaf(e, __uint_as_float((unsigned)c[q][1].x), acc.z);
+                acc.w = fmaf(e, __uint_as_float((unsigned)c[q][1].y), acc.w);
+            }
+        }
+    }
+    if (!ll::all_ok(wt)) return false;
+    if (owner) *(float4 *)(red + (sg * G + gh) * D + 4 * j4) = acc;
+    __syncthreads();
+    for (int i = tid; i < G * D; i += NT) {
+        const int h = i / D, j = i % D;
+        float sum = 0.0f;
+        for (int q = 0; q < SG; ++q) sum += red[(q * G + h) * D + j];
+        ll::put((uint64_t *)a.out + (int64_t)(kh * G + h) * D + j, sum / L[h], io.ep_out);
+    }
+    return true;
+}
+
+template <int D, int NT>
+__host__ __device__ constexpr int combine_cells_lds_floats(int G, int splits) {
+    return 2 * splits * G + G + (NT / (G * (D / 4)) > 0 ? NT / (G * (D / 4)) : 1) * G * D;
 }
 
 }  // namespace att

@@ -98,21 +98,56 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
     return (float)h;
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Lane exchanges within rows of 16 lanes (DPP, no LDS round trip).
+// Controls: quad_perm(1,0,3,2) = 0xB1, quad_perm(2,3,0,1) = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140.  Callers keep every lane of
+// the wave active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum (max) over each row of 16 lanes; every lane of the row receives it.
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
     return v;
+}
+
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    v = row_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
-// Sum within aligned groups of `width` lanes (width a power of two <= 64).
+// Sum within aligned groups of `width` lanes (width a power of two <= 64);
+// every lane of a group receives its group's sum.
 __device__ __forceinline__ float group_sum(float v, int width) {
+    if (width >= 16) {
+        v = row_sum(v);
+        if (width >= 32) v += __shfl_xor(v, 16, kWave);
+        if (width == 64) v += __shfl_xor(v, 32, kWave);
+        return v;
+    }
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
 }

@@ -87,8 +87,8 @@ struct mr_model {
     // attention heads' [layers * query_heads]
     unsigned *words = nullptr;
     size_t word_count = 0;
-    uint64_t *part_ml = nullptr;         // attention (m, l) cells
-    size_t part_ml_count = 0;
+    uint64_t *part_cells = nullptr;      // attention partials (m, l, o) as cells
+    size_t part_cell_count = 0;
     int xbuf = 0;                        // floats of one GEMV input staging buffer
     void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end
     int *err = nullptr;                  // wait timeout flag

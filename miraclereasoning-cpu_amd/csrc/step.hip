@@ -453,7 +453,7 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
     const int active = (g.total + split_len - 1) / split_len;
     for (int kh = 0; kh < a.kv_heads; ++kh) {
         if ((kh * splits) % (int)gridDim.x != (int)blockIdx.x) continue;
-        if (!combine<D, true, NT>(a, kh, active, lds, io)) return false;
+        if (!combine_cells<D, NT>(a, kh, active, lds, io)) return false;
         __syncthreads();
         if (threadIdx.x == 0) ll::mark(ph.heads_done + kh, ep_out);
     }
@@ -544,9 +544,9 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
         if (ph.kind != PH_ATTN) continue;
         const int G = ph.at.s.heads / ph.at.s.kv_heads, d = ph.at.s.dim, sp = ph.at.s.splits;
         size_t f;
-        if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_lds_floats<128, NT>(G, sp));
-        else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_lds_floats<64, NT>(G, sp));
-        else f = std::max(unit_lds_floats<32>(G), combine_lds_floats<32, NT>(G, sp));
+        if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_cells_lds_floats<128, NT>(G, sp));
+        else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_cells_lds_floats<64, NT>(G, sp));
+        else f = std::max(unit_lds_floats<32>(G), combine_cells_lds_floats<32, NT>(G, sp));
         need = std::max(need, f);
     }
     return need * sizeof(float);
