@@ -141,6 +141,12 @@ typedef struct mr_model_desc {
     int32_t global_block_size, global_slots;
     float router_temperature, alibi_slope_scale;
     uint64_t global_layer_mask_lo, global_layer_mask_hi;   /* bit i = layer i is global (i < 128) */
+    /* heavy-medium-2.0 scales, each computed by the host in double precision from
+     * the config's floats and rounded to FP32 once, as the reference's host code
+     * does before its kernel calls: residual_scale / sqrt(inner_loop_steps)
+     * (model.py:262), residual_scale / shared_experts (model.py:255) and
+     * alibi_slope_scale / sqrt(head_dim) (model.py:218). */
+    float heavy_step_scale, heavy_shared_scale, block_slope, reserved0;
 } mr_model_desc;
 
 /* Weight kinds (canonical names of weights.py:211-245). */
@@ -204,6 +210,16 @@ MR_API int mr_model_get_step_mode(mr_model *model, int *mode);
  * 2: barrier release}].  `capacity` is the number of uint64 in `out`;
  * *phases and *grid receive the program size.  The step advances the sequence
  * like any decode step. */
+/* Routing decisions of every position so far (heavy-medium-2.0): per position,
+ * layer and inner loop one record of 1 + router_top_k_max + query_heads *
+ * global_slots ints: the adaptive width, the chosen experts in descending
+ * probability (-1 past the width), then per query head the chosen global blocks
+ * in ascending order (-1 padded).  The reference makes these choices on the host
+ * (model.py:220-249); no reference function returns them, they are what its
+ * trace records for parity checks.  *per_position receives the ints per
+ * position. */
+MR_API int mr_model_choices(mr_model *model, int32_t *out, int64_t capacity, int *per_position);
+
 MR_API int mr_model_trace_step(mr_model *model, uint64_t *out, int64_t capacity, int *phases, int *grid);
 
 /* Device milliseconds of the last mr_model_generate_greedy call (HIP events

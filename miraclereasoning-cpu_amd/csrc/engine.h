@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "attention.h"
+#include "heavy.h"
 #include "linear.h"
 #include "step.h"
 
@@ -33,9 +34,11 @@ struct Layer {
     float *cbr_queries = nullptr;  // RMS-normalized queries (fixed per model)
     // flashlighting-2.0
     Weight latent, latent_norm, k_up, v_up, attention_gate, ffn_gate;
-    // heavy-medium-2.0
-    Weight kv_up, router_coarse, router_coarse_bias, router_fine, router_fine_bias, group_bias, expert_bias;
+    // heavy-medium-2.0: qkv packs [Wq; Wlatent], router packs [Wcoarse; Wfine]
+    Weight kv_up, router, router_coarse_bias, router_fine_bias, group_bias, expert_bias;
     std::vector<Mlp> experts, shared;
+    void **expert_tab = nullptr;       // device [3][experts + shared]: gate, up, down pointers
+    float *bsum_k = nullptr, *bsum_v = nullptr;   // [inner][blocks, kvw] running block sums
     // caches
     float *ring_k = nullptr, *ring_v = nullptr;        // [capacity, kv_heads*dim] (per inner loop for heavy)
     float *relay_k = nullptr, *relay_v = nullptr;      // flashnano-1.6 relay
@@ -68,6 +71,11 @@ struct mr_model {
     float *part = nullptr;
     unsigned *counters = nullptr;
     float *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;
+    // heavy-medium-2.0 step buffers and the per-position choice log
+    float *q_rot = nullptr, *kvbuf = nullptr, *router_out = nullptr, *moe_w = nullptr, *moe_act = nullptr;
+    int *moe_ids = nullptr, *moe_active = nullptr;
+    int *choices = nullptr;              // [context + 1][layers][inner][choice_rec]
+    int choice_rec = 0;                  // ints per record: active, kmax ids, heads x slots blocks
     // step execution: persistent kernel (when the model fits its phases) or
     // per-layer kernels replayed from a hipGraph / launched eagerly
     int mode = MR_STEP_PERSISTENT;

@@ -302,9 +302,7 @@ Weight *weight_slot(mr_model *m, int kind, int layer, int expert) {
         case MR_W_ATTENTION_GATE: return &L.attention_gate;
         case MR_W_FFN_GATE: return &L.ffn_gate;
         case MR_W_CBR: return &L.cbr;
-        case MR_W_ROUTER_COARSE: return &L.router_coarse;
         case MR_W_ROUTER_COARSE_BIAS: return &L.router_coarse_bias;
-        case MR_W_ROUTER_FINE: return &L.router_fine;
         case MR_W_ROUTER_FINE_BIAS: return &L.router_fine_bias;
         case MR_W_ROUTER_GROUP_BIAS: return &L.group_bias;
         case MR_W_ROUTER_EXPERT_BIAS: return &L.expert_bias;
@@ -405,6 +403,64 @@ int record_gqa_layer(mr_model *m, Layer &L) {
     return MR_OK;
 }
 
+// One heavy-medium-2.0 layer: inner_loop_steps passes, each latent-KV sparse
+// attention + residual, then grouped adaptive MoE + residual (model.py:259-263).
+int record_heavy_layer(mr_model *m, Layer &L, int li) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    const int inner = d.inner_loop_steps, blocks = ceil_div(d.context_length, d.global_block_size);
+    const int kmax = d.router_top_k_max;
+    for (int loop = 0; loop < inner; ++loop) {
+        GemvArgs g;   // RMSNorm -> [Wq; Wlatent]
+        g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
+        g.n = qd + d.latent_dim; g.k = h; g.y = m->qkv; g.done = m->done_dev;
+        MR_TRY(launch_gemv(s, L.qkv.dtype, PRO_RMS, EPI_STORE, g));
+        GemvArgs u;   // latent -> [K; V]
+        u.w = L.kv_up.ptr; u.x = m->qkv + qd; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
+        MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
+        HeavyAttnArgs a;
+        a.q = m->qkv; a.kv = m->kvbuf; a.rope = m->rope; a.pos = m->pos_dev; a.done = m->done_dev;
+        a.q_rot = m->q_rot;
+        a.ring_k = L.ring_k + (size_t)loop * d.context_length * kvw;
+        a.ring_v = L.ring_v + (size_t)loop * d.context_length * kvw;
+        a.bsum_k = L.bsum_k + (size_t)loop * blocks * kvw;
+        a.bsum_v = L.bsum_v + (size_t)loop * blocks * kvw;
+        a.out = m->attn;
+        a.choice = m->choices + ((size_t)li * inner + loop) * m->choice_rec;
+        a.choice_stride = d.layers * inner * m->choice_rec;
+        a.choice_blocks = 1 + kmax;
+        a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.window = d.window;
+        a.block = d.global_block_size; a.slots = d.global_slots; a.slope = d.block_slope;
+        MR_TRY(launch_heavy_attention(s, a, d.context_length));
+        GemvArgs o;   // hidden += step_scale * Wo . attended
+        o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->hidden; o.scale = d.heavy_step_scale;
+        o.done = m->done_dev;
+        MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_RESIDUAL, o));
+        GemvArgs r;   // RMSNorm -> [Wcoarse; Wfine]; the normalized input feeds the experts
+        r.w = L.router.ptr; r.x = m->hidden; r.gain = L.f_norm.f(); r.eps = d.norm_eps;
+        r.n = d.router_groups + d.routed_experts; r.k = h; r.y = m->router_out; r.x_out = m->xnorm;
+        r.done = m->done_dev;
+        MR_TRY(launch_gemv(s, L.router.dtype, PRO_RMS, EPI_STORE, r));
+        MoeArgs e;
+        const size_t n = d.routed_experts + d.shared_experts;
+        e.router = m->router_out;
+        e.coarse_bias = L.router_coarse_bias.f(); e.group_bias = L.group_bias.f();
+        e.fine_bias = L.router_fine_bias.f(); e.expert_bias = L.expert_bias.f();
+        e.x = m->xnorm; e.gate = L.expert_tab; e.up = L.expert_tab + n; e.down = L.expert_tab + 2 * n;
+        e.dtype = L.experts[0].gate.dtype; e.done = m->done_dev; e.pos = m->pos_dev;
+        e.ids = m->moe_ids; e.weights = m->moe_w; e.active = m->moe_active; e.act = m->moe_act; e.hidden = m->hidden;
+        e.choice = a.choice; e.choice_stride = a.choice_stride;
+        e.experts = d.routed_experts; e.groups = d.router_groups; e.kmin = d.router_top_k_min; e.kmax = kmax;
+        e.shared = d.shared_experts; e.ffn = d.ffn_dim; e.h = h;
+        e.inv_temperature_div = d.router_temperature;
+        e.log_experts = std::max((float)std::log((double)d.routed_experts), 1.0f);
+        e.shared_scale = d.heavy_shared_scale; e.scale = d.heavy_step_scale;
+        MR_TRY(launch_moe(s, e));
+    }
+    return MR_OK;
+}
+
 int launch_lm_head(mr_model *m) {
     const mr_model_desc &d = m->d;
     const Weight &head = d.tie_embeddings ? m->embed : m->output;
@@ -442,7 +498,9 @@ int record_step(mr_model *m, int kind) {
     k_embed<<<ceil_div(d.hidden_size, 256), 256, 0, s>>>(m->embed.ptr, m->embed.dtype, m->ids_dev, m->pos_dev,
                                                          m->done_dev, m->hidden, d.hidden_size);
     MR_LAUNCHED("enqueue embed");
-    for (int li = 0; li < d.layers; ++li) MR_TRY(record_gqa_layer(m, m->layers[li]));
+    for (int li = 0; li < d.layers; ++li)
+        MR_TRY(d.family == MR_FAMILY_HEAVY_MEDIUM_20 ? record_heavy_layer(m, m->layers[li], li)
+                                                     : record_gqa_layer(m, m->layers[li]));
     return record_head(m, kind);
 }
 
@@ -670,6 +728,44 @@ int setup_persistent(mr_model *m) {
     return MR_OK;
 }
 
+// heavy-medium-2.0 layer: packed projections present, experts complete,
+// per-inner-loop rings (capacity = context) and block sums, expert table.
+int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
+    const mr_model_desc &d = m->d;
+    const int hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    const std::string at = " in layer " + std::to_string(i);
+    for (const Weight *w : {&L.kv_up, &L.router_coarse_bias, &L.router_fine_bias, &L.group_bias, &L.expert_bias})
+        if (!w->ptr) return fail(MR_ERR_STATE, "missing heavy-medium weight" + at);
+    if (L.qkv.rows != 3) return fail(MR_ERR_STATE, "missing q/latent weight" + at);
+    L.qkv.rows = qd + d.latent_dim;
+    if (L.router.rows != 3) return fail(MR_ERR_STATE, "missing router weight" + at);
+    L.router.rows = d.router_groups + d.routed_experts;
+    const int dt = L.experts[0].gate.dtype;
+    std::vector<void *> tab(3 * (size_t)(d.routed_experts + d.shared_experts));
+    const size_t n = d.routed_experts + d.shared_experts;
+    for (size_t e = 0; e < n; ++e) {
+        const Mlp &mlp = e < (size_t)d.routed_experts ? L.experts[e] : L.shared[e - d.routed_experts];
+        if (!mlp.gate.ptr || !mlp.up.ptr || !mlp.down.ptr) return fail(MR_ERR_STATE, "missing expert weight" + at);
+        if (mlp.gate.dtype != dt || mlp.up.dtype != dt || mlp.down.dtype != dt)
+            return fail(MR_ERR_INVALID, "experts must share one dtype" + at);
+        tab[e] = mlp.gate.ptr;
+        tab[n + e] = mlp.up.ptr;
+        tab[2 * n + e] = mlp.down.ptr;
+    }
+    MR_TRY(device_alloc(m, tab.size() * sizeof(void *), (void **)&L.expert_tab));
+    MR_HIP(hipMemcpy(L.expert_tab, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice), "upload expert table");
+    const size_t ring = (size_t)d.inner_loop_steps * d.context_length * kvw * sizeof(float);
+    const int blocks = ceil_div(d.context_length, d.global_block_size);
+    const size_t bsum = (size_t)d.inner_loop_steps * blocks * kvw * sizeof(float);
+    MR_TRY(device_alloc(m, ring, (void **)&L.ring_k));
+    MR_TRY(device_alloc(m, ring, (void **)&L.ring_v));
+    MR_TRY(device_alloc(m, bsum, (void **)&L.bsum_k));
+    MR_TRY(device_alloc(m, bsum, (void **)&L.bsum_v));
+    for (void *p : {(void *)L.ring_k, (void *)L.ring_v, (void *)L.bsum_k, (void *)L.bsum_v})
+        MR_HIP(hipMemset(p, 0, p == L.ring_k || p == L.ring_v ? ring : bsum), "clear heavy caches");
+    return MR_OK;
+}
+
 void destroy_graphs(mr_model *m) {
     for (auto &e : m->exec)
         if (e) {
@@ -692,9 +788,17 @@ int mr_model_create(mr_ctx *ctx, const mr_model_desc *desc, mr_model **out) {
                    d.kv_heads > 0 && d.head_dim > 0 && d.head_dim % 2 == 0 && d.ffn_dim > 0 &&
                    d.context_length > 0 && d.query_heads % d.kv_heads == 0,
                "invalid model geometry");
-    if (!is_gqa(d.family))
-        return fail(MR_ERR_INVALID, "this library build runs the GQA families (flashnano-1.5/1.6/1.7, "
-                                    "flashlite-2.0) only");
+    const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20;
+    if (!is_gqa(d.family) && !heavy)
+        return fail(MR_ERR_INVALID, "this library build runs flashnano-1.5/1.6/1.7, flashlite-2.0 and "
+                                    "heavy-medium-2.0; flashlighting-2.0 is not available yet");
+    if (heavy)
+        MR_REQUIRE(d.latent_dim > 0 && d.inner_loop_steps >= 1 && d.routed_experts >= 1 &&
+                       d.routed_experts <= 256 && d.router_groups >= 1 && d.router_groups <= d.routed_experts &&
+                       d.router_top_k_min >= 1 && d.router_top_k_min <= d.router_top_k_max &&
+                       d.router_top_k_max <= std::min(d.routed_experts, 16) && d.shared_experts >= 0 &&
+                       d.global_block_size > 0 && d.global_slots > 0 && d.window > 0,
+                   "invalid heavy-medium-2.0 geometry");
     if (d.family == MR_FAMILY_FLASHNANO_16)
         MR_REQUIRE(d.cbr_chunk_size > 0 && d.cbr_slots > 0, "FlashNano 1.6 requires CBR chunk size and slots");
     mr_model *m = new mr_model();
@@ -709,6 +813,13 @@ int mr_model_create(mr_ctx *ctx, const mr_model_desc *desc, mr_model **out) {
         // model.py:105 capacity = min(window or ctx, ctx)
         int win = L.global ? 0 : d.window;
         L.capacity = win > 0 ? std::min(win, d.context_length) : d.context_length;
+        if (heavy) {   // model.py:203: each inner loop keeps every position
+            L.global = false;
+            L.kv_heads = d.kv_heads;
+            L.capacity = d.context_length;
+            L.experts.resize(d.routed_experts);
+            L.shared.resize(d.shared_experts);
+        }
         MR_REQUIRE(d.query_heads % L.kv_heads == 0, "query heads must divide into KV groups");
     }
     *out = m;
@@ -726,14 +837,16 @@ int mr_model_destroy(mr_model *m) {
     for (Layer &L : m->layers) {
         for (Weight *w : {&L.a_norm, &L.f_norm, &L.qkv, &L.q_norm, &L.k_norm, &L.o, &L.ffn.gate, &L.ffn.up,
                           &L.ffn.down, &L.cbr, &L.latent, &L.latent_norm, &L.k_up, &L.v_up, &L.attention_gate,
-                          &L.ffn_gate, &L.kv_up, &L.router_coarse, &L.router_coarse_bias, &L.router_fine,
-                          &L.router_fine_bias, &L.group_bias, &L.expert_bias})
+                          &L.ffn_gate, &L.kv_up, &L.router, &L.router_coarse_bias, &L.router_fine_bias,
+                          &L.group_bias, &L.expert_bias})
             free_weight(*w);
         for (Mlp &e : L.experts) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
         for (Mlp &e : L.shared) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
-        for (float *p : {L.ring_k, L.ring_v, L.relay_k, L.relay_v, L.pending, L.cbr_queries})
+        for (float *p : {L.ring_k, L.ring_v, L.relay_k, L.relay_v, L.pending, L.cbr_queries, L.bsum_k, L.bsum_v})
             if (p) hipFree(p);
+        if (L.expert_tab) hipFree(L.expert_tab);
     }
+    if (m->choices) hipFree(m->choices);
     if (m->freq) hipFree(m->freq);
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
@@ -778,6 +891,29 @@ int mr_model_set_weight(mr_model *m, int kind, int layer, int expert, const void
         MR_HIP(hipMemcpy(dst, host, (size_t)rows * cols * dtype_bytes(dtype), hipMemcpyHostToDevice),
                "upload weight");
         L.qkv.rows |= kind == MR_W_Q ? 1 : kind == MR_W_K ? 2 : 4;   // presence bits until finalize
+        return MR_OK;
+    }
+    if (m->d.family == MR_FAMILY_HEAVY_MEDIUM_20 &&
+        (kind == MR_W_Q || kind == MR_W_LATENT || kind == MR_W_ROUTER_COARSE || kind == MR_W_ROUTER_FINE)) {
+        // Pack [Wq; Wlatent] and [Wcoarse; Wfine]: one GEMV each.
+        Layer &L = m->layers[layer];
+        const bool qpair = kind == MR_W_Q || kind == MR_W_LATENT;
+        Weight &w = qpair ? L.qkv : L.router;
+        const int64_t h = m->d.hidden_size;
+        const int64_t first = qpair ? (int64_t)m->d.query_heads * m->d.head_dim : m->d.router_groups;
+        const int64_t second = qpair ? m->d.latent_dim : m->d.routed_experts;
+        if (!w.ptr) {
+            MR_TRY(device_alloc(m, (size_t)(first + second) * h * dtype_bytes(dtype), &w.ptr));
+            w.dtype = dtype;
+            w.rows = 0;
+            w.cols = h;
+        }
+        MR_REQUIRE(w.dtype == dtype, "set_weight: packed projections must share one dtype");
+        const bool lead = kind == MR_W_Q || kind == MR_W_ROUTER_COARSE;
+        char *dst = (char *)w.ptr + (size_t)(lead ? 0 : first) * h * dtype_bytes(dtype);
+        MR_HIP(hipMemcpy(dst, host, (size_t)rows * cols * dtype_bytes(dtype), hipMemcpyHostToDevice),
+               "upload weight");
+        w.rows |= lead ? 1 : 2;   // presence bits until finalize
         return MR_OK;
     }
     Weight *slot = weight_slot(m, kind, layer, expert);
@@ -827,11 +963,19 @@ int mr_model_finalize(mr_model *m) {
     const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd;
     int max_kvw = 0, max_kvh = 0;
     size_t max_part = 0;
+    const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20;
+    const int inner = heavy ? d.inner_loop_steps : 1;
     for (int i = 0; i < d.layers; ++i) {
         Layer &L = m->layers[i];
         MR_TRY(need(L.a_norm, "a_norm", i));
         MR_TRY(need(L.f_norm, "f_norm", i));
         MR_TRY(need(L.o, "o", i));
+        if (heavy) {
+            MR_TRY(finalize_heavy_layer(m, L, i));
+            max_kvw = std::max(max_kvw, L.kv_heads * hd);
+            max_kvh = std::max(max_kvh, L.kv_heads);
+            continue;
+        }
         if (L.qkv.rows != 7) return fail(MR_ERR_STATE, "missing q/k/v weight in layer " + std::to_string(i));
         L.qkv.rows = qd + 2 * (int64_t)L.kv_heads * hd;
         if (d.qk_norm) {
@@ -882,7 +1026,14 @@ int mr_model_finalize(mr_model *m) {
     size_t o_gen = take((size_t)ctxn * sizeof(int));
     size_t o_hidden = take((size_t)h * sizeof(float));
     size_t o_xnorm = take((size_t)h * sizeof(float));
-    size_t o_qkv = take((size_t)(qd + 2 * max_kvw) * sizeof(float));
+    size_t o_qkv = take((size_t)(qd + std::max(2 * max_kvw, d.latent_dim)) * sizeof(float));
+    const int kmax = std::max(d.router_top_k_max, 1), moe_slots = kmax + d.shared_experts;
+    size_t o_qrot = take(heavy ? (size_t)qd * sizeof(float) : 0);
+    size_t o_kvbuf = take(heavy ? (size_t)2 * max_kvw * sizeof(float) : 0);
+    size_t o_router = take(heavy ? (size_t)(d.router_groups + d.routed_experts) * sizeof(float) : 0);
+    size_t o_moe_ids = take(heavy ? (size_t)(kmax + 1) * sizeof(int) : 0);
+    size_t o_moe_w = take(heavy ? (size_t)kmax * sizeof(float) : 0);
+    size_t o_moe_act = take(heavy ? (size_t)moe_slots * d.ffn_dim * sizeof(float) : 0);
     size_t o_attn = take((size_t)qd * sizeof(float));
     size_t o_act = take((size_t)d.ffn_dim * sizeof(float));
     size_t o_logits = take((size_t)d.vocab_size * sizeof(float));
@@ -913,6 +1064,19 @@ int mr_model_finalize(mr_model *m) {
     m->cbr_pooled = (float *)(base + o_pool);
     m->cbr_anchor = (float *)(base + o_anchor);
     m->cbr_kv = (float *)(base + o_cbrkv);
+    if (heavy) {
+        m->q_rot = (float *)(base + o_qrot);
+        m->kvbuf = (float *)(base + o_kvbuf);
+        m->router_out = (float *)(base + o_router);
+        m->moe_ids = (int *)(base + o_moe_ids);
+        m->moe_active = m->moe_ids + kmax;
+        m->moe_w = (float *)(base + o_moe_w);
+        m->moe_act = (float *)(base + o_moe_act);
+        m->choice_rec = 1 + kmax + d.query_heads * d.global_slots;
+        const size_t n = (size_t)(d.context_length + 1) * d.layers * inner * m->choice_rec;
+        MR_TRY(device_alloc(m, n * sizeof(int), (void **)&m->choices));
+        MR_HIP(hipMemset(m->choices, 0xff, n * sizeof(int)), "clear choice log");
+    }
     MR_HIP(hipDeviceSynchronize(), "finalize model");
     MR_TRY(setup_persistent(m));
     m->finalized = true;
@@ -1039,6 +1203,8 @@ int mr_model_generate_greedy(mr_model *m, int max_new, int eos, int32_t *tokens,
 int mr_model_time_kernel(mr_model *m, int which, int reps, float *avg_ms) {
     MR_TRY(check_ctx(m, "time_kernel"));
     MR_REQUIRE(avg_ms && reps >= 1 && which >= MR_KERNEL_QKV && which <= MR_KERNEL_HEAD, "time_kernel: bad arguments");
+    MR_REQUIRE(is_gqa(m->d.family) || which == MR_KERNEL_HEAD,
+               "time_kernel: the per-layer kernels are those of the GQA families");
     hipStream_t s = m->ctx->stream;
     hipEvent_t e0, e1;
     MR_HIP(hipEventCreate(&e0), "create event");
@@ -1067,6 +1233,19 @@ int mr_model_time_kernel(mr_model *m, int which, int reps, float *avg_ms) {
     if (rc != MR_OK) return rc;
     MR_HIP(e, "time kernel");
     *avg_ms = ms / (float)std::max(launches, 1);
+    return MR_OK;
+}
+
+int mr_model_choices(mr_model *m, int32_t *out, int64_t capacity, int *per_position) {
+    MR_TRY(check_ctx(m, "choices"));
+    MR_REQUIRE(out && per_position, "choices: null argument");
+    MR_REQUIRE(m->choices, "choices: the model makes no routing choices (heavy-medium-2.0 only)");
+    const int64_t per = (int64_t)m->d.layers * m->d.inner_loop_steps * m->choice_rec;
+    const int64_t n = per * m->position;
+    MR_REQUIRE(n <= capacity, "choices: output too small");
+    *per_position = (int)per;
+    MR_HIP(hipStreamSynchronize(m->ctx->stream), "choices");
+    if (n) MR_HIP(hipMemcpy(out, m->choices, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost), "read choices");
     return MR_OK;
 }
 

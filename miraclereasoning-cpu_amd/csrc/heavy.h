@@ -1,0 +1,53 @@
+// heavy-medium-2.0 token-step kernels (model.py:192-255): latent KV with
+// block-mean sparse attention and grouped adaptive MoE, all control on device.
+#pragma once
+
+#include "common.h"
+
+namespace mr {
+
+struct HeavyAttnArgs {
+    const float *q = nullptr;        // [heads*d] raw projection (the Q rows of the packed Q/latent GEMV)
+    const float *kv = nullptr;       // [2*kv_heads*d] kv_up output: keys then values
+    const float *rope = nullptr;     // [positions][d/2][2] cos, sin
+    const int *pos = nullptr, *done = nullptr;
+    float *q_rot = nullptr;          // [heads*d] normalized, rotated queries
+    float *ring_k = nullptr, *ring_v = nullptr;   // [context, kv_heads*d] of this inner loop
+    float *bsum_k = nullptr, *bsum_v = nullptr;   // [blocks, kv_heads*d] running block sums
+    float *out = nullptr;            // [heads*d] attended values
+    int *choice = nullptr;           // choice record of this layer/loop at position 0 (or null)
+    int choice_stride = 0;           // ints between the records of consecutive positions
+    int choice_blocks = 0;           // offset of the block lists inside a record
+    int heads = 0, kv_heads = 0, d = 0, window = 0, block = 0, slots = 0;
+    float slope = 0.0f;              // alibi_slope_scale / sqrt(d), FP32
+};
+
+int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context);
+
+struct MoeArgs {
+    const float *router = nullptr;   // [groups + experts] coarse then fine logits (no biases)
+    const float *coarse_bias = nullptr, *group_bias = nullptr, *fine_bias = nullptr, *expert_bias = nullptr;
+    const float *x = nullptr;        // [h] RMS-normalized input of the experts
+    void *const *gate = nullptr;     // [experts + shared] weight pointers: routed, then shared
+    void *const *up = nullptr;
+    void *const *down = nullptr;
+    int dtype = MR_BF16;
+    const int *done = nullptr;
+    const int *pos = nullptr;
+    int *ids = nullptr;              // [kmax] chosen experts, descending probability
+    float *weights = nullptr;        // [kmax] renormalized weights (0 beyond active)
+    int *active = nullptr;           // adaptive width
+    float *act = nullptr;            // [(kmax + shared) * ffn] SwiGLU activations per slot
+    float *hidden = nullptr;         // residual stream, updated in place
+    int *choice = nullptr;           // choice record of this layer/loop at position 0 (or null)
+    int choice_stride = 0;
+    int experts = 0, groups = 0, kmin = 0, kmax = 0, shared = 0, ffn = 0, h = 0;
+    float inv_temperature_div = 1.0f;   // max(temperature, 1e-4), FP32 (logits are divided by it)
+    float log_experts = 1.0f;           // max(float32(log(E)), 1)
+    float shared_scale = 1.0f;          // residual_scale / shared, FP32
+    float scale = 1.0f;                 // residual_scale / sqrt(inner_loop_steps), FP32
+};
+
+int launch_moe(hipStream_t s, const MoeArgs &a);
+
+}  // namespace mr

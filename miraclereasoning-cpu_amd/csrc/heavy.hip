@@ -1,0 +1,357 @@
+// heavy-medium-2.0 token-step kernels (model.py:192-255).
+//
+// Attention of one inner-loop pass:
+//   k_heavy_prep   queries and the new key: RMSNorm without affine (eps 1e-6,
+//                  kernels.cl:19-28 order) + interleaved RoPE; the key and value
+//                  are appended to the pass's ring at the position and added to
+//                  the running sums of their 64-row block, in row order, so the
+//                  block means equal kernels.cl's block_means bit for bit.
+//   k_heavy_attn   one workgroup per query head: window scores and block-mean
+//                  scores (sequential dot products, kernels.cl:58-73), the
+//                  distance penalty on block columns, the per-head stable
+//                  top-k of blocks (descending score, ties to the lower block;
+//                  model.py:220-226), softmax and the value mix in kernels.cl's
+//                  sequential orders.
+// MoE:
+//   k_moe_route    one workgroup: biases, group broadcast, temperature,
+//                  softmax, stable top-k, confidence / entropy / adaptive
+//                  width and renormalization in numpy's FP32 arithmetic
+//                  (model.py:231-250; numpy float32 sums are pairwise).
+//   k_moe_gate_up  SwiGLU activations of every active routed slot and every
+//                  shared expert, weight pointers taken from a device table by
+//                  the device-side expert ids.
+//   k_moe_down     per output row: the routed experts accumulated in chosen
+//                  order with their weights, then the shared experts with
+//                  residual_scale / shared (kernels.cl:52-56 axpy chain), then
+//                  the residual add.
+#include "heavy.h"
+
+namespace mr {
+namespace {
+
+// ------------------------------------------------------------------ attention
+__global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
+    extern __shared__ float row[];
+    if (a.done && *a.done) return;
+    const int pos = *a.pos, d = a.d, half = d / 2;
+    const bool isq = (int)blockIdx.x < a.heads;
+    const int hh = isq ? blockIdx.x : blockIdx.x - a.heads;
+    const int kvw = a.kv_heads * d;
+    const float *src = isq ? a.q + (int64_t)hh * d : a.kv + (int64_t)hh * d;
+    __shared__ float scale;
+    if (threadIdx.x == 0) {   // kernels.cl:19-28: one sequential sum of squares
+        float v = 0.0f;
+        for (int j = 0; j < d; ++j) {
+            const float x = src[j];
+            v += x * x;
+        }
+        scale = 1.0f / sqrtf(v / (float)d + 1e-6f);
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = src[j] * scale * 1.0f;
+    __syncthreads();
+    const float *cs = a.rope + (int64_t)pos * half * 2;
+    for (int p = threadIdx.x; p < half; p += blockDim.x) {   // interleaved pairs (kernels.cl:30-44)
+        float u = row[2 * p], v = row[2 * p + 1];
+        rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
+        row[2 * p] = u;
+        row[2 * p + 1] = v;
+    }
+    __syncthreads();
+    if (isq) {
+        for (int j = threadIdx.x; j < d; j += blockDim.x) a.q_rot[(int64_t)hh * d + j] = row[j];
+        return;
+    }
+    const int64_t slot = (int64_t)pos * kvw + (int64_t)hh * d;
+    const int64_t bslot = (int64_t)(pos / a.block) * kvw + (int64_t)hh * d;
+    const bool first = pos % a.block == 0;
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+        const float k = row[j], v = a.kv[kvw + (int64_t)hh * d + j];
+        a.ring_k[slot + j] = k;
+        a.ring_v[slot + j] = v;
+        a.bsum_k[bslot + j] = (first ? 0.0f : a.bsum_k[bslot + j]) + k;
+        a.bsum_v[bslot + j] = (first ? 0.0f : a.bsum_v[bslot + j]) + v;
+    }
+}
+
+constexpr int kAttnThreads = 256;
+
+__global__ void __launch_bounds__(kAttnThreads) k_heavy_attn(HeavyAttnArgs a) {
+    extern __shared__ float sh[];
+    if (a.done && *a.done) return;
+    const int pos = *a.pos, d = a.d, tid = threadIdx.x;
+    const int count = pos + 1, length = min(a.window, count), start = count - length;
+    const int blocks = (count + a.block - 1) / a.block, total = length + blocks;
+    const int h = blockIdx.x, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * d;
+    float *qs = sh;              // [d]
+    float *sc = qs + d;          // [total] scores, then probabilities
+    int *keep_flag = (int *)(sc + total);   // [blocks]
+    __shared__ float red[kAttnThreads / 64];
+    __shared__ float denom;
+    for (int j = tid; j < d; j += kAttnThreads) qs[j] = a.q_rot[(int64_t)h * d + j];
+    __syncthreads();
+    const float root = sqrtf((float)d);
+    for (int t = tid; t < total; t += kAttnThreads) {
+        float v = 0.0f;
+        if (t < length) {
+            const float *kr = a.ring_k + (int64_t)(start + t) * kvw + (int64_t)kh * d;
+            for (int j = 0; j < d; ++j) v += qs[j] * kr[j];
+            sc[t] = v / root;
+        } else {
+            const int b = t - length;
+            const float n = (float)min(a.block, count - b * a.block);
+            const float *kb = a.bsum_k + (int64_t)b * kvw + (int64_t)kh * d;
+            for (int j = 0; j < d; ++j) v += qs[j] * (kb[j] / n);
+            const int end = min((b + 1) * a.block - 1, pos);
+            sc[t] = v / root - a.slope * log1pf((float)(pos - end));
+        }
+    }
+    __syncthreads();
+    // Stable top-k of the block columns: rank = blocks scoring higher, or equal
+    // with a lower index.
+    const int keep = min(a.slots, blocks);
+    for (int b = tid; b < blocks; b += kAttnThreads) {
+        const float s = sc[length + b];
+        int rank = 0;
+        for (int c = 0; c < blocks; ++c) {
+            const float o = sc[length + c];
+            rank += o > s || (o == s && c < b);
+        }
+        keep_flag[b] = rank < keep;
+    }
+    __syncthreads();
+    if (a.choice) {   // chosen blocks in ascending order, -1 padded
+        int *rec = a.choice + (int64_t)pos * a.choice_stride + a.choice_blocks + h * a.slots;
+        for (int b = tid; b < blocks; b += kAttnThreads)
+            if (keep_flag[b]) {
+                int at = 0;
+                for (int c = 0; c < b; ++c) at += keep_flag[c];
+                rec[at] = b;
+            }
+        for (int i = keep + tid; i < a.slots; i += kAttnThreads) rec[i] = -1;
+    }
+    for (int b = tid; b < blocks; b += kAttnThreads)
+        if (!keep_flag[b]) sc[length + b] = -INFINITY;
+    __syncthreads();
+    // Softmax (kernels.cl:75-84): max, one sequential sum of exponentials, quotient.
+    float mx = -INFINITY;
+    for (int t = tid; t < total; t += kAttnThreads) mx = fmaxf(mx, sc[t]);
+    mx = block_max(mx, red);
+    if (tid == 0) {
+        float den = 0.0f;
+        for (int t = 0; t < total; ++t) den += expf(sc[t] - mx);
+        denom = den;
+    }
+    __syncthreads();
+    for (int t = tid; t < total; t += kAttnThreads) sc[t] = expf(sc[t] - mx) / denom;
+    __syncthreads();
+    // Mix (kernels.cl:93-107): one sequential sum over keys per output element.
+    for (int j = tid; j < d; j += kAttnThreads) {
+        float acc = 0.0f;
+        for (int t = 0; t < total; ++t) {
+            float v;
+            if (t < length) {
+                v = a.ring_v[(int64_t)(start + t) * kvw + (int64_t)kh * d + j];
+            } else {
+                const int b = t - length;
+                const float n = (float)min(a.block, count - b * a.block);
+                v = a.bsum_v[(int64_t)b * kvw + (int64_t)kh * d + j] / n;
+            }
+            acc += sc[t] * v;
+        }
+        a.out[(int64_t)h * d + j] = acc;
+    }
+}
+
+// ------------------------------------------------------------------ MoE
+// numpy's float32 add.reduce: pairwise summation, blocks of 8 accumulators
+// up to 128 elements, sequential below 8 elements; longer arrays split in two
+// halves (a multiple of 8 first), which covers up to 256 elements here.
+__device__ float np_block_sum(const float *a, int n) {
+    if (n < 8) {
+        float r = 0.0f;
+        for (int i = 0; i < n; ++i) r += a[i];
+        return r;
+    }
+    float r[8];
+    for (int k = 0; k < 8; ++k) r[k] = a[k];
+    int i = 8;
+    for (; i < n - (n % 8); i += 8)
+        for (int k = 0; k < 8; ++k) r[k] += a[i + k];
+    float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+}
+
+__device__ float np_pairwise_sum(const float *a, int n) {
+    if (n <= 128) return np_block_sum(a, n);
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    return np_block_sum(a, n2) + np_block_sum(a + n2, n - n2);
+}
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 16;
+
+__global__ void __launch_bounds__(kMaxExperts) k_moe_route(MoeArgs a) {
+    if (a.done && *a.done) return;
+    __shared__ float coarse[kMaxExperts], logits[kMaxExperts], probs[kMaxExperts], terms[kMaxExperts];
+    __shared__ int chosen[kMaxTopK];
+    const int tid = threadIdx.x, E = a.experts, G = a.groups;
+    if (tid < G) coarse[tid] = a.router[tid] + (a.coarse_bias[tid] + a.group_bias[tid]);
+    __syncthreads();
+    if (tid < E) {
+        const int size = (E + G - 1) / G;
+        const int g = min(tid / size, G - 1);
+        const float fine = a.router[G + tid] + (a.fine_bias[tid] + a.expert_bias[tid]);
+        logits[tid] = (fine + coarse[g]) / a.inv_temperature_div;
+    }
+    __syncthreads();
+    if (tid == 0) {   // kernels.cl:75-84 softmax
+        float m = -INFINITY;
+        for (int e = 0; e < E; ++e) m = fmaxf(m, logits[e]);
+        float den = 0.0f;
+        for (int e = 0; e < E; ++e) den += expf(logits[e] - m);
+        for (int e = 0; e < E; ++e) probs[e] = expf(logits[e] - m) / den;
+    }
+    __syncthreads();
+    if (tid < E) {   // stable argsort of -probs (model.py:241)
+        const float p = probs[tid];
+        int rank = 0;
+        for (int f = 0; f < E; ++f) rank += probs[f] > p || (probs[f] == p && f < tid);
+        if (rank < a.kmax) chosen[rank] = tid;
+        terms[tid] = p * logf(fmaxf(p, 1e-9f));
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    const int kmax = a.kmax;
+    float w[kMaxTopK];
+    for (int r = 0; r < kmax; ++r) w[r] = probs[chosen[r]];
+    const float confidence = w[0] - w[min(kmax - 1, 1)];
+    const float entropy = -np_pairwise_sum(terms, E);
+    const float spread = rintf((1.0f - confidence) * 2.0f + entropy / a.log_experts);
+    const float width = fminf(fmaxf((float)a.kmin + spread, (float)a.kmin), (float)kmax);
+    const int active = (int)width;
+    for (int r = active; r < kmax; ++r) w[r] = 0.0f;
+    const float den = fmaxf(np_pairwise_sum(w, kmax), 1e-9f);
+    for (int r = 0; r < kmax; ++r) {
+        a.ids[r] = chosen[r];
+        a.weights[r] = w[r] / den;
+    }
+    *a.active = active;
+    if (a.choice) {
+        int *rec = a.choice + (int64_t)(*a.pos) * a.choice_stride;
+        rec[0] = active;
+        for (int r = 0; r < kmax; ++r) rec[1 + r] = r < active ? chosen[r] : -1;
+    }
+}
+
+constexpr int kMoeThreads = 512;
+constexpr int kMoeRows = kMoeThreads / kWave;   // one wave per output row
+
+__device__ __forceinline__ float dot_row(const void *w, int dt, int64_t row, int k, const float *xs) {
+    const int lane = threadIdx.x & 63;
+    float acc = 0.0f;
+    if (dt == MR_BF16 && (k % 8) == 0) {
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 *r = (const u32x4 *)((const uint16_t *)w + row * k);
+        for (int v = lane; v < k / 8; v += kWave) {
+            const u32x4 q = __builtin_nontemporal_load(gmem(r + v));
+            const float *x = xs + v * 8;
+            acc = fmaf(__uint_as_float(q.x << 16), x[0], acc);
+            acc = fmaf(__uint_as_float(q.x & 0xffff0000u), x[1], acc);
+            acc = fmaf(__uint_as_float(q.y << 16), x[2], acc);
+            acc = fmaf(__uint_as_float(q.y & 0xffff0000u), x[3], acc);
+            acc = fmaf(__uint_as_float(q.z << 16), x[4], acc);
+            acc = fmaf(__uint_as_float(q.z & 0xffff0000u), x[5], acc);
+            acc = fmaf(__uint_as_float(q.w << 16), x[6], acc);
+            acc = fmaf(__uint_as_float(q.w & 0xffff0000u), x[7], acc);
+        }
+    } else {
+        for (int j = lane; j < k; j += kWave) {
+            float wv;
+            if (dt == MR_F32) wv = ((const float *)w)[row * k + j];
+            else if (dt == MR_BF16) wv = bf16_to_f32(((const uint16_t *)w)[row * k + j]);
+            else wv = f16_to_f32(((const uint16_t *)w)[row * k + j]);
+            acc = fmaf(wv, xs[j], acc);
+        }
+    }
+    return wave_sum(acc);
+}
+
+// grid (ceil(ffn / kMoeRows), kmax + shared)
+__global__ void __launch_bounds__(kMoeThreads) k_moe_gate_up(MoeArgs a) {
+    extern __shared__ float xs[];
+    if (a.done && *a.done) return;
+    const int slot = blockIdx.y;
+    int e;
+    if (slot < a.kmax) {
+        if (slot >= *a.active) return;
+        e = a.ids[slot];
+    } else {
+        e = a.experts + (slot - a.kmax);
+    }
+    for (int j = threadIdx.x; j < a.h; j += kMoeThreads) xs[j] = a.x[j];
+    __syncthreads();
+    const int row = blockIdx.x * kMoeRows + (threadIdx.x >> 6);
+    if (row >= a.ffn) return;
+    const float g = dot_row(a.gate[e], a.dtype, row, a.h, xs);
+    const float u = dot_row(a.up[e], a.dtype, row, a.h, xs);
+    if ((threadIdx.x & 63) == 0) a.act[(int64_t)slot * a.ffn + row] = (g / (1.0f + expf(-g))) * u;   // kernels.cl:46-50
+}
+
+// grid ceil(h / kMoeRows)
+__global__ void __launch_bounds__(kMoeThreads) k_moe_down(MoeArgs a) {
+    extern __shared__ float acts[];
+    if (a.done && *a.done) return;
+    const int slots = a.kmax + a.shared, active = *a.active;
+    for (int i = threadIdx.x; i < slots * a.ffn; i += kMoeThreads) {
+        const int s = i / a.ffn;
+        acts[i] = (s < a.kmax && s >= active) ? 0.0f : a.act[i];
+    }
+    __syncthreads();
+    const int row = blockIdx.x * kMoeRows + (threadIdx.x >> 6);
+    if (row >= a.h) return;
+    float total = 0.0f;
+    for (int s = 0; s < active; ++s) {
+        const float y = dot_row(a.down[a.ids[s]], a.dtype, row, a.ffn, acts + (int64_t)s * a.ffn);
+        total = total + a.weights[s] * y;
+    }
+    for (int s = 0; s < a.shared; ++s) {
+        const float y = dot_row(a.down[a.experts + s], a.dtype, row, a.ffn, acts + (int64_t)(a.kmax + s) * a.ffn);
+        total = total + a.shared_scale * y;
+    }
+    if ((threadIdx.x & 63) == 0) a.hidden[row] = a.hidden[row] + a.scale * total;
+}
+
+}  // namespace
+
+int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context) {
+    MR_REQUIRE(a.heads % a.kv_heads == 0 && a.d % 2 == 0 && a.block > 0 && a.slots > 0, "heavy attention: bad geometry");
+    k_heavy_prep<<<a.heads + a.kv_heads, 64, (size_t)a.d * sizeof(float), s>>>(a);
+    MR_LAUNCHED("enqueue heavy attention prologue");
+    const int blocks = (context + a.block - 1) / a.block;
+    const size_t lds = (size_t)(a.d + std::min(a.window, context) + blocks) * sizeof(float) + (size_t)blocks * sizeof(int);
+    MR_REQUIRE(lds <= 64 * 1024, "heavy attention: window and block count exceed shared memory");
+    k_heavy_attn<<<a.heads, kAttnThreads, lds, s>>>(a);
+    MR_LAUNCHED("enqueue heavy attention");
+    return MR_OK;
+}
+
+int launch_moe(hipStream_t s, const MoeArgs &a) {
+    MR_REQUIRE(a.experts >= 1 && a.experts <= kMaxExperts && a.groups >= 1 && a.groups <= a.experts &&
+                   a.kmin >= 1 && a.kmin <= a.kmax && a.kmax <= std::min(a.experts, kMaxTopK),
+               "moe: routing geometry out of range");
+    k_moe_route<<<1, kMaxExperts, 0, s>>>(a);
+    MR_LAUNCHED("enqueue moe routing");
+    const int slots = a.kmax + a.shared;
+    k_moe_gate_up<<<dim3(ceil_div(a.ffn, kMoeRows), slots), kMoeThreads, (size_t)a.h * sizeof(float), s>>>(a);
+    MR_LAUNCHED("enqueue moe gate/up");
+    const size_t lds = (size_t)slots * a.ffn * sizeof(float);
+    MR_REQUIRE(lds <= 64 * 1024, "moe: expert activations exceed shared memory");
+    k_moe_down<<<ceil_div(a.h, kMoeRows), kMoeThreads, lds, s>>>(a);
+    MR_LAUNCHED("enqueue moe down");
+    return MR_OK;
+}
+
+}  // namespace mr

@@ -50,7 +50,8 @@ class ModelDesc(C.Structure):
         [(n, C.c_int32) for n in ("routed_experts", "router_groups", "router_top_k_min", "router_top_k_max",
                                    "shared_experts", "global_block_size", "global_slots")] + \
         [(n, C.c_float) for n in ("router_temperature", "alibi_slope_scale")] + \
-        [("global_layer_mask_lo", C.c_uint64), ("global_layer_mask_hi", C.c_uint64)]
+        [("global_layer_mask_lo", C.c_uint64), ("global_layer_mask_hi", C.c_uint64)] + \
+        [(n, C.c_float) for n in ("heavy_step_scale", "heavy_shared_scale", "block_slope", "reserved0")]
 
 
 _P, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
@@ -92,6 +93,7 @@ _SIGNATURES = {
     "mr_model_get_step_mode": [_P, C.POINTER(C.c_int)],
     "mr_model_last_decode_ms": [_P, C.POINTER(C.c_float)],
     "mr_model_trace_step": [_P, _P, C.c_int64, C.POINTER(C.c_int), C.POINTER(C.c_int)],
+    "mr_model_choices": [_P, _P, C.c_int64, C.POINTER(_i)],
     "mr_model_time_kernel": [_P, _i, _i, C.POINTER(C.c_float)],
     "mr_debug_fail_next": [_P],
 }

@@ -69,7 +69,10 @@ def model_desc(config, context_length):
         shared_experts=s.get("shared_experts", 0), global_block_size=long.get("global_block_size", 0),
         global_slots=long.get("global_slots", 0), router_temperature=max(s.get("router_temperature", 1.0), 1e-4),
         alibi_slope_scale=long.get("alibi_slope_scale", 0.015),
-        global_layer_mask_lo=mask & ((1 << 64) - 1), global_layer_mask_hi=mask >> 64)
+        global_layer_mask_lo=mask & ((1 << 64) - 1), global_layer_mask_hi=mask >> 64,
+        heavy_step_scale=c.residual_scale / math.sqrt(max(c.inner_loop_steps, 1)),
+        heavy_shared_scale=c.residual_scale / max(s.get("shared_experts", 0), 1),
+        block_slope=long.get("alibi_slope_scale", 0.015) / math.sqrt(c.head_dim))
 
 
 class Engine:
@@ -155,6 +158,19 @@ class Engine:
         t = buf[:phases.value * grid.value * 3].reshape(phases.value, grid.value, 3).astype(np.int64)
         t0 = t[0, :, 0].min()
         return np.where(t > 0, (t - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
+
+    def choices(self):
+        """Routing decisions of every position so far (heavy-medium-2.0):
+        array [positions, layers, inner_loop_steps, record] of int32; a record
+        is (width, experts..., per query head its chosen blocks...), -1 padded."""
+        c = self.config
+        kmax = c.source["router_top_k_max"]
+        rec = 1 + kmax + c.query_heads * c.source["long_context"]["global_slots"]
+        pos = self.position()
+        buf = np.zeros(max(pos, 1) * c.layers * c.inner_loop_steps * rec, np.int32)
+        per = C.c_int()
+        _check(self.lib.mr_model_choices(self.handle, buf.ctypes.data, buf.size, C.byref(per)), "read choices")
+        return buf[:pos * per.value].reshape(pos, c.layers, c.inner_loop_steps, rec)
 
     def last_decode_ms(self):
         ms = C.c_float()

@@ -37,8 +37,8 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_descriptor_layout_matches_header():
-    # mr_model_desc: 19 int32, 3 float, 7 int32, 2 float, 2 uint64 -> 31*4 + 4 pad + 16 = 144
-    assert ctypes.sizeof(hip.ModelDesc) == 144
+    # mr_model_desc: 19 int32, 3 float, 7 int32, 2 float, 2 uint64, 4 float -> 31*4 + 4 pad + 16 + 16 = 160
+    assert ctypes.sizeof(hip.ModelDesc) == 160
     assert ctypes.sizeof(hip._DeviceInfo) == 256 + 64 + 16 + 24
 
 

@@ -153,3 +153,58 @@ def test_persistent_decode_equals_prefill(backend):
     whole = model.prefill(ids, return_all=True)
     model.reset()
     np.testing.assert_array_equal(np.stack([model.decode(int(i)) for i in ids]), whole)
+
+
+def _heavy_variants():
+    from conftest import GOLDEN
+    return sorted(p.stem[len("micro_"):] for p in GOLDEN.glob("micro_heavy-medium-2.0*.npz"))
+
+
+def _choice_logs(choices, cfg):
+    """Expert log and block masks in the reference trace's order (per position,
+    layer and inner loop: attention blocks, then experts)."""
+    s = cfg.source
+    kmax, slots, block = s["router_top_k_max"], s["long_context"]["global_slots"], \
+        s["long_context"]["global_block_size"]
+    experts, masks = [], []
+    for pos in range(choices.shape[0]):
+        count = pos + 1
+        length, blocks = min(cfg.window, count), -(-count // block)
+        for layer in range(cfg.layers):
+            for loop in range(cfg.inner_loop_steps):
+                rec = choices[pos, layer, loop]
+                m = np.zeros((cfg.query_heads, length + blocks), bool)
+                m[:, :length] = True
+                for h in range(cfg.query_heads):
+                    chosen = rec[1 + kmax + h * slots: 1 + kmax + (h + 1) * slots]
+                    m[h, [length + b for b in chosen if b >= 0]] = True
+                masks.append(m)
+                experts.append((layer, -1))
+                experts.extend((layer, int(e)) for e in rec[1:1 + rec[0]])
+    return np.asarray(experts, np.int64).reshape(-1, 2), masks
+
+
+@pytest.mark.parametrize("variant", _heavy_variants())
+def test_heavy_micro_matches_reference(backend, golden_dir, variant):
+    """heavy-medium-2.0 on device: logits, chunked prefill, streams, and the
+    routed experts / adaptive widths / global blocks bit-exact against the
+    reference's own trace."""
+    from test_oracle_model import _load
+    z, bundle, weights = _load(golden_dir, variant)
+    print("case", variant, flush=True)
+    cfg = ModelConfig.from_dict(bundle)
+    model = MiracleModel(cfg, weights, backend=backend, context_length=32)
+    ids = z["ids"]
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), z["logits"], atol=2e-5, rtol=2e-4)
+    experts, masks = _choice_logs(model.engine.choices(), cfg)
+    np.testing.assert_array_equal(experts, z["experts"])
+    widths = z["block_mask_widths"]
+    assert [m.shape[1] for m in masks] == widths.tolist()
+    for i, m in enumerate(masks):
+        np.testing.assert_array_equal(m, z["block_masks"][i, :, :widths[i]])
+    model.reset()
+    chunked = np.concatenate([model.prefill(ids[:5], return_all=True), model.prefill(ids[5:], return_all=True)])
+    np.testing.assert_allclose(chunked, z["chunked"], atol=2e-5, rtol=2e-4)
+    assert model.generate(list(ids[:4]), max_new_tokens=8) == z["greedy"].tolist()
+    assert model.generate([1, 3], max_new_tokens=4, temperature=0.8, top_k=5, top_p=0.9, seed=7) == \
+        z["sampled"].tolist()
