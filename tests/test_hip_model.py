@@ -208,3 +208,38 @@ def test_heavy_micro_matches_reference(backend, golden_dir, variant):
     assert model.generate(list(ids[:4]), max_new_tokens=8) == z["greedy"].tolist()
     assert model.generate([1, 3], max_new_tokens=4, temperature=0.8, top_k=5, top_p=0.9, seed=7) == \
         z["sampled"].tolist()
+
+
+HEAVY_MID = {"family": "heavy-medium-2.0", "vocab_size": 512, "hidden_size": 256, "layers": 2, "query_heads": 4,
+             "kv_heads": 2, "head_dim": 64, "ffn_dim": 128, "max_positions": 256, "window": 32, "latent_dim": 32,
+             "inner_loop_steps": 2, "rope_theta": 1000000.0,
+             "source": {"routed_experts": 16, "router_groups": 4, "router_top_k_max": 4, "router_top_k_min": 2,
+                        "shared_experts": 1, "router_temperature": 1.0,
+                        "long_context": {"global_block_size": 16, "global_slots": 3, "rope_local_fraction": 0.6,
+                                         "alibi_slope_scale": 0.015}},
+             "backend_format": 1}
+
+
+def test_heavy_geometry_matches_oracle(backend):
+    """A BF16 heavy-medium-2.0 geometry over 100 tokens (window overflow, seven
+    blocks, three chosen per head, 16 experts in 4 groups with adaptive width
+    2..4) against the oracle: logits, greedy stream, and every routing choice
+    bit-exact."""
+    from test_oracle_model import _block_masks, _expert_log
+    weights = synthetic.synthetic_weights(HEAVY_MID, 11, "bf16")
+    ids = synthetic.prompt_ids(HEAVY_MID["vocab_size"], 100, 11)
+    trace = []
+    ref = OracleModel(HEAVY_MID, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=160, trace=trace)
+    want = ref.prefill(ids, return_all=True)
+    cfg = ModelConfig.from_dict(HEAVY_MID)
+    model = MiracleModel(cfg, weights, backend=backend, context_length=160)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    experts, masks = _choice_logs(model.engine.choices(), cfg)
+    np.testing.assert_array_equal(experts, _expert_log(trace))
+    ref_masks = _block_masks(trace, ref.cfg, cfg.query_heads)
+    assert len(masks) == len(ref_masks)
+    for ours, theirs in zip(masks, ref_masks):
+        np.testing.assert_array_equal(ours, theirs)
+    stream = ref.generate(list(ids), max_new_tokens=8)
+    assert model.generate(list(ids), max_new_tokens=8) == stream
