@@ -6,6 +6,7 @@
 
 #include "attention.h"
 #include "heavy.h"
+#include "lighting.h"
 #include "linear.h"
 #include "step.h"
 
@@ -39,6 +40,11 @@ struct Layer {
     std::vector<Mlp> experts, shared;
     void **expert_tab = nullptr;       // device [3][experts + shared]: gate, up, down pointers
     float *bsum_k = nullptr, *bsum_v = nullptr;   // [inner][blocks, kvw] running block sums
+    // flashlighting-2.0: qkv packs [Wq; Wlatent], kv_up packs [Wk; Wv]; latent
+    // memory ring of light_cap rows with per-row key/value caches
+    int light_cap = 0;
+    float *arena = nullptr, *positions = nullptr, *counts = nullptr, *kcache = nullptr, *vcache = nullptr;
+    LightState *light = nullptr;
     // caches
     float *ring_k = nullptr, *ring_v = nullptr;        // [capacity, kv_heads*dim] (per inner loop for heavy)
     float *relay_k = nullptr, *relay_v = nullptr;      // flashnano-1.6 relay
@@ -74,6 +80,7 @@ struct mr_model {
     // heavy-medium-2.0 step buffers and the per-position choice log
     float *q_rot = nullptr, *kvbuf = nullptr, *router_out = nullptr, *moe_w = nullptr, *moe_act = nullptr;
     int *moe_ids = nullptr, *moe_active = nullptr;
+    float *lat_new = nullptr, *branch_o = nullptr, *branch_f = nullptr;   // flashlighting-2.0
     int *choices = nullptr;              // [context + 1][layers][inner][choice_rec]
     int choice_rec = 0;                  // ints per record: active, kmax ids, heads x slots blocks
     // step execution: persistent kernel (when the model fits its phases) or

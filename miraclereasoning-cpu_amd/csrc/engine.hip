@@ -461,6 +461,46 @@ int record_heavy_layer(mr_model *m, Layer &L, int li) {
     return MR_OK;
 }
 
+// One flashlighting-2.0 layer (model.py:146-190, 271-279).
+int record_light_layer(mr_model *m, Layer &L) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    GemvArgs g;   // RMSNorm -> [Wq; Wlatent]; the normalized input also feeds the FFN
+    g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
+    g.n = qd + d.latent_dim; g.k = h; g.y = m->qkv; g.x_out = m->xnorm; g.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.qkv.dtype, PRO_RMS, EPI_STORE, g));
+    LightArgs a;
+    a.qlat = m->qkv; a.q_gain = L.q_norm.f(); a.k_gain = L.k_norm.f(); a.latent_gain = L.latent_norm.f();
+    a.eps = d.norm_eps; a.rope = m->rope; a.split_half = d.split_half_rope; a.pos = m->pos_dev;
+    a.done = m->done_dev; a.q_rot = m->q_rot; a.arena = L.arena; a.positions = L.positions; a.counts = L.counts;
+    a.kcache = L.kcache; a.vcache = L.vcache; a.lat_new = m->lat_new; a.kv = m->kvbuf; a.st = L.light;
+    a.out = m->attn; a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.latent = d.latent_dim;
+    a.window = d.window; a.memory_slots = d.memory_slots; a.cap = L.light_cap;
+    MR_TRY(launch_light_prep(s, a));
+    GemvArgs u;   // [Wk; Wv] . new latent row
+    u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
+    MR_TRY(launch_light_store_kv(s, a, false));
+    MR_TRY(launch_light_attend(s, a));
+    GemvArgs um = u;   // [Wk; Wv] . merged row, skipped unless compaction merged
+    um.done = &L.light->skip_merged;
+    MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, um));
+    MR_TRY(launch_light_store_kv(s, a, true));
+    GemvArgs o;
+    o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->branch_o; o.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_STORE, o));
+    GemvArgs gu;
+    gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->xnorm; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act;
+    gu.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_COPY, EPI_SWIGLU, gu));
+    GemvArgs dn;
+    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->branch_f; dn.done = m->done_dev;
+    MR_TRY(launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_STORE, dn));
+    return launch_light_residual(s, m->hidden, m->branch_o, m->branch_f, L.attention_gate.f(), L.ffn_gate.f(),
+                                 d.residual_scale, h, m->done_dev);
+}
+
 int launch_lm_head(mr_model *m) {
     const mr_model_desc &d = m->d;
     const Weight &head = d.tie_embeddings ? m->embed : m->output;
@@ -499,8 +539,9 @@ int record_step(mr_model *m, int kind) {
                                                          m->done_dev, m->hidden, d.hidden_size);
     MR_LAUNCHED("enqueue embed");
     for (int li = 0; li < d.layers; ++li)
-        MR_TRY(d.family == MR_FAMILY_HEAVY_MEDIUM_20 ? record_heavy_layer(m, m->layers[li], li)
-                                                     : record_gqa_layer(m, m->layers[li]));
+        MR_TRY(d.family == MR_FAMILY_HEAVY_MEDIUM_20    ? record_heavy_layer(m, m->layers[li], li)
+               : d.family == MR_FAMILY_FLASHLIGHTING_20 ? record_light_layer(m, m->layers[li])
+                                                        : record_gqa_layer(m, m->layers[li]));
     return record_head(m, kind);
 }
 
@@ -766,6 +807,32 @@ int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     return MR_OK;
 }
 
+// flashlighting-2.0 layer: packed projections, norms, gates and FFN present;
+// latent ring of window + memory_slots + 1 rows with key/value caches.
+int finalize_light_layer(mr_model *m, Layer &L, int i) {
+    const mr_model_desc &d = m->d;
+    const int hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    const std::string at = " in layer " + std::to_string(i);
+    for (const Weight *w : {&L.q_norm, &L.k_norm, &L.latent_norm, &L.attention_gate, &L.ffn_gate, &L.ffn.gate,
+                            &L.ffn.up, &L.ffn.down})
+        if (!w->ptr) return fail(MR_ERR_STATE, "missing flashlighting weight" + at);
+    if (L.qkv.rows != 3) return fail(MR_ERR_STATE, "missing q/latent weight" + at);
+    L.qkv.rows = qd + d.latent_dim;
+    if (L.kv_up.rows != 3) return fail(MR_ERR_STATE, "missing k/v weight" + at);
+    L.kv_up.rows = 2 * kvw;
+    MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
+    L.light_cap = d.window + d.memory_slots + 1;
+    const size_t cap = L.light_cap;
+    MR_TRY(device_alloc(m, cap * d.latent_dim * sizeof(float), (void **)&L.arena));
+    MR_TRY(device_alloc(m, cap * sizeof(float), (void **)&L.positions));
+    MR_TRY(device_alloc(m, cap * sizeof(float), (void **)&L.counts));
+    MR_TRY(device_alloc(m, cap * kvw * sizeof(float), (void **)&L.kcache));
+    MR_TRY(device_alloc(m, cap * kvw * sizeof(float), (void **)&L.vcache));
+    MR_TRY(device_alloc(m, sizeof(LightState), (void **)&L.light));
+    MR_HIP(hipMemset(L.light, 0, sizeof(LightState)), "clear latent state");
+    return MR_OK;
+}
+
 void destroy_graphs(mr_model *m) {
     for (auto &e : m->exec)
         if (e) {
@@ -789,9 +856,8 @@ int mr_model_create(mr_ctx *ctx, const mr_model_desc *desc, mr_model **out) {
                    d.context_length > 0 && d.query_heads % d.kv_heads == 0,
                "invalid model geometry");
     const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20;
-    if (!is_gqa(d.family) && !heavy)
-        return fail(MR_ERR_INVALID, "this library build runs flashnano-1.5/1.6/1.7, flashlite-2.0 and "
-                                    "heavy-medium-2.0; flashlighting-2.0 is not available yet");
+    if (d.family == MR_FAMILY_FLASHLIGHTING_20)
+        MR_REQUIRE(d.latent_dim > 0 && d.window > 0 && d.memory_slots >= 0, "invalid flashlighting-2.0 geometry");
     if (heavy)
         MR_REQUIRE(d.latent_dim > 0 && d.inner_loop_steps >= 1 && d.routed_experts >= 1 &&
                        d.routed_experts <= 256 && d.router_groups >= 1 && d.router_groups <= d.routed_experts &&
@@ -842,8 +908,10 @@ int mr_model_destroy(mr_model *m) {
             free_weight(*w);
         for (Mlp &e : L.experts) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
         for (Mlp &e : L.shared) { free_weight(e.gate); free_weight(e.up); free_weight(e.down); }
-        for (float *p : {L.ring_k, L.ring_v, L.relay_k, L.relay_v, L.pending, L.cbr_queries, L.bsum_k, L.bsum_v})
+        for (float *p : {L.ring_k, L.ring_v, L.relay_k, L.relay_v, L.pending, L.cbr_queries, L.bsum_k, L.bsum_v,
+                         L.arena, L.positions, L.counts, L.kcache, L.vcache})
             if (p) hipFree(p);
+        if (L.light) hipFree(L.light);
         if (L.expert_tab) hipFree(L.expert_tab);
     }
     if (m->choices) hipFree(m->choices);
@@ -893,15 +961,19 @@ int mr_model_set_weight(mr_model *m, int kind, int layer, int expert, const void
         L.qkv.rows |= kind == MR_W_Q ? 1 : kind == MR_W_K ? 2 : 4;   // presence bits until finalize
         return MR_OK;
     }
-    if (m->d.family == MR_FAMILY_HEAVY_MEDIUM_20 &&
-        (kind == MR_W_Q || kind == MR_W_LATENT || kind == MR_W_ROUTER_COARSE || kind == MR_W_ROUTER_FINE)) {
-        // Pack [Wq; Wlatent] and [Wcoarse; Wfine]: one GEMV each.
+    const bool lighting = m->d.family == MR_FAMILY_FLASHLIGHTING_20;
+    if ((m->d.family == MR_FAMILY_HEAVY_MEDIUM_20 &&
+         (kind == MR_W_Q || kind == MR_W_LATENT || kind == MR_W_ROUTER_COARSE || kind == MR_W_ROUTER_FINE)) ||
+        (lighting && (kind == MR_W_Q || kind == MR_W_LATENT || kind == MR_W_K || kind == MR_W_V))) {
+        // Pack [Wq; Wlatent], [Wcoarse; Wfine] and [Wk; Wv]: one GEMV each.
         Layer &L = m->layers[layer];
         const bool qpair = kind == MR_W_Q || kind == MR_W_LATENT;
-        Weight &w = qpair ? L.qkv : L.router;
-        const int64_t h = m->d.hidden_size;
-        const int64_t first = qpair ? (int64_t)m->d.query_heads * m->d.head_dim : m->d.router_groups;
-        const int64_t second = qpair ? m->d.latent_dim : m->d.routed_experts;
+        const bool kvpair = kind == MR_W_K || kind == MR_W_V;
+        Weight &w = qpair ? L.qkv : kvpair ? L.kv_up : L.router;
+        const int64_t kvw = (int64_t)L.kv_heads * m->d.head_dim;
+        const int64_t h = kvpair ? m->d.latent_dim : m->d.hidden_size;
+        const int64_t first = qpair ? (int64_t)m->d.query_heads * m->d.head_dim : kvpair ? kvw : m->d.router_groups;
+        const int64_t second = qpair ? m->d.latent_dim : kvpair ? kvw : m->d.routed_experts;
         if (!w.ptr) {
             MR_TRY(device_alloc(m, (size_t)(first + second) * h * dtype_bytes(dtype), &w.ptr));
             w.dtype = dtype;
@@ -909,7 +981,7 @@ int mr_model_set_weight(mr_model *m, int kind, int layer, int expert, const void
             w.cols = h;
         }
         MR_REQUIRE(w.dtype == dtype, "set_weight: packed projections must share one dtype");
-        const bool lead = kind == MR_W_Q || kind == MR_W_ROUTER_COARSE;
+        const bool lead = kind == MR_W_Q || kind == MR_W_ROUTER_COARSE || kind == MR_W_K;
         char *dst = (char *)w.ptr + (size_t)(lead ? 0 : first) * h * dtype_bytes(dtype);
         MR_HIP(hipMemcpy(dst, host, (size_t)rows * cols * dtype_bytes(dtype), hipMemcpyHostToDevice),
                "upload weight");
@@ -964,12 +1036,19 @@ int mr_model_finalize(mr_model *m) {
     int max_kvw = 0, max_kvh = 0;
     size_t max_part = 0;
     const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20;
+    const bool lighting = d.family == MR_FAMILY_FLASHLIGHTING_20;
     const int inner = heavy ? d.inner_loop_steps : 1;
     for (int i = 0; i < d.layers; ++i) {
         Layer &L = m->layers[i];
         MR_TRY(need(L.a_norm, "a_norm", i));
-        MR_TRY(need(L.f_norm, "f_norm", i));
         MR_TRY(need(L.o, "o", i));
+        if (lighting) {
+            MR_TRY(finalize_light_layer(m, L, i));
+            max_kvw = std::max(max_kvw, L.kv_heads * hd);
+            max_kvh = std::max(max_kvh, L.kv_heads);
+            continue;
+        }
+        MR_TRY(need(L.f_norm, "f_norm", i));
         if (heavy) {
             MR_TRY(finalize_heavy_layer(m, L, i));
             max_kvw = std::max(max_kvw, L.kv_heads * hd);
@@ -1028,8 +1107,11 @@ int mr_model_finalize(mr_model *m) {
     size_t o_xnorm = take((size_t)h * sizeof(float));
     size_t o_qkv = take((size_t)(qd + std::max(2 * max_kvw, d.latent_dim)) * sizeof(float));
     const int kmax = std::max(d.router_top_k_max, 1), moe_slots = kmax + d.shared_experts;
-    size_t o_qrot = take(heavy ? (size_t)qd * sizeof(float) : 0);
-    size_t o_kvbuf = take(heavy ? (size_t)2 * max_kvw * sizeof(float) : 0);
+    const bool latent_family = heavy || lighting;
+    size_t o_qrot = take(latent_family ? (size_t)qd * sizeof(float) : 0);
+    size_t o_kvbuf = take(latent_family ? (size_t)2 * max_kvw * sizeof(float) : 0);
+    size_t o_latnew = take(lighting ? (size_t)d.latent_dim * sizeof(float) : 0);
+    size_t o_branch = take(lighting ? (size_t)2 * h * sizeof(float) : 0);
     size_t o_router = take(heavy ? (size_t)(d.router_groups + d.routed_experts) * sizeof(float) : 0);
     size_t o_moe_ids = take(heavy ? (size_t)(kmax + 1) * sizeof(int) : 0);
     size_t o_moe_w = take(heavy ? (size_t)kmax * sizeof(float) : 0);
@@ -1064,9 +1146,16 @@ int mr_model_finalize(mr_model *m) {
     m->cbr_pooled = (float *)(base + o_pool);
     m->cbr_anchor = (float *)(base + o_anchor);
     m->cbr_kv = (float *)(base + o_cbrkv);
-    if (heavy) {
+    if (latent_family) {
         m->q_rot = (float *)(base + o_qrot);
         m->kvbuf = (float *)(base + o_kvbuf);
+    }
+    if (lighting) {
+        m->lat_new = (float *)(base + o_latnew);
+        m->branch_o = (float *)(base + o_branch);
+        m->branch_f = m->branch_o + h;
+    }
+    if (heavy) {
         m->router_out = (float *)(base + o_router);
         m->moe_ids = (int *)(base + o_moe_ids);
         m->moe_active = m->moe_ids + kmax;
@@ -1091,6 +1180,8 @@ int mr_model_reset(mr_model *m) {
     // Caches are overwritten before they are read (ring rows by position, the
     // relay by chunk), so a reset only rewinds the position.
     MR_HIP(hipMemsetAsync(m->pos_dev, 0, 4 * sizeof(int), m->ctx->stream), "reset position");
+    for (mr::Layer &L : m->layers)   // latent memory starts empty
+        if (L.light) MR_HIP(hipMemsetAsync(L.light, 0, sizeof(mr::LightState), m->ctx->stream), "reset latent memory");
     if (m->persistent_ok) {   // epochs restart with the position
         MR_HIP(hipMemsetAsync(m->cells, 0, m->cell_count * sizeof(uint64_t), m->ctx->stream), "reset step cells");
         MR_HIP(hipMemsetAsync(m->sync, 0, m->sync_count * sizeof(unsigned), m->ctx->stream), "reset step counters");

@@ -1,0 +1,47 @@
+// flashlighting-2.0 token-step kernels (model.py:146-190): latent memory with
+// per-row key/value caches, window masking of non-memory rows, and compaction
+// (two oldest rows merged by their counts, or dropped without memory slots).
+#pragma once
+
+#include "common.h"
+
+namespace mr {
+
+// Device state of one layer's latent memory: rows live in a ring of `cap`
+// slots; logical row t is slot (start + t) % cap.
+struct LightState {
+    int start, rows, memory, skip_merged, merged_slot, pad[3];
+};
+
+struct LightArgs {
+    const float *qlat = nullptr;     // [heads*d + latent] raw Q and latent projections
+    const float *q_gain = nullptr, *k_gain = nullptr, *latent_gain = nullptr;
+    float eps = 0.0f;
+    const float *rope = nullptr;     // [positions][d/2][2] cos, sin
+    int split_half = 0;
+    const int *pos = nullptr, *done = nullptr;
+    float *q_rot = nullptr;          // [heads*d]
+    float *arena = nullptr;          // [cap, latent] latent rows
+    float *positions = nullptr;      // [cap] row positions (integers)
+    float *counts = nullptr;         // [cap] rows folded into each row
+    float *kcache = nullptr, *vcache = nullptr;   // [cap, kv_heads*d] keys (normed, rotated) and values
+    float *lat_new = nullptr;        // [latent] the row whose K/V the next projection computes
+    const float *kv = nullptr;       // [2*kv_heads*d] that projection's output
+    LightState *st = nullptr;
+    float *out = nullptr;            // [heads*d] attended values
+    int heads = 0, kv_heads = 0, d = 0, latent = 0, window = 0, memory_slots = 0, cap = 0;
+};
+
+// Queries, the new latent row (appended), then - after the K/V projection of
+// lat_new - its key/value cache row.
+int launch_light_prep(hipStream_t s, const LightArgs &a);
+int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged);
+// Attention over every row, then compaction (which leaves the merged row in
+// lat_new and clears skip_merged when a merge happened).
+int launch_light_attend(hipStream_t s, const LightArgs &a);
+
+// hidden += rs * ((0 + ag * o) + fg * f)  (model.py:171-176 parallel gated residual)
+int launch_light_residual(hipStream_t s, float *hidden, const float *o, const float *f, const float *attention_gate,
+                          const float *ffn_gate, float rs, int n, const int *done);
+
+}  // namespace mr

@@ -16,7 +16,7 @@ from oracle.model import OracleModel
 
 pytestmark = pytest.mark.gpu
 
-GQA = ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
+GQA = ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0", "flashlighting-2.0")
 
 
 def _variants():
@@ -243,3 +243,26 @@ def test_heavy_geometry_matches_oracle(backend):
         np.testing.assert_array_equal(ours, theirs)
     stream = ref.generate(list(ids), max_new_tokens=8)
     assert model.generate(list(ids), max_new_tokens=8) == stream
+
+
+LIGHT_MID = {"family": "flashlighting-2.0", "vocab_size": 512, "hidden_size": 256, "layers": 2, "query_heads": 4,
+             "kv_heads": 4, "head_dim": 64, "ffn_dim": 384, "max_positions": 4096, "window": 24, "latent_dim": 32,
+             "memory_slots": 4, "rope_theta": 1000000.0,
+             "source": {"rope_scaling_type": "yarn", "rope_scaling_factor": 4.0, "max_position_embeddings": 64},
+             "backend_format": 1}
+
+
+@pytest.mark.parametrize("slots", [4, 0])
+def test_lighting_geometry_matches_oracle(backend, slots):
+    """A BF16 flashlighting-2.0 geometry over 90 tokens: YaRN RoPE, latent rows
+    past the window merged into memory slots (or dropped without slots), against
+    the oracle's logits and greedy stream."""
+    config = dict(LIGHT_MID, memory_slots=slots)
+    weights = synthetic.synthetic_weights(config, 13, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 90, 13)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=128)
+    want = ref.prefill(ids, return_all=True)
+    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=128)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    assert model.generate(list(ids), max_new_tokens=8) == ref.generate(list(ids), max_new_tokens=8)
