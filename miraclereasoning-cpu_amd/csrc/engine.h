@@ -8,6 +8,7 @@
 #include "heavy.h"
 #include "lighting.h"
 #include "linear.h"
+#include "prefill.h"
 #include "step.h"
 
 namespace mr {
@@ -110,6 +111,9 @@ struct mr_model {
     float *best_val = nullptr;
     int *best_idx = nullptr, *bad = nullptr;
     float last_ms = 0.0f;                // device time of the last greedy loop
+    // batched prefill workspace, grown on demand
+    void *pf = nullptr;
+    size_t pf_bytes = 0;
     std::array<hipGraphExec_t, mr::STEP_KINDS> exec{};
     std::array<int, mr::STEP_KINDS> eager_runs{};
 };

@@ -27,6 +27,13 @@ bool is_gqa(int family) {
            family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
 }
 
+// Families whose prompt can run as whole-chunk kernels: attention state is the
+// ring alone (flashnano-1.6's relay rows, the latent memory and the heavy
+// caches change token by token and take the token loop).
+bool batched_prefill_family(int family) {
+    return family == MR_FAMILY_FLASHNANO_15 || family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
+}
+
 int dtype_bytes(int dt) { return dt == MR_F32 ? 4 : 2; }
 
 __device__ __forceinline__ float widen_any(const void *p, int dt, int64_t i) {
@@ -918,6 +925,7 @@ int mr_model_destroy(mr_model *m) {
     if (m->freq) hipFree(m->freq);
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
+    if (m->pf) hipFree(m->pf);
     for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_cells, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);
@@ -1221,6 +1229,129 @@ int mr_model_last_decode_ms(mr_model *m, float *ms) {
     return MR_OK;
 }
 
+namespace {
+
+__global__ void k_set_int(int *p, int v) { *p = v; }
+
+constexpr int kPrefillRows = 4096;   // prompt rows per batched prefill chunk
+
+// One chunk's activations (FP32, rows of the chunk): hidden, normalized input,
+// q|k|v, attended values, SwiGLU activations and, with return_all, logits.
+struct PrefillWs {
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *lg = nullptr;
+};
+
+int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
+    const mr_model_desc &d = m->d;
+    int max_kvw = 0;
+    for (const Layer &L : m->layers) max_kvw = std::max(max_kvw, L.kv_heads * d.head_dim);
+    const size_t r = (size_t)rows, qd = (size_t)d.query_heads * d.head_dim;
+    auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
+    const size_t sizes[6] = {up(r * d.hidden_size), up(r * d.hidden_size), up(r * (qd + 2 * (size_t)max_kvw)),
+                             up(r * qd), up(r * d.ffn_dim), all ? up(r * d.vocab_size) : 0};
+    size_t total = 0;
+    for (size_t z : sizes) total += z;
+    total *= sizeof(float);
+    if (total > m->pf_bytes) {
+        MR_HIP(hipStreamSynchronize(m->ctx->stream), "prefill workspace");
+        if (m->pf) hipFree(m->pf);
+        m->pf = nullptr;
+        m->pf_bytes = 0;
+        MR_TRY(device_alloc(m, total, &m->pf));
+        m->pf_bytes = total;
+    }
+    float *p = (float *)m->pf;
+    float **slots[6] = {&w->x, &w->xn, &w->qkv, &w->att, &w->act, &w->lg};
+    for (int i = 0; i < 6; ++i) {
+        *slots[i] = sizes[i] ? p : nullptr;
+        p += sizes[i];
+    }
+    return MR_OK;
+}
+
+// Batched prefill of ids already in ids_dev[position .. position + n): every
+// layer runs once per chunk of up to kPrefillRows rows, projections as MFMA
+// GEMMs, attention over the chunk's keys plus the ring, then the chunk's last
+// min(rows, capacity) keys/values go into the ring.  Leaves the last row's
+// logits in m->logits (as the token loop does) and advances the position.
+int prefill_batched(mr_model *m, int n, bool all, float *logits) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, V = d.vocab_size;
+    MR_REQUIRE(h % 8 == 0 && ffn % 8 == 0 && qd % 8 == 0 && hd % 4 == 0 && hd <= 128,
+               "batched prefill: hidden, ffn and query widths must be multiples of 8 and head_dim a multiple of 4 "
+               "up to 128");
+    const int chunk = std::min(n, kPrefillRows);
+    PrefillWs w;
+    MR_TRY(prefill_workspace(m, chunk, all, &w));
+    const Weight &head = d.tie_embeddings ? m->embed : m->output;
+    for (int start = 0; start < n; start += chunk) {
+        const int T = std::min(chunk, n - start), p0 = m->position + start;
+        MR_TRY(launch_embed_rows(s, m->embed.ptr, m->embed.dtype, m->ids_dev, p0, T, w.x, h));
+        for (Layer &L : m->layers) {
+            const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
+            MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+            GemmArgs g;
+            g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
+            g.m = T; g.n = ld; g.k = h;
+            MR_TRY(launch_gemm(s, GEMM_STORE, g));
+            MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
+                                  d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
+                                  d.norm_eps, d.qk_norm, m->rope, d.split_half_rope));
+            PrefillAttnArgs a;
+            a.qkv = w.qkv; a.ld = ld; a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.cap = L.capacity;
+            a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
+            a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+            MR_TRY(launch_prefill_attention(s, a));
+            MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
+            GemmArgs o;
+            o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
+            o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale;
+            MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
+            MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
+            GemmArgs gu;
+            gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
+            gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
+            MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
+            GemmArgs dn;
+            dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;
+            dn.m = T; dn.n = h; dn.k = ffn; dn.scale = d.residual_scale;
+            MR_TRY(launch_gemm(s, GEMM_RESIDUAL, dn));
+        }
+        if (all) {
+            MR_TRY(launch_rms_rows(s, w.x, h, m->norm.f(), d.norm_eps, h, w.xn, h, T));
+            GemmArgs lm;
+            lm.a = w.xn; lm.lda = h; lm.w = head.ptr; lm.dtype = head.dtype; lm.c = w.lg; lm.ldc = V;
+            lm.m = T; lm.n = V; lm.k = h;
+            MR_TRY(launch_gemm(s, GEMM_STORE, lm));
+            if (logits)
+                MR_HIP(hipMemcpyAsync(logits + (size_t)start * V, w.lg, (size_t)T * V * sizeof(float),
+                                      hipMemcpyDeviceToHost, s),
+                       "read logits");
+            if (start + T == n)
+                MR_HIP(hipMemcpyAsync(m->logits, w.lg + (size_t)(T - 1) * V, (size_t)V * sizeof(float),
+                                      hipMemcpyDeviceToDevice, s),
+                       "keep last logits");
+        } else if (start + T == n) {
+            MR_HIP(hipMemcpyAsync(m->hidden, w.x + (size_t)(T - 1) * h, (size_t)h * sizeof(float),
+                                  hipMemcpyDeviceToDevice, s),
+                   "keep last hidden row");
+            MR_TRY(launch_lm_head(m));
+            if (logits)
+                MR_HIP(hipMemcpyAsync(logits, m->logits, (size_t)V * sizeof(float), hipMemcpyDeviceToHost, s),
+                       "read logits");
+        }
+    }
+    k_set_int<<<1, 1, 0, s>>>(m->pos_dev, m->position + n);
+    MR_LAUNCHED("enqueue position update");
+    MR_HIP(hipStreamSynchronize(s), "batched prefill");
+    MR_TRY(check_step_error(m));
+    m->position += n;
+    return MR_OK;
+}
+
+}  // namespace
+
 int mr_model_forward(mr_model *m, const int32_t *ids, int n, int flags, float *logits) {
     MR_TRY(check_ctx(m, "forward"));
     MR_REQUIRE(ids && n > 0, "forward: input_ids must be a non-empty 1D integer sequence");
@@ -1229,13 +1360,12 @@ int mr_model_forward(mr_model *m, const int32_t *ids, int n, int flags, float *l
         MR_REQUIRE(ids[i] >= 0 && ids[i] < d.vocab_size, "forward: input token is outside the vocabulary");
     if (m->position + n > d.context_length)
         return fail(MR_ERR_INVALID, "input would exceed context_length; reset or allocate a larger context");
-    if (flags & MR_FWD_BATCHED)
-        return fail(MR_ERR_INVALID, "forward: batched prefill is not available in this build");
     hipStream_t s = m->ctx->stream;
     MR_HIP(hipMemcpyAsync(m->ids_dev + m->position, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s),
            "upload token ids");
     MR_HIP(hipMemsetAsync(m->done_dev, 0, sizeof(int), s), "clear stop flag");
     const bool all = (flags & MR_FWD_RETURN_ALL) != 0;
+    if ((flags & MR_FWD_BATCHED) && n > 1 && batched_prefill_family(d.family)) return prefill_batched(m, n, all, logits);
     for (int i = 0; i < n; ++i) {
         const bool want = all || i == n - 1;
         MR_TRY(run_step(m, want ? STEP_LOGITS : STEP_PLAIN));

@@ -1,0 +1,43 @@
+// Batched prefill for the GQA families: a whole prompt chunk per kernel, with
+// the projections on the matrix cores (gemm.h) and causal windowed attention
+// over the chunk's own keys plus the ring (keys of earlier positions).
+#pragma once
+
+#include "gemm.h"
+
+namespace mr {
+
+struct PrefillAttnArgs {
+    const float *qkv = nullptr;     // [rows, ld]: q (heads*d) | k (kvw) | v (kvw), normalized and rotated
+    int ld = 0;
+    const float *ring_k = nullptr;  // [cap, kvw]: position p < p0 at slot p % cap
+    const float *ring_v = nullptr;
+    int cap = 0;                    // ring rows = attention window (model.py:105)
+    float *out = nullptr;           // [rows, ldo] attended values per query head
+    int ldo = 0;
+    int p0 = 0, rows = 0;           // position of row 0, rows in the chunk
+    int heads = 0, kv_heads = 0, d = 0;
+    float inv_root = 1.0f;          // 1 / sqrt(d)
+};
+
+// out = softmax(q . k / sqrt(d)) . v per query head over the keys at
+// positions max(0, p - cap + 1) .. p of each query position p.
+int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a);
+
+// y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * gain (gain may be null).
+int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width, float *y,
+                    int ldy, int rows);
+
+// Per-head RMSNorm (q_norm / k_norm, when `norm`) and RoPE at position p0 + r of
+// the q and k heads of each qkv row, in place (model.py:100-103).
+int launch_qk_rows(hipStream_t s, float *qkv, int ld, int rows, int p0, int heads, int kv_heads, int d,
+                   const float *q_gain, const float *k_gain, float eps, int norm, const float *rope, int split_half);
+
+// Ring rows of the chunk's last min(rows, cap) positions (model.py:21-25).
+int launch_ring_store(hipStream_t s, const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,
+                      int p0, int rows);
+
+// x[r] = embed[ids[p0 + r]] widened to FP32 (model.py:259).
+int launch_embed_rows(hipStream_t s, const void *table, int dtype, const int *ids, int p0, int rows, float *x, int h);
+
+}  // namespace mr

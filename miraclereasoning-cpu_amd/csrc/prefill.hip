@@ -1,0 +1,289 @@
+// Batched prefill kernels for the GQA families (model.py:95-116, 257-285 over a
+// prompt chunk): row RMSNorm, per-head norm + RoPE, causal windowed attention
+// on the matrix cores, ring fill, embedding gather.
+//
+// Attention (k_attn_prefill) works in transposed form so that no operand ever
+// changes lanes: with v_mfma_f32_16x16x4f32 (lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16], and holds C[4 (l / 16) + j][l % 16]),
+//   S^T = K . Q^T     leaves lane l the scores of query l % 16 against keys
+//                     4 (l / 16) + j of each 16-key tile;
+//   O^T += V^T . P^T  takes exactly those probabilities as its B operand when
+//                     k-step s of a 16-key tile covers keys 4 (l / 16) + s,
+// and O^T's C layout again gives lane l query l % 16 (dims 4 (l / 16) + j), so
+// the running max, sum and rescale of the online softmax are per lane.
+#include "prefill.h"
+
+#include <algorithm>
+
+namespace mr {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kKeys = 32;        // keys per LDS tile
+constexpr int kAttnThreads = 256;
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// grid (ceil(rows / (64 / gb)), kv_heads * G / gb), 256 threads.  A workgroup
+// serves gb query heads of one KV group (gb = 4, 2 or 1) on 64 / gb query
+// rows: wave w takes head (w % gb) and rows 16 (w / gb) .. +15.
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a, int gb) {
+    constexpr int NG = D / 16;                                   // 16-dim groups
+    constexpr int KP = D + 4;                                    // LDS pitch of key rows (floats)
+    constexpr int VP = kKeys + 4;                                // LDS pitch of value columns
+    constexpr int NL = (kKeys * (D / 4) + kAttnThreads - 1) / kAttnThreads;   // float4 per thread
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * KP];   // ks[key][dim]
+    __shared__ __attribute__((aligned(16))) float vt[D * VP];       // vt[dim][key]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 / gb;
+    const int kh = blockIdx.y / sub_groups, hsub = blockIdx.y % sub_groups;
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * tile_rows;   // latest rows (most keys) first
+    const int h = kh * G + hsub * gb + wave % gb;
+    const int tq = t0 + (wave / gb) * 16 + lr;                  // this lane's query row
+    const bool qvalid = tq < a.rows;
+    const int qp = a.p0 + tq;
+    const int d = a.d, kvw = a.kv_heads * d, qd = a.heads * d;
+
+    float4 q[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int dim = g * 16 + 4 * lq;
+        q[g] = qvalid && dim < d ? load_f4(a.qkv + (int64_t)tq * a.ld + h * d + dim) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    const int last = min(t0 + tile_rows, a.rows) - 1;
+    const int klo = max(0, a.p0 + t0 - a.cap + 1), khi = a.p0 + last;
+    const int ntiles = (khi - klo) / kKeys + 1;
+
+    float4 kr[NL], vr[NL];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = tid + kAttnThreads * i;
+            kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            const int r = e / (D / 4), c = (e % (D / 4)) * 4, kp = kb + r;
+            if (e < kKeys * (D / 4) && kp <= khi && c < d) {
+                const float *kbase, *vbase;
+                if (kp >= a.p0) {
+                    kbase = a.qkv + (int64_t)(kp - a.p0) * a.ld + qd + kh * d;
+                    vbase = kbase + kvw;
+                } else {
+                    const int64_t slot = kp % a.cap;
+                    kbase = a.ring_k + slot * kvw + kh * d;
+                    vbase = a.ring_v + slot * kvw + kh * d;
+                }
+                kr[i] = load_f4(kbase + c);
+                vr[i] = load_f4(vbase + c);
+            }
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = tid + kAttnThreads * i;
+            if (e < kKeys * (D / 4)) {
+                const int r = e / (D / 4), c = (e % (D / 4)) * 4;
+                *(float4 *)&ks[r * KP + c] = kr[i];
+                vt[(c + 0) * VP + r] = vr[i].x;
+                vt[(c + 1) * VP + r] = vr[i].y;
+                vt[(c + 2) * VP + r] = vr[i].z;
+                vt[(c + 3) * VP + r] = vr[i].w;
+            }
+        }
+    };
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 o[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) o[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    fetch(klo);
+    for (int it = 0; it < ntiles; ++it) {
+        const int kb = klo + it * kKeys;
+        if (it) lds_barrier();
+        stash();
+        lds_barrier();
+        if (it + 1 < ntiles) fetch(kb + kKeys);
+
+        f32x4 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            sc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const float4 kk = *(const float4 *)&ks[(t * 16 + lr) * KP + g * 16 + 4 * lq];
+                sc[t] = mfma4(kk.x, q[g].x, sc[t]);
+                sc[t] = mfma4(kk.y, q[g].y, sc[t]);
+                sc[t] = mfma4(kk.z, q[g].z, sc[t]);
+                sc[t] = mfma4(kk.w, q[g].w, sc[t]);
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int kp = kb + t * 16 + 4 * lq + j;
+                const bool ok = qvalid && kp <= qp && kp > qp - a.cap;
+                const float v = ok ? sc[t][j] * a.inv_root : -INFINITY;
+                sc[t][j] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = expf(m_run - m_ref);
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p = expf(sc[t][j] - m_ref);
+                sc[t][j] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) o[g] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const float4 vv = *(const float4 *)&vt[(g * 16 + lr) * VP + t * 16 + 4 * lq];
+                o[g] = mfma4(vv.x, sc[t][0], o[g]);
+                o[g] = mfma4(vv.y, sc[t][1], o[g]);
+                o[g] = mfma4(vv.z, sc[t][2], o[g]);
+                o[g] = mfma4(vv.w, sc[t][3], o[g]);
+            }
+    }
+    if (!qvalid) return;
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int dim = g * 16 + 4 * lq;
+        if (dim < d)
+            *(float4 *)(a.out + (int64_t)tq * a.ldo + h * d + dim) =
+                make_float4(o[g][0] * inv, o[g][1] * inv, o[g][2] * inv, o[g][3] * inv);
+    }
+}
+
+__global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const float *gain, float eps, int width,
+                                                  float *y, int ldy) {
+    __shared__ float red[4];
+    const float *xr = x + (int64_t)blockIdx.x * ldx;
+    float *yr = y + (int64_t)blockIdx.x * ldy;
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) ss += xr[j] * xr[j];
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)width + eps);
+    for (int j = threadIdx.x; j < width; j += blockDim.x) yr[j] = xr[j] * scale * (gain ? gain[j] : 1.0f);
+}
+
+// grid (rows, ceil((heads + kv_heads) / 4)), 256 threads: one wave per head.
+__global__ void __launch_bounds__(256) k_qk_rows(float *qkv, int ld, int p0, int heads, int kv_heads, int d,
+                                                 const float *q_gain, const float *k_gain, float eps, int norm,
+                                                 const float *rope, int split_half) {
+    const int lane = threadIdx.x & 63, hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (hh >= heads + kv_heads) return;
+    float *row = qkv + (int64_t)blockIdx.x * ld + (int64_t)hh * d;   // k heads follow the q heads
+    const float *gain = hh < heads ? q_gain : k_gain;
+    float scale = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+        for (int j = lane; j < d; j += kWave) ss += row[j] * row[j];
+        scale = 1.0f / sqrtf(wave_sum(ss) / (float)d + eps);
+    }
+    const int half = d / 2;
+    const float *cs = rope + (int64_t)(p0 + (int)blockIdx.x) * half * 2;
+    for (int i = lane; i < half; i += kWave) {
+        const int j = split_half ? i : 2 * i, k = split_half ? i + half : 2 * i + 1;
+        float u = row[j], v = row[k];
+        if (norm) {
+            u = u * scale * (gain ? gain[j] : 1.0f);
+            v = v * scale * (gain ? gain[k] : 1.0f);
+        }
+        rope_rotate(u, v, cs[2 * i], cs[2 * i + 1]);
+        row[j] = u;
+        row[k] = v;
+    }
+}
+
+__global__ void k_ring_store(const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,
+                             int first, int p0) {
+    const int p = first + blockIdx.x;
+    const float *src = qkv + (int64_t)(p - p0) * ld + qd;
+    const int64_t slot = p % cap;
+    for (int j = threadIdx.x; j < kvw; j += blockDim.x) {
+        ring_k[slot * kvw + j] = src[j];
+        ring_v[slot * kvw + j] = src[kvw + j];
+    }
+}
+
+__global__ void k_embed_rows(const void *table, int dt, const int *ids, int p0, float *x, int h) {
+    const int64_t base = (int64_t)ids[p0 + blockIdx.x] * h;
+    float *xr = x + (int64_t)blockIdx.x * h;
+    for (int j = threadIdx.x; j < h; j += blockDim.x) {
+        if (dt == MR_F32) xr[j] = ((const float *)table)[base + j];
+        else if (dt == MR_BF16) xr[j] = bf16_to_f32(((const uint16_t *)table)[base + j]);
+        else xr[j] = f16_to_f32(((const uint16_t *)table)[base + j]);
+    }
+}
+
+}  // namespace
+
+int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
+    MR_REQUIRE(a.qkv && a.ring_k && a.ring_v && a.out && a.rows > 0 && a.cap > 0, "prefill attention: bad arguments");
+    MR_REQUIRE(a.kv_heads > 0 && a.heads % a.kv_heads == 0, "prefill attention: heads must be a multiple of kv_heads");
+    MR_REQUIRE(a.d % 4 == 0 && a.d <= 128 && a.ld % 4 == 0 && a.ldo % 4 == 0,
+               "prefill attention: head_dim must be a multiple of 4 and at most 128");
+    const int G = a.heads / a.kv_heads;
+    const int gb = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+    const dim3 grid(ceil_div(a.rows, 64 / gb), a.kv_heads * (G / gb));
+    if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else if (a.d <= 32) k_attn_prefill<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else if (a.d <= 64) k_attn_prefill<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else k_attn_prefill<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    MR_LAUNCHED("enqueue prefill attention");
+    return MR_OK;
+}
+
+int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width, float *y,
+                    int ldy, int rows) {
+    k_rms_rows<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, y, ldy);
+    MR_LAUNCHED("enqueue row RMSNorm");
+    return MR_OK;
+}
+
+int launch_qk_rows(hipStream_t s, float *qkv, int ld, int rows, int p0, int heads, int kv_heads, int d,
+                   const float *q_gain, const float *k_gain, float eps, int norm, const float *rope, int split_half) {
+    k_qk_rows<<<dim3(rows, ceil_div(heads + kv_heads, 4)), 256, 0, s>>>(qkv, ld, p0, heads, kv_heads, d, q_gain,
+                                                                       k_gain, eps, norm, rope, split_half);
+    MR_LAUNCHED("enqueue q/k norm and RoPE");
+    return MR_OK;
+}
+
+int launch_ring_store(hipStream_t s, const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,
+                      int p0, int rows) {
+    const int first = std::max(p0, p0 + rows - cap);
+    k_ring_store<<<p0 + rows - first, 256, 0, s>>>(qkv, ld, qd, kvw, ring_k, ring_v, cap, first, p0);
+    MR_LAUNCHED("enqueue ring fill");
+    return MR_OK;
+}
+
+int launch_embed_rows(hipStream_t s, const void *table, int dtype, const int *ids, int p0, int rows, float *x, int h) {
+    k_embed_rows<<<rows, 256, 0, s>>>(table, dtype, ids, p0, x, h);
+    MR_LAUNCHED("enqueue embedding rows");
+    return MR_OK;
+}
+
+}  // namespace mr
