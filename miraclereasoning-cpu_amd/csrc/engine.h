@@ -99,7 +99,7 @@ struct mr_model {
     uint64_t *c_hidden = nullptr, *c_qkv = nullptr, *c_attn = nullptr, *c_act = nullptr;
     unsigned *sync = nullptr;
     size_t sync_count = 0;
-    // progress words: the stream waves' [grid * kStreamWaves], then the merged
+    // progress words: one per workgroup [grid], then the merged
     // attention heads' [layers * query_heads]
     unsigned *words = nullptr;
     size_t word_count = 0;

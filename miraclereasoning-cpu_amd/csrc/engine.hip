@@ -565,7 +565,7 @@ int run_persistent(mr_model *m, int kind, unsigned long long *trace = nullptr) {
     a.eos = m->eos_dev; a.err = m->err; a.exits = m->sync + m->sync_count - 1;
     a.best_val = m->best_val; a.best_idx = m->best_idx; a.bad = m->bad;
     a.embed = m->embed.ptr; a.embed_dtype = m->embed.dtype; a.dummy = m->dummy; a.xbuf = m->xbuf;
-    a.progress = m->words; a.nprogress = m->grid * kStreamWaves;
+    a.progress = m->words; a.nprogress = m->grid;
     return launch_step(m->ctx->stream, a, m->grid, m->step_lds);
 }
 
@@ -643,7 +643,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         Phase a;
         a.kind = PH_ATTN;
         a.x_phase = qkv_at;
-        a.heads_done = m->words + (size_t)m->grid * kStreamWaves + (size_t)li * d.query_heads;
+        a.heads_done = m->words + (size_t)m->grid + (size_t)li * d.query_heads;
         AttnStepArgs &t = a.at.s;
         t.q = (const float *)m->c_qkv;
         t.k_new = (const float *)(m->c_qkv + qd);
@@ -738,7 +738,7 @@ int setup_persistent(mr_model *m) {
     m->c_act = m->c_attn + n_attn;
     m->sync_count = 1;   // the launch exit counter
     MR_TRY(device_alloc(m, m->sync_count * sizeof(unsigned), (void **)&m->sync));
-    m->word_count = (size_t)m->grid * kStreamWaves + (size_t)d.layers * d.query_heads;
+    m->word_count = (size_t)m->grid + (size_t)d.layers * d.query_heads;
     MR_TRY(device_alloc(m, m->word_count * sizeof(unsigned), (void **)&m->words));
     MR_HIP(hipMemset(m->words, 0, m->word_count * sizeof(unsigned)), "clear step progress");
     m->part_cell_count = 0;

@@ -49,7 +49,7 @@ struct StepArgs {
     int *pos = nullptr, *done = nullptr, *ids = nullptr, *gen = nullptr, *count = nullptr;
     const int *eos = nullptr;
     int *err = nullptr;                 // 1 = a wait timed out
-    unsigned *progress = nullptr;       // [grid * kStreamWaves] progress words of the stream waves
+    unsigned *progress = nullptr;       // [grid] progress words, one per workgroup
     int nprogress = 0;
     unsigned *exits = nullptr;          // workgroups that left this launch (last one finishes)
     float *best_val = nullptr;          // [grid] per-workgroup argmax partials

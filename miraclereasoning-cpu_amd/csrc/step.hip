@@ -71,6 +71,18 @@ __device__ __forceinline__ void stamp(unsigned long long *tr, int i) {
 // waves fill the other for the next phase) and take the RMSNorm sum.
 constexpr int NC = kControlWaves;
 constexpr int NS = kStreamWaves;
+
+// Stream waves of this workgroup that have finished a phase (an LDS count):
+// the last of them to finish marks the workgroup's progress word, so a
+// consumer polls one word per workgroup.  Polls of shared words and cells all
+// land on a few memory channels, and every weight load that touches those
+// channels queues behind them: fewer, rarer polls keep the streams fast.
+__shared__ unsigned finished_waves;
+
+__device__ __forceinline__ void wg_mark(const StepArgs &s, unsigned ep) {
+    const unsigned old = atomicAdd(&finished_waves, 1u);
+    if ((old + 1) % NS == 0) ll::mark(s.progress + blockIdx.x, ep);
+}
 constexpr int kVC = 4;
 constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
 
@@ -364,7 +376,7 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
                 else ll::put(ph.y + row, outs[row - g.r0], ep_y);
             }
         }
-        if (!HEAD && lane == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
+        if (!HEAD && lane == 0) wg_mark(s, ep_y);
         if (tr && tid == NC * kWave) tr[2] = wall_clock64();   // first stream wave done
     }
     if (HEAD) {   // per-workgroup greedy partial
@@ -427,14 +439,16 @@ __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, 
         else v = f16_to_f32(gmem((const uint16_t *)s.embed)[i]);
         ll::put(ph.y + j, v, ep_y);
     }
-    if ((threadIdx.x & 63) == 0) ll::mark(s.progress + blockIdx.x * NS + (wave - NC), ep_y);
+    if ((threadIdx.x & 63) == 0) wg_mark(s, ep_y);
 }
 
 // Attention units (kv head, split) dealt round-robin to the workgroups write
 // their partials; then the workgroup that held split 0 of a head merges the
 // head's splits (kernels.cl:58-107) and reports it in the head's progress
-// word.  Every unit runs before any merge waits, so a merge never waits on a
-// unit queued behind another merge.
+// word.  Units poll their Q/K/V cells directly (a progress-word round first
+// costs more than the polls of these few cells), and every unit runs before
+// any merge waits, so a merge never waits on a unit queued behind another
+// merge.
 template <int D>
 __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
                                            unsigned ep_out, float *lds) {
@@ -464,6 +478,8 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
     extern __shared__ float lds[];
     __shared__ int last;
     if (ldci(s.done) || ldci(s.err)) return;
+    if (threadIdx.x == 0) finished_waves = 0;
+    __syncthreads();
     const int pos = *s.pos;
     const MR_CONST Phase *prog = (const MR_CONST Phase *)s.phases;
     int gemvs = 0;   // GEMV phases so far: their inputs alternate between two LDS buffers
