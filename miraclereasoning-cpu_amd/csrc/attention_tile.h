@@ -477,21 +477,25 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int
     float *red = L + G;                  // [SG][G*D] partial sums
     ll::Wait wt = ll::waiter(io.err);
     ll::u64x2 c[kChunk][2];
+    // Loads of splits past `active` (and of non-owner threads) fall outside
+    // the head's partials and read zero without touching memory.
+    const int limit = active * G * (D + 2);
     // Round 1: the first chunk of o and this thread's (m, l) pair.
     {
-        const int i = tid < active * G ? tid : 0;
+        const int i = tid < active * G ? tid : active * G;
         ll::u64x2 ml;
         bool ready;
         do {
 #pragma unroll
             for (int q = 0; q < kChunk; ++q) {
-                const int s = min(sg + q * SG, active - 1);
+                const int s = owner ? sg + q * SG : active;
                 const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
-                c[q][0] = ll::peek2(base, off);
-                c[q][1] = ll::peek2(base, off + 2);
+                c[q][0] = ll::peek2(base, off, limit);
+                c[q][1] = ll::peek2(base, off + 2, limit);
             }
-            ml = ll::peek2(base, i * (D + 2));
-            ready = (unsigned)(ml.x >> 32) == io.ep_out && (unsigned)(ml.y >> 32) == io.ep_out;
+            ml = ll::peek2(base, i * (D + 2), limit);
+            ready = tid >= active * G ||
+                    ((unsigned)(ml.x >> 32) == io.ep_out && (unsigned)(ml.y >> 32) == io.ep_out);
 #pragma unroll
             for (int q = 0; q < kChunk; ++q)
                 ready &= !owner || sg + q * SG >= active ||
@@ -517,10 +521,10 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int
             do {
 #pragma unroll
                 for (int q = 0; q < kChunk; ++q) {
-                    const int s = min(s0 + sg + q * SG, active - 1);
+                    const int s = owner ? s0 + sg + q * SG : active;
                     const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
-                    c[q][0] = ll::peek2(base, off);
-                    c[q][1] = ll::peek2(base, off + 2);
+                    c[q][0] = ll::peek2(base, off, limit);
+                    c[q][1] = ll::peek2(base, off + 2, limit);
                 }
                 ready = true;
 #pragma unroll

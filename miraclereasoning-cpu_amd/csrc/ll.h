@@ -40,8 +40,10 @@ __device__ __forceinline__ uint64_t peek(const uint64_t *p) {
 // stored.  `base` must be the same for the whole wave (it becomes a buffer
 // resource, which lives in scalar registers: a per-lane base would make the
 // compiler issue the load once per distinct lane value); i varies per lane.
-__device__ __forceinline__ u64x2 peek2(const uint64_t *base, int i) {
-    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+// Pairs at or past `limit` cells read as zero without touching memory (the
+// buffer's bounds check), so lanes with nothing to read add no traffic.
+__device__ __forceinline__ u64x2 peek2(const uint64_t *base, int i, int limit = 0x0fffffff) {
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, limit * 8, 0x00020000);
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, i * 8, 0, 16);
     u64x2 r;
@@ -110,7 +112,7 @@ __device__ __forceinline__ float read_pairs(const uint64_t *x, int n, unsigned e
         bool ready;
         do {
 #pragma unroll
-            for (int i = 0; i < B; ++i) c[i] = peek2(x, 2 * min(base + i * lanes, n - 1));
+            for (int i = 0; i < B; ++i) c[i] = peek2(x, 2 * (base + i * lanes), 2 * n);
             ready = true;
 #pragma unroll
             for (int i = 0; i < B; ++i)
@@ -156,7 +158,7 @@ __device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigne
         do {
             unsigned v[B];
 #pragma unroll
-            for (int i = 0; i < B; ++i) v[i] = word(words + min(base + i * kWave, n - 1));
+            for (int i = 0; i < B; ++i) v[i] = base + i * kWave < n ? word(words + base + i * kWave) : ep;
             ready = true;
 #pragma unroll
             for (int i = 0; i < B; ++i) ready &= base + i * kWave >= n || v[i] >= ep;

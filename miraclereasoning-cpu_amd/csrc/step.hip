@@ -256,7 +256,7 @@ __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, c
         bool ready;
         do {
 #pragma unroll
-            for (int i = 0; i < B; ++i) c[i] = ll::peek2(ph.x, 2 * min(base + i * lanes, n2 - 1));
+            for (int i = 0; i < B; ++i) c[i] = ll::peek2(ph.x, 2 * (base + i * lanes), 2 * n2);
             ready = true;
 #pragma unroll
             for (int i = 0; i < B; ++i)
