@@ -89,6 +89,7 @@ struct mr_model {
     int mode = MR_STEP_PERSISTENT;
     bool persistent_ok = false;
     int grid = 0;                        // persistent workgroups (one per CU)
+    int step_dtype = MR_BF16;            // weight dtype of every GEMV phase
     size_t step_lds = 0;
     mr::Phase *prog_plain = nullptr, *prog_head = nullptr;
     int n_plain = 0, n_head = 0;

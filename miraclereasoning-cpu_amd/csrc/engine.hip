@@ -566,7 +566,7 @@ int run_persistent(mr_model *m, int kind, unsigned long long *trace = nullptr) {
     a.best_val = m->best_val; a.best_idx = m->best_idx; a.bad = m->bad;
     a.embed = m->embed.ptr; a.embed_dtype = m->embed.dtype; a.dummy = m->dummy; a.xbuf = m->xbuf;
     a.progress = m->words; a.nprogress = m->grid;
-    return launch_step(m->ctx->stream, a, m->grid, m->step_lds);
+    return launch_step(m->ctx->stream, a, m->grid, m->step_lds, m->step_dtype, m->d.head_dim);
 }
 
 int run_step(mr_model *m, int kind) {
@@ -643,7 +643,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         Phase a;
         a.kind = PH_ATTN;
         a.x_phase = qkv_at;
-        a.heads_done = m->words + (size_t)m->grid + (size_t)li * d.query_heads;
+        a.heads_done = m->words + (size_t)kWordCopies * kWordCopyStride + (size_t)li * d.query_heads;
         AttnStepArgs &t = a.at.s;
         t.q = (const float *)m->c_qkv;
         t.k_new = (const float *)(m->c_qkv + qd);
@@ -701,13 +701,16 @@ bool persistent_fits(mr_model *m) {
         return k % e == 0 && ((uintptr_t)w.ptr % 16) == 0;
     };
     const int h = d.hidden_size;
-    if (!vec_ok(d.tie_embeddings ? m->embed : m->output, h)) return false;
+    const Weight &head = d.tie_embeddings ? m->embed : m->output;
+    if (!vec_ok(head, h)) return false;
+    m->step_dtype = head.dtype;   // one weight dtype for every GEMV phase (the kernel's instantiation)
     for (Layer &L : m->layers) {
         if (d.query_heads / L.kv_heads > 16) return false;
         if (!vec_ok(L.qkv, h) || !vec_ok(L.o, d.query_heads * d.head_dim) || !vec_ok(L.ffn.gate, h) ||
             !vec_ok(L.ffn.up, h) || !vec_ok(L.ffn.down, d.ffn_dim))
             return false;
-        if (L.ffn.gate.dtype != L.ffn.up.dtype) return false;
+        for (const Weight *w : {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down})
+            if (w->dtype != m->step_dtype) return false;
     }
     return true;
 }
@@ -738,7 +741,8 @@ int setup_persistent(mr_model *m) {
     m->c_act = m->c_attn + n_attn;
     m->sync_count = 1;   // the launch exit counter
     MR_TRY(device_alloc(m, m->sync_count * sizeof(unsigned), (void **)&m->sync));
-    m->word_count = (size_t)m->grid + (size_t)d.layers * d.query_heads;
+    if (m->grid > kWordCopyStride) return MR_OK;   // more workgroups than a progress-word copy holds
+    m->word_count = (size_t)kWordCopies * kWordCopyStride + (size_t)d.layers * d.query_heads;
     MR_TRY(device_alloc(m, m->word_count * sizeof(unsigned), (void **)&m->words));
     MR_HIP(hipMemset(m->words, 0, m->word_count * sizeof(unsigned)), "clear step progress");
     m->part_cell_count = 0;
@@ -762,7 +766,7 @@ int setup_persistent(mr_model *m) {
     m->step_lds = std::max(step_lds_bytes(plain, m->grid), step_lds_bytes(head, m->grid));
     if (m->step_lds > 64 * 1024) return MR_OK;
     int per_cu = 0;   // every workgroup must be resident at once (one per CU)
-    MR_TRY(step_blocks_per_cu(m->step_lds, &per_cu));
+    MR_TRY(step_blocks_per_cu(m->step_lds, m->step_dtype, d.head_dim, &per_cu));
     if (per_cu < 1) return MR_OK;
     m->n_plain = (int)plain.size();
     m->n_head = (int)head.size();

@@ -49,7 +49,7 @@ struct StepArgs {
     int *pos = nullptr, *done = nullptr, *ids = nullptr, *gen = nullptr, *count = nullptr;
     const int *eos = nullptr;
     int *err = nullptr;                 // 1 = a wait timed out
-    unsigned *progress = nullptr;       // [grid] progress words, one per workgroup
+    unsigned *progress = nullptr;       // [kWordCopies][kWordCopyStride] progress words, one per workgroup
     int nprogress = 0;
     unsigned *exits = nullptr;          // workgroups that left this launch (last one finishes)
     float *best_val = nullptr;          // [grid] per-workgroup argmax partials
@@ -67,10 +67,18 @@ constexpr int kStepThreads = 512;
 constexpr int kControlWaves = 4;
 constexpr int kStreamWaves = kStepThreads / 64 - kControlWaves;
 
+// Progress words are written in kWordCopies copies kWordCopyStride words apart
+// (4 KB + 256 B, so the copies sit on different memory channels) and each
+// workgroup polls copy blockIdx % kWordCopies: every copy is polled by an
+// eighth of the grid.
+constexpr int kWordCopies = 8;
+constexpr int kWordCopyStride = 1088;
+
 // Floats of one GEMV input staging buffer, and the dynamic LDS of the kernel.
 int step_xbuf_floats(const std::vector<Phase> &program, int grid);
 size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
-int step_blocks_per_cu(size_t lds, int *blocks);
-int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds);
+// The kernel is instantiated per (weight dtype of every GEMV phase, head dim).
+int step_blocks_per_cu(size_t lds, int dtype, int dim, int *blocks);
+int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds, int dtype, int dim);
 
 }  // namespace mr

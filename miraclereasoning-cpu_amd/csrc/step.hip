@@ -81,7 +81,9 @@ __shared__ unsigned finished_waves;
 
 __device__ __forceinline__ void wg_mark(const StepArgs &s, unsigned ep) {
     const unsigned old = atomicAdd(&finished_waves, 1u);
-    if ((old + 1) % NS == 0) ll::mark(s.progress + blockIdx.x, ep);
+    if ((old + 1) % NS == 0)
+#pragma unroll
+        for (int c = 0; c < kWordCopies; ++c) ll::mark(s.progress + c * kWordCopyStride + blockIdx.x, ep);
 }
 constexpr int kVC = 4;
 constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
@@ -232,7 +234,7 @@ __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, c
     __shared__ unsigned released;
     if (me < kWave) {
         if (ph.ready) ll::wait_words(ph.ready, ph.nready, ep_x, me, w);
-        else ll::wait_words(s.progress, s.nprogress, ep_x, me, w);
+        else ll::wait_words(s.progress + (blockIdx.x % kWordCopies) * kWordCopyStride, s.nprogress, ep_x, me, w);
         const bool ok = __all(w.ok);
         if (me == 0) __hip_atomic_store(&released, ok ? ep_x : ~0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else {
@@ -408,18 +410,11 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
     return true;
 }
 
-template <bool HEAD>
+template <int DT, bool HEAD>
 __device__ __forceinline__ bool gemv_dispatch(const Phase &ph, const StepArgs &s, unsigned ep_x, unsigned ep_res,
                                               unsigned ep_y, float *xs, unsigned long long *tr) {
-    const int dt = ph.dtype;
-    if (!HEAD && ph.epi == EPI_SWIGLU) {
-        if (dt == MR_BF16) return gemv_phase<MR_BF16, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
-        if (dt == MR_F32) return gemv_phase<MR_F32, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
-        return gemv_phase<MR_F16, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
-    }
-    if (dt == MR_BF16) return gemv_phase<MR_BF16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
-    if (dt == MR_F32) return gemv_phase<MR_F32, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
-    return gemv_phase<MR_F16, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+    if (!HEAD && ph.epi == EPI_SWIGLU) return gemv_phase<DT, 2, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+    return gemv_phase<DT, 1, HEAD>(ph, s, ep_x, ep_res, ep_y, xs, tr);
 }
 
 // ------------------------------------------------------------------ other phases
@@ -474,6 +469,11 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
     return true;
 }
 
+// One instantiation per (weight dtype, head dim): a step executes only its
+// model's variants, so the code a layer runs stays small enough for the
+// instruction cache (a kernel holding every variant is several times larger,
+// and each phase then starts with a run of instruction fetches from L2).
+template <int DT, int D>
 __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
     extern __shared__ float lds[];
     __shared__ int last;
@@ -497,18 +497,16 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
                 stamp(tr, 1);
                 break;
             case PH_GEMV:
-                ok = gemv_dispatch<false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+                ok = gemv_dispatch<DT, false>(ph, s, ep_x, ep_res, ep_y, xs, tr);
                 ++gemvs;
                 break;
             case PH_HEAD:
-                ok = gemv_dispatch<true>(ph, s, ep_x, ep_res, ep_y, xs, tr);
+                ok = gemv_dispatch<DT, true>(ph, s, ep_x, ep_res, ep_y, xs, tr);
                 ++gemvs;
                 break;
             case PH_ATTN:
                 stamp(tr, 1);
-                if (ph.at.s.dim == 128) ok = attn_phase<128>(ph, s, pos, ep_x, ep_y, lds);
-                else if (ph.at.s.dim == 64) ok = attn_phase<64>(ph, s, pos, ep_x, ep_y, lds);
-                else ok = attn_phase<32>(ph, s, pos, ep_x, ep_y, lds);
+                ok = attn_phase<D>(ph, s, pos, ep_x, ep_y, lds);
                 break;
         }
         if (!ok) return;
@@ -568,8 +566,25 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
     return need * sizeof(float);
 }
 
-int step_blocks_per_cu(size_t lds, int *blocks) {
-    MR_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)k_step, NT, lds),
+namespace {
+
+template <int DT>
+const void *step_kernel_dim(int dim) {
+    if (dim == 128) return (const void *)k_step<DT, 128>;
+    if (dim == 64) return (const void *)k_step<DT, 64>;
+    return (const void *)k_step<DT, 32>;
+}
+
+const void *step_kernel(int dtype, int dim) {
+    if (dtype == MR_BF16) return step_kernel_dim<MR_BF16>(dim);
+    if (dtype == MR_F16) return step_kernel_dim<MR_F16>(dim);
+    return step_kernel_dim<MR_F32>(dim);
+}
+
+}  // namespace
+
+int step_blocks_per_cu(size_t lds, int dtype, int dim, int *blocks) {
+    MR_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, step_kernel(dtype, dim), NT, lds),
            "query step kernel occupancy");
     return MR_OK;
 }
@@ -578,9 +593,9 @@ int step_blocks_per_cu(size_t lds, int *blocks) {
 // a CU, so the dispatcher places one workgroup on every CU at once (the setup
 // checks the occupancy).  Should a workgroup not start, the others' bounded
 // waits end the step with an error rather than hanging.
-int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds) {
-    k_step<<<grid, NT, lds, s>>>(a);
-    MR_LAUNCHED("launch step kernel");
+int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds, int dtype, int dim) {
+    void *args[] = {(void *)&a};
+    MR_HIP(hipLaunchKernel(step_kernel(dtype, dim), dim3(grid), dim3(NT), args, lds, s), "launch step kernel");
     return MR_OK;
 }
 
