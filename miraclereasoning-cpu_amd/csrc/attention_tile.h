@@ -558,6 +558,235 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int
     return true;
 }
 
+// Persistent-kernel unit with no barrier per tile: every wave scores and mixes
+// its own keys of the split, keeping a running max, sum and weighted values
+// per head; the waves' (m, l, o) are then combined in LDS into the unit's
+// partial.  A lane holds 16 dims of a key (kWaveVec float4 of K and of V), so
+// D/16 lanes share a key: a dot product is 16 FMAs and at most three in-row
+// lane steps.  A round is kWaveKeys keys per lane; the first round's K/V
+// loads (keys of earlier steps only) go out before the Q/K/V cells are
+// awaited.  G <= kWaveUnitMaxG.
+constexpr int kWaveVec = 4;          // float4 per lane per key (16 dims)
+constexpr int kWaveKeys = 1;         // keys per lane per round
+constexpr int kWaveUnitMaxG = 4;
+
+template <int D>
+__host__ __device__ constexpr int keys_per_wave_round() {
+    return kWaveKeys * (kWave / (D / (4 * kWaveVec)));
+}
+
+template <int D, int NT>
+__host__ __device__ constexpr int unit_waves_lds_floats(int G) {
+    return G * D + 2 * D + 2 * (NT / kWave) * G + (NT / kWave) * G * D;
+}
+
+// Sum over aligned groups of LPK <= 16 lanes (every lane of a group receives it).
+template <int LPK>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (LPK >= 2) v += dpp_f<0xB1>(v);    // lane ^ 1
+    if constexpr (LPK >= 4) v += dpp_f<0x4E>(v);    // lane ^ 2
+    if constexpr (LPK >= 8) v += dpp_f<0x141>(v);   // the other half of the 8 (values uniform per quad)
+    if constexpr (LPK >= 16) v += dpp_f<0x140>(v);  // the other half of the row (uniform per 8)
+    return v;
+}
+
+// Sum / max over the key groups of a wave (lanes l, l ^ LPK, l ^ 2 LPK, ...);
+// the value is uniform within each group of LPK lanes.
+template <int LPK>
+__device__ __forceinline__ float keygroups_sum(float v) {
+    if constexpr (LPK < 2) v += dpp_f<0xB1>(v);
+    if constexpr (LPK < 4) v += dpp_f<0x4E>(v);
+    if constexpr (LPK < 8) v += dpp_f<0x141>(v);
+    if constexpr (LPK < 16) v += dpp_f<0x140>(v);
+    return xor32_sum(xor16_sum(v));
+}
+// Sum over lanes l, l ^ LPK, l ^ 2 LPK, ... for values that differ within a
+// key group (lane l ^ 8 in a row is row_ror:8; smaller strides go through
+// LDS swizzles).
+template <int LPK>
+__device__ __forceinline__ float keygroups_sum_lanes(float v) {
+#pragma unroll
+    for (int off = LPK; off < 8; off <<= 1) v += __shfl_xor(v, off, kWave);
+    if constexpr (LPK <= 8) v += dpp_f<0x128>(v);
+    return xor32_sum(xor16_sum(v));
+}
+template <int LPK>
+__device__ __forceinline__ float keygroups_max(float v) {
+    if constexpr (LPK < 2) v = fmaxf(v, dpp_f<0xB1>(v));
+    if constexpr (LPK < 4) v = fmaxf(v, dpp_f<0x4E>(v));
+    if constexpr (LPK < 8) v = fmaxf(v, dpp_f<0x141>(v));
+    if constexpr (LPK < 16) v = fmaxf(v, dpp_f<0x140>(v));
+    return xor32_max(xor16_max(v));
+}
+
+template <int D, int NT>
+__device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, int kh, int split, float *lds,
+                                                const Io &io) {
+    const AttnStepArgs &a = ka.s;
+    constexpr int LPK = D / (4 * kWaveVec);   // lanes per key: 8, 4, 2
+    constexpr int KPI = kWave / LPK;          // keys side by side in a wave
+    constexpr int NWV = NT / kWave;
+    constexpr int RK = kWaveKeys * KPI;       // keys per wave per round
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane % LPK, kg = lane / LPK;
+    const int G = a.heads / a.kv_heads, kvw = a.kv_heads * D;
+    int t0, t1, split_len;
+    split_range<D>(g, a.splits, split, &t0, &t1, &split_len);
+    float *qs = lds;                  // [G][D]
+    float *kn = qs + G * D;           // [D] newest key (normalized, rotated)
+    float *vn = kn + D;               // [D] newest value
+    float *wm = vn + D;               // [NWV][G] per-wave max
+    float *wl = wm + NWV * G;         // [NWV][G] per-wave sum
+    float *wo = wl + NWV * G;         // [NWV][G][D] per-wave weighted values
+    const int newest = g.length - 1;
+    const int d0 = sub * 4 * kWaveVec;   // this lane's first dim
+
+    float4 kr[kWaveKeys][kWaveVec], vr[kWaveKeys][kWaveVec];
+    auto key_of = [&](int round, int i) { return t0 + (round * NWV + wave) * RK + i * KPI + kg; };
+    auto fetch = [&](int round) {
+#pragma unroll
+        for (int i = 0; i < kWaveKeys; ++i) {
+            const int t = key_of(round, i);
+            const float *kb = nullptr, *vb = nullptr;
+            if (t < t1 && t != newest) {
+                if (t < g.length) {
+                    const int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D + d0;
+                    kb = a.ring_k + off;
+                    vb = a.ring_v + off;
+                } else {
+                    const int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D + d0;
+                    kb = a.extra_k + off;
+                    vb = a.extra_v + off;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < kWaveVec; ++c) {
+                kr[i][c] = kb ? load_f4(kb + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[i][c] = vb ? load_f4(vb + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    if (t0 >= t1) return true;   // no keys at this position (the newest key is in another split)
+    const int per_round = NWV * RK;
+    const int rounds = (t1 - t0 + per_round - 1) / per_round;
+    fetch(0);
+    if (!prepare<true, NT>(ka, g, kh, G, D, qs, kn, vn, t0, t1, io)) return false;
+
+    // scores carry the 1/sqrt(D) of kernels.cl:72 through the queries
+    const float inv_root = 1.0f / sqrtf((float)D);
+    float m_run[kWaveUnitMaxG], l_run[kWaveUnitMaxG];
+    float4 acc[kWaveUnitMaxG][kWaveVec];
+#pragma unroll
+    for (int h = 0; h < kWaveUnitMaxG; ++h) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kWaveVec; ++c) acc[h][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int round = 0; round < rounds; ++round) {
+        if (round > 0) fetch(round);
+#pragma unroll
+        for (int i = 0; i < kWaveKeys; ++i)
+            if (key_of(round, i) == newest)
+#pragma unroll
+                for (int c = 0; c < kWaveVec; ++c) {
+                    kr[i][c] = *(const float4 *)(kn + d0 + 4 * c);
+                    vr[i][c] = *(const float4 *)(vn + d0 + 4 * c);
+                }
+#pragma unroll
+        for (int h = 0; h < kWaveUnitMaxG; ++h) {
+            if (h >= G) break;
+            float4 q[kWaveVec];
+#pragma unroll
+            for (int c = 0; c < kWaveVec; ++c) {
+                const float4 t = *(const float4 *)(qs + h * D + d0 + 4 * c);
+                q[c] = make_float4(t.x * inv_root, t.y * inv_root, t.z * inv_root, t.w * inv_root);
+            }
+            float sc[kWaveKeys];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < kWaveKeys; ++i) {
+                float d = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kWaveVec; ++c) {
+                    d = fmaf(q[c].x, kr[i][c].x, d);
+                    d = fmaf(q[c].y, kr[i][c].y, d);
+                    d = fmaf(q[c].z, kr[i][c].z, d);
+                    d = fmaf(q[c].w, kr[i][c].w, d);
+                }
+                d = lanes_sum<LPK>(d);
+                sc[i] = key_of(round, i) < t1 ? d : -INFINITY;
+                mx = fmaxf(mx, sc[i]);
+            }
+            mx = keygroups_max<LPK>(mx);
+            const float m_new = fmaxf(m_run[h], mx);   // -inf while this wave has seen no key
+            const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = m_run[h] == -INFINITY ? 0.0f : __expf(m_run[h] - m_ref);
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kWaveVec; ++c)
+                acc[h][c] = make_float4(acc[h][c].x * alpha, acc[h][c].y * alpha, acc[h][c].z * alpha,
+                                        acc[h][c].w * alpha);
+#pragma unroll
+            for (int i = 0; i < kWaveKeys; ++i) {
+                const float p = __expf(sc[i] - m_ref);
+                sum += p;
+#pragma unroll
+                for (int c = 0; c < kWaveVec; ++c) {
+                    acc[h][c].x = fmaf(p, vr[i][c].x, acc[h][c].x);
+                    acc[h][c].y = fmaf(p, vr[i][c].y, acc[h][c].y);
+                    acc[h][c].z = fmaf(p, vr[i][c].z, acc[h][c].z);
+                    acc[h][c].w = fmaf(p, vr[i][c].w, acc[h][c].w);
+                }
+            }
+            // each key group holds a part of the sum (its own keys)
+            sum = keygroups_sum<LPK>(sum);
+            m_run[h] = m_new;
+            l_run[h] = l_run[h] * alpha + sum;
+        }
+    }
+    // Waves without keys of this unit keep m = -inf, l = 0, o = 0.
+#pragma unroll
+    for (int h = 0; h < kWaveUnitMaxG; ++h) {
+        if (h >= G) break;
+#pragma unroll
+        for (int c = 0; c < kWaveVec; ++c) {
+            float4 o = acc[h][c];
+            o.x = keygroups_sum_lanes<LPK>(o.x);
+            o.y = keygroups_sum_lanes<LPK>(o.y);
+            o.z = keygroups_sum_lanes<LPK>(o.z);
+            o.w = keygroups_sum_lanes<LPK>(o.w);
+            if (kg == 0) *(float4 *)(wo + (wave * G + h) * D + d0 + 4 * c) = o;
+        }
+        if (lane == 0) {
+            wm[wave * G + h] = m_run[h];
+            wl[wave * G + h] = l_run[h];
+        }
+    }
+    __syncthreads();
+    uint64_t *part = a.part_cells + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
+    for (int e = tid; e < G * D; e += NT) {
+        const int h = e / D, j = e % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) M = fmaxf(M, wm[w * G + h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+            const float m = wm[w * G + h];
+            const float f = m == -INFINITY ? 0.0f : __expf(m - M);
+            L = fmaf(wl[w * G + h], f, L);
+            O = fmaf(wo[(w * G + h) * D + j], f, O);
+        }
+        ll::put(part + h * (D + 2) + 2 + j, O, io.ep_out);
+        if (j == 0) {
+            ll::put(part + h * (D + 2), M, io.ep_out);
+            ll::put(part + h * (D + 2) + 1, L, io.ep_out);
+        }
+    }
+    return true;
+}
+
 template <int D, int NT>
 __host__ __device__ constexpr int combine_cells_lds_floats(int G, int splits) {
     return 2 * splits * G + G + (NT / (G * (D / 4)) > 0 ? NT / (G * (D / 4)) : 1) * G * D;

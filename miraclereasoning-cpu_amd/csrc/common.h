@@ -139,13 +139,33 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// v of lane l combined with v of lane l ^ 16 (l ^ 32), in VALU lane swaps
+// (v_permlane16/32_swap: each returns the two halves of a lane pair, so both
+// lanes of a pair compute the same commutative sum or max).
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Sum within aligned groups of `width` lanes (width a power of two <= 64);
 // every lane of a group receives its group's sum.
 __device__ __forceinline__ float group_sum(float v, int width) {
     if (width >= 16) {
         v = row_sum(v);
-        if (width >= 32) v += __shfl_xor(v, 16, kWave);
-        if (width == 64) v += __shfl_xor(v, 32, kWave);
+        if (width >= 32) v = xor16_sum(v);
+        if (width == 64) v = xor32_sum(v);
         return v;
     }
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);

@@ -52,6 +52,7 @@ struct Layer {
     int relay_capacity = 0;
     float *pending = nullptr;                          // flashnano-1.6 chunk rows
     int splits = 0, split_len = 0;                     // attention plan
+    int step_splits = 0;                               // attention splits in the step kernel
 };
 
 }  // namespace mr
@@ -105,6 +106,8 @@ struct mr_model {
     unsigned *words = nullptr;
     size_t word_count = 0;
     uint64_t *part_cells = nullptr;      // attention partials (m, l, o) as cells
+    unsigned *merge_counts = nullptr;    // [layers][max kv heads] finished attention units (only grow)
+    size_t merge_count_n = 0;
     size_t part_cell_count = 0;
     int xbuf = 0;                        // floats of one GEMV input staging buffer
     void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end

@@ -652,8 +652,9 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         t.eps = d.norm_eps; t.rope = m->rope; t.split_half = d.split_half_rope;
         t.ring_k = L.ring_k; t.ring_v = L.ring_v; t.capacity = L.capacity;
         t.heads = d.query_heads; t.kv_heads = L.kv_heads; t.dim = hd;
-        t.part = m->part; t.out = (float *)m->c_attn; t.splits = L.splits; t.split_len = L.split_len;
+        t.part = m->part; t.out = (float *)m->c_attn; t.splits = L.step_splits; t.split_len = 0;
         t.part_cells = m->part_cells;
+        t.counters = m->merge_counts + (size_t)li * m->merge_count_n / d.layers;
         a.at.mode = 1;
         a.at.ring_k_ro = L.ring_k; a.at.ring_v_ro = L.ring_v;
         prog.push_back(a);
@@ -746,10 +747,17 @@ int setup_persistent(mr_model *m) {
     MR_TRY(device_alloc(m, m->word_count * sizeof(unsigned), (void **)&m->words));
     MR_HIP(hipMemset(m->words, 0, m->word_count * sizeof(unsigned)), "clear step progress");
     m->part_cell_count = 0;
-    for (Layer &L : m->layers)
-        m->part_cell_count = std::max(m->part_cell_count, (size_t)d.query_heads * L.splits * (d.head_dim + 2));
+    for (Layer &L : m->layers) {
+        L.step_splits = step_attention_splits(L.capacity, L.kv_heads, d.head_dim, m->grid);
+        m->part_cell_count = std::max(m->part_cell_count, (size_t)d.query_heads * L.step_splits * (d.head_dim + 2));
+    }
     MR_TRY(device_alloc(m, m->part_cell_count * sizeof(uint64_t), (void **)&m->part_cells));
     MR_HIP(hipMemset(m->part_cells, 0, m->part_cell_count * sizeof(uint64_t)), "clear attention cells");
+    int max_kvh = 1;
+    for (Layer &L : m->layers) max_kvh = std::max(max_kvh, L.kv_heads);
+    m->merge_count_n = (size_t)d.layers * max_kvh;
+    MR_TRY(device_alloc(m, m->merge_count_n * sizeof(unsigned), (void **)&m->merge_counts));
+    MR_HIP(hipMemset(m->merge_counts, 0, m->merge_count_n * sizeof(unsigned)), "clear attention counters");
     MR_TRY(device_alloc(m, 256, &m->dummy));
     MR_TRY(device_alloc(m, sizeof(int), (void **)&m->err));
     MR_TRY(device_alloc(m, m->grid * sizeof(float), (void **)&m->best_val));
@@ -930,7 +938,7 @@ int mr_model_destroy(mr_model *m) {
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
     if (m->pf) hipFree(m->pf);
-    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_cells, m->dummy,
+    for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_cells, (void *)m->merge_counts, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);
     delete m;
@@ -1198,6 +1206,8 @@ int mr_model_reset(mr_model *m) {
         MR_HIP(hipMemsetAsync(m->cells, 0, m->cell_count * sizeof(uint64_t), m->ctx->stream), "reset step cells");
         MR_HIP(hipMemsetAsync(m->sync, 0, m->sync_count * sizeof(unsigned), m->ctx->stream), "reset step counters");
         MR_HIP(hipMemsetAsync(m->words, 0, m->word_count * sizeof(unsigned), m->ctx->stream), "reset step progress");
+        MR_HIP(hipMemsetAsync(m->merge_counts, 0, m->merge_count_n * sizeof(unsigned), m->ctx->stream),
+               "reset attention counters");
         MR_HIP(hipMemsetAsync(m->part_cells, 0, m->part_cell_count * sizeof(uint64_t), m->ctx->stream),
                "reset attention cells");
         MR_HIP(hipMemsetAsync(m->err, 0, sizeof(int), m->ctx->stream), "reset step status");

@@ -77,6 +77,9 @@ constexpr int kWordCopyStride = 1088;
 // Floats of one GEMV input staging buffer, and the dynamic LDS of the kernel.
 int step_xbuf_floats(const std::vector<Phase> &program, int grid);
 size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
+// Attention splits per KV head in the step kernel: enough units that each
+// covers its keys in one round of its waves' loads, at most cus / kv_heads.
+int step_attention_splits(int max_total, int kv_heads, int dim, int cus);
 // The kernel is instantiated per (weight dtype of every GEMV phase, head dim).
 int step_blocks_per_cu(size_t lds, int dtype, int dim, int *blocks);
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds, int dtype, int dim);

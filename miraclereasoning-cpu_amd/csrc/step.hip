@@ -438,33 +438,47 @@ __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, 
 }
 
 // Attention units (kv head, split) dealt round-robin to the workgroups write
-// their partials; then the workgroup that held split 0 of a head merges the
-// head's splits (kernels.cl:58-107) and reports it in the head's progress
-// word.  Units poll their Q/K/V cells directly (a progress-word round first
-// costs more than the polls of these few cells), and every unit runs before
-// any merge waits, so a merge never waits on a unit queued behind another
-// merge.
+// their partials and count themselves in the head's counter; the unit that
+// completes the count merges the head's splits (kernels.cl:58-107) at once
+// and reports it in the head's progress word.  The counters only grow (one
+// count per unit per step), so "last" is the count reaching a multiple of the
+// split count.  A unit counts itself once its partial's stores are
+// acknowledged, so the merger finds them in one read (it still checks the
+// cells' epochs).
 template <int D>
 __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
                                            unsigned ep_out, float *lds) {
     const AttnStepArgs &a = ph.at.s;
     const int splits = a.splits, units = a.kv_heads * splits;
     if ((int)blockIdx.x >= units) return true;
+    __shared__ int merge_it;
     __syncthreads();   // the previous phase's readers of this LDS are done
     const Geo g = geometry(ph.at, pos);
     const Io io{ep_in, ep_out, s.err, nullptr, 0};
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
-        if (!attn_unit<D, true, NT>(ph.at, g, u / splits, u % splits, lds, io)) return false;
-        __syncthreads();
-    }
     int t0, t1, split_len;
     split_range<D>(g, splits, 0, &t0, &t1, &split_len);
     const int active = (g.total + split_len - 1) / split_len;
-    for (int kh = 0; kh < a.kv_heads; ++kh) {
-        if ((kh * splits) % (int)gridDim.x != (int)blockIdx.x) continue;
-        if (!combine_cells<D, NT>(a, kh, active, lds, io)) return false;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const int kh = u / splits;
+        const bool ok = a.heads / a.kv_heads <= kWaveUnitMaxG
+                            ? attn_unit_waves<D, NT>(ph.at, g, kh, u % splits, lds, io)
+                            : attn_unit<D, true, NT>(ph.at, g, kh, u % splits, lds, io);
+        if (!ok) return false;
+        // Every partial store of the unit is acknowledged (visible to the
+        // merger) before the unit counts itself.
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (threadIdx.x == 0) ll::mark(ph.heads_done + kh, ep_out);
+        if (threadIdx.x == 0) {
+            const unsigned old =
+                __hip_atomic_fetch_add(gmem(a.counters + kh), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            merge_it = (old + 1) % (unsigned)splits == 0;
+        }
+        __syncthreads();
+        if (merge_it) {
+            if (!combine_cells<D, NT>(a, kh, active, lds, io)) return false;
+            __syncthreads();
+            if (threadIdx.x == 0) ll::mark(ph.heads_done + kh, ep_out);
+        }
     }
     return true;
 }
@@ -558,9 +572,16 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid) {
         if (ph.kind != PH_ATTN) continue;
         const int G = ph.at.s.heads / ph.at.s.kv_heads, d = ph.at.s.dim, sp = ph.at.s.splits;
         size_t f;
-        if (d == 128) f = std::max(unit_lds_floats<128>(G), combine_cells_lds_floats<128, NT>(G, sp));
-        else if (d == 64) f = std::max(unit_lds_floats<64>(G), combine_cells_lds_floats<64, NT>(G, sp));
-        else f = std::max(unit_lds_floats<32>(G), combine_cells_lds_floats<32, NT>(G, sp));
+        const bool waves = G <= kWaveUnitMaxG;
+        if (d == 128)
+            f = std::max(waves ? unit_waves_lds_floats<128, NT>(G) : unit_lds_floats<128>(G),
+                         combine_cells_lds_floats<128, NT>(G, sp));
+        else if (d == 64)
+            f = std::max(waves ? unit_waves_lds_floats<64, NT>(G) : unit_lds_floats<64>(G),
+                         combine_cells_lds_floats<64, NT>(G, sp));
+        else
+            f = std::max(waves ? unit_waves_lds_floats<32, NT>(G) : unit_lds_floats<32>(G),
+                         combine_cells_lds_floats<32, NT>(G, sp));
         need = std::max(need, f);
     }
     return need * sizeof(float);
@@ -582,6 +603,14 @@ const void *step_kernel(int dtype, int dim) {
 }
 
 }  // namespace
+
+int step_attention_splits(int max_total, int kv_heads, int dim, int cus) {
+    const int per_unit = (NT / kWave) * (dim == 128   ? keys_per_wave_round<128>()
+                                         : dim == 64 ? keys_per_wave_round<64>()
+                                                     : keys_per_wave_round<32>());
+    const int want = std::max(1, cus / std::max(kv_heads, 1));
+    return std::max(1, std::min(want, ceil_div(max_total, per_unit)));
+}
 
 int step_blocks_per_cu(size_t lds, int dtype, int dim, int *blocks) {
     MR_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, step_kernel(dtype, dim), NT, lds),
