@@ -70,6 +70,22 @@ def decode_bytes(cfg, context, position):
     return body + head + embed_row + kv + V * 4
 
 
+def prefill_flops(cfg, context, tokens):
+    """Algorithmic FLOPs of a batched prefill of `tokens` from position 0: the
+    projections (2 per weight per token), attention scores and mixing
+    (4 * query heads * head_dim per query-key pair inside each layer's window)
+    and the LM head of the last token."""
+    h, d, hq, f, V = cfg.hidden_size, cfg.head_dim, cfg.query_heads, cfg.ffn_dim, cfg.vocab_size
+    proj = attn = 0
+    for layer in range(cfg.layers):
+        kvw = cfg.layer_kv_heads(layer) * d
+        proj += h * (hq * d + 2 * kvw) + hq * d * h + 3 * h * f
+        cap = min(cfg.layer_window(layer) or context, context)
+        keys = sum(min(t + 1, cap) for t in range(tokens))
+        attn += 4 * hq * d * keys
+    return 2 * tokens * proj + attn + 2 * h * V
+
+
 def gate_up_bytes(cfg):
     """Algorithmic bytes of one fused RMSNorm + gate/up GEMV + SwiGLU launch."""
     h, f = cfg.hidden_size, cfg.ffn_dim
@@ -101,7 +117,9 @@ def main():
     ap.add_argument("--steps", type=int, default=511, help="timed decode steps")
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode steps before timing")
     ap.add_argument("--prompt", type=int, default=None, help="prompt length (default: the workload's 4096)")
-    ap.add_argument("--prefill-mode", choices=("exact", "batched"), default="exact")
+    ap.add_argument("--prefill-mode", choices=("exact", "batched"), default="batched",
+                    help="batched: one pass per layer over the prompt (MFMA GEMMs, windowed attention); "
+                         "exact: the reference's token loop")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU-baseline budget; 0 skips it")
     ap.add_argument("--kernel-reps", type=int, default=3)
     ap.add_argument("--traffic-probe", action="store_true",
@@ -143,7 +161,8 @@ def main():
     t0 = time.perf_counter()
     model.prefill(prompt)
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {prompt_len / prefill_s:.1f} tok/s")
+    pf_flops = prefill_flops(cfg, wl["context"], prompt_len)
+    log(f"prefill {prompt_len / prefill_s:.1f} tok/s, {pf_flops / prefill_s / 1e12:.1f} TFLOP/s algorithmic")
 
     if args.traffic_probe:
         n = 64 * 1024 * 1024
@@ -202,7 +221,10 @@ def main():
                        "achieved_gbs": round(avg_bytes * tok_s / 1e9, 1),
                        "peak_gbs": HBM_PEAK_GBS, "frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
         "prefill": {"tok_s": round(prompt_len / prefill_s, 1), "seconds": round(prefill_s, 4),
-                    "mode": args.prefill_mode},
+                    "mode": args.prefill_mode, "algorithmic_tflop": round(pf_flops / 1e12, 3),
+                    "achieved_tflops": round(pf_flops / prefill_s / 1e12, 1),
+                    "peak_bf16_dense_tflops": MFMA_BF16_PEAK_TFLOPS,
+                    "frac": round(pf_flops / prefill_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
         "roofline": roof,
         "decode_device_ms": round(device_ms, 3),
         "layer_kernels_ms": {k: round(v, 5) for k, v in kernels.items()},
