@@ -29,8 +29,15 @@ struct LightArgs {
     const float *kv = nullptr;       // [2*kv_heads*d] that projection's output
     LightState *st = nullptr;
     float *out = nullptr;            // [heads*d] attended values
+    float *part = nullptr;           // [heads][splits][d + 2] split partials (m, l, o)
     int heads = 0, kv_heads = 0, d = 0, latent = 0, window = 0, memory_slots = 0, cap = 0;
 };
+
+// Rows of the latent memory per attention split (head dims 32, 64, 128 take
+// the split path; other dims the single-workgroup kernel).
+constexpr int kLightRows = 64;
+inline int light_splits(int cap) { return (cap + kLightRows - 1) / kLightRows; }
+inline bool light_split_dim(int d) { return d == 32 || d == 64 || d == 128; }
 
 // Queries, the new latent row (appended), then - after the K/V projection of
 // lat_new - its key/value cache row.

@@ -266,3 +266,20 @@ def test_lighting_geometry_matches_oracle(backend, slots):
     model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=128)
     np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
     assert model.generate(list(ids), max_new_tokens=8) == ref.generate(list(ids), max_new_tokens=8)
+
+
+
+def test_lighting_split_attention_matches_oracle(backend):
+    """The split-key latent attention (64 memory rows per workgroup, merged per
+    head) over a window of 150 rows and 8 memory slots: 230 tokens fill three
+    splits, push rows past the window (masked) and merge the oldest into the
+    slots; logits and greedy stream against the oracle."""
+    config = dict(LIGHT_MID, window=150, memory_slots=8)
+    weights = synthetic.synthetic_weights(config, 17, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 230, 17)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=256)
+    want = ref.prefill(ids, return_all=True)
+    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=256)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    assert model.generate(list(ids), max_new_tokens=8) == ref.generate(list(ids), max_new_tokens=8)
