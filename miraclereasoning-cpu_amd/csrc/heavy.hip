@@ -26,6 +26,8 @@
 //                  the residual add.
 #include "heavy.h"
 
+#include "attention_tile.h"
+
 namespace mr {
 namespace {
 
@@ -160,6 +162,140 @@ __global__ void __launch_bounds__(kAttnThreads) k_heavy_attn(HeavyAttnArgs a) {
             acc += sc[t] * v;
         }
         a.out[(int64_t)h * d + j] = acc;
+    }
+}
+
+// Head dims 32/64/128: the same attention with the window scores, the softmax
+// sum and the value mix spread over the workgroup (a lane holds 16 dims of a
+// key, D/16 lanes per key).  The block-mean scores keep the sequential
+// per-thread order above, so the block choices are the same bit for bit; the
+// window scores and the mix differ from the sequential orders by rounding.
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) k_heavy_attn_lanes(HeavyAttnArgs a) {
+    constexpr int LPK = D / 16, KPW = kWave / LPK, NWV = kAttnThreads / kWave;
+    extern __shared__ float sh[];
+    __shared__ float red[NWV];
+    __shared__ float wo[NWV][D];
+    if (a.done && *a.done) return;
+    const int pos = *a.pos, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK, kg = lane / LPK;
+    const int count = pos + 1, length = min(a.window, count), start = count - length;
+    const int blocks = (count + a.block - 1) / a.block, total = length + blocks;
+    const int h = blockIdx.x, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
+    float *qs = sh;                          // [D]
+    float *sc = qs + D;                      // [total] scores, then exponentials
+    int *keep_flag = (int *)(sc + total);    // [blocks]
+    for (int j = tid; j < D; j += kAttnThreads) qs[j] = a.q_rot[(int64_t)h * D + j];
+    __syncthreads();
+    const float root = sqrtf((float)D);
+    float4 q[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = *(const float4 *)(qs + 16 * sub + 4 * c);
+    for (int r0 = wave * KPW; r0 < length; r0 += NWV * KPW) {   // window scores
+        const int t = r0 + kg;
+        float dot = 0.0f;
+        if (t < length) {
+            const float *kr = a.ring_k + (int64_t)(start + t) * kvw + (int64_t)kh * D + 16 * sub;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float4 k4 = load_f4(kr + 4 * c);
+                dot = fmaf(q[c].x, k4.x, dot);
+                dot = fmaf(q[c].y, k4.y, dot);
+                dot = fmaf(q[c].z, k4.z, dot);
+                dot = fmaf(q[c].w, k4.w, dot);
+            }
+        }
+        dot = att::lanes_sum<LPK>(dot);
+        if (t < length && sub == 0) sc[t] = dot / root;
+    }
+    for (int b = tid; b < blocks; b += kAttnThreads) {   // block-mean scores, sequential (kernels.cl:58-73)
+        float v = 0.0f;
+        const float n = (float)min(a.block, count - b * a.block);
+        const float *kb = a.bsum_k + (int64_t)b * kvw + (int64_t)kh * D;
+        for (int j = 0; j < D; ++j) v += qs[j] * (kb[j] / n);
+        const int end = min((b + 1) * a.block - 1, pos);
+        sc[length + b] = v / root - a.slope * log1pf((float)(pos - end));
+    }
+    __syncthreads();
+    const int keep = min(a.slots, blocks);
+    for (int b = tid; b < blocks; b += kAttnThreads) {   // stable top-k (model.py:220-226)
+        const float s = sc[length + b];
+        int rank = 0;
+        for (int c = 0; c < blocks; ++c) {
+            const float o = sc[length + c];
+            rank += o > s || (o == s && c < b);
+        }
+        keep_flag[b] = rank < keep;
+    }
+    __syncthreads();
+    if (a.choice) {
+        int *rec = a.choice + (int64_t)pos * a.choice_stride + a.choice_blocks + h * a.slots;
+        for (int b = tid; b < blocks; b += kAttnThreads)
+            if (keep_flag[b]) {
+                int at = 0;
+                for (int c = 0; c < b; ++c) at += keep_flag[c];
+                rec[at] = b;
+            }
+        for (int i = keep + tid; i < a.slots; i += kAttnThreads) rec[i] = -1;
+    }
+    for (int b = tid; b < blocks; b += kAttnThreads)
+        if (!keep_flag[b]) sc[length + b] = -INFINITY;
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int t = tid; t < total; t += kAttnThreads) mx = fmaxf(mx, sc[t]);
+    mx = block_max(mx, red);
+    float den = 0.0f;
+    for (int t = tid; t < total; t += kAttnThreads) {
+        const float p = expf(sc[t] - mx);
+        sc[t] = p;
+        den += p;
+    }
+    den = block_sum(den, red);   // its barriers also publish sc
+    float4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int r0 = wave * KPW; r0 < total; r0 += NWV * KPW) {   // weighted values
+        const int t = r0 + kg;
+        const float p = t < total ? sc[t] : 0.0f;
+        if (p != 0.0f) {
+            if (t < length) {
+                const float *vr = a.ring_v + (int64_t)(start + t) * kvw + (int64_t)kh * D + 16 * sub;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 v = load_f4(vr + 4 * c);
+                    acc[c].x = fmaf(p, v.x, acc[c].x);
+                    acc[c].y = fmaf(p, v.y, acc[c].y);
+                    acc[c].z = fmaf(p, v.z, acc[c].z);
+                    acc[c].w = fmaf(p, v.w, acc[c].w);
+                }
+            } else {
+                const int b = t - length;
+                const float n = (float)min(a.block, count - b * a.block);
+                const float *vb = a.bsum_v + (int64_t)b * kvw + (int64_t)kh * D + 16 * sub;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 v = load_f4(vb + 4 * c);
+                    acc[c].x = fmaf(p, v.x / n, acc[c].x);
+                    acc[c].y = fmaf(p, v.y / n, acc[c].y);
+                    acc[c].z = fmaf(p, v.z / n, acc[c].z);
+                    acc[c].w = fmaf(p, v.w / n, acc[c].w);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float ox = att::keygroups_sum_lanes<LPK>(acc[c].x);
+        const float oy = att::keygroups_sum_lanes<LPK>(acc[c].y);
+        const float oz = att::keygroups_sum_lanes<LPK>(acc[c].z);
+        const float ow = att::keygroups_sum_lanes<LPK>(acc[c].w);
+        if (kg == 0) *(float4 *)&wo[wave][16 * sub + 4 * c] = make_float4(ox, oy, oz, ow);
+    }
+    __syncthreads();
+    for (int j = tid; j < D; j += kAttnThreads) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) o += wo[w][j];
+        a.out[(int64_t)h * D + j] = o / den;
     }
 }
 
@@ -333,7 +469,12 @@ int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context) {
     const int blocks = (context + a.block - 1) / a.block;
     const size_t lds = (size_t)(a.d + std::min(a.window, context) + blocks) * sizeof(float) + (size_t)blocks * sizeof(int);
     MR_REQUIRE(lds <= 64 * 1024, "heavy attention: window and block count exceed shared memory");
-    k_heavy_attn<<<a.heads, kAttnThreads, lds, s>>>(a);
+    switch (a.d) {
+        case 128: k_heavy_attn_lanes<128><<<a.heads, kAttnThreads, lds, s>>>(a); break;
+        case 64: k_heavy_attn_lanes<64><<<a.heads, kAttnThreads, lds, s>>>(a); break;
+        case 32: k_heavy_attn_lanes<32><<<a.heads, kAttnThreads, lds, s>>>(a); break;
+        default: k_heavy_attn<<<a.heads, kAttnThreads, lds, s>>>(a); break;
+    }
     MR_LAUNCHED("enqueue heavy attention");
     return MR_OK;
 }
