@@ -54,20 +54,52 @@ def weight_bytes(cfg, dtype_bytes=2):
     return total
 
 
-def decode_bytes(cfg, context, position):
-    """Algorithmic HBM bytes of one decode step at `position` (0-based):
-    every projection weight once, the LM head, one embedding row, the KV rows
-    the attention reads (FP32), the new K/V rows written, and the logits."""
+def decode_bytes(cfg, context, position, dtype_bytes=2):
+    """Algorithmic HBM bytes of one decode step at `position` (0-based).
+
+    GQA families: every projection weight once, the LM head, one embedding
+    row, the KV rows the attention reads (FP32), the new K/V rows, the logits.
+    flashlighting-2.0: the same weights; the key and value cache rows of every
+    latent-memory row (min(position + 1, window + memory slots)).
+    heavy-medium-2.0: per inner-loop pass the attention weights, the router and
+    the active experts (top-k max routed + shared) again; the window rows and
+    the block sums of keys (all blocks) and values (the chosen ones) of that
+    pass's cache."""
+    from miracle_hip.weights import expected_shapes
     h, d, V = cfg.hidden_size, cfg.head_dim, cfg.vocab_size
-    head = V * h * 2
-    embed_row = h * 2
-    body = weight_bytes(cfg) - V * h * 2 * (1 if cfg.tie_embeddings else 2)   # layers + final norm
+    head = V * h * dtype_bytes
+    fixed = head + h * dtype_bytes + V * 4   # LM head, embedding row, logits
+    shapes = expected_shapes(cfg)
+
+    def tensor(name):
+        n = int(np.prod(shapes[name]))
+        return n * (4 if len(shapes[name]) == 1 else dtype_bytes)
+
+    if cfg.family == "heavy-medium-2.0":
+        src = cfg.source
+        active = src["router_top_k_max"] + src["shared_experts"]
+        lc = src["long_context"]
+        total = fixed + tensor("norm")
+        for layer in range(cfg.layers):
+            pre = f"layers.{layer}."
+            attn = sum(tensor(pre + k) for k in ("a_norm", "q", "o", "latent", "kv_up", "f_norm"))
+            router = sum(tensor(n) for n in shapes if n.startswith(pre + "router."))
+            expert = sum(tensor(pre + f"experts.0.{k}") for k in ("gate", "up", "down"))
+            kvw = cfg.kv_heads * d
+            blocks = -(-(position + 1) // lc["global_block_size"])
+            kv = (2 * min(position + 1, cfg.window) + blocks + min(lc["global_slots"], blocks) + 4) * kvw * 4
+            total += cfg.inner_loop_steps * (attn + router + active * expert + kv)
+        return total
+    body = weight_bytes(cfg, dtype_bytes) - V * h * dtype_bytes * (1 if cfg.tie_embeddings else 2)
     kv = 0
     for layer in range(cfg.layers):
         kvw = cfg.layer_kv_heads(layer) * d
-        cap = min(cfg.layer_window(layer) or context, context)
-        kv += 2 * min(position + 1, cap) * kvw * 4 + 2 * kvw * 4
-    return body + head + embed_row + kv + V * 4
+        if cfg.family == "flashlighting-2.0":
+            rows = min(position + 1, cfg.window + cfg.memory_slots)
+        else:
+            rows = min(position + 1, min(cfg.layer_window(layer) or context, context))
+        kv += 2 * rows * kvw * 4 + 2 * kvw * 4
+    return body + fixed + kv
 
 
 def prefill_flops(cfg, context, tokens):
@@ -92,7 +124,7 @@ def gate_up_bytes(cfg):
     return 2 * f * h * 2 + h * 4 + h * 4 + f * 4   # weights + hidden + gain + activations out
 
 
-def cpu_baseline(wl, weights, budget_s):
+def cpu_baseline(name, wl, weights, budget_s):
     """Oracle token steps on the host (FP32 weights resident, all affine cores)."""
     from oracle import kernels as K
     from oracle.model import OracleModel
@@ -106,7 +138,7 @@ def cpu_baseline(wl, weights, budget_s):
         n += 1
     elapsed = time.perf_counter() - t0
     return {"value": round(n / elapsed, 3), "unit": "tok/s", "cores": K.threads(), "kind": "port",
-            "sample": f"{n} token steps (positions 1..{n}) of {WORKLOAD} through the oracle's C restatement of "
+            "sample": f"{n} token steps (positions 1..{n}) of {name} through the oracle's C restatement of "
                       f"the reference kernels, FP32 weights resident, the reference's token-by-token loop; "
                       f"{elapsed:.1f} s"}
 
@@ -114,6 +146,8 @@ def cpu_baseline(wl, weights, budget_s):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=sorted(presets.WORKLOADS), default=WORKLOAD,
+                    help="the measured configuration (default: the headline flashnano-1.7)")
     ap.add_argument("--steps", type=int, default=511, help="timed decode steps")
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode steps before timing")
     ap.add_argument("--prompt", type=int, default=None, help="prompt length (default: the workload's 4096)")
@@ -136,8 +170,12 @@ def main():
 
     from miracle_hip import HIPBackend, MiracleModel
 
-    wl = presets.workload(WORKLOAD)
+    name = args.workload
+    wl = presets.workload(name)
     cfg = ModelConfig.from_dict(wl["config"])
+    gqa = cfg.family in ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
+    # batched prefill covers the GQA families without relay rows; the others take the token loop
+    prefill_mode = args.prefill_mode if cfg.family in ("flashnano-1.5", "flashnano-1.7", "flashlite-2.0") else "exact"
     prompt_len = args.prompt or wl["prompt"]
     if prompt_len + args.warmup + args.steps > wl["context"]:
         raise SystemExit("prompt + warmup + steps exceed the context")
@@ -154,15 +192,16 @@ def main():
     log(f"step mode {step_mode}")
 
     # Prefill: the whole prompt, logits of the last token.
-    log(f"prefill {prompt_len} tokens ({args.prefill_mode})")
+    log(f"prefill {prompt_len} tokens ({prefill_mode})")
     # First launches, graph capture and the batched workspace outside the timed region.
-    model.prefill(prompt if args.prefill_mode == "batched" else prompt[:8])
+    model.prefill(prompt if prefill_mode == "batched" else prompt[:8])
     model.reset()
     t0 = time.perf_counter()
     model.prefill(prompt)
     prefill_s = time.perf_counter() - t0
-    pf_flops = prefill_flops(cfg, wl["context"], prompt_len)
-    log(f"prefill {prompt_len / prefill_s:.1f} tok/s, {pf_flops / prefill_s / 1e12:.1f} TFLOP/s algorithmic")
+    pf_flops = prefill_flops(cfg, wl["context"], prompt_len) if gqa else None
+    log(f"prefill {prompt_len / prefill_s:.1f} tok/s" +
+        (f", {pf_flops / prefill_s / 1e12:.1f} TFLOP/s algorithmic" if pf_flops else ""))
 
     if args.traffic_probe:
         n = 64 * 1024 * 1024
@@ -189,7 +228,8 @@ def main():
 
     # Per-kernel device time (HIP events) of the per-layer kernels, each launched
     # for every layer in turn.
-    kernels = {k: eng.time_kernel(k, args.kernel_reps) for k in ("qkv", "attention", "o", "gate_up", "down", "head")}
+    kinds = ("qkv", "attention", "o", "gate_up", "down", "head") if gqa else ("head",)
+    kernels = {k: eng.time_kernel(k, args.kernel_reps) for k in kinds}
     if step_mode == "persistent":
         # The dominant (and only) kernel of a decode step is the step kernel.
         # HBM traffic per launch comes from the committed rocprofv3 counter
@@ -197,12 +237,19 @@ def main():
         # by a copy of known size); it is not measured in this run.
         step_ms = device_ms / args.steps
         traffic = None
-        tf = ROOT / "profiles" / "k_step_flashnano-1.7_traffic.json"
+        tf = ROOT / "profiles" / f"k_step_{name}_traffic.json"
         if tf.exists():
             traffic = json.loads(tf.read_text()).get("traffic_bytes")
-        roof = {"kernel": "persistent decode step (24 layers + LM head + greedy choice)", "bound": "hbm",
+        roof = {"kernel": f"persistent decode step ({cfg.layers} layers + LM head + greedy choice)", "bound": "hbm",
                 "achieved": round(avg_bytes / (step_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(avg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "algorithmic_bytes": int(avg_bytes), "avg_ms": round(step_ms, 5)}
+    elif not gqa:
+        # heavy / latent families: the graph-captured step (many small kernels) as one unit
+        step_ms = device_ms / args.steps
+        roof = {"kernel": f"graph-captured decode step ({cfg.layers} layers + LM head + greedy choice)",
+                "bound": "hbm", "achieved": round(avg_bytes / (step_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(avg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                 "algorithmic_bytes": int(avg_bytes), "avg_ms": round(step_ms, 5)}
     else:
         gu_ms = kernels["gate_up"]
@@ -211,20 +258,21 @@ def main():
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                 "algorithmic_bytes": gate_up_bytes(cfg), "avg_ms": round(gu_ms, 5)}
     result = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC if name == WORKLOAD else METRIC.replace(WORKLOAD, name), "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(1e3 * decode_s / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": WORKLOAD, "weights": "bf16 random-init seed 2", "prompt": prompt_len,
+        "config": {"workload": name, "weights": f"{wl['dtype']} random-init seed {wl['seed']}", "prompt": prompt_len,
                    "decode_positions": [prompt_len, prompt_len + args.steps - 1], "context": wl["context"],
-                   "prefill_mode": args.prefill_mode, "step_mode": step_mode},
+                   "prefill_mode": prefill_mode, "step_mode": step_mode},
         "decode_hbm": {"algorithmic_bytes_per_token": int(avg_bytes),
                        "achieved_gbs": round(avg_bytes * tok_s / 1e9, 1),
                        "peak_gbs": HBM_PEAK_GBS, "frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
         "prefill": {"tok_s": round(prompt_len / prefill_s, 1), "seconds": round(prefill_s, 4),
-                    "mode": args.prefill_mode, "algorithmic_tflop": round(pf_flops / 1e12, 3),
-                    "achieved_tflops": round(pf_flops / prefill_s / 1e12, 1),
+                    "mode": prefill_mode,
+                    "algorithmic_tflop": round(pf_flops / 1e12, 3) if pf_flops else None,
+                    "achieved_tflops": round(pf_flops / prefill_s / 1e12, 1) if pf_flops else None,
                     "peak_bf16_dense_tflops": MFMA_BF16_PEAK_TFLOPS,
-                    "frac": round(pf_flops / prefill_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+                    "frac": round(pf_flops / prefill_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4) if pf_flops else None},
         "roofline": roof,
         "decode_device_ms": round(device_ms, 3),
         "layer_kernels_ms": {k: round(v, 5) for k, v in kernels.items()},
@@ -232,7 +280,7 @@ def main():
     }
     if args.cpu_seconds > 0:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(wl, weights, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(name, wl, weights, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
