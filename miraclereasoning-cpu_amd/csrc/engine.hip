@@ -849,7 +849,7 @@ int finalize_light_layer(mr_model *m, Layer &L, int i) {
     MR_TRY(device_alloc(m, cap * kvw * sizeof(float), (void **)&L.vcache));
     MR_TRY(device_alloc(m, sizeof(LightState), (void **)&L.light));
     MR_HIP(hipMemset(L.light, 0, sizeof(LightState)), "clear latent state");
-    if (light_split_dim(hd) && !m->light_part) {   // split partials, shared by the layers (one at a time)
+    if (light_split_path(hd, L.light_cap) && !m->light_part) {   // split partials, shared by the layers (one at a time)
         const size_t n = (size_t)d.query_heads * light_splits(L.light_cap) * (hd + 2);
         MR_TRY(device_alloc(m, n * sizeof(float), (void **)&m->light_part));
     }

@@ -41,16 +41,18 @@ __global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
     const int kvw = a.kv_heads * d;
     const float *src = isq ? a.q + (int64_t)hh * d : a.kv + (int64_t)hh * d;
     __shared__ float scale;
-    if (threadIdx.x == 0) {   // kernels.cl:19-28: one sequential sum of squares
+    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = src[j];
+    __syncthreads();
+    if (threadIdx.x == 0) {   // kernels.cl:19-28: one sequential sum of squares (row staged in LDS)
         float v = 0.0f;
         for (int j = 0; j < d; ++j) {
-            const float x = src[j];
+            const float x = row[j];
             v += x * x;
         }
         scale = 1.0f / sqrtf(v / (float)d + 1e-6f);
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = src[j] * scale * 1.0f;
+    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = row[j] * scale * 1.0f;
     __syncthreads();
     const float *cs = a.rope + (int64_t)pos * half * 2;
     for (int p = threadIdx.x; p < half; p += blockDim.x) {   // interleaved pairs (kernels.cl:30-44)
@@ -343,13 +345,19 @@ __global__ void __launch_bounds__(kMaxExperts) k_moe_route(MoeArgs a) {
         logits[tid] = (fine + coarse[g]) / a.inv_temperature_div;
     }
     __syncthreads();
-    if (tid == 0) {   // kernels.cl:75-84 softmax
-        float m = -INFINITY;
-        for (int e = 0; e < E; ++e) m = fmaxf(m, logits[e]);
-        float den = 0.0f;
-        for (int e = 0; e < E; ++e) den += expf(logits[e] - m);
-        for (int e = 0; e < E; ++e) probs[e] = expf(logits[e] - m) / den;
+    // kernels.cl:75-84 softmax: the maximum (order-free), each exponent by its
+    // own lane, the denominator summed sequentially by lane 0
+    __shared__ float red[kMaxExperts / kWave], softmax_den;
+    const float m = block_max(tid < E ? logits[tid] : -INFINITY, red);
+    if (tid < E) terms[tid] = expf(logits[tid] - m);
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.0f;
+        for (int e = 0; e < E; ++e) t += terms[e];
+        softmax_den = t;
     }
+    __syncthreads();
+    if (tid < E) probs[tid] = terms[tid] / softmax_den;
     __syncthreads();
     if (tid < E) {   // stable argsort of -probs (model.py:241)
         const float p = probs[tid];
@@ -460,6 +468,158 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down(MoeArgs a) {
     if ((threadIdx.x & 63) == 0) a.hidden[row] = a.hidden[row] + a.scale * total;
 }
 
+// BF16 expert kernels (h and ffn multiples of 8).  A wave issues all of its
+// 16-byte weight loads for a round (gate and up of two rows, or one row of
+// every slot's down matrix) before the workgroup stages its input vector in
+// LDS, so the weight latency and the staging overlap; the products keep the
+// per-row wave sums and the accumulation order of the kernels above.
+typedef unsigned moe_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kMoeGuRows = 2;        // rows per wave in the gate/up kernel
+constexpr int kMoeGuVec = 4;         // 16-byte vectors per lane and matrix row in one round
+constexpr int kMoeDnVec = 2;         // 16-byte vectors per lane and slot row in one round
+constexpr int kMoeMaxSlots = 16;     // routed top-k + shared experts in the down kernel's slot chunk
+
+__device__ __forceinline__ float dot8_bf16(moe_u32x4 q, const float *x, float acc) {
+    const float4 x0 = *(const float4 *)x, x1 = *(const float4 *)(x + 4);
+    acc = fmaf(__uint_as_float(q.x << 16), x0.x, acc);
+    acc = fmaf(__uint_as_float(q.x & 0xffff0000u), x0.y, acc);
+    acc = fmaf(__uint_as_float(q.y << 16), x0.z, acc);
+    acc = fmaf(__uint_as_float(q.y & 0xffff0000u), x0.w, acc);
+    acc = fmaf(__uint_as_float(q.z << 16), x1.x, acc);
+    acc = fmaf(__uint_as_float(q.z & 0xffff0000u), x1.y, acc);
+    acc = fmaf(__uint_as_float(q.w << 16), x1.z, acc);
+    acc = fmaf(__uint_as_float(q.w & 0xffff0000u), x1.w, acc);
+    return acc;
+}
+
+// grid (ceil(ffn / (kMoeRows * kMoeGuRows)), kmax + shared)
+__global__ void __launch_bounds__(kMoeThreads) k_moe_gate_up_bf16(MoeArgs a) {
+    extern __shared__ __align__(16) float xs[];
+    if (a.done && *a.done) return;
+    const int slot = blockIdx.y;
+    int e;
+    if (slot < a.kmax) {
+        if (slot >= *a.active) return;
+        e = a.ids[slot];
+    } else {
+        e = a.experts + (slot - a.kmax);
+    }
+    const int lane = threadIdx.x & 63, nv = a.h / 8;
+    const int r0 = (blockIdx.x * kMoeRows + (threadIdx.x >> 6)) * kMoeGuRows;
+    const moe_u32x4 *gw = (const moe_u32x4 *)a.gate[e], *uw = (const moe_u32x4 *)a.up[e];
+    int64_t rb[kMoeGuRows];
+#pragma unroll
+    for (int r = 0; r < kMoeGuRows; ++r) rb[r] = (int64_t)min(r0 + r, a.ffn - 1) * nv;
+    moe_u32x4 qg[kMoeGuRows][kMoeGuVec], qu[kMoeGuRows][kMoeGuVec];
+#pragma unroll
+    for (int i = 0; i < kMoeGuVec; ++i) {
+        const int v = min(lane + kWave * i, nv - 1);
+#pragma unroll
+        for (int r = 0; r < kMoeGuRows; ++r) {
+            qg[r][i] = __builtin_nontemporal_load(gmem(gw + rb[r] + v));
+            qu[r][i] = __builtin_nontemporal_load(gmem(uw + rb[r] + v));
+        }
+    }
+    for (int j = threadIdx.x * 4; j < a.h; j += kMoeThreads * 4) *(float4 *)&xs[j] = load_f4(a.x + j);
+    __syncthreads();
+    if (r0 >= a.ffn) return;
+    float g[kMoeGuRows] = {}, u[kMoeGuRows] = {};
+    for (int base = 0;;) {
+#pragma unroll
+        for (int i = 0; i < kMoeGuVec; ++i) {
+            const int v = base + lane + kWave * i;
+            if (v < nv) {
+#pragma unroll
+                for (int r = 0; r < kMoeGuRows; ++r) {
+                    g[r] = dot8_bf16(qg[r][i], xs + 8 * v, g[r]);
+                    u[r] = dot8_bf16(qu[r][i], xs + 8 * v, u[r]);
+                }
+            }
+        }
+        base += kWave * kMoeGuVec;
+        if (base >= nv) break;
+#pragma unroll
+        for (int i = 0; i < kMoeGuVec; ++i) {
+            const int v = min(base + lane + kWave * i, nv - 1);
+#pragma unroll
+            for (int r = 0; r < kMoeGuRows; ++r) {
+                qg[r][i] = __builtin_nontemporal_load(gmem(gw + rb[r] + v));
+                qu[r][i] = __builtin_nontemporal_load(gmem(uw + rb[r] + v));
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kMoeGuRows; ++r) {
+        const float gs = wave_sum(g[r]), us = wave_sum(u[r]);
+        if (lane == 0 && r0 + r < a.ffn)
+            a.act[(int64_t)slot * a.ffn + r0 + r] = (gs / (1.0f + expf(-gs))) * us;   // kernels.cl:46-50
+    }
+}
+
+// grid ceil(h / kMoeRows): one wave per output row over the active routed
+// slots in chosen order, then the shared experts.
+__global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
+    extern __shared__ __align__(16) float acts[];
+    __shared__ const moe_u32x4 *wp[kMoeMaxSlots];
+    __shared__ float wsc[kMoeMaxSlots];
+    __shared__ int aoff[kMoeMaxSlots];
+    if (a.done && *a.done) return;
+    const int tid = threadIdx.x, lane = tid & 63, nv = a.ffn / 8;
+    const int active = *a.active, n = active + a.shared;
+    if (tid < n) {   // slot table: routed slots 0..active-1, then the shared experts
+        const bool routed = tid < active;
+        const int s = routed ? tid : a.kmax + (tid - active);
+        wp[tid] = (const moe_u32x4 *)a.down[routed ? a.ids[tid] : a.experts + (tid - active)];
+        wsc[tid] = routed ? a.weights[tid] : a.shared_scale;
+        aoff[tid] = s * a.ffn;
+    }
+    __syncthreads();
+    const int row = min((int)(blockIdx.x * kMoeRows + (tid >> 6)), a.h - 1);
+    moe_u32x4 q[kMoeMaxSlots][kMoeDnVec];
+#pragma unroll
+    for (int k = 0; k < kMoeMaxSlots; ++k) {
+        const moe_u32x4 *w = wp[min(k, n - 1)] + (int64_t)row * nv;
+#pragma unroll
+        for (int i = 0; i < kMoeDnVec; ++i)
+            if (k < n) q[k][i] = __builtin_nontemporal_load(gmem(w + min(lane + kWave * i, nv - 1)));
+    }
+    const int total4 = (a.kmax + a.shared) * a.ffn;
+    for (int j = tid * 4; j < total4; j += kMoeThreads * 4) *(float4 *)&acts[j] = load_f4(a.act + j);
+    __syncthreads();
+    if ((int)(blockIdx.x * kMoeRows + (tid >> 6)) >= a.h) return;
+    float acc[kMoeMaxSlots] = {};
+    for (int base = 0;;) {
+#pragma unroll
+        for (int k = 0; k < kMoeMaxSlots; ++k) {
+            if (k < n) {
+#pragma unroll
+                for (int i = 0; i < kMoeDnVec; ++i) {
+                    const int v = base + lane + kWave * i;
+                    if (v < nv) acc[k] = dot8_bf16(q[k][i], acts + aoff[k] + 8 * v, acc[k]);
+                }
+            }
+        }
+        base += kWave * kMoeDnVec;
+        if (base >= nv) break;
+#pragma unroll
+        for (int k = 0; k < kMoeMaxSlots; ++k) {
+            const moe_u32x4 *w = wp[min(k, n - 1)] + (int64_t)row * nv;
+#pragma unroll
+            for (int i = 0; i < kMoeDnVec; ++i)
+                if (k < n) q[k][i] = __builtin_nontemporal_load(gmem(w + min(base + lane + kWave * i, nv - 1)));
+        }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMoeMaxSlots; ++k) {
+        if (k < n) {
+            const float y = wave_sum(acc[k]);
+            total = total + wsc[k] * y;
+        }
+    }
+    if (lane == 0) a.hidden[row] = a.hidden[row] + a.scale * total;
+}
+
 }  // namespace
 
 int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context) {
@@ -486,11 +646,20 @@ int launch_moe(hipStream_t s, const MoeArgs &a) {
     k_moe_route<<<1, kMaxExperts, 0, s>>>(a);
     MR_LAUNCHED("enqueue moe routing");
     const int slots = a.kmax + a.shared;
-    k_moe_gate_up<<<dim3(ceil_div(a.ffn, kMoeRows), slots), kMoeThreads, (size_t)a.h * sizeof(float), s>>>(a);
-    MR_LAUNCHED("enqueue moe gate/up");
     const size_t lds = (size_t)slots * a.ffn * sizeof(float);
     MR_REQUIRE(lds <= 64 * 1024, "moe: expert activations exceed shared memory");
-    k_moe_down<<<ceil_div(a.h, kMoeRows), kMoeThreads, lds, s>>>(a);
+    const bool fast = a.dtype == MR_BF16 && a.h % 8 == 0 && a.ffn % 8 == 0 && a.kmax + a.shared <= kMoeMaxSlots;
+    if (fast) {
+        k_moe_gate_up_bf16<<<dim3(ceil_div(a.ffn, kMoeRows * kMoeGuRows), slots), kMoeThreads,
+                             (size_t)a.h * sizeof(float), s>>>(a);
+    } else {
+        k_moe_gate_up<<<dim3(ceil_div(a.ffn, kMoeRows), slots), kMoeThreads, (size_t)a.h * sizeof(float), s>>>(a);
+    }
+    MR_LAUNCHED("enqueue moe gate/up");
+    if (fast)
+        k_moe_down_bf16<<<ceil_div(a.h, kMoeRows), kMoeThreads, lds, s>>>(a);
+    else
+        k_moe_down<<<ceil_div(a.h, kMoeRows), kMoeThreads, lds, s>>>(a);
     MR_LAUNCHED("enqueue moe down");
     return MR_OK;
 }

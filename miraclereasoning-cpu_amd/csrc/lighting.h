@@ -37,7 +37,11 @@ struct LightArgs {
 // the split path; other dims the single-workgroup kernel).
 constexpr int kLightRows = 64;
 inline int light_splits(int cap) { return (cap + kLightRows - 1) / kLightRows; }
-inline bool light_split_dim(int d) { return d == 32 || d == 64 || d == 128; }
+constexpr int kLightMaxSplits = 1024;   // split weights held in the merge kernel's LDS
+// The split-key attention covers head dims 32/64/128 and up to 64 Ki memory rows.
+inline bool light_split_path(int d, int cap) {
+    return (d == 32 || d == 64 || d == 128) && light_splits(cap) <= kLightMaxSplits;
+}
 
 // Queries, the new latent row (appended), then - after the K/V projection of
 // lat_new - its key/value cache row.

@@ -22,18 +22,21 @@
 namespace mr {
 namespace {
 
-// RMSNorm of one row (kernels.cl:19-28): one sequential sum of squares.
+// RMSNorm of one row (kernels.cl:19-28) by one 64-lane workgroup: the row is
+// staged in LDS, each lane sums the squares of its strided elements and a
+// wave reduction adds the lanes (an FP32 reordering of the reference's
+// sequential sum).
 __device__ __forceinline__ void rms_row(const float *x, const float *gain, float eps, int width, float *y, float *scale) {
-    if (threadIdx.x == 0) {
-        float v = 0.0f;
-        for (int j = 0; j < width; ++j) {
-            const float a = x[j];
-            v += a * a;
-        }
-        *scale = 1.0f / sqrtf(v / (float)width + eps);
+    float v = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) {
+        const float t = x[j];
+        y[j] = t;
+        v = fmaf(t, t, v);
     }
-    __syncthreads();
-    for (int j = threadIdx.x; j < width; j += blockDim.x) y[j] = x[j] * *scale * (gain ? gain[j] : 1.0f);
+    v = wave_sum(v);
+    const float sc = 1.0f / sqrtf(v / (float)width + eps);
+    if (threadIdx.x == 0) *scale = sc;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) y[j] = y[j] * sc * (gain ? gain[j] : 1.0f);
     __syncthreads();
 }
 
@@ -252,24 +255,65 @@ __global__ void __launch_bounds__(kPartThreads) k_light_attend_part(LightArgs a)
     }
 }
 
-// grid heads, D threads: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// grid heads, kMergeThreads: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// The split weights e^(m_s - M) go to LDS; lane quads cover D/4 float4
+// columns and kMergeThreads / (D/4) split groups stride the splits, folded
+// through LDS at the end.
+constexpr int kMergeThreads = 256;
+
 template <int D>
-__global__ void __launch_bounds__(D) k_light_attend_merge(LightArgs a, int splits) {
+__global__ void __launch_bounds__(kMergeThreads) k_light_attend_merge(LightArgs a, int splits) {
+    constexpr int Q = D / 4, G = kMergeThreads / Q;
+    __shared__ float e[kLightMaxSplits], red[kMergeThreads / kWave];
+    __shared__ float4 fold[G][Q];
+    __shared__ float lsum[G];
     if (a.done && *a.done) return;
     const int n = a.st->rows + 1, active = min(splits, (n + kLightRows - 1) / kLightRows);
-    const int h = blockIdx.x, j = threadIdx.x;
+    const int h = blockIdx.x, tid = threadIdx.x;
     const float *part = a.part + (int64_t)h * splits * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < active; ++s) M = fmaxf(M, part[(int64_t)s * (D + 2)]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < active; ++s) {
+    float mx = -INFINITY;
+    for (int s = tid; s < active; s += kMergeThreads) {
         const float ms = part[(int64_t)s * (D + 2)];
-        if (ms == -INFINITY) continue;
-        const float e = __expf(ms - M);
-        L = fmaf(part[(int64_t)s * (D + 2) + 1], e, L);
-        O = fmaf(part[(int64_t)s * (D + 2) + 2 + j], e, O);
+        e[s] = ms;
+        mx = fmaxf(mx, ms);
     }
-    a.out[(int64_t)h * D + j] = O / L;
+    const float M = block_max(mx, red);
+    for (int s = tid; s < active; s += kMergeThreads) e[s] = e[s] == -INFINITY ? 0.0f : __expf(e[s] - M);
+    __syncthreads();
+    const int g = tid / Q, c = tid % Q;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float l = 0.0f;
+#pragma unroll 4
+    for (int s = g; s < active; s += G) {
+        const float w = e[s];
+        const float *ps = part + (int64_t)s * (D + 2);
+        const float4 v = make_float4(ps[2 + 4 * c], ps[3 + 4 * c], ps[4 + 4 * c], ps[5 + 4 * c]);
+        if (c == 0) l = fmaf(ps[1], w, l);
+        o.x = fmaf(v.x, w, o.x);
+        o.y = fmaf(v.y, w, o.y);
+        o.z = fmaf(v.z, w, o.z);
+        o.w = fmaf(v.w, w, o.w);
+    }
+    fold[g][c] = o;
+    if (c == 0) lsum[g] = l;
+    __syncthreads();
+    if (tid < Q) {
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            t.x += fold[k][tid].x;
+            t.y += fold[k][tid].y;
+            t.z += fold[k][tid].z;
+            t.w += fold[k][tid].w;
+            L += lsum[k];
+        }
+        float *out = a.out + (int64_t)h * D + 4 * tid;
+        out[0] = t.x / L;
+        out[1] = t.y / L;
+        out[2] = t.z / L;
+        out[3] = t.w / L;
+    }
 }
 
 // One workgroup: compaction after this step's attention (model.py:168-188).
@@ -344,24 +388,24 @@ int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged) {
 }
 
 int launch_light_attend(hipStream_t s, const LightArgs &a) {
-    if (light_split_dim(a.d) && a.part) {
+    if (light_split_path(a.d, a.cap) && a.part) {
         const int splits = light_splits(a.cap);
         const dim3 grid(splits, a.heads);
         switch (a.d) {
             case 128:
                 k_light_attend_part<128><<<grid, kPartThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<128><<<a.heads, 128, 0, s>>>(a, splits);
+                k_light_attend_merge<128><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
                 break;
             case 64:
                 k_light_attend_part<64><<<grid, kPartThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<64><<<a.heads, 64, 0, s>>>(a, splits);
+                k_light_attend_merge<64><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
                 break;
             default:
                 k_light_attend_part<32><<<grid, kPartThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<32><<<a.heads, 32, 0, s>>>(a, splits);
+                k_light_attend_merge<32><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
                 break;
         }
         MR_LAUNCHED("enqueue latent attention merge");
