@@ -83,7 +83,7 @@ struct mr_model {
     float *q_rot = nullptr, *kvbuf = nullptr, *router_out = nullptr, *moe_w = nullptr, *moe_act = nullptr;
     int *moe_ids = nullptr, *moe_active = nullptr;
     float *lat_new = nullptr, *branch_o = nullptr, *branch_f = nullptr;   // flashlighting-2.0
-    float *light_part = nullptr;         // flashlighting-2.0 attention split partials
+    float *split_part = nullptr;         // split decode attention partials (latent and block-sparse families)
     int *choices = nullptr;              // [context + 1][layers][inner][choice_rec]
     int choice_rec = 0;                  // ints per record: active, kmax ids, heads x slots blocks
     // step execution: persistent kernel (when the model fits its phases) or

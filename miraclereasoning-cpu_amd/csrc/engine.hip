@@ -434,6 +434,7 @@ int record_heavy_layer(mr_model *m, Layer &L, int li) {
         a.bsum_k = L.bsum_k + (size_t)loop * blocks * kvw;
         a.bsum_v = L.bsum_v + (size_t)loop * blocks * kvw;
         a.out = m->attn;
+        a.part = m->split_part;
         a.choice = m->choices + ((size_t)li * inner + loop) * m->choice_rec;
         a.choice_stride = d.layers * inner * m->choice_rec;
         a.choice_blocks = 1 + kmax;
@@ -483,7 +484,7 @@ int record_light_layer(mr_model *m, Layer &L) {
     a.done = m->done_dev; a.q_rot = m->q_rot; a.arena = L.arena; a.positions = L.positions; a.counts = L.counts;
     a.kcache = L.kcache; a.vcache = L.vcache; a.lat_new = m->lat_new; a.kv = m->kvbuf; a.st = L.light;
     a.out = m->attn; a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.latent = d.latent_dim;
-    a.window = d.window; a.memory_slots = d.memory_slots; a.cap = L.light_cap; a.part = m->light_part;
+    a.window = d.window; a.memory_slots = d.memory_slots; a.cap = L.light_cap; a.part = m->split_part;
     MR_TRY(launch_light_prep(s, a));
     GemvArgs u;   // [Wk; Wv] . new latent row
     u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
@@ -823,6 +824,11 @@ int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     MR_TRY(device_alloc(m, bsum, (void **)&L.bsum_v));
     for (void *p : {(void *)L.ring_k, (void *)L.ring_v, (void *)L.bsum_k, (void *)L.bsum_v})
         MR_HIP(hipMemset(p, 0, p == L.ring_k || p == L.ring_v ? ring : bsum), "clear heavy caches");
+    if (heavy_split_path(hd, d.window, d.context_length, d.global_block_size, d.global_slots) && !m->split_part) {
+        // split partials, shared by the layers and inner-loop passes (one at a time)
+        const size_t n = (size_t)d.query_heads * heavy_parts(d.window, d.context_length) * (hd + 2);
+        MR_TRY(device_alloc(m, n * sizeof(float), (void **)&m->split_part));
+    }
     return MR_OK;
 }
 
@@ -849,9 +855,9 @@ int finalize_light_layer(mr_model *m, Layer &L, int i) {
     MR_TRY(device_alloc(m, cap * kvw * sizeof(float), (void **)&L.vcache));
     MR_TRY(device_alloc(m, sizeof(LightState), (void **)&L.light));
     MR_HIP(hipMemset(L.light, 0, sizeof(LightState)), "clear latent state");
-    if (light_split_path(hd, L.light_cap) && !m->light_part) {   // split partials, shared by the layers (one at a time)
+    if (light_split_path(hd, L.light_cap) && !m->split_part) {   // split partials, shared by the layers (one at a time)
         const size_t n = (size_t)d.query_heads * light_splits(L.light_cap) * (hd + 2);
-        MR_TRY(device_alloc(m, n * sizeof(float), (void **)&m->light_part));
+        MR_TRY(device_alloc(m, n * sizeof(float), (void **)&m->split_part));
     }
     return MR_OK;
 }
@@ -942,7 +948,7 @@ int mr_model_destroy(mr_model *m) {
     if (m->rope) hipFree(m->rope);
     if (m->state) hipFree(m->state);
     if (m->pf) hipFree(m->pf);
-    if (m->light_part) hipFree(m->light_part);
+    if (m->split_part) hipFree(m->split_part);
     for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_cells, (void *)m->merge_counts, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);

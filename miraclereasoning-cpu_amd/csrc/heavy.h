@@ -2,6 +2,8 @@
 // block-mean sparse attention and grouped adaptive MoE, all control on device.
 #pragma once
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace mr {
@@ -15,12 +17,22 @@ struct HeavyAttnArgs {
     float *ring_k = nullptr, *ring_v = nullptr;   // [context, kv_heads*d] of this inner loop
     float *bsum_k = nullptr, *bsum_v = nullptr;   // [blocks, kv_heads*d] running block sums
     float *out = nullptr;            // [heads*d] attended values
+    float *part = nullptr;           // [heads][heavy_parts(window, context)][d + 2] split partials (or null)
     int *choice = nullptr;           // choice record of this layer/loop at position 0 (or null)
     int choice_stride = 0;           // ints between the records of consecutive positions
     int choice_blocks = 0;           // offset of the block lists inside a record
     int heads = 0, kv_heads = 0, d = 0, window = 0, block = 0, slots = 0;
     float slope = 0.0f;              // alibi_slope_scale / sqrt(d), FP32
 };
+
+// Split form of the attention (head dims 32/64/128): one partial per 32 rows
+// of the window and one for the chosen blocks.
+constexpr int kHeavyRows = 32;
+inline int heavy_window_splits(int window, int context) {
+    return (std::min(window, context) + kHeavyRows - 1) / kHeavyRows;
+}
+inline int heavy_parts(int window, int context) { return heavy_window_splits(window, context) + 1; }
+bool heavy_split_path(int d, int window, int context, int block, int slots);
 
 int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context);
 

@@ -17,6 +17,8 @@
 //                  softmax, stable top-k, confidence / entropy / adaptive
 //                  width and renormalization in numpy's FP32 arithmetic
 //                  (model.py:231-250; numpy float32 sums are pairwise).
+//                  With BF16 experts every routed-slot workgroup of the
+//                  gate/up kernel routes the token itself instead.
 //   k_moe_gate_up  SwiGLU activations of every active routed slot and every
 //                  shared expert, weight pointers taken from a device table by
 //                  the device-side expert ids.
@@ -26,24 +28,41 @@
 //                  the residual add.
 #include "heavy.h"
 
-#include "attention_tile.h"
+#include "split_attention.h"
 
 namespace mr {
 namespace {
 
 // ------------------------------------------------------------------ attention
+// grid heads + kv_heads, 64 threads.  LDS: the row, its rotation angles and,
+// for a key, the value and the old block sums, all loaded up front (none
+// depends on the norm).
 __global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
     extern __shared__ float row[];
+    __shared__ float scale;
     if (a.done && *a.done) return;
     const int pos = *a.pos, d = a.d, half = d / 2;
     const bool isq = (int)blockIdx.x < a.heads;
     const int hh = isq ? blockIdx.x : blockIdx.x - a.heads;
     const int kvw = a.kv_heads * d;
     const float *src = isq ? a.q + (int64_t)hh * d : a.kv + (int64_t)hh * d;
-    __shared__ float scale;
-    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = src[j];
+    const float *cs = a.rope + (int64_t)pos * half * 2;
+    float *ang = row + d, *val = ang + d, *bk = val + d, *bv = bk + d;
+    const int64_t slot = (int64_t)pos * kvw + (int64_t)hh * d;
+    const int64_t bslot = (int64_t)(pos / a.block) * kvw + (int64_t)hh * d;
+    const bool first = pos % a.block == 0;
+#pragma unroll 4
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+        row[j] = src[j];
+        ang[j] = cs[j];
+        if (!isq) {
+            val[j] = a.kv[kvw + (int64_t)hh * d + j];
+            bk[j] = first ? 0.0f : a.bsum_k[bslot + j];
+            bv[j] = first ? 0.0f : a.bsum_v[bslot + j];
+        }
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {   // kernels.cl:19-28: one sequential sum of squares (row staged in LDS)
+    if (threadIdx.x == 0) {   // kernels.cl:19-28: one sequential sum of squares
         float v = 0.0f;
         for (int j = 0; j < d; ++j) {
             const float x = row[j];
@@ -52,12 +71,9 @@ __global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
         scale = 1.0f / sqrtf(v / (float)d + 1e-6f);
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < d; j += blockDim.x) row[j] = row[j] * scale * 1.0f;
-    __syncthreads();
-    const float *cs = a.rope + (int64_t)pos * half * 2;
     for (int p = threadIdx.x; p < half; p += blockDim.x) {   // interleaved pairs (kernels.cl:30-44)
-        float u = row[2 * p], v = row[2 * p + 1];
-        rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
+        float u = row[2 * p] * scale * 1.0f, v = row[2 * p + 1] * scale * 1.0f;
+        rope_rotate(u, v, ang[2 * p], ang[2 * p + 1]);
         row[2 * p] = u;
         row[2 * p + 1] = v;
     }
@@ -66,15 +82,12 @@ __global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
         for (int j = threadIdx.x; j < d; j += blockDim.x) a.q_rot[(int64_t)hh * d + j] = row[j];
         return;
     }
-    const int64_t slot = (int64_t)pos * kvw + (int64_t)hh * d;
-    const int64_t bslot = (int64_t)(pos / a.block) * kvw + (int64_t)hh * d;
-    const bool first = pos % a.block == 0;
     for (int j = threadIdx.x; j < d; j += blockDim.x) {
-        const float k = row[j], v = a.kv[kvw + (int64_t)hh * d + j];
+        const float k = row[j], v = val[j];
         a.ring_k[slot + j] = k;
         a.ring_v[slot + j] = v;
-        a.bsum_k[bslot + j] = (first ? 0.0f : a.bsum_k[bslot + j]) + k;
-        a.bsum_v[bslot + j] = (first ? 0.0f : a.bsum_v[bslot + j]) + v;
+        a.bsum_k[bslot + j] = bk[j] + k;
+        a.bsum_v[bslot + j] = bv[j] + v;
     }
 }
 
@@ -301,6 +314,132 @@ __global__ void __launch_bounds__(kAttnThreads) k_heavy_attn_lanes(HeavyAttnArgs
     }
 }
 
+// Split form for head dims 32/64/128, grid (window splits + 1, heads): the
+// workgroups x < splits write the partial of window rows [32 x, 32 x + 32);
+// the last one scores the block columns (the block-sum quotients of a chunk of
+// blocks staged in LDS by every thread, then one sequential dot product per
+// block in kernels.cl:58-73's order, so the block choices are the same bit for
+// bit), takes the stable top-k and writes the chosen blocks' partial in
+// ascending block order.  k_heavy_attn_merge combines the partials.
+constexpr int kBlockChunkFloats = 4096;   // block-sum quotients staged per pass
+constexpr int kHeavyMaxChosen = 32;       // chosen blocks per head
+constexpr int kChosenBatch = 8;           // chosen blocks' value loads in flight together
+
+inline size_t heavy_split_lds(int d, int blocks) {
+    return (size_t)(d + 2 * blocks + kBlockChunkFloats + kBlockChunkFloats / d) * sizeof(float);
+}
+
+template <int D>
+__global__ void __launch_bounds__(split::kThreads) k_heavy_attn_split(HeavyAttnArgs a) {
+    constexpr int NT = split::kThreads;
+    extern __shared__ float sh[];
+    if (a.done && *a.done) return;
+    const int pos = *a.pos, tid = threadIdx.x;
+    const int count = pos + 1, length = min(a.window, count), start = count - length;
+    const int h = blockIdx.y, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
+    const int wsplits = gridDim.x - 1;
+    float *part = a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2);
+    if ((int)blockIdx.x < wsplits) {
+        const int t0 = blockIdx.x * kHeavyRows;
+        if (t0 >= length) return;
+        const auto rows = [&](int t, const float **k, const float **v) {
+            *k = a.ring_k + (int64_t)(start + t) * kvw + (int64_t)kh * D;
+            *v = a.ring_v + (int64_t)(start + t) * kvw + (int64_t)kh * D;
+            return true;
+        };
+        split::partial<D>(a.q_rot + (int64_t)h * D, t0, min(length, t0 + kHeavyRows), rows, part);
+        return;
+    }
+    __shared__ int chosen[kHeavyMaxChosen];
+    const int blocks = (count + a.block - 1) / a.block;
+    float *qs = sh, *sc = qs + D;            // [D] query, [blocks] block scores
+    int *keep_flag = (int *)(sc + blocks);   // [blocks]
+    float *quo = (float *)(keep_flag + blocks);
+    for (int j = tid; j < D; j += NT) qs[j] = a.q_rot[(int64_t)h * D + j];
+    const float root = sqrtf((float)D);
+    constexpr int CB = kBlockChunkFloats / D;
+    for (int b0 = 0; b0 < blocks; b0 += CB) {
+        const int nb = min(CB, blocks - b0);
+        float kv[kBlockChunkFloats / NT];   // every load of the chunk in flight before the quotients
+#pragma unroll
+        for (int k = 0; k < kBlockChunkFloats / NT; ++k) {   // unguarded (clamped) loads issue back to back
+            const int i = min(tid + k * NT, nb * D - 1), b = b0 + i / D, j = i % D;
+            kv[k] = a.bsum_k[(int64_t)b * kvw + (int64_t)kh * D + j];
+        }
+#pragma unroll
+        for (int k = 0; k < kBlockChunkFloats / NT; ++k) {
+            const int i = tid + k * NT, b = b0 + i / D;
+            if (i < nb * D) quo[i + i / D] = kv[k] / (float)min(a.block, count - b * a.block);
+        }
+        __syncthreads();
+        for (int b = b0 + tid; b < b0 + nb; b += NT) {
+            const float *qb = quo + (b - b0) * (D + 1);   // rows padded by one float: no bank conflicts
+            float v = 0.0f;
+            for (int j = 0; j < D; ++j) v += qs[j] * qb[j];
+            const int end = min((b + 1) * a.block - 1, pos);
+            sc[b] = v / root - a.slope * log1pf((float)(pos - end));
+        }
+        __syncthreads();
+    }
+    const int keep = min(a.slots, blocks);
+    for (int b = tid; b < blocks; b += NT) {   // stable top-k (model.py:220-226)
+        const float s = sc[b];
+        int rank = 0;
+        for (int c = 0; c < blocks; ++c) {
+            const float o = sc[c];
+            rank += o > s || (o == s && c < b);
+        }
+        keep_flag[b] = rank < keep;
+    }
+    __syncthreads();
+    for (int b = tid; b < blocks; b += NT)   // chosen blocks in ascending order
+        if (keep_flag[b]) {
+            int at = 0;
+            for (int c = 0; c < b; ++c) at += keep_flag[c];
+            chosen[at] = b;
+        }
+    __syncthreads();
+    if (a.choice) {
+        int *rec = a.choice + (int64_t)pos * a.choice_stride + a.choice_blocks + h * a.slots;
+        for (int i = tid; i < a.slots; i += NT) rec[i] = i < keep ? chosen[i] : -1;
+    }
+    float m = -INFINITY;
+    for (int i = 0; i < keep; ++i) m = fmaxf(m, sc[chosen[i]]);
+    for (int j = tid; j < D; j += NT) {
+        float o = 0.0f, l = 0.0f;
+        for (int i0 = 0; i0 < keep; i0 += kChosenBatch) {
+            float vals[kChosenBatch];
+#pragma unroll
+            for (int i = 0; i < kChosenBatch; ++i)
+                vals[i] = a.bsum_v[(int64_t)chosen[min(i0 + i, keep - 1)] * kvw + (int64_t)kh * D + j];
+#pragma unroll
+            for (int i = 0; i < kChosenBatch; ++i) {
+                if (i0 + i < keep) {
+                    const int b = chosen[i0 + i];
+                    const float p = __expf(sc[b] - m);
+                    const float n = (float)min(a.block, count - b * a.block);
+                    o = fmaf(p, vals[i] / n, o);
+                    l += p;
+                }
+            }
+        }
+        part[2 + j] = o;
+        if (j == 0) {
+            part[0] = m;
+            part[1] = l;
+        }
+    }
+}
+
+// grid heads, split::kThreads: the active window partials and the block partial.
+template <int D>
+__global__ void __launch_bounds__(split::kThreads) k_heavy_attn_merge(HeavyAttnArgs a, int parts) {
+    if (a.done && *a.done) return;
+    const int length = min(a.window, *a.pos + 1);
+    split::merge<D>(a.part + (int64_t)blockIdx.x * parts * (D + 2), (length + kHeavyRows - 1) / kHeavyRows, parts - 1,
+                    a.out + (int64_t)blockIdx.x * D);
+}
+
 // ------------------------------------------------------------------ MoE
 // numpy's float32 add.reduce: pairwise summation, blocks of 8 accumulators
 // up to 128 elements, sequential below 8 elements; longer arrays split in two
@@ -331,63 +470,96 @@ __device__ float np_pairwise_sum(const float *a, int n) {
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
 
-__global__ void __launch_bounds__(kMaxExperts) k_moe_route(MoeArgs a) {
-    if (a.done && *a.done) return;
-    __shared__ float coarse[kMaxExperts], logits[kMaxExperts], probs[kMaxExperts], terms[kMaxExperts];
-    __shared__ int chosen[kMaxTopK];
-    const int tid = threadIdx.x, E = a.experts, G = a.groups;
-    if (tid < G) coarse[tid] = a.router[tid] + (a.coarse_bias[tid] + a.group_bias[tid]);
-    __syncthreads();
-    if (tid < E) {
-        const int size = (E + G - 1) / G;
-        const int g = min(tid / size, G - 1);
-        const float fine = a.router[G + tid] + (a.fine_bias[tid] + a.expert_bias[tid]);
-        logits[tid] = (fine + coarse[g]) / a.inv_temperature_div;
-    }
-    __syncthreads();
-    // kernels.cl:75-84 softmax: the maximum (order-free), each exponent by its
-    // own lane, the denominator summed sequentially by lane 0
-    __shared__ float red[kMaxExperts / kWave], softmax_den;
-    const float m = block_max(tid < E ? logits[tid] : -INFINITY, red);
-    if (tid < E) terms[tid] = expf(logits[tid] - m);
-    __syncthreads();
-    if (tid == 0) {
-        float t = 0.0f;
-        for (int e = 0; e < E; ++e) t += terms[e];
-        softmax_den = t;
-    }
-    __syncthreads();
-    if (tid < E) probs[tid] = terms[tid] / softmax_den;
-    __syncthreads();
-    if (tid < E) {   // stable argsort of -probs (model.py:241)
-        const float p = probs[tid];
-        int rank = 0;
-        for (int f = 0; f < E; ++f) rank += probs[f] > p || (probs[f] == p && f < tid);
-        if (rank < a.kmax) chosen[rank] = tid;
-        terms[tid] = p * logf(fmaxf(p, 1e-9f));
-    }
-    __syncthreads();
-    if (tid != 0) return;
-    const int kmax = a.kmax;
+// Routing of one token by one wave (experts <= kMaxExperts, up to four per
+// lane): biases, group broadcast, temperature, softmax, stable top-k, adaptive
+// width and renormalized weights, left in r for the wave; with publish, also
+// stored as the layer's ids, weights, width and choice record.  No workgroup
+// barrier: the lanes exchange values through LDS, which a wave reads back in
+// issue order.
+struct RouteLds {
+    float probs[kMaxExperts], terms[kMaxExperts];
+    int chosen[kMaxTopK];
     float w[kMaxTopK];
-    for (int r = 0; r < kmax; ++r) w[r] = probs[chosen[r]];
-    const float confidence = w[0] - w[min(kmax - 1, 1)];
-    const float entropy = -np_pairwise_sum(terms, E);
-    const float spread = rintf((1.0f - confidence) * 2.0f + entropy / a.log_experts);
-    const float width = fminf(fmaxf((float)a.kmin + spread, (float)a.kmin), (float)kmax);
-    const int active = (int)width;
-    for (int r = active; r < kmax; ++r) w[r] = 0.0f;
-    const float den = fmaxf(np_pairwise_sum(w, kmax), 1e-9f);
-    for (int r = 0; r < kmax; ++r) {
-        a.ids[r] = chosen[r];
-        a.weights[r] = w[r] / den;
+    int active;
+};
+
+__device__ __forceinline__ void route_wave(const MoeArgs &a, RouteLds &r, bool publish) {
+    constexpr int PER = kMaxExperts / kWave;
+    const int lane = threadIdx.x & 63, E = a.experts, G = a.groups, size = (E + G - 1) / G;
+    float logit[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {   // clamped indices: every load issues at once
+        const int e = min(lane + kWave * i, E - 1), g = min(e / size, G - 1);
+        const float fine = a.router[G + e] + (a.fine_bias[e] + a.expert_bias[e]);
+        const float coarse = a.router[g] + (a.coarse_bias[g] + a.group_bias[g]);
+        logit[i] = (fine + coarse) / a.inv_temperature_div;
     }
-    *a.active = active;
-    if (a.choice) {
-        int *rec = a.choice + (int64_t)(*a.pos) * a.choice_stride;
-        rec[0] = active;
-        for (int r = 0; r < kmax; ++r) rec[1 + r] = r < active ? chosen[r] : -1;
+    // kernels.cl:75-84 softmax: the maximum (order-free), each exponent by its
+    // own lane, the denominator summed in expert order by every lane
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+        if (lane + kWave * i < E) m = fmaxf(m, logit[i]);
+    m = wave_max(m);
+    float ex[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        ex[i] = expf(logit[i] - m);
+        if (lane + kWave * i < E) r.terms[lane + kWave * i] = ex[i];
     }
+    __builtin_amdgcn_wave_barrier();
+    float den = 0.0f;
+    for (int e = 0; e < E; ++e) den += r.terms[e];
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+        if (lane + kWave * i < E) r.probs[lane + kWave * i] = ex[i] / den;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {   // stable argsort of -probs (model.py:241)
+        const int e = lane + kWave * i;
+        if (e < E) {
+            const float p = r.probs[e];
+            int rank = 0;
+            for (int f = 0; f < E; ++f) rank += r.probs[f] > p || (r.probs[f] == p && f < e);
+            if (rank < a.kmax) r.chosen[rank] = e;
+            r.terms[e] = p * logf(fmaxf(p, 1e-9f));
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {   // model.py:242-250; the weights stay in LDS (a private array would live in scratch memory)
+        const int kmax = a.kmax;
+        float *w = r.w;
+        for (int k = 0; k < kmax; ++k) w[k] = r.probs[r.chosen[k]];
+        const float confidence = w[0] - w[min(kmax - 1, 1)];
+        const float entropy = -np_pairwise_sum(r.terms, E);
+        const float spread = rintf((1.0f - confidence) * 2.0f + entropy / a.log_experts);
+        const float width = fminf(fmaxf((float)a.kmin + spread, (float)a.kmin), (float)kmax);
+        const int active = (int)width;
+        for (int k = active; k < kmax; ++k) w[k] = 0.0f;
+        const float wden = fmaxf(np_pairwise_sum(w, kmax), 1e-9f);
+        for (int k = 0; k < kmax; ++k) w[k] = w[k] / wden;
+        r.active = active;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (publish) {
+        const int active = r.active;
+        if (lane < a.kmax) {
+            a.ids[lane] = r.chosen[lane];
+            a.weights[lane] = r.w[lane];
+        }
+        if (lane == 0) *a.active = active;
+        if (a.choice) {
+            int *rec = a.choice + (int64_t)(*a.pos) * a.choice_stride;
+            if (lane == 0) rec[0] = active;
+            if (lane < a.kmax) rec[1 + lane] = lane < active ? r.chosen[lane] : -1;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_moe_route(MoeArgs a) {
+    __shared__ RouteLds r;
+    if (a.done && *a.done) return;
+    route_wave(a, r, true);
 }
 
 constexpr int kMoeThreads = 512;
@@ -478,6 +650,7 @@ constexpr int kMoeGuRows = 2;        // rows per wave in the gate/up kernel
 constexpr int kMoeGuVec = 4;         // 16-byte vectors per lane and matrix row in one round
 constexpr int kMoeDnVec = 2;         // 16-byte vectors per lane and slot row in one round
 constexpr int kMoeMaxSlots = 16;     // routed top-k + shared experts in the down kernel's slot chunk
+constexpr int kMoeStage = 4;         // activation float4 loads per thread in flight while staging
 
 __device__ __forceinline__ float dot8_bf16(moe_u32x4 q, const float *x, float acc) {
     const float4 x0 = *(const float4 *)x, x1 = *(const float4 *)(x + 4);
@@ -493,14 +666,23 @@ __device__ __forceinline__ float dot8_bf16(moe_u32x4 q, const float *x, float ac
 }
 
 // grid (ceil(ffn / (kMoeRows * kMoeGuRows)), kmax + shared)
+//
+// The routed-slot workgroups route the token themselves (route_wave in wave
+// 0: the same arithmetic in every workgroup, so the same experts) while the
+// other waves stage the input; workgroup (0, 0) publishes the routing for
+// k_moe_down and the choice log.
 __global__ void __launch_bounds__(kMoeThreads) k_moe_gate_up_bf16(MoeArgs a) {
     extern __shared__ __align__(16) float xs[];
+    __shared__ RouteLds route;
     if (a.done && *a.done) return;
     const int slot = blockIdx.y;
     int e;
     if (slot < a.kmax) {
-        if (slot >= *a.active) return;
-        e = a.ids[slot];
+        if (threadIdx.x < kWave) route_wave(a, route, blockIdx.x == 0 && slot == 0);
+        for (int j = threadIdx.x * 4; j < a.h; j += kMoeThreads * 4) *(float4 *)&xs[j] = load_f4(a.x + j);
+        __syncthreads();
+        if (slot >= route.active) return;
+        e = route.chosen[slot];
     } else {
         e = a.experts + (slot - a.kmax);
     }
@@ -520,7 +702,8 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_gate_up_bf16(MoeArgs a) {
             qu[r][i] = __builtin_nontemporal_load(gmem(uw + rb[r] + v));
         }
     }
-    for (int j = threadIdx.x * 4; j < a.h; j += kMoeThreads * 4) *(float4 *)&xs[j] = load_f4(a.x + j);
+    if (slot >= a.kmax)
+        for (int j = threadIdx.x * 4; j < a.h; j += kMoeThreads * 4) *(float4 *)&xs[j] = load_f4(a.x + j);
     __syncthreads();
     if (r0 >= a.ffn) return;
     float g[kMoeGuRows] = {}, u[kMoeGuRows] = {};
@@ -569,8 +752,10 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
     if (tid < n) {   // slot table: routed slots 0..active-1, then the shared experts
         const bool routed = tid < active;
         const int s = routed ? tid : a.kmax + (tid - active);
-        wp[tid] = (const moe_u32x4 *)a.down[routed ? a.ids[tid] : a.experts + (tid - active)];
-        wsc[tid] = routed ? a.weights[tid] : a.shared_scale;
+        const int id = a.ids[min(tid, a.kmax - 1)];   // loaded with the width, not after it
+        const float w = a.weights[min(tid, a.kmax - 1)];
+        wp[tid] = (const moe_u32x4 *)a.down[routed ? id : a.experts + (tid - active)];
+        wsc[tid] = routed ? w : a.shared_scale;
         aoff[tid] = s * a.ffn;
     }
     __syncthreads();
@@ -584,7 +769,16 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
             if (k < n) q[k][i] = __builtin_nontemporal_load(gmem(w + min(lane + kWave * i, nv - 1)));
     }
     const int total4 = (a.kmax + a.shared) * a.ffn;
-    for (int j = tid * 4; j < total4; j += kMoeThreads * 4) *(float4 *)&acts[j] = load_f4(a.act + j);
+    for (int j0 = 0; j0 < total4; j0 += kMoeThreads * 4 * kMoeStage) {   // kMoeStage loads in flight
+        float4 t[kMoeStage];
+#pragma unroll
+        for (int k = 0; k < kMoeStage; ++k) t[k] = load_f4(a.act + min(j0 + (tid + k * kMoeThreads) * 4, total4 - 4));
+#pragma unroll
+        for (int k = 0; k < kMoeStage; ++k) {
+            const int j = j0 + (tid + k * kMoeThreads) * 4;
+            if (j < total4) *(float4 *)&acts[j] = t[k];
+        }
+    }
     __syncthreads();
     if ((int)(blockIdx.x * kMoeRows + (tid >> 6)) >= a.h) return;
     float acc[kMoeMaxSlots] = {};
@@ -622,11 +816,41 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
 
 }  // namespace
 
+bool heavy_split_path(int d, int window, int context, int block, int slots) {
+    const int blocks = (context + block - 1) / block;
+    return split::head_dim_ok(d) && heavy_parts(window, context) <= split::kMaxParts && slots <= kHeavyMaxChosen &&
+           heavy_split_lds(d, blocks) <= 64 * 1024;
+}
+
 int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context) {
     MR_REQUIRE(a.heads % a.kv_heads == 0 && a.d % 2 == 0 && a.block > 0 && a.slots > 0, "heavy attention: bad geometry");
-    k_heavy_prep<<<a.heads + a.kv_heads, 64, (size_t)a.d * sizeof(float), s>>>(a);
+    k_heavy_prep<<<a.heads + a.kv_heads, 64, (size_t)5 * a.d * sizeof(float), s>>>(a);
     MR_LAUNCHED("enqueue heavy attention prologue");
     const int blocks = (context + a.block - 1) / a.block;
+    if (a.part && heavy_split_path(a.d, a.window, context, a.block, a.slots)) {
+        const int parts = heavy_parts(a.window, context);
+        const dim3 grid(parts, a.heads);
+        const size_t lds = heavy_split_lds(a.d, blocks);
+        switch (a.d) {
+            case 128:
+                k_heavy_attn_split<128><<<grid, split::kThreads, lds, s>>>(a);
+                MR_LAUNCHED("enqueue heavy attention splits");
+                k_heavy_attn_merge<128><<<a.heads, split::kThreads, 0, s>>>(a, parts);
+                break;
+            case 64:
+                k_heavy_attn_split<64><<<grid, split::kThreads, lds, s>>>(a);
+                MR_LAUNCHED("enqueue heavy attention splits");
+                k_heavy_attn_merge<64><<<a.heads, split::kThreads, 0, s>>>(a, parts);
+                break;
+            default:
+                k_heavy_attn_split<32><<<grid, split::kThreads, lds, s>>>(a);
+                MR_LAUNCHED("enqueue heavy attention splits");
+                k_heavy_attn_merge<32><<<a.heads, split::kThreads, 0, s>>>(a, parts);
+                break;
+        }
+        MR_LAUNCHED("enqueue heavy attention merge");
+        return MR_OK;
+    }
     const size_t lds = (size_t)(a.d + std::min(a.window, context) + blocks) * sizeof(float) + (size_t)blocks * sizeof(int);
     MR_REQUIRE(lds <= 64 * 1024, "heavy attention: window and block count exceed shared memory");
     switch (a.d) {
@@ -643,12 +867,14 @@ int launch_moe(hipStream_t s, const MoeArgs &a) {
     MR_REQUIRE(a.experts >= 1 && a.experts <= kMaxExperts && a.groups >= 1 && a.groups <= a.experts &&
                    a.kmin >= 1 && a.kmin <= a.kmax && a.kmax <= std::min(a.experts, kMaxTopK),
                "moe: routing geometry out of range");
-    k_moe_route<<<1, kMaxExperts, 0, s>>>(a);
-    MR_LAUNCHED("enqueue moe routing");
     const int slots = a.kmax + a.shared;
     const size_t lds = (size_t)slots * a.ffn * sizeof(float);
     MR_REQUIRE(lds <= 64 * 1024, "moe: expert activations exceed shared memory");
     const bool fast = a.dtype == MR_BF16 && a.h % 8 == 0 && a.ffn % 8 == 0 && a.kmax + a.shared <= kMoeMaxSlots;
+    if (!fast) {
+        k_moe_route<<<1, kWave, 0, s>>>(a);
+        MR_LAUNCHED("enqueue moe routing");
+    }
     if (fast) {
         k_moe_gate_up_bf16<<<dim3(ceil_div(a.ffn, kMoeRows * kMoeGuRows), slots), kMoeThreads,
                              (size_t)a.h * sizeof(float), s>>>(a);

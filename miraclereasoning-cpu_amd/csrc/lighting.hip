@@ -17,9 +17,10 @@
 // projection of the merged row and its cache row at its new position.
 #include "lighting.h"
 
-#include "attention_tile.h"
+#include "split_attention.h"
 
 namespace mr {
+static_assert(kLightRows == split::kRows && kLightMaxSplits == split::kMaxParts, "latent split geometry");
 namespace {
 
 // RMSNorm of one row (kernels.cl:19-28) by one 64-lane workgroup: the row is
@@ -147,173 +148,34 @@ __global__ void __launch_bounds__(kThreads) k_light_attend(LightArgs a) {
 
 // Split-key form of the same attention for head dims 32/64/128: workgroup
 // (split s, head h) scores rows [64 s, 64 s + 64) of the memory with the
-// latent mask and writes its partial (m, l, o); a second kernel merges the
-// splits of each head.  A lane holds 16 dims of a row (D/16 lanes per row),
-// each lane group keeps its own running max, sum and weighted values.
-constexpr int kPartThreads = 256;
-
+// latent mask (kernels.cl:86-91: non-memory rows older than the window) and
+// writes its partial; a second kernel merges the splits of each head.
 template <int D>
-__global__ void __launch_bounds__(kPartThreads) k_light_attend_part(LightArgs a) {
-    constexpr int LPK = D / 16;                 // lanes per row
-    constexpr int KPW = kWave / LPK;            // rows side by side in a wave
-    constexpr int NWV = kPartThreads / kWave;
-    __shared__ float wm[NWV], wl[NWV], wo[NWV][D];
+__global__ void __launch_bounds__(split::kThreads) k_light_attend_part(LightArgs a) {
     if (a.done && *a.done) return;
     const LightState st = *a.st;
     const int n = st.rows + 1;                  // with this step's row
     const int t0 = blockIdx.x * kLightRows;
     if (t0 >= n) return;
-    const int t1 = min(n, t0 + kLightRows);
     const int h = blockIdx.y, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane % LPK, kg = lane / LPK;
     const float earliest = (float)(*a.pos - a.window + 1);
-    const float inv_root = 1.0f / sqrtf((float)D);
-    float4 q[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float4 t = load_f4(a.q_rot + (int64_t)h * D + 16 * sub + 4 * c);
-        q[c] = make_float4(t.x * inv_root, t.y * inv_root, t.z * inv_root, t.w * inv_root);
-    }
-    float m = -INFINITY, l = 0.0f;
-    float4 acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int r0 = t0 + wave * KPW; r0 < t1; r0 += NWV * KPW) {
-        const int t = r0 + kg;
-        float s = -INFINITY;
-        float4 v[4];
-        if (t < t1) {
-            const int slot = (st.start + t) % a.cap;
-            // latent_mask (kernels.cl:86-91): non-memory rows older than the window
-            if (!(t >= st.memory && a.positions[slot] < earliest)) {
-                const float *kr = a.kcache + (int64_t)slot * kvw + (int64_t)kh * D + 16 * sub;
-                const float *vr = a.vcache + (int64_t)slot * kvw + (int64_t)kh * D + 16 * sub;
-                float dot = 0.0f;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float4 k4 = load_f4(kr + 4 * c);
-                    v[c] = load_f4(vr + 4 * c);
-                    dot = fmaf(q[c].x, k4.x, dot);
-                    dot = fmaf(q[c].y, k4.y, dot);
-                    dot = fmaf(q[c].z, k4.z, dot);
-                    dot = fmaf(q[c].w, k4.w, dot);
-                }
-                s = dot;
-            }
-        }
-        s = att::lanes_sum<LPK>(s == -INFINITY ? 0.0f : s) + (s == -INFINITY ? -INFINITY : 0.0f);
-        const float m_new = fmaxf(m, s);
-        if (m_new != -INFINITY) {
-            const float alpha = m == -INFINITY ? 0.0f : __expf(m - m_new);
-            const float p = s == -INFINITY ? 0.0f : __expf(s - m_new);
-            l = l * alpha + p;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                acc[c].x = acc[c].x * alpha + (p != 0.0f ? p * v[c].x : 0.0f);
-                acc[c].y = acc[c].y * alpha + (p != 0.0f ? p * v[c].y : 0.0f);
-                acc[c].z = acc[c].z * alpha + (p != 0.0f ? p * v[c].z : 0.0f);
-                acc[c].w = acc[c].w * alpha + (p != 0.0f ? p * v[c].w : 0.0f);
-            }
-            m = m_new;
-        }
-    }
-    // fold the wave's row groups: common max, rescale, sum
-    const float M = att::keygroups_max<LPK>(m);
-    const float f = m == -INFINITY ? 0.0f : __expf(m - M);
-    const float L = att::keygroups_sum<LPK>(l * f);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float ox = att::keygroups_sum_lanes<LPK>(acc[c].x * f);
-        const float oy = att::keygroups_sum_lanes<LPK>(acc[c].y * f);
-        const float oz = att::keygroups_sum_lanes<LPK>(acc[c].z * f);
-        const float ow = att::keygroups_sum_lanes<LPK>(acc[c].w * f);
-        if (kg == 0) *(float4 *)&wo[wave][16 * sub + 4 * c] = make_float4(ox, oy, oz, ow);
-    }
-    if (lane == 0) {
-        wm[wave] = M;
-        wl[wave] = L;
-    }
-    __syncthreads();
-    float *part = a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2);
-    float Mb = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NWV; ++w) Mb = fmaxf(Mb, wm[w]);
-    for (int j = threadIdx.x; j < D; j += kPartThreads) {
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NWV; ++w)
-            if (wm[w] != -INFINITY) o = fmaf(wo[w][j], __expf(wm[w] - Mb), o);
-        part[2 + j] = o;
-    }
-    if (threadIdx.x == 0) {
-        float Lb = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NWV; ++w)
-            if (wm[w] != -INFINITY) Lb = fmaf(wl[w], __expf(wm[w] - Mb), Lb);
-        part[0] = Mb;
-        part[1] = Lb;
-    }
+    const auto rows = [&](int t, const float **k, const float **v) {
+        const int slot = (st.start + t) % a.cap;
+        if (t >= st.memory && a.positions[slot] < earliest) return false;
+        *k = a.kcache + (int64_t)slot * kvw + (int64_t)kh * D;
+        *v = a.vcache + (int64_t)slot * kvw + (int64_t)kh * D;
+        return true;
+    };
+    split::partial<D>(a.q_rot + (int64_t)h * D, t0, min(n, t0 + kLightRows), rows,
+                      a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2));
 }
 
-// grid heads, kMergeThreads: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
-// The split weights e^(m_s - M) go to LDS; lane quads cover D/4 float4
-// columns and kMergeThreads / (D/4) split groups stride the splits, folded
-// through LDS at the end.
-constexpr int kMergeThreads = 256;
-
+// grid heads, split::kThreads
 template <int D>
-__global__ void __launch_bounds__(kMergeThreads) k_light_attend_merge(LightArgs a, int splits) {
-    constexpr int Q = D / 4, G = kMergeThreads / Q;
-    __shared__ float e[kLightMaxSplits], red[kMergeThreads / kWave];
-    __shared__ float4 fold[G][Q];
-    __shared__ float lsum[G];
+__global__ void __launch_bounds__(split::kThreads) k_light_attend_merge(LightArgs a, int splits) {
     if (a.done && *a.done) return;
     const int n = a.st->rows + 1, active = min(splits, (n + kLightRows - 1) / kLightRows);
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const float *part = a.part + (int64_t)h * splits * (D + 2);
-    float mx = -INFINITY;
-    for (int s = tid; s < active; s += kMergeThreads) {
-        const float ms = part[(int64_t)s * (D + 2)];
-        e[s] = ms;
-        mx = fmaxf(mx, ms);
-    }
-    const float M = block_max(mx, red);
-    for (int s = tid; s < active; s += kMergeThreads) e[s] = e[s] == -INFINITY ? 0.0f : __expf(e[s] - M);
-    __syncthreads();
-    const int g = tid / Q, c = tid % Q;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    float l = 0.0f;
-#pragma unroll 4
-    for (int s = g; s < active; s += G) {
-        const float w = e[s];
-        const float *ps = part + (int64_t)s * (D + 2);
-        const float4 v = make_float4(ps[2 + 4 * c], ps[3 + 4 * c], ps[4 + 4 * c], ps[5 + 4 * c]);
-        if (c == 0) l = fmaf(ps[1], w, l);
-        o.x = fmaf(v.x, w, o.x);
-        o.y = fmaf(v.y, w, o.y);
-        o.z = fmaf(v.z, w, o.z);
-        o.w = fmaf(v.w, w, o.w);
-    }
-    fold[g][c] = o;
-    if (c == 0) lsum[g] = l;
-    __syncthreads();
-    if (tid < Q) {
-        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-        float L = 0.0f;
-#pragma unroll
-        for (int k = 0; k < G; ++k) {
-            t.x += fold[k][tid].x;
-            t.y += fold[k][tid].y;
-            t.z += fold[k][tid].z;
-            t.w += fold[k][tid].w;
-            L += lsum[k];
-        }
-        float *out = a.out + (int64_t)h * D + 4 * tid;
-        out[0] = t.x / L;
-        out[1] = t.y / L;
-        out[2] = t.z / L;
-        out[3] = t.w / L;
-    }
+    split::merge<D>(a.part + (int64_t)blockIdx.x * splits * (D + 2), active, -1, a.out + (int64_t)blockIdx.x * D);
 }
 
 // One workgroup: compaction after this step's attention (model.py:168-188).
@@ -393,19 +255,19 @@ int launch_light_attend(hipStream_t s, const LightArgs &a) {
         const dim3 grid(splits, a.heads);
         switch (a.d) {
             case 128:
-                k_light_attend_part<128><<<grid, kPartThreads, 0, s>>>(a);
+                k_light_attend_part<128><<<grid, split::kThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<128><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<128><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
             case 64:
-                k_light_attend_part<64><<<grid, kPartThreads, 0, s>>>(a);
+                k_light_attend_part<64><<<grid, split::kThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<64><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<64><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
             default:
-                k_light_attend_part<32><<<grid, kPartThreads, 0, s>>>(a);
+                k_light_attend_part<32><<<grid, split::kThreads, 0, s>>>(a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<32><<<a.heads, kMergeThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<32><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
         }
         MR_LAUNCHED("enqueue latent attention merge");
