@@ -423,10 +423,17 @@ int record_heavy_layer(mr_model *m, Layer &L, int li) {
         g.w = L.qkv.ptr; g.x = m->hidden; g.gain = L.a_norm.f(); g.eps = d.norm_eps;
         g.n = qd + d.latent_dim; g.k = h; g.y = m->qkv; g.done = m->done_dev;
         MR_TRY(launch_gemv(s, L.qkv.dtype, PRO_RMS, EPI_STORE, g));
-        GemvArgs u;   // latent -> [K; V]
-        u.w = L.kv_up.ptr; u.x = m->qkv + qd; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
-        MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
+        const bool fused = heavy_kv_fused(L.kv_up.dtype, d.latent_dim);
+        if (!fused) {
+            GemvArgs u;   // latent -> [K; V]
+            u.w = L.kv_up.ptr; u.x = m->qkv + qd; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf;
+            u.done = m->done_dev;
+            MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
+        }
         HeavyAttnArgs a;
+        if (fused) {   // the projection runs in the attention prologue
+            a.kv_w = L.kv_up.ptr; a.kv_dtype = L.kv_up.dtype; a.latent_x = m->qkv + qd; a.latent = d.latent_dim;
+        }
         a.q = m->qkv; a.kv = m->kvbuf; a.rope = m->rope; a.pos = m->pos_dev; a.done = m->done_dev;
         a.q_rot = m->q_rot;
         a.ring_k = L.ring_k + (size_t)loop * d.context_length * kvw;
@@ -485,16 +492,28 @@ int record_light_layer(mr_model *m, Layer &L) {
     a.kcache = L.kcache; a.vcache = L.vcache; a.lat_new = m->lat_new; a.kv = m->kvbuf; a.st = L.light;
     a.out = m->attn; a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.latent = d.latent_dim;
     a.window = d.window; a.memory_slots = d.memory_slots; a.cap = L.light_cap; a.part = m->split_part;
-    MR_TRY(launch_light_prep(s, a));
+    a.kv_w = L.kv_up.ptr; a.kv_dtype = L.kv_up.dtype;
+    // queries, the appended row and its cache row: one launch where the
+    // geometry allows, else prologue, projection and cache row apart
+    const bool fused = light_kv_fused(L.kv_up.dtype, d.latent_dim, hd);
     GemvArgs u;   // [Wk; Wv] . new latent row
     u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
-    MR_TRY(launch_light_store_kv(s, a, false));
+    if (fused) {
+        MR_TRY(launch_light_kv(s, a, false));
+    } else {
+        MR_TRY(launch_light_prep(s, a));
+        MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
+        MR_TRY(launch_light_store_kv(s, a, false));
+    }
     MR_TRY(launch_light_attend(s, a));
-    GemvArgs um = u;   // [Wk; Wv] . merged row, skipped unless compaction merged
-    um.done = &L.light->skip_merged;
-    MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, um));
-    MR_TRY(launch_light_store_kv(s, a, true));
+    if (fused) {   // the merged row's cache row (skipped unless compaction merged)
+        MR_TRY(launch_light_kv(s, a, true));
+    } else {
+        GemvArgs um = u;   // [Wk; Wv] . merged row, skipped unless compaction merged
+        um.done = &L.light->skip_merged;
+        MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, um));
+        MR_TRY(launch_light_store_kv(s, a, true));
+    }
     GemvArgs o;
     o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->branch_o; o.done = m->done_dev;
     MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_STORE, o));
@@ -502,11 +521,11 @@ int record_light_layer(mr_model *m, Layer &L) {
     gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->xnorm; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act;
     gu.done = m->done_dev;
     MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_COPY, EPI_SWIGLU, gu));
-    GemvArgs dn;
-    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->branch_f; dn.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_STORE, dn));
-    return launch_light_residual(s, m->hidden, m->branch_o, m->branch_f, L.attention_gate.f(), L.ffn_gate.f(),
-                                 d.residual_scale, h, m->done_dev);
+    GemvArgs dn;   // hidden += rs * ((0 + ag * o) + fg * down(act)) in the down projection's epilogue
+    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden; dn.done = m->done_dev;
+    dn.scale = d.residual_scale; dn.aux = m->branch_o; dn.scale_ptr = L.attention_gate.f();
+    dn.scale_ptr2 = L.ffn_gate.f();
+    return launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_GATED, dn);
 }
 
 int launch_lm_head(mr_model *m) {

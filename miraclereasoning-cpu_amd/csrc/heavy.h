@@ -18,6 +18,11 @@ struct HeavyAttnArgs {
     float *bsum_k = nullptr, *bsum_v = nullptr;   // [blocks, kv_heads*d] running block sums
     float *out = nullptr;            // [heads*d] attended values
     float *part = nullptr;           // [heads][heavy_parts(window, context)][d + 2] split partials (or null)
+    // With kv_w set, the K/V projection of the latent runs inside the
+    // attention prologue (heavy_kv_fused geometries) and kv is not read.
+    const void *kv_w = nullptr;      // [2*kv_heads*d, latent] kv_up weight
+    const float *latent_x = nullptr; // [latent] the latent projection
+    int kv_dtype = MR_BF16, latent = 0;
     int *choice = nullptr;           // choice record of this layer/loop at position 0 (or null)
     int choice_stride = 0;           // ints between the records of consecutive positions
     int choice_blocks = 0;           // offset of the block lists inside a record
@@ -33,6 +38,7 @@ inline int heavy_window_splits(int window, int context) {
 }
 inline int heavy_parts(int window, int context) { return heavy_window_splits(window, context) + 1; }
 bool heavy_split_path(int d, int window, int context, int block, int slots);
+bool heavy_kv_fused(int dtype, int latent);
 
 int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context);
 

@@ -28,6 +28,7 @@
 //                  the residual add.
 #include "heavy.h"
 
+#include "block_gemv.h"
 #include "split_attention.h"
 
 namespace mr {
@@ -88,6 +89,75 @@ __global__ void __launch_bounds__(64) k_heavy_prep(HeavyAttnArgs a) {
         a.ring_v[slot + j] = v;
         a.bsum_k[bslot + j] = bk[j] + k;
         a.bsum_v[bslot + j] = bv[j] + v;
+    }
+}
+
+// The K/V projection and the prologue in one launch: grid heads + 2 kv_heads,
+// 256 threads.  Blocks < heads: query h as in k_heavy_prep.  The others: the
+// K rows (first kv_heads blocks) or V rows of KV head kh, kv_up . latent
+// (block_gemv), then k_heavy_prep's key and value work on them: the key's
+// sequential sum of squares and interleaved rotation, the ring append and the
+// block sums.
+constexpr int kKvThreads = 256;
+
+template <int DT>
+__global__ void __launch_bounds__(kKvThreads) k_heavy_kv(HeavyAttnArgs a) {
+    constexpr int EB = DT == MR_F32 ? 4 : 2;   // bytes per weight element
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float scale;
+    const int d = a.d, half = d / 2, tid = threadIdx.x;
+    const int kvw = a.kv_heads * d;
+    float *xs = sm, *row = sm + ((a.latent + 3) & ~3);
+    const bool isq = (int)blockIdx.x < a.heads;
+    const int b = isq ? blockIdx.x : blockIdx.x - a.heads;
+    const bool isk = !isq && b < a.kv_heads;
+    const int hh = isq ? b : (isk ? b : b - a.kv_heads);
+    // The weight loads depend on nothing this step computes: they go out
+    // before the flag and position loads.
+    BlockGemv<DT> gemv;
+    if (!isq)
+        gemv.issue((const char *)a.kv_w + ((int64_t)(isk ? 0 : kvw) + (int64_t)hh * d) * a.latent * EB, d, a.latent);
+    if (a.done && *a.done) return;
+    const int pos = *a.pos;
+    if (isq) {
+        for (int j = tid; j < d; j += kKvThreads) row[j] = a.q[(int64_t)hh * d + j];
+    } else {
+        for (int j = tid; j < a.latent; j += kKvThreads) xs[j] = a.latent_x[j];
+        __syncthreads();
+        gemv.finish(xs, row);
+    }
+    __syncthreads();
+    if (isq || isk) {
+        if (tid == 0) {   // kernels.cl:19-28: one sequential sum of squares
+            float v = 0.0f;
+            for (int j = 0; j < d; ++j) {
+                const float x = row[j];
+                v += x * x;
+            }
+            scale = 1.0f / sqrtf(v / (float)d + 1e-6f);
+        }
+        __syncthreads();
+        const float *cs = a.rope + (int64_t)pos * half * 2;
+        for (int p = tid; p < half; p += kKvThreads) {   // interleaved pairs (kernels.cl:30-44)
+            float u = row[2 * p] * scale * 1.0f, v = row[2 * p + 1] * scale * 1.0f;
+            rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
+            row[2 * p] = u;
+            row[2 * p + 1] = v;
+        }
+        __syncthreads();
+    }
+    if (isq) {
+        for (int j = tid; j < d; j += kKvThreads) a.q_rot[(int64_t)hh * d + j] = row[j];
+        return;
+    }
+    const int64_t slot = (int64_t)pos * kvw + (int64_t)hh * d;
+    const int64_t bslot = (int64_t)(pos / a.block) * kvw + (int64_t)hh * d;
+    const bool first = pos % a.block == 0;
+    float *ring = isk ? a.ring_k : a.ring_v, *bsum = isk ? a.bsum_k : a.bsum_v;
+    for (int j = tid; j < d; j += kKvThreads) {
+        const float v = row[j];
+        ring[slot + j] = v;
+        bsum[bslot + j] = (first ? 0.0f : bsum[bslot + j]) + v;
     }
 }
 
@@ -816,6 +886,13 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
 
 }  // namespace
 
+bool heavy_kv_fused(int dtype, int latent) {
+    return dtype == MR_F32    ? block_gemv_fits<MR_F32>(latent)
+           : dtype == MR_BF16 ? block_gemv_fits<MR_BF16>(latent)
+           : dtype == MR_F16  ? block_gemv_fits<MR_F16>(latent)
+                              : false;
+}
+
 bool heavy_split_path(int d, int window, int context, int block, int slots) {
     const int blocks = (context + block - 1) / block;
     return split::head_dim_ok(d) && heavy_parts(window, context) <= split::kMaxParts && slots <= kHeavyMaxChosen &&
@@ -824,7 +901,16 @@ bool heavy_split_path(int d, int window, int context, int block, int slots) {
 
 int launch_heavy_attention(hipStream_t s, const HeavyAttnArgs &a, int context) {
     MR_REQUIRE(a.heads % a.kv_heads == 0 && a.d % 2 == 0 && a.block > 0 && a.slots > 0, "heavy attention: bad geometry");
-    k_heavy_prep<<<a.heads + a.kv_heads, 64, (size_t)5 * a.d * sizeof(float), s>>>(a);
+    if (a.kv_w) {
+        MR_REQUIRE(heavy_kv_fused(a.kv_dtype, a.latent), "heavy attention: unsupported latent projection");
+        const size_t lds = (size_t)(((a.latent + 3) & ~3) + a.d) * sizeof(float);
+        const int grid = a.heads + 2 * a.kv_heads;
+        if (a.kv_dtype == MR_BF16) k_heavy_kv<MR_BF16><<<grid, kKvThreads, lds, s>>>(a);
+        else if (a.kv_dtype == MR_F16) k_heavy_kv<MR_F16><<<grid, kKvThreads, lds, s>>>(a);
+        else k_heavy_kv<MR_F32><<<grid, kKvThreads, lds, s>>>(a);
+    } else {
+        k_heavy_prep<<<a.heads + a.kv_heads, 64, (size_t)5 * a.d * sizeof(float), s>>>(a);
+    }
     MR_LAUNCHED("enqueue heavy attention prologue");
     const int blocks = (context + a.block - 1) / a.block;
     if (a.part && heavy_split_path(a.d, a.window, context, a.block, a.slots)) {

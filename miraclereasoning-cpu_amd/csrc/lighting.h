@@ -30,6 +30,8 @@ struct LightArgs {
     LightState *st = nullptr;
     float *out = nullptr;            // [heads*d] attended values
     float *part = nullptr;           // [heads][splits][d + 2] split partials (m, l, o)
+    const void *kv_w = nullptr;      // [2*kv_heads*d, latent] packed [Wk; Wv] (fused row kernel)
+    int kv_dtype = MR_BF16;
     int heads = 0, kv_heads = 0, d = 0, latent = 0, window = 0, memory_slots = 0, cap = 0;
 };
 
@@ -47,6 +49,12 @@ inline bool light_split_path(int d, int cap) {
 // lat_new - its key/value cache row.
 int launch_light_prep(hipStream_t s, const LightArgs &a);
 int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged);
+// The same three steps in one launch (queries, the appended row, and the K/V
+// projection with the cache row computed per KV head from the normalized
+// latent), or for the merged row the projection and its cache row; for the
+// dtypes and latent widths light_kv_fused accepts.
+bool light_kv_fused(int dtype, int latent, int d);
+int launch_light_kv(hipStream_t s, const LightArgs &a, bool merged);
 // Attention over every row, then compaction (which leaves the merged row in
 // lat_new and clears skip_merged when a merge happened).
 int launch_light_attend(hipStream_t s, const LightArgs &a);

@@ -17,6 +17,7 @@
 // projection of the merged row and its cache row at its new position.
 #include "lighting.h"
 
+#include "block_gemv.h"
 #include "split_attention.h"
 
 namespace mr {
@@ -98,6 +99,92 @@ __global__ void __launch_bounds__(64) k_light_store(LightArgs a, int merged) {
         a.kcache[(int64_t)slot * kvw + (int64_t)kh * a.d + j] = row[j];
         a.vcache[(int64_t)slot * kvw + (int64_t)kh * a.d + j] = a.kv[kvw + (int64_t)kh * a.d + j];
     }
+}
+
+// ------------------------------------------------------------------ fused row kernel
+// grid heads + 1 + 2 kv_heads (new row) or 2 kv_heads (merged row), 256
+// threads.  Blocks < heads: query h, RMSNorm with q_norm, RoPE at pos ->
+// q_rot.  Block heads: the new latent row (RMSNorm with latent_norm) appended
+// with its position and count 1.  The last 2 kv_heads blocks: the K rows of KV
+// head kh (blocks < kv_heads) or its V rows, [Wk; Wv] . latent with the latent
+// normalized by the block itself (the same arithmetic as the appending block,
+// so the same bits) or, for the merged row, lat_new; a K row then takes
+// RMSNorm with k_norm and RoPE at the row's position; the rows go to the
+// caches.
+constexpr int kKvThreads = 256;
+
+// RMSNorm of x[0, width) (kernels.cl:19-28, the sum of squares reduced over
+// the block) times gain into y (LDS); all threads return after y is written.
+__device__ __forceinline__ void block_rms_row(const float *x, const float *gain, float eps, int width, float *y,
+                                              float *red) {
+    float v = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) {
+        const float t = x[j];
+        y[j] = t;
+        v = fmaf(t, t, v);
+    }
+    const float sc = 1.0f / sqrtf(block_sum(v, red) / (float)width + eps);
+    for (int j = threadIdx.x; j < width; j += blockDim.x) y[j] = y[j] * sc * (gain ? gain[j] : 1.0f);
+    __syncthreads();
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged) {
+    constexpr int EB = DT == MR_F32 ? 4 : 2;   // bytes per weight element
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[kKvThreads / kWave];
+    const int tid = threadIdx.x, d = a.d, kvw = a.kv_heads * d;
+    const int nq = merged ? 0 : a.heads + 1;   // query and appending blocks
+    const int b = (int)blockIdx.x - nq;
+    const bool isk = b >= 0 && b < a.kv_heads;
+    const int kh = isk ? b : b - a.kv_heads;
+    // The weight loads depend on nothing this step computes: they go out
+    // before the flag, position and state loads.
+    BlockGemv<DT> gemv;
+    if (b >= 0) gemv.issue((const char *)a.kv_w + ((int64_t)(isk ? 0 : kvw) + (int64_t)kh * d) * a.latent * EB, d,
+                           a.latent);
+    if (a.done && *a.done) return;
+    const LightState st = *a.st;
+    if (merged && st.skip_merged) return;
+    const int pos = *a.pos;
+    const int slot = merged ? st.merged_slot : (st.start + st.rows) % a.cap;
+    const float *raw_latent = a.qlat + (int64_t)a.heads * d;
+    if (b < 0) {
+        if ((int)blockIdx.x < a.heads) {   // query blockIdx.x
+            const int h = blockIdx.x;
+            block_rms_row(a.qlat + (int64_t)h * d, a.q_gain, a.eps, d, sm, red);
+            rope_row(sm, a.rope, pos, d, a.split_half);
+            for (int j = tid; j < d; j += kKvThreads) a.q_rot[(int64_t)h * d + j] = sm[j];
+            return;
+        }
+        block_rms_row(raw_latent, a.latent_gain, a.eps, a.latent, sm, red);   // the new latent row
+        for (int j = tid; j < a.latent; j += kKvThreads) a.arena[(int64_t)slot * a.latent + j] = sm[j];
+        if (tid == 0) {
+            a.positions[slot] = (float)pos;
+            a.counts[slot] = 1.0f;
+        }
+        return;
+    }
+    float *xs = sm, *ys = sm + ((a.latent + 3) & ~3);
+    if (merged) {
+        for (int j = tid; j < a.latent; j += kKvThreads) xs[j] = a.lat_new[j];
+        __syncthreads();
+    } else {
+        block_rms_row(raw_latent, a.latent_gain, a.eps, a.latent, xs, red);
+    }
+    gemv.finish(xs, ys);
+    __syncthreads();
+    float *cache = (isk ? a.kcache : a.vcache) + (int64_t)slot * kvw + (int64_t)kh * d;
+    if (isk) {   // RMSNorm with k_norm, RoPE at the row's position
+        const int p = merged ? (int)a.positions[slot] : pos;
+        float v = 0.0f;
+        for (int j = tid; j < d; j += kKvThreads) v = fmaf(ys[j], ys[j], v);
+        const float sc = 1.0f / sqrtf(block_sum(v, red) / (float)d + a.eps);
+        for (int j = tid; j < d; j += kKvThreads) ys[j] = ys[j] * sc * (a.k_gain ? a.k_gain[j] : 1.0f);
+        __syncthreads();
+        rope_row(ys, a.rope, p, d, a.split_half);
+    }
+    for (int j = tid; j < d; j += kKvThreads) cache[j] = ys[j];
 }
 
 constexpr int kThreads = 256;
@@ -246,6 +333,25 @@ int launch_light_prep(hipStream_t s, const LightArgs &a) {
 int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged) {
     k_light_store<<<a.kv_heads, 64, (size_t)a.d * sizeof(float), s>>>(a, merged ? 1 : 0);
     MR_LAUNCHED("enqueue latent key/value row");
+    return MR_OK;
+}
+
+bool light_kv_fused(int dtype, int latent, int d) {
+    const bool fits = dtype == MR_F32    ? block_gemv_fits<MR_F32>(latent)
+                      : dtype == MR_BF16 ? block_gemv_fits<MR_BF16>(latent)
+                      : dtype == MR_F16  ? block_gemv_fits<MR_F16>(latent)
+                                         : false;
+    return fits && d % 2 == 0;
+}
+
+int launch_light_kv(hipStream_t s, const LightArgs &a, bool merged) {
+    MR_REQUIRE(light_kv_fused(a.kv_dtype, a.latent, a.d) && a.kv_w, "latent rows: unsupported projection geometry");
+    const int grid = merged ? 2 * a.kv_heads : a.heads + 1 + 2 * a.kv_heads;
+    const size_t lds = (size_t)(((a.latent + 3) & ~3) + std::max(a.d, a.latent)) * sizeof(float);
+    if (a.kv_dtype == MR_BF16) k_light_kv<MR_BF16><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
+    else if (a.kv_dtype == MR_F16) k_light_kv<MR_F16><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
+    else k_light_kv<MR_F32><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
+    MR_LAUNCHED(merged ? "enqueue merged latent row" : "enqueue latent rows");
     return MR_OK;
 }
 

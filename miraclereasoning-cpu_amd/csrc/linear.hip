@@ -88,6 +88,9 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int row, float acc
         a.y[row] = a.y[row] + a.scale * acc;
     } else if constexpr (EPI == EPI_SCALE_ADD) {
         a.y[row] = a.y[row] + (*a.scale_ptr) * acc;
+    } else if constexpr (EPI == EPI_GATED) {
+        const float branch = (0.0f + (*a.scale_ptr) * a.aux[row]) + (*a.scale_ptr2) * acc;
+        a.y[row] = a.y[row] + a.scale * branch;
     } else {
         // SwiGLU (kernels.cl:46-50): (g / (1 + exp(-g))) * u
         a.y[row] = (acc / (1.0f + expf(-acc))) * acc2;
@@ -97,7 +100,6 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int row, float acc
 template <int DT, int R, int U, int PRO, int EPI>
 __global__ void __launch_bounds__(kGemvThreads) k_gemv_vec(GemvArgs a, int lpr) {
     extern __shared__ float smem[];
-    if (a.done && *a.done) return;
     using V = Vec16<DT>;
     constexpr int E = V::E;
     constexpr int M = EPI == EPI_SWIGLU ? 2 : 1;   // matrices read per row
@@ -126,8 +128,10 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv_vec(GemvArgs a, int lpr) 
             }
         }
     };
-    // The first batch is in flight while the prologue stages x.
+    // The first batch is in flight while the flag is read and the prologue
+    // stages x.
     issue(0);
+    if (a.done && *a.done) return;
     float *xs = smem;
     float *red = smem + ((a.k + 3) & ~3);
     stage_x<PRO>(a, xs, red);
@@ -231,6 +235,7 @@ int launch_gemv_dt(hipStream_t s, int pro, int epi, const GemvArgs &a) {
             case EPI_RESIDUAL: return launch_gemv_t<DT, PRO_COPY, EPI_RESIDUAL>(s, a);
             case EPI_SWIGLU: return launch_gemv_t<DT, PRO_COPY, EPI_SWIGLU>(s, a);
             case EPI_SCALE_ADD: return launch_gemv_t<DT, PRO_COPY, EPI_SCALE_ADD>(s, a);
+            case EPI_GATED: return launch_gemv_t<DT, PRO_COPY, EPI_GATED>(s, a);
         }
     } else {
         switch (epi) {
