@@ -119,6 +119,12 @@ __global__ void __launch_bounds__(kKvThreads) k_heavy_kv(HeavyAttnArgs a) {
         gemv.issue((const char *)a.kv_w + ((int64_t)(isk ? 0 : kvw) + (int64_t)hh * d) * a.latent * EB, d, a.latent);
     if (a.done && *a.done) return;
     const int pos = *a.pos;
+    const float *cs = a.rope + (int64_t)pos * half * 2;
+    float rc = 1.0f, rsn = 0.0f;   // this thread's rotation pair, loaded ahead of the norm
+    if (tid < half) {
+        rc = cs[2 * tid];
+        rsn = cs[2 * tid + 1];
+    }
     if (isq) {
         for (int j = tid; j < d; j += kKvThreads) row[j] = a.q[(int64_t)hh * d + j];
     } else {
@@ -137,10 +143,9 @@ __global__ void __launch_bounds__(kKvThreads) k_heavy_kv(HeavyAttnArgs a) {
             scale = 1.0f / sqrtf(v / (float)d + 1e-6f);
         }
         __syncthreads();
-        const float *cs = a.rope + (int64_t)pos * half * 2;
         for (int p = tid; p < half; p += kKvThreads) {   // interleaved pairs (kernels.cl:30-44)
             float u = row[2 * p] * scale * 1.0f, v = row[2 * p + 1] * scale * 1.0f;
-            rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
+            rope_rotate(u, v, p == tid ? rc : cs[2 * p], p == tid ? rsn : cs[2 * p + 1]);
             row[2 * p] = u;
             row[2 * p + 1] = v;
         }

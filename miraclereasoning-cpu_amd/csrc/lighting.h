@@ -10,7 +10,7 @@ namespace mr {
 // Device state of one layer's latent memory: rows live in a ring of `cap`
 // slots; logical row t is slot (start + t) % cap.
 struct LightState {
-    int start, rows, memory, skip_merged, merged_slot, pad[3];
+    int start, rows, memory, skip_merged, merged_slot, merged_pos, pad[2];   // merged_pos: the merged row's position
 };
 
 struct LightArgs {

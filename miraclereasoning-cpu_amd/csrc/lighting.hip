@@ -113,6 +113,20 @@ __global__ void __launch_bounds__(64) k_light_store(LightArgs a, int merged) {
 // caches.
 constexpr int kKvThreads = 256;
 
+// RoPE of a row in LDS whose (cos, sin) for pair tid (tid < d/2 <= blockDim)
+// the thread loaded beforehand (kernels.cl:30-44).
+__device__ __forceinline__ void rope_row_pre(float *row, float c, float s, int d, int split_half) {
+    const int half = d / 2, i = threadIdx.x;
+    if (i < half) {
+        const int j = split_half ? i : 2 * i, k = split_half ? i + half : 2 * i + 1;
+        float u = row[j], v = row[k];
+        rope_rotate(u, v, c, s);
+        row[j] = u;
+        row[k] = v;
+    }
+    __syncthreads();
+}
+
 // RMSNorm of x[0, width) (kernels.cl:19-28, the sum of squares reduced over
 // the block) times gain into y (LDS); all threads return after y is written.
 __device__ __forceinline__ void block_rms_row(const float *x, const float *gain, float eps, int width, float *y,
@@ -149,11 +163,20 @@ __global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged
     const int pos = *a.pos;
     const int slot = merged ? st.merged_slot : (st.start + st.rows) % a.cap;
     const float *raw_latent = a.qlat + (int64_t)a.heads * d;
+    // the rotation angles of this thread's pair at the row's position
+    const bool pre = d / 2 <= kKvThreads;
+    float rc = 1.0f, rsn = 0.0f;
+    if (pre && tid < d / 2) {
+        const float *cs = a.rope + ((int64_t)(merged ? st.merged_pos : pos) * (d / 2) + tid) * 2;
+        rc = cs[0];
+        rsn = cs[1];
+    }
     if (b < 0) {
         if ((int)blockIdx.x < a.heads) {   // query blockIdx.x
             const int h = blockIdx.x;
             block_rms_row(a.qlat + (int64_t)h * d, a.q_gain, a.eps, d, sm, red);
-            rope_row(sm, a.rope, pos, d, a.split_half);
+            if (pre) rope_row_pre(sm, rc, rsn, d, a.split_half);
+            else rope_row(sm, a.rope, pos, d, a.split_half);
             for (int j = tid; j < d; j += kKvThreads) a.q_rot[(int64_t)h * d + j] = sm[j];
             return;
         }
@@ -176,13 +199,14 @@ __global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged
     __syncthreads();
     float *cache = (isk ? a.kcache : a.vcache) + (int64_t)slot * kvw + (int64_t)kh * d;
     if (isk) {   // RMSNorm with k_norm, RoPE at the row's position
-        const int p = merged ? (int)a.positions[slot] : pos;
+        const int p = merged ? st.merged_pos : pos;
         float v = 0.0f;
         for (int j = tid; j < d; j += kKvThreads) v = fmaf(ys[j], ys[j], v);
         const float sc = 1.0f / sqrtf(block_sum(v, red) / (float)d + a.eps);
         for (int j = tid; j < d; j += kKvThreads) ys[j] = ys[j] * sc * (a.k_gain ? a.k_gain[j] : 1.0f);
         __syncthreads();
-        rope_row(ys, a.rope, p, d, a.split_half);
+        if (pre) rope_row_pre(ys, rc, rsn, d, a.split_half);
+        else rope_row(ys, a.rope, p, d, a.split_half);
     }
     for (int j = tid; j < d; j += kKvThreads) cache[j] = ys[j];
 }
@@ -301,6 +325,7 @@ __global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
         if (threadIdx.x == 0) {
             const float centre = (a.positions[s0] * ca + a.positions[s1] * cb) / (ca + cb);
             a.positions[s1] = rintf(centre);
+            st.merged_pos = (int)rintf(centre);
             a.counts[s1] = ca + cb;
             st.start = s1;
             st.rows = st.rows;   // n - 1 = previous rows

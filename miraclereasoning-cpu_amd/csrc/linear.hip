@@ -57,26 +57,68 @@ __device__ __forceinline__ u32x4 load16(const void *base, int64_t elem) {
 }
 
 // Stage x into LDS, applying the RMSNorm prologue (kernels.cl:19-28 arithmetic:
-// scale = 1/sqrt(sum/k + eps), x * scale * gain).
+// scale = 1/sqrt(sum/k + eps), x * scale * gain).  With k a multiple of 4 and
+// 16-byte aligned vectors, each thread has kStageBatch float4 loads of x (and
+// of the gain, parked in LDS after xs until the scale is known) in flight at
+// once; otherwise element by element.
+constexpr int kStageBatch = 8;
+
+__host__ __device__ inline int gemv_xs_floats(int k) { return (k + 3) & ~3; }
+
 template <int PRO>
 __device__ __forceinline__ void stage_x(const GemvArgs &a, float *xs, float *red) {
     const int tid = threadIdx.x;
-    for (int j = tid; j < a.k; j += blockDim.x) xs[j] = a.x[j];
-    if constexpr (PRO == PRO_RMS) {
-        float ss = 0.0f;
+    const float *gain = PRO == PRO_RMS ? a.gain : nullptr;
+    float *gs = xs + gemv_xs_floats(a.k);   // PRO_RMS with a gain: the gain (red follows it)
+    float ss = 0.0f;
+    const bool vec = (a.k & 3) == 0 && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)gain & 15) == 0;
+    if (vec) {
+        const int n4 = a.k / 4;
+        for (int base = tid; base < n4; base += kGemvThreads * kStageBatch) {
+            float4 xv[kStageBatch], gv[kStageBatch];
+#pragma unroll
+            for (int i = 0; i < kStageBatch; ++i) {   // clamped, unguarded: the loads issue together
+                const int j = min(base + i * kGemvThreads, n4 - 1);
+                xv[i] = *(const float4 *)(a.x + 4 * j);
+                if (gain) gv[i] = *(const float4 *)(gain + 4 * j);
+            }
+#pragma unroll
+            for (int i = 0; i < kStageBatch; ++i) {
+                const int j = base + i * kGemvThreads;
+                if (j < n4) {
+                    *(float4 *)(xs + 4 * j) = xv[i];
+                    if (gain) *(float4 *)(gs + 4 * j) = gv[i];
+                    ss = fmaf(xv[i].x, xv[i].x, ss);
+                    ss = fmaf(xv[i].y, xv[i].y, ss);
+                    ss = fmaf(xv[i].z, xv[i].z, ss);
+                    ss = fmaf(xv[i].w, xv[i].w, ss);
+                }
+            }
+        }
+    } else {
         for (int j = tid; j < a.k; j += blockDim.x) {
-            float v = xs[j];
+            const float v = a.x[j];
+            xs[j] = v;
+            if (gain) gs[j] = gain[j];
             ss = fmaf(v, v, ss);
         }
-        ss = block_sum(ss, red);
-        float scale = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+    }
+    if constexpr (PRO == PRO_RMS) {
+        ss = block_sum(ss, red);   // its barriers also publish xs and gs
+        const float scale = 1.0f / sqrtf(ss / (float)a.k + a.eps);
         for (int j = tid; j < a.k; j += blockDim.x) {
-            float v = xs[j] * scale * (a.gain ? a.gain[j] : 1.0f);
+            const float v = xs[j] * scale * (gain ? gs[j] : 1.0f);
             xs[j] = v;
             if (a.x_out && blockIdx.x == 0) a.x_out[j] = v;
         }
     }
     __syncthreads();
+}
+
+// LDS of a GEMV workgroup: xs, the gain (RMS prologue with a gain), then the
+// reduction scratch.
+__host__ __device__ inline int gemv_red_offset(const GemvArgs &a, int pro) {
+    return gemv_xs_floats(a.k) * (pro == PRO_RMS && a.gain ? 2 : 1);
 }
 
 template <int EPI>
@@ -133,7 +175,7 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv_vec(GemvArgs a, int lpr) 
     issue(0);
     if (a.done && *a.done) return;
     float *xs = smem;
-    float *red = smem + ((a.k + 3) & ~3);
+    float *red = smem + gemv_red_offset(a, PRO);
     stage_x<PRO>(a, xs, red);
 
     float acc[R][M];
@@ -183,7 +225,7 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv_scalar(GemvArgs a) {
     extern __shared__ float smem[];
     if (a.done && *a.done) return;
     float *xs = smem;
-    float *red = smem + ((a.k + 3) & ~3);
+    float *red = smem + gemv_red_offset(a, PRO);
     stage_x<PRO>(a, xs, red);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = blockIdx.x * kGemvWaves + wave;
@@ -202,7 +244,7 @@ template <int DT, int PRO, int EPI>
 int launch_gemv_t(hipStream_t s, const GemvArgs &a) {
     constexpr int E = Vec16<DT>::E;
     const int bytes = DT == MR_F32 ? 4 : 2;
-    size_t lds = (size_t)(((a.k + 3) & ~3) + kGemvWaves) * sizeof(float);
+    size_t lds = (size_t)(gemv_red_offset(a, PRO) + kGemvWaves) * sizeof(float);
     bool aligned = (a.k % E) == 0 && ((uintptr_t)a.w % 16) == 0 &&
                    (EPI != EPI_SWIGLU || ((uintptr_t)a.w2 % 16) == 0) && ((int64_t)a.k * bytes) % 16 == 0;
     if (aligned) {
