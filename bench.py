@@ -143,6 +143,36 @@ def cpu_baseline(name, wl, weights, budget_s):
                       f"{elapsed:.1f} s"}
 
 
+def summarize_trace(path, steps):
+    """Per-kernel decode summary of a rocprofv3 kernel trace (csv) of this
+    bench in eager or graph step mode: the dispatches of the last `steps`
+    greedy decode steps (after the steps + 1-th last greedy choice, k_argmax,
+    which ends a step), as a markdown table."""
+    import collections
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    ends = [i for i, r in enumerate(rows) if "k_argmax" in r[2]]
+    steps = max(1, min(steps, len(ends) - 1))
+    dec = rows[ends[-steps - 1] + 1:ends[-1] + 1]
+    span = (dec[-1][1] - dec[0][0]) / 1e3
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for t0, t1, n in dec:
+        n = n.replace("mr::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        agg[n][0] += 1
+        agg[n][1] += (t1 - t0) / 1e3
+    tot = sum(v[1] for v in agg.values())
+    print(f"decode steps {steps}, span {span:.1f} us ({span / steps:.1f} us per step), kernel time {tot:.1f} us")
+    print("| Kernel | Calls per step | Avg µs | µs per step | % of kernel time |")
+    print("|---|---|---|---|---|")
+    for n, (c, us) in sorted(agg.items(), key=lambda x: -x[1][1]):
+        print(f"| `{n}` | {c / steps:.1f} | {us / c:.1f} | {us / steps:.1f} | {100 * us / tot:.1f} |")
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -162,7 +192,12 @@ def main():
     ap.add_argument("--step-mode", choices=("persistent", "graph", "eager"), default="persistent",
                     help="persistent: one cooperative kernel per token step; graph: five kernels per layer "
                          "replayed from a hipGraph; eager: the same kernels launched one by one")
+    ap.add_argument("--summarize-trace", metavar="CSV", default=None,
+                    help="print the per-kernel summary of the last --steps decode steps in a rocprofv3 kernel "
+                         "trace of this bench and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        return summarize_trace(args.summarize_trace, args.steps)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no multi-GPU "
               "sharding: bs=1 decode of one sequence runs on one GPU).", file=sys.stderr)

@@ -1,24 +1,32 @@
 // heavy-medium-2.0 token-step kernels (model.py:192-255).
 //
 // Attention of one inner-loop pass:
+//   k_heavy_kv     the kv_up projection of the latent (one workgroup per KV
+//                  head's K rows or V rows) with k_heavy_prep's work on the
+//                  result, and the queries; the general path runs the
+//                  projection as a GEMV and then:
 //   k_heavy_prep   queries and the new key: RMSNorm without affine (eps 1e-6,
 //                  kernels.cl:19-28 order) + interleaved RoPE; the key and value
 //                  are appended to the pass's ring at the position and added to
 //                  the running sums of their 64-row block, in row order, so the
 //                  block means equal kernels.cl's block_means bit for bit.
-//   k_heavy_attn   one workgroup per query head: window scores and block-mean
-//                  scores (sequential dot products, kernels.cl:58-73), the
-//                  distance penalty on block columns, the per-head stable
-//                  top-k of blocks (descending score, ties to the lower block;
-//                  model.py:220-226), softmax and the value mix in kernels.cl's
-//                  sequential orders.
+//   k_heavy_attn_split + k_heavy_attn_merge (head dims 32/64/128): window
+//                  rows in 32-row split partials; one workgroup per head
+//                  scores the block columns (sequential dot products of the
+//                  block means, kernels.cl:58-73), adds the distance penalty,
+//                  takes the per-head stable top-k of blocks (descending score,
+//                  ties to the lower block; model.py:220-226) and writes the
+//                  chosen blocks' partial; the merge combines the partials.
+//   k_heavy_attn / k_heavy_attn_lanes  one workgroup per query head, the
+//                  same attention in kernels.cl's sequential orders (other head
+//                  dims, and the path without a partial buffer).
 // MoE:
-//   k_moe_route    one workgroup: biases, group broadcast, temperature,
-//                  softmax, stable top-k, confidence / entropy / adaptive
-//                  width and renormalization in numpy's FP32 arithmetic
-//                  (model.py:231-250; numpy float32 sums are pairwise).
-//                  With BF16 experts every routed-slot workgroup of the
-//                  gate/up kernel routes the token itself instead.
+//   k_moe_route    one wave: biases, group broadcast, temperature, softmax,
+//                  stable top-k, confidence / entropy / adaptive width and
+//                  renormalization in numpy's FP32 arithmetic (model.py:231-250;
+//                  numpy float32 sums are pairwise).  With BF16 experts every
+//                  routed-slot workgroup of the gate/up kernel routes the token
+//                  itself instead.
 //   k_moe_gate_up  SwiGLU activations of every active routed slot and every
 //                  shared expert, weight pointers taken from a device table by
 //                  the device-side expert ids.

@@ -6,15 +6,17 @@
 // key and a value cache row per latent row and computes one only when a row is
 // created: the new row of each step, and the row a merge produces.
 //
-// Per layer and step: k_light_prep (queries: RMSNorm with q_norm + RoPE; the
-// new latent: RMSNorm with latent_norm, appended with its position and count
-// 1), the K/V projection of the new latent, k_light_store (its K: RMSNorm with
-// k_norm + RoPE at its position; its V), k_light_attend (scores over every row,
-// latent_mask, softmax, mix: kernels.cl's sequential orders), k_light_compact
-// (model.py:168-188: drop the overflow without memory slots; merge the two
-// oldest rows by their counts when the overflow exceeds the slots; else mark
-// the overflow as memory rows), then - when a merge happened - the K/V
-// projection of the merged row and its cache row at its new position.
+// Per layer and step: the queries (RMSNorm with q_norm + RoPE), the new latent
+// (RMSNorm with latent_norm, appended with its position and count 1) and its
+// cache rows (the K/V projection; K: RMSNorm with k_norm + RoPE at its
+// position; V as projected) - one launch of k_light_kv, or k_light_prep, a
+// GEMV and k_light_store where its geometry does not fit; the attention over
+// every row with latent_mask (split partials and a merge for head dims
+// 32/64/128, else k_light_attend in kernels.cl's sequential orders);
+// k_light_compact (model.py:168-188: drop the overflow without memory slots;
+// merge the two oldest rows by their counts when the overflow exceeds the
+// slots; else mark the overflow as memory rows); then - when a merge happened
+// - the merged row's cache rows at its new position.
 #include "lighting.h"
 
 #include "block_gemv.h"
