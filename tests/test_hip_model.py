@@ -245,6 +245,32 @@ def test_heavy_geometry_matches_oracle(backend):
     assert model.generate(list(ids), max_new_tokens=8) == stream
 
 
+def test_heavy_general_paths_match_oracle(backend):
+    """heavy-medium-2.0 with a latent width the fused K/V prologue does not take
+    (36: the projection runs as a GEMV and k_heavy_prep follows) and head dim 48
+    (the single-workgroup attention instead of the split one): logits, every
+    routing and block choice bit-exact, and the greedy stream, against the
+    oracle."""
+    from test_oracle_model import _block_masks, _expert_log
+    config = dict(HEAVY_MID, latent_dim=36, head_dim=48)
+    weights = synthetic.synthetic_weights(config, 19, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 70, 19)
+    trace = []
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=128, trace=trace)
+    want = ref.prefill(ids, return_all=True)
+    cfg = ModelConfig.from_dict(config)
+    model = MiracleModel(cfg, weights, backend=backend, context_length=128)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    experts, masks = _choice_logs(model.engine.choices(), cfg)
+    np.testing.assert_array_equal(experts, _expert_log(trace))
+    ref_masks = _block_masks(trace, ref.cfg, cfg.query_heads)
+    assert len(masks) == len(ref_masks)
+    for ours, theirs in zip(masks, ref_masks):
+        np.testing.assert_array_equal(ours, theirs)
+    assert model.generate(list(ids), max_new_tokens=6) == ref.generate(list(ids), max_new_tokens=6)
+
+
 LIGHT_MID = {"family": "flashlighting-2.0", "vocab_size": 512, "hidden_size": 256, "layers": 2, "query_heads": 4,
              "kv_heads": 4, "head_dim": 64, "ffn_dim": 384, "max_positions": 4096, "window": 24, "latent_dim": 32,
              "memory_slots": 4, "rope_theta": 1000000.0,
@@ -283,3 +309,19 @@ def test_lighting_split_attention_matches_oracle(backend):
     model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=256)
     np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
     assert model.generate(list(ids), max_new_tokens=8) == ref.generate(list(ids), max_new_tokens=8)
+
+
+def test_lighting_general_paths_match_oracle(backend):
+    """flashlighting-2.0 with a latent width the fused row kernel does not take
+    (36: prologue, projection GEMV and cache-row kernels apart) and head dim 48
+    (the single-workgroup attention instead of the split one), with merges into
+    memory slots: logits and greedy stream against the oracle."""
+    config = dict(LIGHT_MID, latent_dim=36, head_dim=48, hidden_size=192)
+    weights = synthetic.synthetic_weights(config, 23, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 80, 23)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=128)
+    want = ref.prefill(ids, return_all=True)
+    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=128)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    assert model.generate(list(ids), max_new_tokens=6) == ref.generate(list(ids), max_new_tokens=6)
