@@ -146,25 +146,28 @@ __device__ __forceinline__ unsigned word(const unsigned *p) {
     return __hip_atomic_load(gmem(const_cast<unsigned *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait until words[0..n) all reach ep.  Only the first wave of the caller
-// polls (lane `me` < 64 takes words me, me+64, ...; up to 16 each, all in
+// Wait until at least n - slack of words[0..n) reach ep.  Only the first wave
+// of the caller polls (lane `me` < 64 takes words me, me+64, ...; 16 each in
 // flight per round) and it pauses between rounds: every workgroup polls the
 // same few lines, so the poll rate is kept low.
-__device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigned ep, int me, Wait &w) {
+__device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigned ep, int me, int slack, Wait &w) {
     constexpr int B = 16;
     if (me >= kWave) return;
-    for (int base = me; base < n; base += kWave * B) {
-        bool ready;
-        do {
-            unsigned v[B];
+    bool done;
+    do {
+        int ready = 0;
+        for (int base = me; base < n; base += kWave * B) {
 #pragma unroll
-            for (int i = 0; i < B; ++i) v[i] = base + i * kWave < n ? word(words + base + i * kWave) : ep;
-            ready = true;
+            for (int i = 0; i < B; ++i) {
+                const int idx = base + i * kWave;
+                ready += idx < n && word(words + idx) >= ep;
+            }
+        }
 #pragma unroll
-            for (int i = 0; i < B; ++i) ready &= base + i * kWave >= n || v[i] >= ep;
-            if (!ready) __builtin_amdgcn_s_sleep(16);
-        } while (!ready && backoff(w));
-    }
+        for (int off = 32; off > 0; off >>= 1) ready += __shfl_xor(ready, off);
+        done = ready >= n - slack;
+        if (!done) __builtin_amdgcn_s_sleep(16);
+    } while (!done && backoff(w));
 }
 
 }  // namespace ll

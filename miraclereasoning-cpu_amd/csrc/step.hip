@@ -226,15 +226,24 @@ __device__ __forceinline__ void best_merge(Best &a, float v, int i) {
 // res.  With the RMSNorm prologue (kernels.cl:19-28) xs holds input x gain and
 // red[wave] the wave's sum of squares of the raw input: the 1/rms scale is
 // applied to the dot products, y = scale * W (x * gain).
+constexpr int kStartWords = 32;   // a phase reads its input cells once 1/kStartWords of the producers are done
+
 __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, const StepArgs &s, unsigned ep_x,
                                             unsigned ep_res, float *xs, float *res, float *red, ll::Wait &w) {
     const int me = threadIdx.x, lanes = NC * kWave;
-    // The first control wave waits for the producers, then releases the others
-    // through an LDS word (ep_x, or ~0 when its wait gave up).
+    // The first control wave waits until the producers start finishing (a
+    // 32nd of their progress words), then releases the others through an LDS
+    // word (ep_x, or ~0 when its wait gave up); the cell reads below wait for
+    // the rest cell by cell.  Reading the cells from the first word on saves a
+    // memory round trip per phase over waiting for every word; polling them
+    // from the phase's start loads the memory with polls and is slower.
     __shared__ unsigned released;
     if (me < kWave) {
-        if (ph.ready) ll::wait_words(ph.ready, ph.nready, ep_x, me, w);
-        else ll::wait_words(s.progress + (blockIdx.x % kWordCopies) * kWordCopyStride, s.nprogress, ep_x, me, w);
+        if (ph.ready)
+            ll::wait_words(ph.ready, ph.nready, ep_x, me, ph.nready - max(1, ph.nready / kStartWords), w);
+        else
+            ll::wait_words(s.progress + (blockIdx.x % kWordCopies) * kWordCopyStride, s.nprogress, ep_x, me,
+                           s.nprogress - max(1, s.nprogress / kStartWords), w);
         const bool ok = __all(w.ok);
         if (me == 0) __hip_atomic_store(&released, ok ? ep_x : ~0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     } else {
