@@ -259,43 +259,10 @@ __global__ void __launch_bounds__(kThreads) k_light_attend(LightArgs a) {
     }
 }
 
-// Split-key form of the same attention for head dims 32/64/128: workgroup
-// (split s, head h) scores rows [64 s, 64 s + 64) of the memory with the
-// latent mask (kernels.cl:86-91: non-memory rows older than the window) and
-// writes its partial; a second kernel merges the splits of each head.
-template <int D>
-__global__ void __launch_bounds__(split::kThreads) k_light_attend_part(LightArgs a) {
-    if (a.done && *a.done) return;
-    const LightState st = *a.st;
-    const int n = st.rows + 1;                  // with this step's row
-    const int t0 = blockIdx.x * kLightRows;
-    if (t0 >= n) return;
-    const int h = blockIdx.y, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
-    const float earliest = (float)(*a.pos - a.window + 1);
-    const auto rows = [&](int t, const float **k, const float **v) {
-        const int slot = (st.start + t) % a.cap;
-        if (t >= st.memory && a.positions[slot] < earliest) return false;
-        *k = a.kcache + (int64_t)slot * kvw + (int64_t)kh * D;
-        *v = a.vcache + (int64_t)slot * kvw + (int64_t)kh * D;
-        return true;
-    };
-    split::partial<D>(a.q_rot + (int64_t)h * D, t0, min(n, t0 + kLightRows), rows,
-                      a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2));
-}
-
-// grid heads, split::kThreads
-template <int D>
-__global__ void __launch_bounds__(split::kThreads) k_light_attend_merge(LightArgs a, int splits) {
-    if (a.done && *a.done) return;
-    const int n = a.st->rows + 1, active = min(splits, (n + kLightRows - 1) / kLightRows);
-    split::merge<D>(a.part + (int64_t)blockIdx.x * splits * (D + 2), active, -1, a.out + (int64_t)blockIdx.x * D);
-}
-
-// One workgroup: compaction after this step's attention (model.py:168-188).
-__global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
+// Compaction after this step's attention (model.py:168-188), by one workgroup.
+__device__ __forceinline__ void compact_state(const LightArgs &a) {
     __shared__ LightState st;
     __shared__ int mode;   // 0 keep, 1 drop, 2 merge
-    if (a.done && *a.done) return;
     if (threadIdx.x == 0) {
         st = *a.st;
         const int n = st.rows + 1, overflow = max(0, n - a.window);
@@ -338,6 +305,53 @@ __global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
     }
     __syncthreads();
     if (threadIdx.x == 0) *a.st = st;
+}
+
+// One workgroup: compaction after the single-workgroup attention.
+__global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
+    if (a.done && *a.done) return;
+    compact_state(a);
+}
+
+// Split-key form of the same attention for head dims 32/64/128: workgroup
+// (split s, head h) scores rows [64 s, 64 s + 64) of the memory with the
+// latent mask (kernels.cl:86-91: non-memory rows older than the window) and
+// writes its partial; a second kernel merges the splits of each head.
+template <int D>
+__global__ void __launch_bounds__(split::kThreads) k_light_attend_part(LightArgs a) {
+    if (a.done && *a.done) return;
+    const LightState st = *a.st;
+    const int n = st.rows + 1;                  // with this step's row
+    const int t0 = blockIdx.x * kLightRows;
+    const int h = blockIdx.y, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
+    if (t0 >= n) {   // no rows in this split yet: an empty partial, so the merge needs no row count
+        float *part = a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2);
+        for (int j = threadIdx.x; j < D + 2; j += split::kThreads) part[j] = j == 0 ? -INFINITY : 0.0f;
+        return;
+    }
+    const float earliest = (float)(*a.pos - a.window + 1);
+    const auto rows = [&](int t, const float **k, const float **v) {
+        const int slot = (st.start + t) % a.cap;
+        if (t >= st.memory && a.positions[slot] < earliest) return false;
+        *k = a.kcache + (int64_t)slot * kvw + (int64_t)kh * D;
+        *v = a.vcache + (int64_t)slot * kvw + (int64_t)kh * D;
+        return true;
+    };
+    split::partial<D>(a.q_rot + (int64_t)h * D, t0, min(n, t0 + kLightRows), rows,
+                      a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2));
+}
+
+// grid heads, split::kThreads: every split's partial (empty ones included),
+// then workgroup 0 compacts the memory (its rows were all read by the split
+// kernel before this launch).
+template <int D>
+__global__ void __launch_bounds__(split::kThreads) k_light_attend_merge(LightArgs a, int splits) {
+    if (a.done && *a.done) return;
+    split::merge<D>(a.part + (int64_t)blockIdx.x * splits * (D + 2), splits, -1, a.out + (int64_t)blockIdx.x * D);
+    if (blockIdx.x == 0) {
+        __syncthreads();
+        compact_state(a);
+    }
 }
 
 __global__ void k_light_residual(float *hidden, const float *o, const float *f, const float *ag, const float *fg,
@@ -403,13 +417,13 @@ int launch_light_attend(hipStream_t s, const LightArgs &a) {
                 k_light_attend_merge<32><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
         }
-        MR_LAUNCHED("enqueue latent attention merge");
-    } else {
-        const size_t lds = (size_t)(a.d + a.cap) * sizeof(float);
-        MR_REQUIRE(lds <= 64 * 1024, "latent attention: window and memory slots exceed shared memory");
-        k_light_attend<<<a.heads, kThreads, lds, s>>>(a);
-        MR_LAUNCHED("enqueue latent attention");
+        MR_LAUNCHED("enqueue latent attention merge and compaction");
+        return MR_OK;
     }
+    const size_t lds = (size_t)(a.d + a.cap) * sizeof(float);
+    MR_REQUIRE(lds <= 64 * 1024, "latent attention: window and memory slots exceed shared memory");
+    k_light_attend<<<a.heads, kThreads, lds, s>>>(a);
+    MR_LAUNCHED("enqueue latent attention");
     k_light_compact<<<1, 64, 0, s>>>(a);
     MR_LAUNCHED("enqueue latent compaction");
     return MR_OK;
