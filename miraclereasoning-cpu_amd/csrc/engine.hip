@@ -499,16 +499,14 @@ int record_light_layer(mr_model *m, Layer &L) {
     GemvArgs u;   // [Wk; Wv] . new latent row
     u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
     if (fused) {
-        MR_TRY(launch_light_kv(s, a, false));
+        MR_TRY(launch_light_kv(s, a));
     } else {
         MR_TRY(launch_light_prep(s, a));
         MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, u));
         MR_TRY(launch_light_store_kv(s, a, false));
     }
     MR_TRY(launch_light_attend(s, a));
-    if (fused) {   // the merged row's cache row (skipped unless compaction merged)
-        MR_TRY(launch_light_kv(s, a, true));
-    } else {
+    if (!fused) {   // the merged row's cache row now (the fused row kernel does it at the next step's start)
         GemvArgs um = u;   // [Wk; Wv] . merged row, skipped unless compaction merged
         um.done = &L.light->skip_merged;
         MR_TRY(launch_gemv(s, L.kv_up.dtype, PRO_COPY, EPI_STORE, um));

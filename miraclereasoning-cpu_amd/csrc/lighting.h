@@ -9,8 +9,11 @@ namespace mr {
 
 // Device state of one layer's latent memory: rows live in a ring of `cap`
 // slots; logical row t is slot (start + t) % cap.
+// skip_merged / merged_slot / merged_pos describe the row the last compaction
+// merged (its cache row not yet computed); pending says the same for the fused
+// row kernel, which computes it at the start of the next step.
 struct LightState {
-    int start, rows, memory, skip_merged, merged_slot, merged_pos, pad[2];   // merged_pos: the merged row's position
+    int start, rows, memory, skip_merged, merged_slot, merged_pos, pending, pad;
 };
 
 struct LightArgs {
@@ -51,10 +54,11 @@ int launch_light_prep(hipStream_t s, const LightArgs &a);
 int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged);
 // The same three steps in one launch (queries, the appended row, and the K/V
 // projection with the cache row computed per KV head from the normalized
-// latent), or for the merged row the projection and its cache row; for the
+// latent), together with the cache row of the row the previous step's
+// compaction merged (no step reads it before this one's attention); for the
 // dtypes and latent widths light_kv_fused accepts.
 bool light_kv_fused(int dtype, int latent, int d);
-int launch_light_kv(hipStream_t s, const LightArgs &a, bool merged);
+int launch_light_kv(hipStream_t s, const LightArgs &a);
 // Attention over every row, then compaction (which leaves the merged row in
 // lat_new and clears skip_merged when a merge happened).
 int launch_light_attend(hipStream_t s, const LightArgs &a);

@@ -104,15 +104,15 @@ __global__ void __launch_bounds__(64) k_light_store(LightArgs a, int merged) {
 }
 
 // ------------------------------------------------------------------ fused row kernel
-// grid heads + 1 + 2 kv_heads (new row) or 2 kv_heads (merged row), 256
-// threads.  Blocks < heads: query h, RMSNorm with q_norm, RoPE at pos ->
-// q_rot.  Block heads: the new latent row (RMSNorm with latent_norm) appended
-// with its position and count 1.  The last 2 kv_heads blocks: the K rows of KV
-// head kh (blocks < kv_heads) or its V rows, [Wk; Wv] . latent with the latent
-// normalized by the block itself (the same arithmetic as the appending block,
-// so the same bits) or, for the merged row, lat_new; a K row then takes
-// RMSNorm with k_norm and RoPE at the row's position; the rows go to the
-// caches.
+// grid heads + 1 + 4 kv_heads, 256 threads.  Blocks < heads: query h, RMSNorm
+// with q_norm, RoPE at pos -> q_rot.  Block heads: the new latent row
+// (RMSNorm with latent_norm) appended with its position and count 1.  The next
+// 2 kv_heads blocks: the K rows of KV head kh (first kv_heads) or its V rows,
+// [Wk; Wv] . latent with the latent normalized by the block itself (the same
+// arithmetic as the appending block, so the same bits); the last 2 kv_heads
+// blocks: the same for the row the previous step's compaction merged (its
+// latent from the arena, at its position), when one is pending.  A K row then takes RMSNorm
+// with k_norm and RoPE at the row's position; the rows go to the caches.
 constexpr int kKvThreads = 256;
 
 // RoPE of a row in LDS whose (cos, sin) for pair tid (tid < d/2 <= blockDim)
@@ -145,13 +145,14 @@ __device__ __forceinline__ void block_rms_row(const float *x, const float *gain,
 }
 
 template <int DT>
-__global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged) {
+__global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a) {
     constexpr int EB = DT == MR_F32 ? 4 : 2;   // bytes per weight element
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[kKvThreads / kWave];
     const int tid = threadIdx.x, d = a.d, kvw = a.kv_heads * d;
-    const int nq = merged ? 0 : a.heads + 1;   // query and appending blocks
-    const int b = (int)blockIdx.x - nq;
+    const int b0 = (int)blockIdx.x - (a.heads + 1);    // cache-row blocks from 0
+    const bool merged = b0 >= 2 * a.kv_heads;          // the pending merged row
+    const int b = merged ? b0 - 2 * a.kv_heads : b0;
     const bool isk = b >= 0 && b < a.kv_heads;
     const int kh = isk ? b : b - a.kv_heads;
     // The weight loads depend on nothing this step computes: they go out
@@ -161,7 +162,7 @@ __global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged
                            a.latent);
     if (a.done && *a.done) return;
     const LightState st = *a.st;
-    if (merged && st.skip_merged) return;
+    if (merged && !st.pending) return;
     const int pos = *a.pos;
     const int slot = merged ? st.merged_slot : (st.start + st.rows) % a.cap;
     const float *raw_latent = a.qlat + (int64_t)a.heads * d;
@@ -191,8 +192,8 @@ __global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a, int merged
         return;
     }
     float *xs = sm, *ys = sm + ((a.latent + 3) & ~3);
-    if (merged) {
-        for (int j = tid; j < a.latent; j += kKvThreads) xs[j] = a.lat_new[j];
+    if (merged) {   // the merged latent, from this layer's arena (lat_new is shared by the layers)
+        for (int j = tid; j < a.latent; j += kKvThreads) xs[j] = a.arena[(int64_t)slot * a.latent + j];
         __syncthreads();
     } else {
         block_rms_row(raw_latent, a.latent_gain, a.eps, a.latent, xs, red);
@@ -267,6 +268,7 @@ __device__ __forceinline__ void compact_state(const LightArgs &a) {
         st = *a.st;
         const int n = st.rows + 1, overflow = max(0, n - a.window);
         st.skip_merged = 1;
+        st.pending = 0;
         if (a.memory_slots == 0 && overflow > 0) {
             mode = 1;
             st.start = (st.start + overflow) % a.cap;
@@ -300,6 +302,7 @@ __device__ __forceinline__ void compact_state(const LightArgs &a) {
             st.rows = st.rows;   // n - 1 = previous rows
             st.memory = a.memory_slots;
             st.skip_merged = 0;
+            st.pending = 1;
             st.merged_slot = s1;
         }
     }
@@ -385,14 +388,14 @@ bool light_kv_fused(int dtype, int latent, int d) {
     return fits && d % 2 == 0;
 }
 
-int launch_light_kv(hipStream_t s, const LightArgs &a, bool merged) {
+int launch_light_kv(hipStream_t s, const LightArgs &a) {
     MR_REQUIRE(light_kv_fused(a.kv_dtype, a.latent, a.d) && a.kv_w, "latent rows: unsupported projection geometry");
-    const int grid = merged ? 2 * a.kv_heads : a.heads + 1 + 2 * a.kv_heads;
+    const int grid = a.heads + 1 + 4 * a.kv_heads;
     const size_t lds = (size_t)(((a.latent + 3) & ~3) + std::max(a.d, a.latent)) * sizeof(float);
-    if (a.kv_dtype == MR_BF16) k_light_kv<MR_BF16><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
-    else if (a.kv_dtype == MR_F16) k_light_kv<MR_F16><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
-    else k_light_kv<MR_F32><<<grid, kKvThreads, lds, s>>>(a, merged ? 1 : 0);
-    MR_LAUNCHED(merged ? "enqueue merged latent row" : "enqueue latent rows");
+    if (a.kv_dtype == MR_BF16) k_light_kv<MR_BF16><<<grid, kKvThreads, lds, s>>>(a);
+    else if (a.kv_dtype == MR_F16) k_light_kv<MR_F16><<<grid, kKvThreads, lds, s>>>(a);
+    else k_light_kv<MR_F32><<<grid, kKvThreads, lds, s>>>(a);
+    MR_LAUNCHED("enqueue latent rows");
     return MR_OK;
 }
 
