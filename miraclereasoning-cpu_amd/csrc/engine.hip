@@ -496,6 +496,10 @@ int record_light_layer(mr_model *m, Layer &L) {
     // queries, the appended row and its cache row: one launch where the
     // geometry allows, else prologue, projection and cache row apart
     const bool fused = light_kv_fused(L.kv_up.dtype, d.latent_dim, hd);
+    GemvArgs gu;   // the FFN branch's gate/up: in the fused row kernel where it fits, else after the O projection
+    gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->xnorm; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act;
+    gu.done = m->done_dev;
+    const bool ffn_early = fused && light_ffn_in_row_kernel(a, gu, L.ffn.gate.dtype);
     GemvArgs u;   // [Wk; Wv] . new latent row
     u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
     if (fused) {
@@ -515,10 +519,7 @@ int record_light_layer(mr_model *m, Layer &L) {
     GemvArgs o;
     o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->branch_o; o.done = m->done_dev;
     MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_STORE, o));
-    GemvArgs gu;
-    gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->xnorm; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act;
-    gu.done = m->done_dev;
-    MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_COPY, EPI_SWIGLU, gu));
+    if (!ffn_early) MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_COPY, EPI_SWIGLU, gu));
     GemvArgs dn;   // hidden += rs * ((0 + ag * o) + fg * down(act)) in the down projection's epilogue
     dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden; dn.done = m->done_dev;
     dn.scale = d.residual_scale; dn.aux = m->branch_o; dn.scale_ptr = L.attention_gate.f();

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "linear.h"
 
 namespace mr {
 
@@ -35,6 +36,11 @@ struct LightArgs {
     float *part = nullptr;           // [heads][splits][d + 2] split partials (m, l, o)
     const void *kv_w = nullptr;      // [2*kv_heads*d, latent] packed [Wk; Wv] (fused row kernel)
     int kv_dtype = MR_BF16;
+    // The FFN branch's gate/up + SwiGLU rows (they read the same normalized
+    // input as the attention branch) in ffn_blocks more workgroups of the fused
+    // row kernel, as a GEMV launch's workgroups would run them; 0 = apart.
+    GemvArgs ffn;
+    int ffn_blocks = 0, ffn_lpr = 0;
     int heads = 0, kv_heads = 0, d = 0, latent = 0, window = 0, memory_slots = 0, cap = 0;
 };
 
@@ -58,6 +64,9 @@ int launch_light_store_kv(hipStream_t s, const LightArgs &a, bool merged);
 // compaction merged (no step reads it before this one's attention); for the
 // dtypes and latent widths light_kv_fused accepts.
 bool light_kv_fused(int dtype, int latent, int d);
+// Whether the gate/up GEMV g (weights of dtype) can ride in the fused row
+// kernel (kv weights of kv_dtype); sets ffn, ffn_blocks and ffn_lpr of a.
+bool light_ffn_in_row_kernel(LightArgs &a, const GemvArgs &g, int dtype);
 int launch_light_kv(hipStream_t s, const LightArgs &a);
 // Attention over every row, then compaction (which leaves the merged row in
 // lat_new and clears skip_merged when a merge happened).

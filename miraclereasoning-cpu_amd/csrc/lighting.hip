@@ -20,6 +20,7 @@
 #include "lighting.h"
 
 #include "block_gemv.h"
+#include "gemv_block.h"
 #include "split_attention.h"
 
 namespace mr {
@@ -144,11 +145,19 @@ __device__ __forceinline__ void block_rms_row(const float *x, const float *gain,
     __syncthreads();
 }
 
+static_assert(kKvThreads == gemv::kGemvThreads, "the row kernel hosts GEMV workgroups");
+constexpr int kFfnVec = 4;   // weight vectors per lane and row in one batch of the hosted gate/up rows
+
 template <int DT>
 __global__ void __launch_bounds__(kKvThreads) k_light_kv(LightArgs a) {
     constexpr int EB = DT == MR_F32 ? 4 : 2;   // bytes per weight element
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[kKvThreads / kWave];
+    const int nrow = a.heads + 1 + 4 * a.kv_heads;
+    if ((int)blockIdx.x >= nrow) {   // the FFN branch's gate/up rows
+        gemv::gemv_vec_block<DT, 1, kFfnVec, PRO_COPY, EPI_SWIGLU>(a.ffn, a.ffn_lpr, blockIdx.x - nrow, sm);
+        return;
+    }
     const int tid = threadIdx.x, d = a.d, kvw = a.kv_heads * d;
     const int b0 = (int)blockIdx.x - (a.heads + 1);    // cache-row blocks from 0
     const bool merged = b0 >= 2 * a.kv_heads;          // the pending merged row
@@ -388,10 +397,26 @@ bool light_kv_fused(int dtype, int latent, int d) {
     return fits && d % 2 == 0;
 }
 
+bool light_ffn_in_row_kernel(LightArgs &a, const GemvArgs &g, int dtype) {
+    a.ffn_blocks = 0;
+    const int e = dtype == MR_F32 ? 4 : 8, bytes = dtype == MR_F32 ? 4 : 2;
+    if (dtype != a.kv_dtype || g.k % e || (uintptr_t)g.w % 16 || (uintptr_t)g.w2 % 16 || ((int64_t)g.k * bytes) % 16)
+        return false;
+    const int nvec = g.k / e;
+    int lpr = 1;
+    while (lpr * 2 <= nvec && lpr < kWave) lpr *= 2;
+    if (ceil_div(nvec, lpr) > kFfnVec) return false;   // one batch of kFfnVec vectors must cover a row
+    a.ffn = g;
+    a.ffn_lpr = lpr;
+    a.ffn_blocks = ceil_div(g.n, gemv::kGemvWaves * (kWave / lpr));
+    return true;
+}
+
 int launch_light_kv(hipStream_t s, const LightArgs &a) {
     MR_REQUIRE(light_kv_fused(a.kv_dtype, a.latent, a.d) && a.kv_w, "latent rows: unsupported projection geometry");
-    const int grid = a.heads + 1 + 4 * a.kv_heads;
-    const size_t lds = (size_t)(((a.latent + 3) & ~3) + std::max(a.d, a.latent)) * sizeof(float);
+    const int grid = a.heads + 1 + 4 * a.kv_heads + a.ffn_blocks;
+    size_t lds = (size_t)(((a.latent + 3) & ~3) + std::max(a.d, a.latent)) * sizeof(float);
+    if (a.ffn_blocks) lds = std::max(lds, (size_t)gemv::gemv_lds_floats(a.ffn, PRO_COPY) * sizeof(float));
     if (a.kv_dtype == MR_BF16) k_light_kv<MR_BF16><<<grid, kKvThreads, lds, s>>>(a);
     else if (a.kv_dtype == MR_F16) k_light_kv<MR_F16><<<grid, kKvThreads, lds, s>>>(a);
     else k_light_kv<MR_F32><<<grid, kKvThreads, lds, s>>>(a);
