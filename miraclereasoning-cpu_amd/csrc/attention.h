@@ -41,6 +41,11 @@ struct AttnStepArgs {
     unsigned *counters = nullptr;      // [kv_heads], zero between launches
     float *out = nullptr;              // [heads*dim]
     int splits = 0, split_len = 0;
+    // Query heads of a KV head split over this many units of each key range
+    // (persistent kernel; 1 elsewhere): unit group v = kh * head_groups + hs
+    // holds query heads [v * G, (v + 1) * G) with G = heads / (kv_heads *
+    // head_groups), its counter, progress word and partials indexed by v.
+    int head_groups = 1;
 };
 
 // Split geometry for at most `max_total` keys with kv_heads heads of `dim`, at

@@ -88,9 +88,11 @@ __device__ __forceinline__ Geo geometry(const Args &ka, int pos) {
 // LDS, then store the new key/value in the ring slot of this position (done by
 // the unit that holds the newest key).
 // Returns false (block-uniform) when an LL wait gave up.
+// hs: the unit's group of the KV head's query heads (AttnStepArgs::head_groups);
+// group 0 stores the new key/value.
 template <bool LL, int NT>
 __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, int G, int d, float *qs, float *kn,
-                                        float *vn, int t0, int t1, const Io &io) {
+                                        float *vn, int t0, int t1, const Io &io, int hs = 0) {
     const AttnStepArgs &a = ka.s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = d / 2;
@@ -115,7 +117,7 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
         // buffer), each thread polling at most a few pairs.
         ll::Wait w = ll::waiter(io.err);
         const uint64_t *cells = (const uint64_t *)a.q;
-        const int q0 = kh * G * d;
+        const int q0 = (kh * a.head_groups + hs) * G * d;
         const int k0 = (int)((const uint64_t *)a.k_new - cells) + kh * d;
         const int v0 = (int)((const uint64_t *)a.v_new - cells) + kh * d;
         for (int i = 2 * tid; i < G * d + 2 * d; i += 2 * NT) {
@@ -127,7 +129,7 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
         }
         if (!ll::all_ok(w)) return false;
     } else {
-        const float *q_src = a.q + (int64_t)kh * G * d;
+        const float *q_src = a.q + (int64_t)(kh * a.head_groups + hs) * G * d;
         for (int i = tid; i < G * d; i += NT) qs[i] = *gmem(q_src + i);
         if (ka.mode != 1) {
             __syncthreads();
@@ -164,7 +166,7 @@ __device__ __forceinline__ bool prepare(const Args &ka, const Geo &g, int kh, in
     }
     __syncthreads();
     const int newest = g.length - 1;
-    if (t0 <= newest && newest < t1) {
+    if (hs == 0 && t0 <= newest && newest < t1) {
         const int kvw = a.kv_heads * d;
         int64_t slot = (int64_t)(g.pos % a.capacity) * kvw + (int64_t)kh * d;
         for (int j = tid; j < d; j += NT) {
@@ -454,20 +456,21 @@ __host__ __device__ constexpr int combine_lds_floats(int G, int splits) {
     return 2 * splits * G + G + (NT / (D / 4)) * G * D;
 }
 
-// The persistent kernel's merge: the partials of the `active` splits of KV
-// head kh are cells of epoch io.ep_out.  Thread (gh, j4, sg) sums float4
+// The persistent kernel's merge: the partials of the `active` splits of unit
+// group v (AttnStepArgs::head_groups) are cells of epoch io.ep_out.  Thread
+// (gh, j4, sg) sums float4
 // column j4 of head gh over splits sg, sg + SG, ...; each thread issues its
 // o cells (up to kChunk float4 per round) together with one (m, l) pair and
 // polls until all carry the epoch, so a merge that starts after its splits
-// finished costs one round trip.  Writes out[(kh*G + g)*D + j] as cells.
+// finished costs one round trip.  Writes out[(v*G + g)*D + j] as cells.
 // Returns false (block-uniform) when a wait gave up.
 template <int D, int NT>
-__device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int active, float *lds, const Io &io) {
+__device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int active, float *lds, const Io &io) {
     constexpr int C4 = D / 4;
     constexpr int kChunk = 8;
     const int tid = threadIdx.x;
-    const int G = a.heads / a.kv_heads;
-    const uint64_t *base = a.part_cells + (int64_t)kh * a.splits * G * (D + 2);
+    const int G = a.heads / (a.kv_heads * a.head_groups);
+    const uint64_t *base = a.part_cells + (int64_t)v * a.splits * G * (D + 2);
     const int SG = max(1, NT / (G * C4));               // split groups per (gh, j4)
     const bool owner = tid < G * C4 * SG;
     const int gh = owner ? tid / (C4 * SG) : 0, j4 = tid % C4, sg = owner ? (tid / C4) % SG : 0;
@@ -553,7 +556,7 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int
         const int h = i / D, j = i % D;
         float sum = 0.0f;
         for (int q = 0; q < SG; ++q) sum += red[(q * G + h) * D + j];
-        ll::put((uint64_t *)a.out + (int64_t)(kh * G + h) * D + j, sum / L[h], io.ep_out);
+        ll::put((uint64_t *)a.out + (int64_t)(v * G + h) * D + j, sum / L[h], io.ep_out);
     }
     return true;
 }
@@ -565,7 +568,11 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int kh, int
 // D/16 lanes share a key: a dot product is 16 FMAs and at most three in-row
 // lane steps.  A round is kWaveKeys keys per lane; the first round's K/V
 // loads (keys of earlier steps only) go out before the Q/K/V cells are
-// awaited.  G <= kWaveUnitMaxG.
+// awaited.  The unit scores G = heads / (kv_heads * head_groups) <=
+// kWaveUnitMaxG query heads (group hs of KV head kh): with head_groups > 1 the
+// groups of one KV head read the same keys, and the cost of a unit (its
+// rounds run the heads one after another, then its partial and merge) falls
+// with G.
 constexpr int kWaveVec = 4;          // float4 per lane per key (16 dims)
 constexpr int kWaveKeys = 1;         // keys per lane per round
 constexpr int kWaveUnitMaxG = 4;
@@ -620,7 +627,7 @@ __device__ __forceinline__ float keygroups_max(float v) {
 }
 
 template <int D, int NT>
-__device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, int kh, int split, float *lds,
+__device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, int kh, int hs, int split, float *lds,
                                                 const Io &io) {
     const AttnStepArgs &a = ka.s;
     constexpr int LPK = D / (4 * kWaveVec);   // lanes per key: 8, 4, 2
@@ -629,7 +636,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
     constexpr int RK = kWaveKeys * KPI;       // keys per wave per round
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane % LPK, kg = lane / LPK;
-    const int G = a.heads / a.kv_heads, kvw = a.kv_heads * D;
+    const int G = a.heads / (a.kv_heads * a.head_groups), kvw = a.kv_heads * D;
     int t0, t1, split_len;
     split_range<D>(g, a.splits, split, &t0, &t1, &split_len);
     float *qs = lds;                  // [G][D]
@@ -670,7 +677,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
     const int per_round = NWV * RK;
     const int rounds = (t1 - t0 + per_round - 1) / per_round;
     fetch(0);
-    if (!prepare<true, NT>(ka, g, kh, G, D, qs, kn, vn, t0, t1, io)) return false;
+    if (!prepare<true, NT>(ka, g, kh, G, D, qs, kn, vn, t0, t1, io, hs)) return false;
 
     // scores carry the 1/sqrt(D) of kernels.cl:72 through the queries
     const float inv_root = 1.0f / sqrtf((float)D);
@@ -764,7 +771,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
         }
     }
     __syncthreads();
-    uint64_t *part = a.part_cells + ((int64_t)(kh * a.splits + split) * G) * (D + 2);
+    uint64_t *part = a.part_cells + ((int64_t)((kh * a.head_groups + hs) * a.splits + split) * G) * (D + 2);
     for (int e = tid; e < G * D; e += NT) {
         const int h = e / D, j = e % D;
         float M = -INFINITY;

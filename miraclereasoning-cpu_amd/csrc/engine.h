@@ -53,6 +53,7 @@ struct Layer {
     float *pending = nullptr;                          // flashnano-1.6 chunk rows
     int splits = 0, split_len = 0;                     // attention plan
     int step_splits = 0;                               // attention splits in the step kernel
+    int step_head_groups = 1;                          // query-head groups per KV head in the step kernel
 };
 
 }  // namespace mr

@@ -673,6 +673,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         t.heads = d.query_heads; t.kv_heads = L.kv_heads; t.dim = hd;
         t.part = m->part; t.out = (float *)m->c_attn; t.splits = L.step_splits; t.split_len = 0;
         t.part_cells = m->part_cells;
+        t.head_groups = L.step_head_groups;
         t.counters = m->merge_counts + (size_t)li * m->merge_count_n / d.layers;
         a.at.mode = 1;
         a.at.ring_k_ro = L.ring_k; a.at.ring_v_ro = L.ring_v;
@@ -681,7 +682,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         Phase o;
         o.kind = PH_GEMV; o.dtype = L.o.dtype; o.n = h; o.k = qd; o.pro = PRO_COPY; o.epi = EPI_RESIDUAL;
         o.w = L.o.ptr; o.x = m->c_attn; o.x_phase = attn_at; o.y = m->c_hidden; o.res_phase = hidden_at;
-        o.ready = a.heads_done; o.nready = L.kv_heads;
+        o.ready = a.heads_done; o.nready = L.kv_heads * L.step_head_groups;
         o.scale = d.residual_scale;
         prog.push_back(o);
         hidden_at = last();
@@ -768,12 +769,13 @@ int setup_persistent(mr_model *m) {
     m->part_cell_count = 0;
     for (Layer &L : m->layers) {
         L.step_splits = step_attention_splits(L.capacity, L.kv_heads, d.head_dim, m->grid);
+        L.step_head_groups = step_attention_head_groups(d.query_heads, L.kv_heads, L.step_splits, m->grid);
         m->part_cell_count = std::max(m->part_cell_count, (size_t)d.query_heads * L.step_splits * (d.head_dim + 2));
     }
     MR_TRY(device_alloc(m, m->part_cell_count * sizeof(uint64_t), (void **)&m->part_cells));
     MR_HIP(hipMemset(m->part_cells, 0, m->part_cell_count * sizeof(uint64_t)), "clear attention cells");
-    int max_kvh = 1;
-    for (Layer &L : m->layers) max_kvh = std::max(max_kvh, L.kv_heads);
+    int max_kvh = 1;   // counters per layer: one per (KV head, query-head group)
+    for (Layer &L : m->layers) max_kvh = std::max(max_kvh, L.kv_heads * L.step_head_groups);
     m->merge_count_n = (size_t)d.layers * max_kvh;
     MR_TRY(device_alloc(m, m->merge_count_n * sizeof(unsigned), (void **)&m->merge_counts));
     MR_HIP(hipMemset(m->merge_counts, 0, m->merge_count_n * sizeof(unsigned)), "clear attention counters");

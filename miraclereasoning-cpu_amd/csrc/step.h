@@ -80,6 +80,9 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
 // Attention splits per KV head in the step kernel: enough units that each
 // covers its keys in one round of its waves' loads, at most cus / kv_heads.
 int step_attention_splits(int max_total, int kv_heads, int dim, int cus);
+// Groups the query heads of a KV head are split into (AttnStepArgs::head_groups)
+// so that the (KV head, group, split) units fill up to `cus` workgroups.
+int step_attention_head_groups(int heads, int kv_heads, int splits, int cus);
 // The kernel is instantiated per (weight dtype of every GEMV phase, head dim).
 int step_blocks_per_cu(size_t lds, int dtype, int dim, int *blocks);
 int launch_step(hipStream_t s, const StepArgs &a, int grid, size_t lds, int dtype, int dim);

@@ -141,6 +141,32 @@ def test_workload_geometry_matches_oracle(backend, name, prompt, mode):
     assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
+# flashnano-1.7 geometries whose persistent step runs several key splits per
+# head and splits the query heads of a KV head over units (4 per local KV head,
+# 2 per global one); the D=128 one also deals those units XCD by XCD.
+SPLIT_MID = {"family": "flashnano-1.7", "vocab_size": 1000, "hidden_size": 1024, "layers": 4, "query_heads": 8,
+             "kv_heads": 2, "global_kv_heads": 4, "head_dim": 128, "ffn_dim": 1024, "max_positions": 1024,
+             "window": 256, "global_layers": [2, 4], "rope_theta": 500000.0, "backend_format": 1}
+
+
+@pytest.mark.parametrize("dim,prompt", [(128, 300), (32, 600)])
+def test_persistent_split_units_match_oracle(backend, dim, prompt):
+    """Persistent step kernel with up to 10 active key splits and query-head
+    groups per KV head (prompts past the local ring): logits of every prompt
+    position and a greedy stream against the oracle."""
+    config = SPLIT_MID if dim == 128 else dict(SPLIT_MID, hidden_size=256, head_dim=32, ffn_dim=512, window=512)
+    weights = synthetic.synthetic_weights(config, 31, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], prompt, 31)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=1024)
+    want = ref.prefill(ids, return_all=True)
+    print("case split units", dim, prompt, flush=True)
+    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=1024)
+    assert model.engine.step_mode() == "persistent"
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
+    assert model.generate(list(ids), max_new_tokens=6) == ref.generate(list(ids), max_new_tokens=6)
+
+
 def test_persistent_decode_equals_prefill(backend):
     """The exact-mode invariant (decode == prefill, bit for bit) on the
     persistent path, which reduces across workgroups in a fixed order."""
