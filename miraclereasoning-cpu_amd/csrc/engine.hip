@@ -500,6 +500,14 @@ int record_light_layer(mr_model *m, Layer &L) {
     gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.x = m->xnorm; gu.n = d.ffn_dim; gu.k = h; gu.y = m->act;
     gu.done = m->done_dev;
     const bool ffn_early = fused && light_ffn_in_row_kernel(a, gu, L.ffn.gate.dtype);
+    GemvArgs dn;   // the FFN branch's down projection
+    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.done = m->done_dev;
+    // With gate/up in the fused row kernel, the down rows ride in the attention
+    // split kernel (the FFN branch into branch_f) and the O projection's
+    // epilogue adds the gated residual; else down's epilogue adds it.
+    GemvArgs dn_early = dn;
+    dn_early.y = m->branch_f;
+    const bool down_early = ffn_early && light_down_in_attend(a, dn_early, L.ffn.down.dtype);
     GemvArgs u;   // [Wk; Wv] . new latent row
     u.w = L.kv_up.ptr; u.x = m->lat_new; u.n = 2 * kvw; u.k = d.latent_dim; u.y = m->kvbuf; u.done = m->done_dev;
     if (fused) {
@@ -517,12 +525,17 @@ int record_light_layer(mr_model *m, Layer &L) {
         MR_TRY(launch_light_store_kv(s, a, true));
     }
     GemvArgs o;
-    o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.y = m->branch_o; o.done = m->done_dev;
+    o.w = L.o.ptr; o.x = m->attn; o.n = h; o.k = qd; o.done = m->done_dev;
+    if (down_early) {   // hidden += rs * ((0 + ag * O(attn)) + fg * f)
+        o.y = m->hidden; o.aux = m->branch_f; o.scale = d.residual_scale; o.scale_ptr = L.attention_gate.f();
+        o.scale_ptr2 = L.ffn_gate.f();
+        return launch_gemv(s, L.o.dtype, PRO_COPY, EPI_GATED_ATTN, o);
+    }
+    o.y = m->branch_o;
     MR_TRY(launch_gemv(s, L.o.dtype, PRO_COPY, EPI_STORE, o));
     if (!ffn_early) MR_TRY(launch_gemv(s, L.ffn.gate.dtype, PRO_COPY, EPI_SWIGLU, gu));
-    GemvArgs dn;   // hidden += rs * ((0 + ag * o) + fg * down(act)) in the down projection's epilogue
-    dn.w = L.ffn.down.ptr; dn.x = m->act; dn.n = h; dn.k = d.ffn_dim; dn.y = m->hidden; dn.done = m->done_dev;
-    dn.scale = d.residual_scale; dn.aux = m->branch_o; dn.scale_ptr = L.attention_gate.f();
+    // hidden += rs * ((0 + ag * o) + fg * down(act)) in the down projection's epilogue
+    dn.y = m->hidden; dn.scale = d.residual_scale; dn.aux = m->branch_o; dn.scale_ptr = L.attention_gate.f();
     dn.scale_ptr2 = L.ffn_gate.f();
     return launch_gemv(s, L.ffn.down.dtype, PRO_COPY, EPI_GATED, dn);
 }

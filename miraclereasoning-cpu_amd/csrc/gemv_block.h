@@ -135,6 +135,9 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int row, float acc
     } else if constexpr (EPI == EPI_GATED) {
         const float branch = (0.0f + (*a.scale_ptr) * a.aux[row]) + (*a.scale_ptr2) * acc;
         a.y[row] = a.y[row] + a.scale * branch;
+    } else if constexpr (EPI == EPI_GATED_ATTN) {
+        const float branch = (0.0f + (*a.scale_ptr) * acc) + (*a.scale_ptr2) * a.aux[row];
+        a.y[row] = a.y[row] + a.scale * branch;
     } else {
         // SwiGLU (kernels.cl:46-50): (g / (1 + exp(-g))) * u
         a.y[row] = (acc / (1.0f + expf(-acc))) * acc2;

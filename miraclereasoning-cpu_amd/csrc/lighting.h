@@ -41,6 +41,11 @@ struct LightArgs {
     // row kernel, as a GEMV launch's workgroups would run them; 0 = apart.
     GemvArgs ffn;
     int ffn_blocks = 0, ffn_lpr = 0;
+    // The FFN branch's down projection (EPI_STORE into its own vector) in
+    // down_blocks more workgroups of the attention split kernel: its input is
+    // ready once the fused row kernel has run the gate/up rows; 0 = apart.
+    GemvArgs down;
+    int down_blocks = 0, down_lpr = 0, down_dtype = MR_BF16;
     int heads = 0, kv_heads = 0, d = 0, latent = 0, window = 0, memory_slots = 0, cap = 0;
 };
 
@@ -68,6 +73,9 @@ bool light_kv_fused(int dtype, int latent, int d);
 // kernel (kv weights of kv_dtype); sets ffn, ffn_blocks and ffn_lpr of a.
 bool light_ffn_in_row_kernel(LightArgs &a, const GemvArgs &g, int dtype);
 int launch_light_kv(hipStream_t s, const LightArgs &a);
+// Whether the down GEMV g (weights of dtype, EPI_STORE) can ride in the
+// attention split kernel; sets down, down_blocks and down_lpr of a.
+bool light_down_in_attend(LightArgs &a, const GemvArgs &g, int dtype);
 // Attention over every row, then compaction (which leaves the merged row in
 // lat_new and clears skip_merged when a merge happened).
 int launch_light_attend(hipStream_t s, const LightArgs &a);

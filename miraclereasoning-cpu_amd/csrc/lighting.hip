@@ -325,12 +325,26 @@ __global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
     compact_state(a);
 }
 
+// Rows per lane group and weight vectors per lane per batch of the down
+// projection rows hosted below (a GEMV launch's choice for long rows).
+constexpr int kDownRows = 2, kDownVec = 6;
+
 // Split-key form of the same attention for head dims 32/64/128: workgroup
 // (split s, head h) scores rows [64 s, 64 s + 64) of the memory with the
 // latent mask (kernels.cl:86-91: non-memory rows older than the window) and
 // writes its partial; a second kernel merges the splits of each head.
-template <int D>
+// grid (splits, heads + extra): the workgroups of the extra rows run the
+// hosted down projection's GEMV blocks (workgroup (x, heads + e) is block
+// e * splits + x) with weights of dtype DT.
+template <int D, int DT>
 __global__ void __launch_bounds__(split::kThreads) k_light_attend_part(LightArgs a) {
+    if ((int)blockIdx.y >= a.heads) {
+        const int b = ((int)blockIdx.y - a.heads) * (int)gridDim.x + (int)blockIdx.x;
+        extern __shared__ float sm[];
+        if (b < a.down_blocks)
+            gemv::gemv_vec_block<DT, kDownRows, kDownVec, PRO_COPY, EPI_STORE>(a.down, a.down_lpr, b, sm);
+        return;
+    }
     if (a.done && *a.done) return;
     const LightState st = *a.st;
     const int n = st.rows + 1;                  // with this step's row
@@ -397,6 +411,22 @@ bool light_kv_fused(int dtype, int latent, int d) {
     return fits && d % 2 == 0;
 }
 
+bool light_down_in_attend(LightArgs &a, const GemvArgs &g, int dtype) {
+    a.down_blocks = 0;
+    const int e = dtype == MR_F32 ? 4 : 8, bytes = dtype == MR_F32 ? 4 : 2;
+    if (!light_split_path(a.d, a.cap) || !a.part || g.k % e || (uintptr_t)g.w % 16 ||
+        ((int64_t)g.k * bytes) % 16)
+        return false;
+    const int nvec = g.k / e;
+    int lpr = 1;
+    while (lpr * 2 <= nvec && lpr < kWave) lpr *= 2;
+    a.down = g;
+    a.down_dtype = dtype;
+    a.down_lpr = lpr;
+    a.down_blocks = ceil_div(g.n, gemv::kGemvWaves * (kWave / lpr) * kDownRows);
+    return true;
+}
+
 bool light_ffn_in_row_kernel(LightArgs &a, const GemvArgs &g, int dtype) {
     a.ffn_blocks = 0;
     const int e = dtype == MR_F32 ? 4 : 8, bytes = dtype == MR_F32 ? 4 : 2;
@@ -424,23 +454,32 @@ int launch_light_kv(hipStream_t s, const LightArgs &a) {
     return MR_OK;
 }
 
+template <int D>
+static void attend_part_launch(hipStream_t s, dim3 grid, size_t lds, const LightArgs &a) {
+    if (a.down_blocks && a.down_dtype == MR_F32) k_light_attend_part<D, MR_F32><<<grid, split::kThreads, lds, s>>>(a);
+    else if (a.down_blocks && a.down_dtype == MR_F16) k_light_attend_part<D, MR_F16><<<grid, split::kThreads, lds, s>>>(a);
+    else k_light_attend_part<D, MR_BF16><<<grid, split::kThreads, lds, s>>>(a);
+}
+
 int launch_light_attend(hipStream_t s, const LightArgs &a) {
     if (light_split_path(a.d, a.cap) && a.part) {
         const int splits = light_splits(a.cap);
-        const dim3 grid(splits, a.heads);
+        const dim3 grid(splits, a.heads + ceil_div(a.down_blocks, splits));
+        const size_t lds = a.down_blocks ? (size_t)gemv::gemv_lds_floats(a.down, PRO_COPY) * sizeof(float) : 0;
+        MR_REQUIRE(lds <= 64 * 1024, "latent attention: hosted down projection exceeds shared memory");
         switch (a.d) {
             case 128:
-                k_light_attend_part<128><<<grid, split::kThreads, 0, s>>>(a);
+                attend_part_launch<128>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
                 k_light_attend_merge<128><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
             case 64:
-                k_light_attend_part<64><<<grid, split::kThreads, 0, s>>>(a);
+                attend_part_launch<64>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
                 k_light_attend_merge<64><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;
             default:
-                k_light_attend_part<32><<<grid, split::kThreads, 0, s>>>(a);
+                attend_part_launch<32>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
                 k_light_attend_merge<32><<<a.heads, split::kThreads, 0, s>>>(a, splits);
                 break;

@@ -75,6 +75,7 @@ int launch_gemv_dt(hipStream_t s, int pro, int epi, const GemvArgs &a) {
             case EPI_SWIGLU: return launch_gemv_t<DT, PRO_COPY, EPI_SWIGLU>(s, a);
             case EPI_SCALE_ADD: return launch_gemv_t<DT, PRO_COPY, EPI_SCALE_ADD>(s, a);
             case EPI_GATED: return launch_gemv_t<DT, PRO_COPY, EPI_GATED>(s, a);
+            case EPI_GATED_ATTN: return launch_gemv_t<DT, PRO_COPY, EPI_GATED_ATTN>(s, a);
         }
     } else {
         switch (epi) {
