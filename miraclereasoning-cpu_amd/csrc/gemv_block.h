@@ -11,6 +11,8 @@
 // shuffles.
 #pragma once
 
+#include <type_traits>
+
 #include "linear.h"
 
 namespace mr {
@@ -74,7 +76,11 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, float *xs, float *red
     float *gs = xs + gemv_xs_floats(a.k);   // PRO_RMS with a gain: the gain (red follows it)
     float ss = 0.0f;
     const bool vec = (a.k & 3) == 0 && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)gain & 15) == 0;
-    if (vec) {
+    // One loop per gain case: a load guarded by a runtime test inside the
+    // batch makes the compiler wait for each load in turn (measured: the RMS
+    // prologue took 8.6 µs of a 2304 x 2048 GEMV instead of 4.6).
+    auto batches = [&](auto with_gain) {
+        constexpr bool G = decltype(with_gain)::value;
         const int n4 = a.k / 4;
         for (int base = tid; base < n4; base += kGemvThreads * kStageBatch) {
             float4 xv[kStageBatch], gv[kStageBatch];
@@ -82,14 +88,14 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, float *xs, float *red
             for (int i = 0; i < kStageBatch; ++i) {   // clamped, unguarded: the loads issue together
                 const int j = min(base + i * kGemvThreads, n4 - 1);
                 xv[i] = *(const float4 *)(a.x + 4 * j);
-                if (gain) gv[i] = *(const float4 *)(gain + 4 * j);
+                if constexpr (G) gv[i] = *(const float4 *)(gain + 4 * j);
             }
 #pragma unroll
             for (int i = 0; i < kStageBatch; ++i) {
                 const int j = base + i * kGemvThreads;
                 if (j < n4) {
                     *(float4 *)(xs + 4 * j) = xv[i];
-                    if (gain) *(float4 *)(gs + 4 * j) = gv[i];
+                    if constexpr (G) *(float4 *)(gs + 4 * j) = gv[i];
                     ss = fmaf(xv[i].x, xv[i].x, ss);
                     ss = fmaf(xv[i].y, xv[i].y, ss);
                     ss = fmaf(xv[i].z, xv[i].z, ss);
@@ -97,6 +103,10 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, float *xs, float *red
                 }
             }
         }
+    };
+    if (vec) {
+        if (gain) batches(std::true_type{});
+        else batches(std::false_type{});
     } else {
         for (int j = tid; j < a.k; j += blockDim.x) {
             const float v = a.x[j];
