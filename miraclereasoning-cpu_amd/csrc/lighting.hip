@@ -326,8 +326,9 @@ __global__ void __launch_bounds__(64) k_light_compact(LightArgs a) {
 }
 
 // Rows per lane group and weight vectors per lane per batch of the down
-// projection rows hosted below (a GEMV launch's choice for long rows).
-constexpr int kDownRows = 2, kDownVec = 6;
+// projection rows hosted below (one row per lane group: twice the
+// workgroups of two, measured 3.7 % faster per step at 2048 x 5632).
+constexpr int kDownRows = 1, kDownVec = 6;
 
 // Split-key form of the same attention for head dims 32/64/128: workgroup
 // (split s, head h) scores rows [64 s, 64 s + 64) of the memory with the
