@@ -368,17 +368,18 @@ __global__ void __launch_bounds__(split::kThreads) k_light_attend_part(LightArgs
                       a.part + ((int64_t)h * gridDim.x + blockIdx.x) * (D + 2));
 }
 
-// grid heads, split::kThreads: every split's partial (empty ones included),
-// then workgroup 0 compacts the memory (its rows were all read by the split
-// kernel before this launch).
+// grid heads + 1, split::kThreads: workgroup h < heads merges every split's
+// partial of head h (empty ones included); the last workgroup compacts the
+// memory beside them (its rows were all read by the split kernel before this
+// launch, and the merges read only partials).
 template <int D>
 __global__ void __launch_bounds__(split::kThreads) k_light_attend_merge(LightArgs a, int splits) {
     if (a.done && *a.done) return;
-    split::merge<D>(a.part + (int64_t)blockIdx.x * splits * (D + 2), splits, -1, a.out + (int64_t)blockIdx.x * D);
-    if (blockIdx.x == 0) {
-        __syncthreads();
+    if ((int)blockIdx.x == a.heads) {
         compact_state(a);
+        return;
     }
+    split::merge<D>(a.part + (int64_t)blockIdx.x * splits * (D + 2), splits, -1, a.out + (int64_t)blockIdx.x * D);
 }
 
 __global__ void k_light_residual(float *hidden, const float *o, const float *f, const float *ag, const float *fg,
@@ -472,17 +473,17 @@ int launch_light_attend(hipStream_t s, const LightArgs &a) {
             case 128:
                 attend_part_launch<128>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<128><<<a.heads, split::kThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<128><<<a.heads + 1, split::kThreads, 0, s>>>(a, splits);
                 break;
             case 64:
                 attend_part_launch<64>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<64><<<a.heads, split::kThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<64><<<a.heads + 1, split::kThreads, 0, s>>>(a, splits);
                 break;
             default:
                 attend_part_launch<32>(s, grid, lds, a);
                 MR_LAUNCHED("enqueue latent attention splits");
-                k_light_attend_merge<32><<<a.heads, split::kThreads, 0, s>>>(a, splits);
+                k_light_attend_merge<32><<<a.heads + 1, split::kThreads, 0, s>>>(a, splits);
                 break;
         }
         MR_LAUNCHED("enqueue latent attention merge and compaction");
