@@ -118,6 +118,11 @@ __device__ __forceinline__ void partial(const float *q_head, int t0, int t1, Row
 // (each D + 2 floats apart) into out[0 .. D).  The split weights e^(m_s - M) go
 // to LDS; lane quads cover D/4 float4 columns and kThreads / (D/4) split
 // groups stride the partials, folded through LDS at the end.
+// The first kPre column groups of each thread are loaded together with the
+// maxima (clamped, so the loads issue at once), which saves the second round
+// trip for up to kPre * G partials.
+constexpr int kPre = 12;
+
 template <int D>
 __device__ __forceinline__ void merge(const float *part, int n, int extra, float *out) {
     constexpr int Q = D / 4, G = kThreads / Q;
@@ -125,6 +130,16 @@ __device__ __forceinline__ void merge(const float *part, int n, int extra, float
     __shared__ float4 fold[G][Q];
     __shared__ float lsum[G];
     const int tid = threadIdx.x, total = n + (extra >= 0 ? 1 : 0);
+    const int g = tid / Q, c = tid % Q;
+    float4 pv[kPre];
+    float pl[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int s = max(0, min(g + i * G, total - 1));
+        const float *ps = part + (int64_t)(s < n ? s : extra) * (D + 2);
+        pv[i] = make_float4(ps[2 + 4 * c], ps[3 + 4 * c], ps[4 + 4 * c], ps[5 + 4 * c]);
+        pl[i] = ps[1];
+    }
     float mx = -INFINITY;
     for (int s = tid; s < total; s += kThreads) {
         const float ms = part[(int64_t)(s < n ? s : extra) * (D + 2)];
@@ -134,11 +149,22 @@ __device__ __forceinline__ void merge(const float *part, int n, int extra, float
     const float M = block_max(mx, red);
     for (int s = tid; s < total; s += kThreads) e[s] = e[s] == -INFINITY ? 0.0f : __expf(e[s] - M);
     __syncthreads();
-    const int g = tid / Q, c = tid % Q;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     float l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int s = g + i * G;
+        if (s < total) {
+            const float w = e[s];
+            if (c == 0) l = fmaf(pl[i], w, l);
+            o.x = fmaf(pv[i].x, w, o.x);
+            o.y = fmaf(pv[i].y, w, o.y);
+            o.z = fmaf(pv[i].z, w, o.z);
+            o.w = fmaf(pv[i].w, w, o.w);
+        }
+    }
 #pragma unroll 4
-    for (int s = g; s < total; s += G) {
+    for (int s = g + kPre * G; s < total; s += G) {
         const float w = e[s];
         const float *ps = part + (int64_t)(s < n ? s : extra) * (D + 2);
         const float4 v = make_float4(ps[2 + 4 * c], ps[3 + 4 * c], ps[4 + 4 * c], ps[5 + 4 * c]);
