@@ -38,7 +38,7 @@ struct AttnStepArgs {
     int heads = 0, kv_heads = 0, dim = 0;
     float *part = nullptr;             // [kv_heads, splits, G, dim + 2]
     uint64_t *part_cells = nullptr;    // persistent kernel: the partials as cells [kv_heads, splits, G, dim + 2]
-    unsigned *counters = nullptr;      // [kv_heads], zero between launches
+    unsigned *counters = nullptr;      // [kv_heads * head_groups]: zero between op-level launches; the step kernel's only grow
     float *out = nullptr;              // [heads*dim]
     int splits = 0, split_len = 0;
     // Query heads of a KV head split over this many units of each key range

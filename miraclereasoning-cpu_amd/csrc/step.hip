@@ -13,10 +13,11 @@
 // weights are in flight while the previous phase finishes elsewhere.
 //
 // No grid barriers: activations travel as flag-in-data cells (ll.h), and a
-// workgroup waits only for the cells it reads.  The split merge of a KV head is
-// done by the last of its attention units to finish (a counter per layer and
-// head), and the step's closing work (greedy choice, position) by the last
-// workgroup to leave the launch.  Every wait is bounded (ll.h).
+// workgroup waits only for the cells it reads.  The split merge of a group of
+// query heads is done by its split-0 unit, which polls the other splits'
+// partial cells (by the last unit to count itself when units outnumber the
+// workgroups), and the step's closing work (greedy choice, position) by the
+// last workgroup to leave the launch.  Every wait is bounded (ll.h).
 //
 // Reuse of a cell buffer within a step is ordered by the data dependencies
 // themselves: a phase that rewrites a buffer consumes, directly or through the
