@@ -58,9 +58,23 @@ class OracleModel:
     ``weights`` maps canonical names to FP32 arrays or BF16 bit arrays (uint16).
     ``trace`` (optional list) receives per-step routing and block-selection
     records for parity checks of discrete decisions.
+
+    ``follow`` (optional): another implementation's record of its heavy-medium
+    choices, int32 [positions, layers, inner loops, record] with a record of
+    (width, the experts in chosen order, -1 past the width, then per query head
+    its chosen blocks ascending, -1 padded).  Two exact FP32 evaluations of the
+    same formulas in different summation orders differ in the last bits, so a
+    choice between values that close can come out either way.  Where the
+    recorded choice differs from the oracle's own, the oracle checks it against
+    its own values: if it is a valid choice within ``NEAR_TIE`` (relative to
+    the compared values) the oracle adopts it, so both continue on the same
+    path, and logs the event in ``adopted``; otherwise it keeps its own choice
+    and logs the event in ``mismatches``.
     """
 
-    def __init__(self, config, weights, context_length=None, trace=None):
+    NEAR_TIE = 1e-4
+
+    def __init__(self, config, weights, context_length=None, trace=None, follow=None):
         cfg = config if isinstance(config, OracleConfig) else OracleConfig.from_bundle(config)
         self.cfg = cfg
         self.ctx = context_length if context_length is not None else min(2048, cfg.max_positions)
@@ -75,6 +89,9 @@ class OracleModel:
             self.w[name] = _widen(a) if len(shape) == 1 else a
         self.freq = inverse_frequencies(cfg)
         self.trace = trace
+        self.follow = follow
+        self.adopted, self.mismatches = [], []
+        self._loop = 0
         self.reset()
 
     # ---------------------------------------------------------------- helpers
@@ -209,10 +226,20 @@ class OracleModel:
         s[:, length:] -= slope * np.log1p((self.position - ends).astype(np.float32))
         keep = min(lc["global_slots"], blocks)
         order = np.argsort(-s[:, length:], axis=1, kind="stable")
-        for h in range(H):
-            s[h, length + order[h, keep:]] = -np.inf
         if self.trace is not None:
-            self.trace.append(("blocks", layer, self.position, [sorted(order[h, :keep].tolist()) for h in range(H)]))
+            # margin: smallest score gap across the slot boundary over the heads
+            # (inf when every block is kept, so there is no choice to flip)
+            ranked = np.take_along_axis(s[:, length:], order, axis=1)
+            margin = float((ranked[:, keep - 1] - ranked[:, keep]).min()) if blocks > keep else math.inf
+            self.trace.append(("blocks", layer, self.position, [sorted(order[h, :keep].tolist()) for h in range(H)],
+                               margin))
+        kept = [order[h, :keep] for h in range(H)]
+        if self.follow is not None and blocks > keep:
+            self._follow_blocks(layer, s[:, length:], kept, blocks)
+        for h in range(H):
+            drop = np.ones(blocks, bool)
+            drop[kept[h]] = False
+            s[h, length + np.flatnonzero(drop)] = -np.inf
         attended = K.mix(K.softmax(s), ring.v, mv, H, kvh, d, ring.capacity, start, length, blocks)
         return K.linear(attended, self.w[p + "o"])
 
@@ -236,16 +263,81 @@ class OracleModel:
         spread = np.rint((np.float32(1) - confidence) * np.float32(2)
                          + entropy / max(np.float32(np.log(E)), np.float32(1)))
         active = int(np.clip(kmin + spread, kmin, kmax))
+        own, own_active = chosen[:active].tolist(), active
+        if self.follow is not None:
+            raw = float((np.float32(1) - confidence) * np.float32(2) + entropy / max(np.float32(np.log(E)),
+                                                                                   np.float32(1)))
+            chosen, active = self._follow_experts(layer, probs, chosen, active, raw)
+            weights = probs[chosen].copy()
         weights[active:] = 0
         weights /= max(weights.sum(), np.float32(1e-9))
         if self.trace is not None:
-            self.trace.append(("experts", layer, self.position, chosen[:active].tolist(), active))
+            # margins: the smallest probability gap between neighbours among the
+            # top kmax + 1 (the chosen order and the cut), and how far the
+            # adaptive width's value lies from a rounding boundary
+            ranked = probs[np.argsort(-probs, kind="stable")[:kmax + 1]]
+            order_gap = float(np.min(ranked[:-1] - ranked[1:])) if ranked.size > 1 else math.inf
+            raw = float((np.float32(1) - confidence) * np.float32(2) + entropy / max(np.float32(np.log(E)),
+                                                                                   np.float32(1)))
+            width_gap = abs(raw - math.floor(raw) - 0.5) if kmin < kmax else math.inf
+            self.trace.append(("experts", layer, self.position, own, own_active, order_gap, width_gap))
         out = np.zeros_like(x)
         for e, wgt in zip(chosen[:active], weights[:active]):
             out = K.axpy(out, self._mlp(x, p + f"experts.{e}."), float(wgt))
         for e in range(s["shared_experts"]):
             out = K.axpy(out, self._mlp(x, p + f"shared.{e}."), c.residual_scale / max(s["shared_experts"], 1))
         return out
+
+    def _follow_blocks(self, layer, scores, kept, blocks):
+        """Adopt the followed per-head block sets that are valid within NEAR_TIE."""
+        c = self.cfg
+        kmax, slots = c.source["router_top_k_max"], c.source["long_context"]["global_slots"]
+        rec = self.follow[self.position, layer, self._loop]
+        for h in range(len(kept)):
+            dev = rec[1 + kmax + h * slots: 1 + kmax + (h + 1) * slots]
+            dev = np.sort(dev[dev >= 0]).astype(np.int64)
+            if np.array_equal(dev, np.sort(kept[h])):
+                continue
+            event = ("blocks", layer, self.position, self._loop, h)
+            if dev.size != kept[h].size or dev.size == 0 or dev[-1] >= blocks or np.unique(dev).size != dev.size:
+                self.mismatches.append(event + (math.nan,))
+                continue
+            rest = np.setdiff1d(np.arange(blocks), dev)
+            inside, outside = float(scores[h, dev].min()), float(scores[h, rest].max())
+            gap = inside - outside            # < 0: the followed set ranks a lower score above a higher one
+            if gap >= -self.NEAR_TIE * max(1.0, abs(outside)):
+                kept[h] = dev
+                self.adopted.append(event + (gap,))
+            else:
+                self.mismatches.append(event + (gap,))
+
+    def _follow_experts(self, layer, probs, chosen, active, raw):
+        """The followed routing (chosen order and width) if valid within
+        NEAR_TIE, else the oracle's own; returns (chosen[:kmax], width)."""
+        s = self.cfg.source
+        kmin, kmax, E = s["router_top_k_min"], s["router_top_k_max"], s["routed_experts"]
+        rec = self.follow[self.position, layer, self._loop]
+        width = int(rec[0])
+        dev = rec[1:1 + width].astype(np.int64) if kmin <= width <= kmax else np.zeros(0, np.int64)
+        if width == active and np.array_equal(dev, chosen[:active]):
+            return chosen, active
+        event = ("experts", layer, self.position, self._loop)
+        if dev.size == 0 or dev.min() < 0 or dev.max() >= E or np.unique(dev).size != dev.size:
+            self.mismatches.append(event + (math.nan,))
+            return chosen, active
+        tol = self.NEAR_TIE * float(probs.max())
+        pd = probs[dev]
+        gap = float(np.min(pd[:-1] - pd[1:])) if dev.size > 1 else math.inf   # the chosen order
+        rest = np.setdiff1d(np.arange(E), dev)
+        if rest.size:
+            gap = min(gap, float(pd[-1] - probs[rest].max()))                  # the cut
+        width_ok = width == active or abs(raw - math.floor(raw) - 0.5) <= self.NEAR_TIE * max(1.0, abs(raw))
+        if gap >= -tol and width_ok:
+            tail = [e for e in np.argsort(-probs, kind="stable") if e not in set(dev.tolist())]
+            self.adopted.append(event + (gap,))
+            return np.concatenate([dev, np.asarray(tail, np.int64)])[:kmax], width
+        self.mismatches.append(event + (gap,))
+        return chosen, active
 
     # --------------------------------------------------------------- one token
     def step(self, token):
@@ -259,7 +351,7 @@ class OracleModel:
             if c.family == "heavy-medium-2.0":
                 loops = state.setdefault("loops", [dict() for _ in range(c.inner_loop_steps)])
                 scale = rs / math.sqrt(c.inner_loop_steps)
-                for inner in loops:
+                for self._loop, inner in enumerate(loops):
                     hidden = K.axpy(hidden, self._heavy_attention(self._rms(hidden, p + "a_norm"), layer, inner, pos),
                                     scale)
                     hidden = K.axpy(hidden, self._moe(self._rms(hidden, p + "f_norm"), layer), scale)

@@ -1,0 +1,151 @@
+"""The measured workload geometries on the GPU against the oracle, at prompt
+lengths that exercise what the short-prompt tests cannot reach.
+
+* flashnano-1.7 over 1100 tokens: the 1024-key local rings wrap, and the
+  persistent step merges many active key splits per KV head (global layers
+  about 18); both step modes.
+* flashnano-1.5 mid over 600 tokens: its 512-key local rings wrap.
+* heavy-medium-2.0 at its full geometry (64 experts in 8 groups, top-6 + 2
+  shared, blocks of 64 with top-8, head dim 128) over 640 tokens: the 512-row
+  window overflows and top-8 of 10 blocks is a real choice.  Every expert id
+  (in chosen order) and every chosen block bit-exact, except near-ties within
+  the oracle's relative 1e-4 band, which are counted and printed.
+* flashlighting-2.0 at its full geometry (head dim 128, latent 256, 16 KV
+  heads, YaRN) over 128 tokens, and the same geometry with a window of 150
+  rows and 8 memory slots over 230 tokens, so the split latent attention masks,
+  merges and compacts across several splits.
+
+Tolerances: rtol 1e-3 / atol 1e-4 on the logits of every prompt position
+(BF16 weights, FP32 arithmetic in a different summation order than the
+oracle's), greedy streams identical, discrete choices bit-exact up to
+near-ties (see the heavy test).  The smallest
+decision margin the oracle saw (router probability gap around the top-k cut
+and inside the chosen order; block-score gap at the slot cut) is printed and
+recorded as a test property, so a near-tie is visible whenever a choice is
+compared.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from miracle_hip import MiracleModel, ModelConfig, presets, synthetic
+from oracle.model import OracleModel
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+TOL = dict(rtol=1e-3, atol=1e-4)
+
+
+def _bits(weights):
+    return {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()}
+
+
+def _oracle_run(config, weights, ids, context, trace=None, follow=None):
+    """Oracle logits of every prompt position and the 6-token greedy stream
+    that continues from the prompt (generate's rule: argmax, stop at EOS)."""
+    ref = OracleModel(config, _bits(weights), context_length=context, trace=trace, follow=follow)
+    parts = []
+    for begin in range(0, len(ids), 128):      # the token loop in pieces, with progress lines
+        parts.append(ref.prefill(ids[begin:begin + 128], return_all=True))
+        print(f"oracle {begin + len(parts[-1])}/{len(ids)} tokens", flush=True)
+    logits = np.concatenate(parts)
+    eos, stream, last = ref.cfg.eos_token_id, [], logits[-1]
+    for i in range(6):
+        tok = int(np.argmax(last))
+        stream.append(tok)
+        if tok == eos or i == 5:
+            break
+        last = ref.decode(tok)
+    return (logits, stream) if follow is None else (logits, stream, ref)
+
+
+_CACHE = {}
+
+
+def _workload(name, prompt):
+    key = (name, prompt)
+    if key not in _CACHE:
+        wl = presets.workload(name)
+        weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+        ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
+        logits, stream = _oracle_run(wl["config"], weights, ids, wl["context"])
+        _CACHE.clear()
+        _CACHE[key] = (wl, weights, ids, logits, stream)
+    return _CACHE[key]
+
+
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("name,prompt", [("flashnano-1.7", 1100), ("flashnano-1.5-mid", 600)])
+def test_long_prompt_matches_oracle(backend, name, prompt, mode):
+    wl, weights, ids, want, stream = _workload(name, prompt)
+    print("case", name, prompt, mode, flush=True)
+    model = MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"])
+    model.engine.set_step_mode(mode)
+    assert model.engine.step_mode() == mode
+    got = model.prefill(ids, return_all=True)
+    np.testing.assert_allclose(got, want, **TOL)
+    assert model.generate(list(ids), max_new_tokens=6) == stream
+
+
+def test_heavy_workload_matches_oracle(backend, record_property):
+    """The device runs first and records its choices; the oracle then follows
+    them wherever they agree with its own values to within its near-tie band
+    (a relative 1e-4: two exact FP32 evaluations in different summation orders
+    can rank values that close either way) and logs every other disagreement
+    as a mismatch.  No mismatch is allowed; each adopted near-tie is printed
+    with its gap, together with the smallest decision margins the oracle saw."""
+    from test_oracle_model import follow_record
+    name, prompt = "heavy-medium-2.0", 640
+    wl = presets.workload(name)
+    cfg = ModelConfig.from_dict(wl["config"])
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    ids = synthetic.prompt_ids(cfg.vocab_size, prompt, wl["seed"])
+    model = MiracleModel(cfg, weights, backend=backend, context_length=wl["context"])
+    got = model.prefill(ids, return_all=True)
+    stream = model.generate(list(ids), max_new_tokens=6)
+    choices = model.engine.choices()
+    assert choices.shape[:3] == (prompt + len(stream) - 1, cfg.layers, cfg.inner_loop_steps)
+    model.close()
+
+    trace = []
+    want, want_stream, ref = _oracle_run(wl["config"], weights, ids, wl["context"], trace, follow=choices)
+    blocks = [r for r in trace if r[0] == "blocks"]
+    experts = [r for r in trace if r[0] == "experts"]
+    real = [r[4] for r in blocks if math.isfinite(r[4])]
+    block_margin, router_margin = min(real), min(r[5] for r in experts)
+    print(f"case {name} {prompt}: {len(blocks)} block choices ({len(real)} with more blocks than slots), smallest "
+          f"block-score gap {block_margin:.3e}; {len(experts)} routings, smallest probability gap "
+          f"{router_margin:.3e}; near-ties adopted {ref.adopted}; mismatches {ref.mismatches}", flush=True)
+    record_property("block_score_margin", block_margin)
+    record_property("router_probability_margin", router_margin)
+    record_property("near_ties_adopted", len(ref.adopted))
+    assert ref.mismatches == []
+    assert len(ref.adopted) <= 4, ref.adopted    # rare, or the two paths are not the same arithmetic
+    # where nothing was adopted, the device's record is the oracle's own choice
+    own = follow_record(trace, cfg, prompt + len(want_stream) - 1)
+    differ = {(int(p), int(l), int(i)) for p, l, i in zip(*np.nonzero((own != choices).any(axis=3)))}
+    assert differ == {(a[2], a[1], a[3]) for a in ref.adopted}
+    np.testing.assert_allclose(got, want, **TOL)
+    assert stream == want_stream
+
+
+LIGHT_SPLIT = dict(presets.workload("flashlighting-2.0")["config"], layers=2, window=150, memory_slots=8,
+                   max_positions=4096)
+
+
+@pytest.mark.parametrize("variant", ["workload", "window150"])
+def test_lighting_workload_matches_oracle(backend, variant):
+    if variant == "workload":
+        wl = presets.workload("flashlighting-2.0")
+        config, seed, prompt, context = wl["config"], wl["seed"], 128, wl["context"]
+        weights = synthetic.synthetic_weights(config, seed, wl["dtype"])
+    else:
+        config, seed, prompt, context = LIGHT_SPLIT, 29, 230, 256
+        weights = synthetic.synthetic_weights(config, seed, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], prompt, seed)
+    want, stream = _oracle_run(config, weights, ids, context)
+    print("case flashlighting-2.0", variant, prompt, flush=True)
+    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=context)
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, **TOL)
+    assert model.generate(list(ids), max_new_tokens=6) == stream

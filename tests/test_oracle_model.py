@@ -156,3 +156,104 @@ def test_native_configs_parse_like_reference(golden_dir):
         got = ModelConfig.from_dict(case["input"]).to_dict()
         got["global_layers"] = list(got["global_layers"])
         assert json.loads(json.dumps(got)) == case["parsed"], name
+
+
+# A heavy-medium-2.0 geometry with a real block choice (7 blocks, 3 kept) and
+# adaptive width 2..4 over 16 experts.
+_FOLLOW = {"family": "heavy-medium-2.0", "vocab_size": 64, "hidden_size": 32, "layers": 2, "query_heads": 4,
+           "kv_heads": 2, "head_dim": 8, "ffn_dim": 16, "max_positions": 64, "window": 8, "latent_dim": 8,
+           "inner_loop_steps": 2, "rope_theta": 1000000.0,
+           "source": {"routed_experts": 16, "router_groups": 4, "router_top_k_max": 4, "router_top_k_min": 2,
+                      "shared_experts": 1, "router_temperature": 1.0,
+                      "long_context": {"global_block_size": 4, "global_slots": 3, "rope_local_fraction": 0.6,
+                                       "alibi_slope_scale": 0.015}},
+           "backend_format": 1}
+
+
+def follow_record(trace, cfg, positions):
+    """The oracle's own choices in the device's record layout
+    (mr_model_choices): width, experts in chosen order, blocks per head."""
+    s = cfg.source
+    kmax, slots = s["router_top_k_max"], s["long_context"]["global_slots"]
+    rec = np.full((positions, cfg.layers, cfg.inner_loop_steps, 1 + kmax + cfg.query_heads * slots), -1, np.int32)
+    blocks = [r for r in trace if r[0] == "blocks"]
+    experts = [r for r in trace if r[0] == "experts"]
+    i = 0
+    for pos in range(positions):
+        for layer in range(cfg.layers):
+            for loop in range(cfg.inner_loop_steps):
+                b, e = blocks[i], experts[i]
+                assert (b[1], b[2], e[1], e[2]) == (layer, pos, layer, pos)
+                r = rec[pos, layer, loop]
+                r[0] = e[4]
+                r[1:1 + e[4]] = e[3]
+                for h, chosen in enumerate(b[3]):
+                    r[1 + kmax + h * slots: 1 + kmax + h * slots + len(chosen)] = chosen
+                i += 1
+    return rec
+
+
+def _follow_setup():
+    weights = synthetic.synthetic_weights(_FOLLOW, 5, "bf16")
+    weights = {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()}
+    ids = synthetic.prompt_ids(64, 40, 5)
+    trace = []
+    base = OracleModel(_FOLLOW, weights, context_length=64, trace=trace)
+    logits = base.prefill(ids, return_all=True)
+    return weights, ids, logits, trace, base.cfg
+
+
+def test_oracle_follow_own_choices_changes_nothing():
+    weights, ids, logits, trace, cfg = _follow_setup()
+    rec = follow_record(trace, cfg, len(ids))
+    assert (rec[:, :, :, 1 + 4:] >= 0).sum() > 0
+    model = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
+    np.testing.assert_array_equal(model.prefill(ids, return_all=True), logits)
+    assert model.adopted == [] and model.mismatches == []
+
+
+def test_oracle_follow_rejects_a_wrong_choice_and_adopts_a_near_tie():
+    weights, ids, logits, trace, cfg = _follow_setup()
+    rec = follow_record(trace, cfg, len(ids))
+    # an expert outside the top-k at position 20, layer 1, loop 0 (a planted wrong routing)
+    r = rec[20, 1, 0]
+    experts = [r for r in trace if r[0] == "experts" and r[1] == 1 and r[2] == 20][0]
+    outsider = next(e for e in range(16) if e not in experts[3])
+    r[1] = outsider
+    wrong = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
+    np.testing.assert_array_equal(wrong.prefill(ids, return_all=True), logits)   # keeps its own choice
+    assert [m[:4] for m in wrong.mismatches] == [("experts", 1, 20, 0)] and wrong.adopted == []
+    # a swapped pair of blocks for one head (a planted wrong block choice)
+    rec = follow_record(trace, cfg, len(ids))
+    b = rec[30, 0, 1, 1 + 4: 1 + 4 + 3]
+    blocks_now = -(-31 // 4)
+    b[0] = next(x for x in range(blocks_now) if x not in b)
+    wrong = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
+    wrong.prefill(ids, return_all=True)
+    assert [m[:5] for m in wrong.mismatches] == [("blocks", 0, 30, 1, 0)]
+    # with a tolerance wide enough to call it a near-tie, the same choice is adopted
+    loose = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
+    loose.NEAR_TIE = 1e3
+    out = loose.prefill(ids, return_all=True)
+    assert [a[:5] for a in loose.adopted] == [("blocks", 0, 30, 1, 0)] and loose.mismatches == []
+    assert loose.adopted[0][5] < 0
+    np.testing.assert_array_equal(out[:30], logits[:30])
+    assert not np.array_equal(out[30:], logits[30:])
+
+
+def test_oracle_follow_adopts_expert_order_and_traces_its_own():
+    weights, ids, logits, trace, cfg = _follow_setup()
+    rec = follow_record(trace, cfg, len(ids))
+    r = rec[25, 0, 1]
+    assert r[0] >= 2
+    r[1], r[2] = r[2], r[1]                        # the two most probable experts swapped
+    loose_trace = []
+    loose = OracleModel(_FOLLOW, weights, context_length=64, follow=rec, trace=loose_trace)
+    loose.NEAR_TIE = 1e3
+    loose.prefill(ids, return_all=True)
+    assert [a[:4] for a in loose.adopted] == [("experts", 0, 25, 1)] and loose.mismatches == []
+    assert follow_record(loose_trace, cfg, len(ids))[25, 0, 1].tolist() == \
+        follow_record(trace, cfg, len(ids))[25, 0, 1].tolist()
+    strict = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
+    np.testing.assert_array_equal(strict.prefill(ids, return_all=True), logits)
+    assert [m[:4] for m in strict.mismatches] == [("experts", 0, 25, 1)]
