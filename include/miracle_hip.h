@@ -36,7 +36,8 @@ enum {
     MR_ERR_NOMEM = 3,       /* allocation failed or above the device limit              */
     MR_ERR_STATE = 4,       /* model not finalized / weights missing                    */
     MR_ERR_NONFINITE = 5,   /* non-finite logits during device-side greedy generation   */
-    MR_ERR_INJECTED = 6     /* failure injected by mr_debug_fail_next (tests only)      */
+    MR_ERR_INJECTED = 6,    /* failure injected by mr_debug_fail_next (tests only)      */
+    MR_ERR_TIMEOUT = 7      /* a persistent step's wait for another workgroup timed out */
 };
 
 /* Storage dtype of a weight tensor.  BF16/F16 stay in their stored bits in HBM
@@ -68,6 +69,9 @@ MR_API int mr_device_get_info(int device, mr_device_info *out);
  *      opencl.py:136-176, 302-303) ------------------------------------- */
 typedef struct mr_ctx mr_ctx;
 MR_API int mr_ctx_create(int device, mr_ctx **out);
+/* Drops the caller's reference.  Each model created on the context holds one
+ * more, so the stream and the context's blocks are released when the last of
+ * the context and its models is destroyed, in whichever order they go. */
 MR_API int mr_ctx_destroy(mr_ctx *ctx);
 MR_API int mr_sync(mr_ctx *ctx);
 
@@ -198,22 +202,21 @@ MR_API int mr_model_forward(mr_model *model, const int32_t *ids, int n, int flag
  * logits were not all finite (tokens before it are still written). */
 MR_API int mr_model_generate_greedy(mr_model *model, int max_new, int eos, int32_t *tokens, int *produced);
 
-/* How a token step runs.  MR_STEP_PERSISTENT (default): one cooperative
- * kernel per step walks the whole layer stack (used when every phase fits it;
- * otherwise the model runs MR_STEP_GRAPH).  MR_STEP_GRAPH: five fused kernels
- * per layer, replayed from a captured hipGraph.  MR_STEP_EAGER: the same
- * kernels launched one by one (for profilers). */
+/* How a token step runs.  MR_STEP_PERSISTENT (default): one kernel launch per
+ * step walks the whole layer stack, one workgroup per CU (used when every
+ * phase fits it; otherwise the model runs MR_STEP_GRAPH).  Its workgroups wait
+ * on each other's results, so they must all be resident at once: a plain
+ * launch whose grid equals the CU count and whose registers fill a CU places
+ * one on every CU when the GPU is otherwise idle.  If other work holds CUs and
+ * a wait times out, the step fails with MR_ERR_TIMEOUT and the model switches to
+ * MR_STEP_GRAPH at the next mr_model_reset (mr_model_get_step_mode reports it).
+ * MR_STEP_GRAPH: five fused kernels per layer, replayed from a captured
+ * hipGraph.  MR_STEP_EAGER: the same kernels launched one by one (for
+ * profilers). */
 enum { MR_STEP_PERSISTENT = 0, MR_STEP_GRAPH = 1, MR_STEP_EAGER = 2 };
 MR_API int mr_model_set_step_mode(mr_model *model, int mode);
 /* The mode steps actually run in (a persistent request may fall back). */
 MR_API int mr_model_get_step_mode(mr_model *model, int *mode);
-/* Phase timeline of the persistent step kernel (diagnostics; no counterpart in
- * the reference).  Runs one greedy decode step at the current position with
- * timestamps (100 MHz device wall clock) written per phase and workgroup:
- * out[(phase * grid + wg) * 3 + {0: phase start, 1: barrier arrival,
- * 2: barrier release}].  `capacity` is the number of uint64 in `out`;
- * *phases and *grid receive the program size.  The step advances the sequence
- * like any decode step. */
 /* Routing decisions of every position so far (heavy-medium-2.0): per position,
  * layer and inner loop one record of 1 + router_top_k_max + query_heads *
  * global_slots ints: the adaptive width, the chosen experts in descending
@@ -224,6 +227,13 @@ MR_API int mr_model_get_step_mode(mr_model *model, int *mode);
  * position. */
 MR_API int mr_model_choices(mr_model *model, int32_t *out, int64_t capacity, int *per_position);
 
+/* Phase timeline of the persistent step kernel (diagnostics; no counterpart in
+ * the reference).  Runs one greedy decode step at the current position with
+ * timestamps (100 MHz device wall clock) written per phase and workgroup:
+ * out[(phase * grid + wg) * 3 + {0: phase start, 1: inputs ready,
+ * 2: phase exit}].  `capacity` is the number of uint64 in `out`;
+ * *phases and *grid receive the program size.  The step advances the sequence
+ * like any decode step. */
 MR_API int mr_model_trace_step(mr_model *model, uint64_t *out, int64_t capacity, int *phases, int *grid);
 
 /* Device milliseconds of the last mr_model_generate_greedy call (HIP events
@@ -246,6 +256,13 @@ MR_API int mr_model_time_kernel(mr_model *model, int which, int reps, float *avg
  * MR_ERR_INJECTED (the reference's failed-device-operation path,
  * model.py:298-311).  Not a counterpart of any reference function. */
 MR_API int mr_debug_fail_next(mr_ctx *ctx);
+
+/* Test hook: the status check after the model's next persistent step reports
+ * MR_ERR_TIMEOUT as if a wait had given up (the host-side half of the
+ * timeout path: the error, the poisoned model, the switch to MR_STEP_GRAPH at
+ * reset).  No kernel is made to wait.  Not a counterpart of any reference
+ * function. */
+MR_API int mr_debug_step_timeout(mr_model *model);
 
 #ifdef __cplusplus
 }

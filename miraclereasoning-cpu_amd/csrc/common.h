@@ -49,12 +49,18 @@ struct mr_ctx {
     // size -> free device blocks (all blocks of one size class)
     std::unordered_map<size_t, std::vector<void *>> free_blocks;
     std::unordered_map<void *, size_t> live;   // block -> size class
+    // The caller's reference plus one per live model; the stream and the
+    // blocks are released when the last one goes (mr_ctx_destroy and
+    // mr_model_destroy may then come in either order).
+    int refs = 1;
 };
 
 namespace mr {
 
 int ctx_alloc(mr_ctx *ctx, size_t bytes, void **ptr);
 void ctx_release(mr_ctx *ctx, void *ptr);
+void ctx_retain(mr_ctx *ctx);
+void ctx_unref(mr_ctx *ctx);
 
 // ---------------------------------------------------------------- device helpers
 constexpr int kWave = 64;

@@ -114,6 +114,8 @@ struct mr_model {
     int xbuf = 0;                        // floats of one GEMV input staging buffer
     void *dummy = nullptr;               // 16 zero bytes for loads past a matrix's end
     int *err = nullptr;                  // wait timeout flag
+    bool timed_out = false;              // a persistent step timed out: graph mode from the next reset
+    bool inject_timeout = false;         // test hook: report the next step status as timed out
     float *best_val = nullptr;
     int *best_idx = nullptr, *bad = nullptr;
     float last_ms = 0.0f;                // device time of the last greedy loop

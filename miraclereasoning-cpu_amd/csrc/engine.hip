@@ -640,12 +640,23 @@ int check_ctx(mr_model *m, const char *what) {
     return MR_OK;
 }
 
-// A persistent step whose wait timed out leaves err set; report it.
+// A persistent step whose wait timed out leaves err set; report it.  The
+// kernel's workgroups wait on each other, so they must all be resident at
+// once: a timeout means some never started while the others waited (other
+// work held CUs).  The model then runs in graph mode from its next reset.
 int check_step_error(mr_model *m) {
     if (!m->persistent_ok) return MR_OK;
     int err = 0;
     MR_HIP(hipMemcpy(&err, m->err, sizeof(int), hipMemcpyDeviceToHost), "read step status");
-    if (err) return fail(MR_ERR_HIP, "persistent step kernel: a wait for another workgroup timed out");
+    if (m->inject_timeout && m->mode == MR_STEP_PERSISTENT) {
+        m->inject_timeout = false;
+        err = 1;
+    }
+    if (err) {
+        m->timed_out = true;
+        return fail(MR_ERR_TIMEOUT, "persistent step kernel: a wait for another workgroup timed out (its "
+                                    "workgroups were not all resident); the model runs in graph mode after reset");
+    }
     return MR_OK;
 }
 
@@ -948,8 +959,14 @@ int mr_model_create(mr_ctx *ctx, const mr_model_desc *desc, mr_model **out) {
             L.experts.resize(d.routed_experts);
             L.shared.resize(d.shared_experts);
         }
-        MR_REQUIRE(d.query_heads % L.kv_heads == 0, "query heads must divide into KV groups");
+        if (d.query_heads % L.kv_heads != 0) {
+            delete m;
+            return fail(MR_ERR_INVALID, "query heads must divide into KV groups");
+        }
     }
+    // The model keeps its context (device, stream) alive: destroying the
+    // context first only drops the caller's reference.
+    ctx_retain(ctx);
     *out = m;
     return MR_OK;
 }
@@ -985,7 +1002,9 @@ int mr_model_destroy(mr_model *m) {
     for (void *p : {(void *)m->prog_plain, (void *)m->prog_head, (void *)m->cells, (void *)m->sync, (void *)m->words, (void *)m->part_cells, (void *)m->merge_counts, m->dummy,
                     (void *)m->err, (void *)m->best_val, (void *)m->best_idx, (void *)m->bad})
         if (p) hipFree(p);
+    mr_ctx *ctx = m->ctx;
     delete m;
+    ctx_unref(ctx);
     return MR_OK;
 }
 
@@ -1258,6 +1277,10 @@ int mr_model_reset(mr_model *m) {
     }
     MR_HIP(hipStreamSynchronize(m->ctx->stream), "reset");
     m->position = 0;
+    if (m->timed_out) {   // persistent steps timed out: fall back to the per-layer kernels
+        m->timed_out = false;
+        if (m->mode == MR_STEP_PERSISTENT) m->mode = MR_STEP_GRAPH;
+    }
     return MR_OK;
 }
 
@@ -1278,6 +1301,12 @@ int mr_model_set_step_mode(mr_model *m, int mode) {
 int mr_model_get_step_mode(mr_model *m, int *mode) {
     MR_REQUIRE(m && mode, "get_step_mode: null argument");
     *mode = m->mode == MR_STEP_PERSISTENT && !m->persistent_ok ? MR_STEP_GRAPH : m->mode;
+    return MR_OK;
+}
+
+int mr_debug_step_timeout(mr_model *m) {
+    MR_REQUIRE(m, "debug_step_timeout: null model");
+    m->inject_timeout = true;
     return MR_OK;
 }
 

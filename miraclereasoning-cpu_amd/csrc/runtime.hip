@@ -1,4 +1,5 @@
 // Devices, contexts, errors and device memory (reference: opencl.py:14-217).
+#include <cstdio>
 #include <cstring>
 #include <string>
 
@@ -58,6 +59,19 @@ void ctx_release(mr_ctx *ctx, void *ptr) {
     ctx->live.erase(it);
 }
 
+void ctx_retain(mr_ctx *ctx) { ++ctx->refs; }
+
+void ctx_unref(mr_ctx *ctx) {
+    if (--ctx->refs > 0) return;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->free_blocks)
+        for (void *p : kv.second) hipFree(p);
+    for (auto &kv : ctx->live) hipFree(kv.first);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
 }  // namespace mr
 
 using namespace mr;
@@ -84,7 +98,9 @@ int mr_device_get_info(int device, mr_device_info *out) {
     hipDeviceProp_t p;
     MR_HIP(hipGetDeviceProperties(&p, device), "query device properties");
     std::memset(out, 0, sizeof(*out));
-    std::strncpy(out->name, p.name, sizeof(out->name) - 1);
+    // Some drivers leave the marketing name empty; name the device by its ISA then.
+    if (p.name[0]) std::strncpy(out->name, p.name, sizeof(out->name) - 1);
+    else std::snprintf(out->name, sizeof(out->name), "AMD GPU %.48s", p.gcnArchName);
     std::strncpy(out->arch, p.gcnArchName, sizeof(out->arch) - 1);
     out->memory_bytes = (int64_t)p.totalGlobalMem;
     // HIP has no per-allocation cap query; a single hipMalloc may use all free HBM.
@@ -124,13 +140,7 @@ int mr_ctx_create(int device, mr_ctx **out) {
 
 int mr_ctx_destroy(mr_ctx *ctx) {
     if (!ctx) return MR_OK;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
-    for (auto &kv : ctx->free_blocks)
-        for (void *p : kv.second) hipFree(p);
-    for (auto &kv : ctx->live) hipFree(kv.first);
-    hipStreamDestroy(ctx->stream);
-    delete ctx;
+    ctx_unref(ctx);
     return MR_OK;
 }
 

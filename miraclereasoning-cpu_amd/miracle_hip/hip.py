@@ -12,9 +12,11 @@ operation; there is no CPU fallback of any kind.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import math
 import os
+import weakref
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -28,6 +30,7 @@ _LIB_DEFAULT = Path(__file__).resolve().parent / "_lib" / "libmiracle_hip.so"
 MR_F32, MR_BF16, MR_F16 = 0, 1, 2
 _DTYPE_TAG = {"f32": MR_F32, "bf16": MR_BF16, "f16": MR_F16}
 MR_ERR_NONFINITE = 5
+MR_ERR_TIMEOUT = 7
 
 
 class HIPError(RuntimeError):
@@ -96,6 +99,7 @@ _SIGNATURES = {
     "mr_model_choices": [_P, _P, C.c_int64, C.POINTER(_i)],
     "mr_model_time_kernel": [_P, _i, _i, C.POINTER(C.c_float)],
     "mr_debug_fail_next": [_P],
+    "mr_debug_step_timeout": [_P],
 }
 
 _lib = None
@@ -122,6 +126,26 @@ def _load():
         lib.mr_last_error.argtypes, lib.mr_last_error.restype = [], C.c_char_p
         _lib = lib
     return _lib
+
+
+# Teardown order.  Models, then contexts, are released by one atexit hook,
+# which Python runs before it tears down modules and before the C runtime's
+# exit handlers (the HIP runtime's among them), so no HIP call is left to a
+# finalizer running during interpreter shutdown.  After the hook every
+# __del__ here does nothing.
+_backends = weakref.WeakSet()
+_shut_down = False
+
+
+def close_all():
+    """Release every live model and context now (also run at interpreter exit)."""
+    global _shut_down
+    for backend in list(_backends):
+        backend.close()
+    _shut_down = True
+
+
+atexit.register(close_all)
 
 
 def _check(code, operation):
@@ -178,7 +202,7 @@ class Tensor:
         return self.size * (4 if self.dtype == "f32" else 2)
 
     def __del__(self):
-        if getattr(self, "handle", None) and getattr(self.backend, "ctx", None):
+        if not _shut_down and getattr(self, "handle", None) and getattr(self.backend, "ctx", None):
             _load().mr_free(self.backend.ctx, self.handle)
             self.handle = None
 
@@ -206,11 +230,21 @@ class HIPBackend:
         _check(lib.mr_ctx_create(self.device.device_index, C.byref(ctx)), "create context")
         self.ctx = ctx
         self.lib = lib
+        self._engines = weakref.WeakSet()   # step-level models created on this context
+        _backends.add(self)
 
-    def __del__(self):
+    def close(self):
+        """Release the models made on this backend, then its stream and buffers.
+        Tensors of a closed backend are not freed again."""
+        for engine in list(getattr(self, "_engines", ())):
+            engine.close()
         if getattr(self, "ctx", None):
             _load().mr_ctx_destroy(self.ctx)
             self.ctx = None
+
+    def __del__(self):
+        if not _shut_down:
+            self.close()
 
     # ------------------------------------------------------------ memory
     def _owns(self, *tensors):

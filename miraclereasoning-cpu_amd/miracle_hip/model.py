@@ -16,8 +16,9 @@ from pathlib import Path
 import numpy as np
 
 from .config import ModelConfig
+from . import hip as _hip
 from .hip import HIPBackend, HIPError, MR_ERR_NONFINITE, ModelDesc, _check, _DTYPE_TAG
-from .weights import SafeTensors, adapt_weights, expected_shapes, storage_of
+from .weights import BF16Array, SafeTensors, adapt_weights, expected_shapes, storage_of
 
 FAMILY_CODE = {"flashnano-1.5": 0, "flashnano-1.6": 1, "flashnano-1.7": 2, "flashlite-2.0": 3,
                "flashlighting-2.0": 4, "heavy-medium-2.0": 5}
@@ -75,15 +76,36 @@ def model_desc(config, context_length):
         block_slope=long.get("alibi_slope_scale", 0.015) / math.sqrt(c.head_dim))
 
 
+class ResidentWeights:
+    """The ``weight_cache`` attribute of the reference's engine (WeightCache,
+    weights.py:258-297), for code that reads it.  The reference stages FP32
+    copies of weights through a cache of at most ``budget`` bytes; here every
+    weight is uploaded once, in its stored dtype, into the model's own HBM
+    buffers, so the cache holds nothing (``used`` is 0) and ``resident`` counts
+    the weight bytes in HBM.  The budget is validated as the reference does."""
+
+    def __init__(self, config, weights, budget_bytes):
+        if type(budget_bytes) is not int or budget_bytes < 4096:
+            raise ValueError("weight_cache_bytes must be an integer >= 4096")
+        self.budget, self.used, self.resident = budget_bytes, 0, 0
+        for name, shape in expected_shapes(config).items():
+            a = weights[name]
+            narrow = len(shape) == 2 and (isinstance(a, BF16Array) or getattr(a, "dtype", None) == np.float16)
+            self.resident += math.prod(shape) * (2 if narrow else 4)
+
+
 class Engine:
     """Owns one mr_model: weights in HBM, caches, step graphs."""
 
     def __init__(self, backend, config, weights, context_length):
         self.backend, self.lib, self.config = backend, backend.lib, config
+        if backend.ctx is None:
+            raise HIPError("create model failed: the backend is closed")
         handle = C.c_void_p()
         desc = model_desc(config, context_length)
         _check(self.lib.mr_model_create(backend.ctx, C.byref(desc), C.byref(handle)), "create model")
         self.handle = handle
+        backend._engines.add(self)
         for name, shape in expected_shapes(config).items():
             kind, layer, expert = weight_target(name)
             array, tag = storage_of(weights[name])
@@ -96,13 +118,22 @@ class Engine:
         _check(self.lib.mr_model_set_rope(handle, freq.ctypes.data, freq.size), "upload rope table")
         _check(self.lib.mr_model_finalize(handle), "finalize model")
 
-    def __del__(self):
+    def close(self):
+        """Free the model's device memory (weights, caches, graphs) now."""
         if getattr(self, "handle", None):
             self.lib.mr_model_destroy(self.handle)
             self.handle = None
 
+    def __del__(self):
+        if not _hip._shut_down:
+            self.close()
+
     def reset(self):
         _check(self.lib.mr_model_reset(self.handle), "reset")
+
+    def debug_step_timeout(self):
+        """Test hook: the next persistent step reports a wait timeout."""
+        _check(self.lib.mr_debug_step_timeout(self.handle), "arm step timeout")
 
     def forward(self, ids, flags, want_logits=True):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -199,18 +230,27 @@ class MiracleModel:
             context_length = min(2048, config.max_positions)
         if type(context_length) is not int or not 0 < context_length <= config.max_positions:
             raise ValueError(f"context_length must be in [1, {config.max_positions}]")
-        if type(weight_cache_bytes) is not int or weight_cache_bytes < 4096:
-            raise ValueError("weight_cache_bytes must be an integer >= 4096")
         if prefill_mode not in ("exact", "batched"):
             raise ValueError("prefill_mode must be 'exact' or 'batched'")
         # Validate the full checkpoint before any device allocation (model.py:50-51).
         self.weights = adapt_weights(config, weights)
         self.backend = backend if backend is not None else HIPBackend()
         self.context_length = context_length
+        self.weight_cache = ResidentWeights(config, self.weights, weight_cache_bytes)   # model.py:54
         self.weight_cache_bytes = weight_cache_bytes
         self.prefill_mode = prefill_mode
         self.engine = Engine(self.backend, config, self.weights, context_length)
         self.reset()
+
+    def close(self):
+        """Free this model's device memory now (it is also freed at exit)."""
+        self.engine.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     @classmethod
     def from_pretrained(cls, directory, *, family=None, **kwargs):

@@ -133,28 +133,52 @@ class ShardedSafeTensors(Mapping):
         return self.shards[self.names[key]][key]
 
 
-def save_safetensors(path, arrays):
-    """Write tensors as F32 safetensors, converting 16 MiB at a time
-    (format of weights.py:102-125)."""
-    header, cursor = {}, 0
-    for name, value in arrays.items():
-        nbytes = math.prod(value.shape) * 4
-        header[name] = {"dtype": "F32", "shape": list(value.shape), "data_offsets": [cursor, cursor + nbytes]}
-        cursor += nbytes
-    blob = json.dumps(header, separators=(",", ":")).encode()
-    blob += b" " * (-len(blob) % 8)
-    with Path(path).open("wb") as handle:
-        handle.write(struct.pack("<Q", len(blob)))
-        handle.write(blob)
-        for value in arrays.values():
-            if not value.shape:
-                handle.write(np.asarray(value, dtype="<f4").tobytes())
-                continue
-            row_bytes = max(math.prod(value.shape[1:]) * 4, 1)
-            step = max(1, (16 << 20) // row_bytes)
-            for begin in range(0, value.shape[0], step):
-                chunk = np.asarray(value[begin:begin + step], dtype="<f4", order="C")
-                handle.write(memoryview(chunk).cast("B"))
+def _stored(value):
+    """(safetensors dtype tag, storage view) of one tensor as this package
+    keeps it: BF16 bits stay BF16, float16 stays F16, the rest is FP32."""
+    if isinstance(value, BF16Array):
+        return "BF16", value.bits
+    if getattr(value, "dtype", None) == np.float16:
+        return "F16", value
+    return "F32", value
+
+
+def write_safetensors(path, tensors, *, widen=False):
+    """Write ``tensors`` (name -> array-like with ``.shape``) as one
+    safetensors file.
+
+    Each tensor keeps its stored dtype (BF16 bits, F16, else FP32) unless
+    ``widen`` asks for FP32 throughout, which is the reference's bundle format
+    (weights.py:102-125).  Values are converted and written about 16 MiB at a
+    time, so memory-mapped inputs are never materialised whole, and the file
+    appears under its name only once complete."""
+    plan, header, offset = [], {}, 0
+    for name, value in tensors.items():
+        tag, view = ("F32", value) if widen else _stored(value)
+        shape = tuple(int(n) for n in view.shape)
+        dtype = np.dtype(_STORAGE[tag])
+        size = math.prod(shape) * dtype.itemsize
+        header[name] = {"dtype": tag, "shape": list(shape), "data_offsets": [offset, offset + size]}
+        plan.append((view, shape, dtype))
+        offset += size
+    text = json.dumps(header, separators=(",", ":")).encode("utf-8")
+    text += b" " * (-(8 + len(text)) % 8)            # payload starts 8-byte aligned
+    path = Path(path)
+    partial = path.with_name(path.name + ".partial")
+    try:
+        with partial.open("wb") as out:
+            out.write(struct.pack("<Q", len(text)) + text)
+            for view, shape, dtype in plan:
+                if not shape:
+                    out.write(np.asarray(view, dtype=dtype).tobytes())
+                    continue
+                rows = max(1, (16 << 20) // max(1, math.prod(shape[1:]) * dtype.itemsize))
+                for r in range(0, shape[0], rows):
+                    out.write(np.ascontiguousarray(view[r:r + rows], dtype=dtype).tobytes())
+        partial.replace(path)
+    finally:
+        partial.unlink(missing_ok=True)
+    return path
 
 
 class AliasedWeights(Mapping):

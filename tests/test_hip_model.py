@@ -351,3 +351,68 @@ def test_lighting_general_paths_match_oracle(backend):
     model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=128)
     np.testing.assert_allclose(model.prefill(ids, return_all=True), want, rtol=1e-3, atol=1e-4)
     assert model.generate(list(ids), max_new_tokens=6) == ref.generate(list(ids), max_new_tokens=6)
+
+
+def test_step_timeout_falls_back_to_graph_mode(backend):
+    """A persistent step whose wait times out (reported from the host-side
+    status check, no kernel is made to wait) fails with a timeout error,
+    poisons the model until reset(), and the reset switches it to graph mode,
+    whose results are the same to the tolerance."""
+    from miracle_hip import HIPError
+    wl = presets.workload("flashnano-1.5-tiny")
+    cfg = ModelConfig.from_dict(wl["config"])
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    model = MiracleModel(cfg, weights, backend=backend, context_length=64)
+    assert model.engine.step_mode() == "persistent"
+    ids = [5, 9, 2, 7]
+    want = model.prefill(ids, return_all=True)
+    model.reset()
+    model.prefill(ids[:2])
+    model.engine.debug_step_timeout()
+    with pytest.raises(HIPError, match="timed out"):
+        model.decode(ids[2])
+    with pytest.raises(RuntimeError, match="reset"):
+        model.decode(ids[2])
+    model.reset()
+    assert model.engine.step_mode() == "graph"
+    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, atol=2e-5, rtol=2e-4)
+    model.close()
+
+
+def test_weight_cache_budget_and_untied_head(backend):
+    # reference tests/test_inference.py:72-84: a 4 KiB weight budget gives the
+    # same logits (here every weight is resident in HBM whatever the budget)
+    bundle = dict(presets.micro("flashnano-1.5"), tie_embeddings=False, vocab_size=161)
+    cfg = ModelConfig.from_dict(bundle)
+    weights = synthetic.micro_weights(bundle)
+    rng = np.random.default_rng(4)
+    weights["embed"] = rng.normal(0, .1, (161, 16)).astype(np.float32)
+    weights["output"] = rng.normal(0, .1, (161, 16)).astype(np.float32)
+    tiled = MiracleModel(cfg, weights, backend=backend, context_length=16, weight_cache_bytes=4096)
+    full = MiracleModel(cfg, weights, backend=backend, context_length=16)
+    np.testing.assert_array_equal(tiled.prefill([1, 5, 8]), full.prefill([1, 5, 8]))
+    assert tiled.weight_cache.used <= 4096 and tiled.weight_cache.budget == 4096
+    assert tiled.weight_cache.resident == sum(np.asarray(v).nbytes for v in weights.values())
+    with pytest.raises(ValueError, match="weight_cache_bytes"):
+        MiracleModel(cfg, weights, backend=backend, context_length=16, weight_cache_bytes=4095)
+
+
+def test_close_releases_models_before_their_backend():
+    """Models may outlive or be outlived by their backend in any order (the
+    library keeps a context alive while a model uses it), and closing twice
+    is harmless."""
+    from miracle_hip import HIPBackend
+    bundle = presets.micro("flashnano-1.7")
+    cfg = ModelConfig.from_dict(bundle)
+    weights = synthetic.micro_weights(bundle)
+    b1 = HIPBackend()
+    m1 = MiracleModel(cfg, weights, backend=b1, context_length=16)
+    want = m1.prefill([1, 2, 3])
+    b1.close()                       # the context goes first; m1 still holds it
+    b1.close()
+    m1.close()
+    m1.close()
+    b2 = HIPBackend()
+    with MiracleModel(cfg, weights, backend=b2, context_length=16) as m2:
+        np.testing.assert_array_equal(m2.prefill([1, 2, 3]), want)
+    b2.close()
