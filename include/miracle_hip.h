@@ -123,6 +123,19 @@ MR_API int mr_block_means(mr_ctx *ctx, const float *x, float *y, int length, int
 MR_API int mr_attention(mr_ctx *ctx, const float *q, const float *k, const float *v, const float *extra_k,
                  const float *extra_v, float *y, int heads, int kv_heads, int dim, int capacity, int start,
                  int length, int extra_length);
+/* No counterpart in the reference.  mr_attention for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation): same arguments, kernels and results, but the split
+ * partials and merge counters live in a static 8 MiB device array per GPU
+ * (held until the process ends) instead of a context allocation, and the
+ * counters are cleared by a kernel, not a memset.  A call needing more scratch
+ * than 8 MiB (kv_heads * splits * (heads / kv_heads) * (dim + 2) floats,
+ * splits <= 512 / kv_heads, plus kv_heads counters) fails with MR_ERR_INVALID.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other contexts, other threads) race. */
+MR_API int mr_attention_noalloc(mr_ctx *ctx, const float *q, const float *k, const float *v, const float *extra_k,
+                                const float *extra_v, float *y, int heads, int kv_heads, int dim, int capacity,
+                                int start, int length, int extra_length);
 
 /* ---- step-level engine: the whole of MiracleModel._step and the LM head
  *      (model.py:257-285, 303-308) for one sequence, device-resident. ------- */

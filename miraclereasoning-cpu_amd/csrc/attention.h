@@ -16,6 +16,10 @@ struct AttnProblem {
 };
 
 int launch_attention_op(mr_ctx *ctx, const AttnProblem &p);
+// Allocation-free variant: partials and counters in the device's static scratch.
+int launch_attention_op_noalloc(mr_ctx *ctx, const AttnProblem &p);
+int static_scratch_address(int device, void **out);
+size_t static_scratch_bytes();
 
 // Engine step: the kernel also RMS-normalizes (optional) and rotates the new
 // query heads and key, writes the new key/value into the ring slot of this

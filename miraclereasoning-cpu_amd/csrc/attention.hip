@@ -5,7 +5,19 @@
 // counter) merges that head's splits.  Head dims 32/64/128 take the tiled
 // unit; other head dims (micro models, op-level calls with dim 6) take a plain
 // per-element path.
+#include <mutex>
+#include <string>
+#include <vector>
+
 #include "attention_tile.h"
+
+// Scratch of the allocation-free entry point (mr_attention_noalloc): the split
+// partials and the per-KV-head merge counters of one call.  Each GPU holds its
+// own copy for the life of the process.  Host code never passes `scratch`
+// itself to a kernel (on the host the name is only a stand-in): it uses the
+// device address looked up once per device by mr::static_scratch_address().
+static constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 namespace mr {
 namespace {
@@ -175,6 +187,70 @@ int launch_attention_step(hipStream_t s, const AttnStepArgs &a) {
     ka.ring_k_ro = a.ring_k;
     ka.ring_v_ro = a.ring_v;
     return launch(s, ka);
+}
+
+namespace {
+
+std::mutex g_scratch_mutex;
+std::vector<void *> g_scratch_address;   // per device ordinal
+
+__global__ void k_zero_words(unsigned *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
+size_t static_scratch_bytes() { return kStaticScratchBytes; }
+
+// Called by mr_ctx_create with `device` current.
+int static_scratch_address(int device, void **out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_address.size() <= device) g_scratch_address.resize(device + 1, nullptr);
+    if (!g_scratch_address[device]) {
+        void *p = nullptr;
+        MR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)), "look up the static attention scratch");
+        g_scratch_address[device] = p;
+    }
+    *out = g_scratch_address[device];
+    return MR_OK;
+}
+
+// The same plan and kernels as launch_attention_op, with the partials and
+// counters in the device's static scratch: no allocation of any kind.  The
+// counters are cleared by a kernel (not a memset), so the call can be
+// captured in a graph.
+int launch_attention_op_noalloc(mr_ctx *ctx, const AttnProblem &p) {
+    MR_REQUIRE(ctx->scratch, "attention_noalloc: the context has no static scratch");
+    KernelArgs ka;
+    AttnStepArgs &a = ka.s;
+    a.q = p.q;
+    a.extra_k = p.extra_k;
+    a.extra_v = p.extra_v;
+    a.heads = p.heads;
+    a.kv_heads = p.kv_heads;
+    a.dim = p.dim;
+    a.capacity = p.capacity;
+    a.out = p.out;
+    attention_plan(p.length + p.extra_length, p.kv_heads, p.dim, 512, &a.splits, &a.split_len);
+    ka.mode = 0;
+    ka.start = p.start;
+    ka.length = p.length;
+    ka.extra_length = p.extra_length;
+    ka.ring_k_ro = p.ring_k;
+    ka.ring_v_ro = p.ring_v;
+    const size_t part = (attention_part_floats(p.heads, p.kv_heads, p.dim, a.splits) * sizeof(float) + 255) /
+                        256 * 256;
+    const size_t need = part + (size_t)p.kv_heads * sizeof(unsigned);
+    if (need > kStaticScratchBytes)
+        return fail(MR_ERR_INVALID, "attention_noalloc: needs " + std::to_string(need) +
+                                        " bytes of scratch, above its static " +
+                                        std::to_string(kStaticScratchBytes) + " (use mr_attention)");
+    a.part = (float *)ctx->scratch;
+    a.counters = (unsigned *)((char *)ctx->scratch + part);
+    k_zero_words<<<ceil_div(p.kv_heads, 256), 256, 0, ctx->stream>>>(a.counters, p.kv_heads);
+    MR_LAUNCHED("attention_noalloc: clear counters");
+    return launch(ctx->stream, ka);
 }
 
 int launch_attention_op(mr_ctx *ctx, const AttnProblem &p) {

@@ -53,6 +53,7 @@ struct mr_ctx {
     // blocks are released when the last one goes (mr_ctx_destroy and
     // mr_model_destroy may then come in either order).
     int refs = 1;
+    void *scratch = nullptr;   // this device's static attention scratch (device address)
 };
 
 namespace mr {

@@ -293,4 +293,20 @@ int mr_attention(mr_ctx *ctx, const float *q, const float *k, const float *v, co
     return launch_attention_op(ctx, pr);
 }
 
+int mr_attention_noalloc(mr_ctx *ctx, const float *q, const float *k, const float *v, const float *extra_k,
+                         const float *extra_v, float *y, int heads, int kv_heads, int dim, int capacity, int start,
+                         int length, int extra_length) {
+    OP_BEGIN("attention_noalloc");
+    (void)s;
+    MR_REQUIRE(q && k && v && y && heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && dim > 0 && capacity > 0 &&
+                   length >= 0 && extra_length >= 0 && length + extra_length > 0 &&
+                   (extra_length == 0 || (extra_k && extra_v)),
+               "attention_noalloc: bad arguments");
+    AttnProblem pr;
+    pr.q = q; pr.ring_k = k; pr.ring_v = v; pr.extra_k = extra_k; pr.extra_v = extra_v;
+    pr.heads = heads; pr.kv_heads = kv_heads; pr.dim = dim; pr.capacity = capacity;
+    pr.start = start; pr.length = length; pr.extra_length = extra_length; pr.out = y;
+    return launch_attention_op_noalloc(ctx, pr);
+}
+
 }  // extern "C"

@@ -3,6 +3,7 @@
 #include <cstring>
 #include <string>
 
+#include "attention.h"
 #include "common.h"
 
 namespace mr {
@@ -126,8 +127,11 @@ int mr_ctx_create(int device, mr_ctx **out) {
     if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(MR_ERR_INVALID, std::string("device ") + p.gcnArchName +
                                         " is not gfx950 (MI355X); this library carries gfx950 code only");
+    void *scratch = nullptr;
+    MR_TRY(static_scratch_address(device, &scratch));
     mr_ctx *ctx = new mr_ctx();
     ctx->device = device;
+    ctx->scratch = scratch;
     ctx->max_alloc = (int64_t)p.totalGlobalMem;
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {

@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mr_merge_rows": [_P, _P, _P, _i, _f, _f],
     "mr_block_means": [_P, _P, _P, _i, _i, _i],
     "mr_attention": [_P, _P, _P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i],
+    "mr_attention_noalloc": [_P, _P, _P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i],
     "mr_model_create": [_P, C.POINTER(ModelDesc), C.POINTER(_P)],
     "mr_model_destroy": [_P],
     "mr_model_set_weight": [_P, _i, _i, _i, _P, _i, C.c_int64, C.c_int64],
