@@ -209,8 +209,10 @@ def main():
     wl = presets.workload(name)
     cfg = ModelConfig.from_dict(wl["config"])
     gqa = cfg.family in ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
-    # batched prefill covers the GQA families without relay rows; the others take the token loop
-    prefill_mode = args.prefill_mode if cfg.family in ("flashnano-1.5", "flashnano-1.7", "flashlite-2.0") else "exact"
+    # batched prefill covers the GQA families without relay rows and heavy-medium-2.0; the others take the
+    # token loop
+    batched_families = ("flashnano-1.5", "flashnano-1.7", "flashlite-2.0", "heavy-medium-2.0", "flashlighting-2.0")
+    prefill_mode = args.prefill_mode if cfg.family in batched_families else "exact"
     prompt_len = args.prompt or wl["prompt"]
     if prompt_len + args.warmup + args.steps > wl["context"]:
         raise SystemExit("prompt + warmup + steps exceed the context")

@@ -27,11 +27,14 @@ bool is_gqa(int family) {
            family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
 }
 
-// Families whose prompt can run as whole-chunk kernels: attention state is the
-// ring alone (flashnano-1.6's relay rows, the latent memory and the heavy
-// caches change token by token and take the token loop).
+// Families whose prompt can run as whole-chunk kernels: the GQA families whose
+// attention state is the ring alone, heavy-medium-2.0, whose block sums and
+// block choices are rebuilt per row from a scan of the chunk, and
+// flashlighting-2.0, whose latent memory is planned per step (flashnano-1.6's
+// relay rows take the token loop).
 bool batched_prefill_family(int family) {
-    return family == MR_FAMILY_FLASHNANO_15 || family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
+    return family == MR_FAMILY_FLASHNANO_15 || family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20 ||
+           family == MR_FAMILY_HEAVY_MEDIUM_20 || family == MR_FAMILY_FLASHLIGHTING_20;
 }
 
 int dtype_bytes(int dt) { return dt == MR_F32 ? 4 : 2; }
@@ -1323,21 +1326,51 @@ __global__ void k_set_int(int *p, int v) { *p = v; }
 constexpr int kPrefillRows = 4096;   // prompt rows per batched prefill chunk
 
 // One chunk's activations (FP32, rows of the chunk): hidden, normalized input,
-// q|k|v, attended values, SwiGLU activations and, with return_all, logits.
+// q|k|v, attended values, SwiGLU activations and, with return_all, logits;
+// for heavy-medium-2.0 also the latent rows, the block scan, the block
+// partials, the router logits, the routing and the expert-major gather; for
+// flashlighting-2.0 the latent rows, logical row 0 of each step, its keys and
+// values and partials, both branches' outputs and the chunk's plan.
 struct PrefillWs {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *lg = nullptr;
+    float *lat = nullptr, *sums = nullptr, *ext = nullptr, *router = nullptr, *mw = nullptr, *xg = nullptr,
+          *y = nullptr;
+    int *ids = nullptr, *active = nullptr, *counts = nullptr, *offsets = nullptr, *fill = nullptr, *map = nullptr;
+    float *slot0 = nullptr, *slot0_final = nullptr, *kv0 = nullptr, *obuf = nullptr, *fbuf = nullptr,
+          *merge_count = nullptr;
+    int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
 };
 
 int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     const mr_model_desc &d = m->d;
+    const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20, light = d.family == MR_FAMILY_FLASHLIGHTING_20;
     int max_kvw = 0;
     for (const Layer &L : m->layers) max_kvw = std::max(max_kvw, L.kv_heads * d.head_dim);
-    const size_t r = (size_t)rows, qd = (size_t)d.query_heads * d.head_dim;
+    const size_t r = (size_t)rows, h = d.hidden_size, qd = (size_t)d.query_heads * d.head_dim, kvw = max_kvw;
+    const size_t slots = heavy ? (size_t)d.router_top_k_max + d.shared_experts : 1;
+    const size_t groups = heavy ? (size_t)d.routed_experts + d.shared_experts : 0;
+    const size_t kmax = heavy ? d.router_top_k_max : 0, lat = heavy || light ? d.latent_dim : 0;
+    const size_t ext = heavy || light ? r * d.query_heads * (d.head_dim + 4) : 0;
+    struct Piece { void **ptr; size_t floats; };
+    const Piece pieces[] = {
+        {(void **)&w->x, r * h}, {(void **)&w->xn, r * h}, {(void **)&w->qkv, r * (qd + 2 * kvw)},
+        {(void **)&w->att, r * qd}, {(void **)&w->act, r * slots * d.ffn_dim}, {(void **)&w->lg, all ? r * d.vocab_size : 0},
+        {(void **)&w->lat, r * lat}, {(void **)&w->ext, ext},
+        // heavy-medium-2.0
+        {(void **)&w->sums, heavy ? r * 2 * kvw : 0}, {(void **)&w->router, heavy ? r * (d.router_groups + groups) : 0},
+        {(void **)&w->mw, r * kmax}, {(void **)&w->xg, heavy ? r * slots * h : 0},
+        {(void **)&w->y, heavy ? r * slots * h : 0}, {(void **)&w->ids, r * kmax}, {(void **)&w->active, heavy ? r : 0},
+        {(void **)&w->counts, groups}, {(void **)&w->offsets, groups}, {(void **)&w->fill, groups},
+        {(void **)&w->map, r * kmax},
+        // flashlighting-2.0
+        {(void **)&w->slot0, light ? r * lat : 0}, {(void **)&w->slot0_final, light ? lat : 0},
+        {(void **)&w->kv0, light ? r * 2 * kvw : 0}, {(void **)&w->obuf, light ? r * h : 0},
+        {(void **)&w->fbuf, light ? r * h : 0}, {(void **)&w->merge_count, light ? r : 0},
+        {(void **)&w->flags, light ? r : 0}, {(void **)&w->extra_index, light ? r : 0},
+        {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
-    const size_t sizes[6] = {up(r * d.hidden_size), up(r * d.hidden_size), up(r * (qd + 2 * (size_t)max_kvw)),
-                             up(r * qd), up(r * d.ffn_dim), all ? up(r * d.vocab_size) : 0};
     size_t total = 0;
-    for (size_t z : sizes) total += z;
+    for (const Piece &pc : pieces) total += up(pc.floats);
     total *= sizeof(float);
     if (total > m->pf_bytes) {
         MR_HIP(hipStreamSynchronize(m->ctx->stream), "prefill workspace");
@@ -1348,26 +1381,317 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         m->pf_bytes = total;
     }
     float *p = (float *)m->pf;
-    float **slots[6] = {&w->x, &w->xn, &w->qkv, &w->att, &w->act, &w->lg};
-    for (int i = 0; i < 6; ++i) {
-        *slots[i] = sizes[i] ? p : nullptr;
-        p += sizes[i];
+    for (const Piece &pc : pieces) {
+        *pc.ptr = pc.floats ? (void *)p : nullptr;
+        p += up(pc.floats);
     }
     return MR_OK;
 }
 
-// Batched prefill of ids already in ids_dev[position .. position + n): every
-// layer runs once per chunk of up to kPrefillRows rows, projections as MFMA
-// GEMMs, attention over the chunk's keys plus the ring, then the chunk's last
-// min(rows, capacity) keys/values go into the ring.  Leaves the last row's
-// logits in m->logits (as the token loop does) and advances the position.
+// The latent-memory bookkeeping of positions p0 .. p0 + rows - 1, planned on
+// the host: the token step's compaction (k_light_compact) depends only on the
+// positions, so it is replayed here from position 0 with logical row 0 kept as
+// (position, count) and the original rows as a position range.  For each step
+// of the chunk: whether it sees logical row 0 as an extra row (a merged row,
+// or row 0 once the window has passed it) and at which position, whether a
+// merge follows it, with row 0's count and the folded row; then the state
+// after the chunk.
+struct LightPlan {
+    std::vector<int> flags, extra_index, merge_row, extra_pos;
+    std::vector<float> merge_count;
+    int extra = 0, window = 0, hole = 0, init_from_arena = 0, init_slot = 0;
+    LightState fin{};
+    int write_slot0 = 0;
+    float slot0_position = 0.0f, slot0_count = 1.0f;
+};
+
+void plan_light_chunk(const mr_model_desc &d, int cap, int p0, int rows, LightPlan &pl) {
+    const int W = d.window, M = d.memory_slots;
+    pl.window = M > 0 ? W + M : W;
+    pl.hole = M > 0 ? W : 0;
+    pl.flags.assign(rows, 0);
+    pl.extra_index.assign(rows, -1);
+    pl.merge_row.assign(rows, 0);
+    pl.merge_count.assign(rows, 0.0f);
+    LightState st{};   // as after a reset
+    int lo = 0;        // position of the oldest original row in the memory
+    bool merged = false;
+    float P0 = 0.0f, C0 = 1.0f;   // logical row 0 when merged
+    bool merged_in_chunk = false;
+    for (int p = 0; p < p0 + rows; ++p) {
+        const int t = p - p0;
+        if (t == 0) {
+            pl.init_from_arena = p0 > 0;
+            pl.init_slot = st.start;
+        }
+        if (t >= 0 && M > 0 && (merged || lo < p - pl.window + 1)) {
+            pl.flags[t] |= 1;
+            pl.extra_index[t] = pl.extra++;
+            pl.extra_pos.push_back(merged ? (int)P0 : lo);
+        }
+        const int n = st.rows + 1, overflow = std::max(0, n - W);
+        st.skip_merged = 1;
+        st.pending = 0;
+        if (M == 0 && overflow > 0) {
+            st.start = (st.start + overflow) % cap;
+            st.rows = n - overflow;
+            st.memory = 0;
+            lo += overflow;
+        } else if (overflow > M) {
+            float ca, pa;
+            if (merged) {
+                ca = C0;
+                pa = P0;
+            } else {
+                ca = 1.0f;
+                pa = (float)lo;
+                ++lo;
+            }
+            const float cb = 1.0f, pb = (float)lo;   // logical row 1, an original row
+            const float centre = (pa * ca + pb * cb) / (ca + cb);
+            if (t >= 0) {
+                pl.flags[t] |= 2;
+                pl.merge_count[t] = ca;
+                pl.merge_row[t] = lo;
+                merged_in_chunk = true;
+            }
+            ++lo;
+            P0 = rintf(centre);
+            C0 = ca + cb;
+            merged = true;
+            st.start = (st.start + 1) % cap;
+            st.memory = M;
+            st.skip_merged = 0;
+            st.pending = 1;
+            st.merged_slot = st.start;
+            st.merged_pos = (int)P0;
+        } else {
+            st.rows = n;
+            st.memory = overflow;
+        }
+    }
+    pl.fin = st;
+    pl.write_slot0 = merged && merged_in_chunk;
+    pl.slot0_position = P0;
+    pl.slot0_count = C0;
+}
+
+// One GQA layer over the chunk's rows (model.py:95-116, 264-266).
+int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim;
+    const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
+    MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    GemmArgs g;
+    g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
+    g.m = T; g.n = ld; g.k = h;
+    MR_TRY(launch_gemm(s, GEMM_STORE, g));
+    MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
+                          d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
+                          d.norm_eps, d.qk_norm, m->rope, d.split_half_rope));
+    PrefillAttnArgs a;
+    a.qkv = w.qkv; a.ld = ld; a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.cap = L.capacity;
+    a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
+    a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+    MR_TRY(launch_prefill_attention(s, a));
+    MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
+    GemmArgs o;
+    o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
+    o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale;
+    MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
+    MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
+    GemmArgs gu;
+    gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
+    gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
+    MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
+    GemmArgs dn;
+    dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;
+    dn.m = T; dn.n = h; dn.k = ffn; dn.scale = d.residual_scale;
+    return launch_gemm(s, GEMM_RESIDUAL, dn);
+}
+
+// One heavy-medium-2.0 layer over the chunk's rows: every inner-loop pass's
+// sparse attention and MoE (model.py:192-255, 259-263) with the token step's
+// per-position semantics.  Keys and values go to the pass's ring first; the
+// block scan gives every row its block sums as of its own position, so each
+// row scores and chooses blocks exactly as its token step would; the window
+// rows and the chosen blocks' partial meet in one softmax.  The experts run as
+// two grouped GEMMs over the rows routed to them.
+int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, int T) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, lat = d.latent_dim;
+    const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw, inner = d.inner_loop_steps;
+    const int blocks = ceil_div(d.context_length, d.global_block_size), kmax = d.router_top_k_max;
+    const int E = d.routed_experts, S = d.shared_experts, groups = E + S, R = d.router_groups + E;
+    for (int loop = 0; loop < inner; ++loop) {
+        float *ring_k = L.ring_k + (size_t)loop * d.context_length * kvw;
+        float *ring_v = L.ring_v + (size_t)loop * d.context_length * kvw;
+        float *bsum_k = L.bsum_k + (size_t)loop * blocks * kvw, *bsum_v = L.bsum_v + (size_t)loop * blocks * kvw;
+        int *choice = m->choices + ((size_t)li * inner + loop) * m->choice_rec;
+        const int choice_stride = d.layers * inner * m->choice_rec;
+        MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+        GemmArgs q;   // the Q rows of the packed [Wq; Wlatent]
+        q.a = w.xn; q.lda = h; q.w = L.qkv.ptr; q.dtype = L.qkv.dtype; q.c = w.qkv; q.ldc = ld;
+        q.m = T; q.n = qd; q.k = h;
+        MR_TRY(launch_gemm(s, GEMM_STORE, q));
+        GemmArgs lt = q;   // its latent rows
+        lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
+        lt.n = lat;
+        MR_TRY(launch_gemm(s, GEMM_STORE, lt));
+        GemmArgs kv;   // latent -> [K | V] beside the queries
+        kv.a = w.lat; kv.lda = lat; kv.w = L.kv_up.ptr; kv.dtype = L.kv_up.dtype; kv.c = w.qkv + qd; kv.ldc = ld;
+        kv.m = T; kv.n = 2 * kvw; kv.k = lat;
+        MR_TRY(launch_gemm(s, GEMM_STORE, kv));
+        MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd, nullptr, nullptr, 1e-6f, 1,
+                              m->rope, d.split_half_rope));
+        MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, ring_k, ring_v, d.context_length, p0, T));
+        HeavyScanArgs sc;
+        sc.ring_k = ring_k; sc.ring_v = ring_v; sc.bsum_k = bsum_k; sc.bsum_v = bsum_v; sc.sums = w.sums;
+        sc.p0 = p0; sc.rows = T; sc.kvw = kvw; sc.block = d.global_block_size;
+        MR_TRY(launch_heavy_scan(s, sc));
+        HeavySelectArgs se;
+        se.qkv = w.qkv; se.ld = ld; se.bsum_k = bsum_k; se.bsum_v = bsum_v; se.sums = w.sums; se.ext = w.ext;
+        se.choice = choice; se.choice_stride = choice_stride; se.choice_blocks = 1 + kmax;
+        se.p0 = p0; se.rows = T; se.heads = d.query_heads; se.kv_heads = L.kv_heads; se.d = hd;
+        se.block = d.global_block_size; se.slots = d.global_slots; se.context = d.context_length;
+        se.slope = d.block_slope;
+        MR_TRY(launch_heavy_select(s, se));
+        PrefillAttnArgs a;
+        a.qkv = w.qkv; a.ld = ld; a.ring_k = ring_k; a.ring_v = ring_v; a.cap = d.context_length;
+        a.window = d.window; a.ext = w.ext;
+        a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
+        a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+        MR_TRY(launch_prefill_attention(s, a));
+        GemmArgs o;   // hidden += step_scale * Wo . attended
+        o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
+        o.m = T; o.n = h; o.k = qd; o.scale = d.heavy_step_scale;
+        MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
+        MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
+        GemmArgs r;   // [Wcoarse; Wfine]
+        r.a = w.xn; r.lda = h; r.w = L.router.ptr; r.dtype = L.router.dtype; r.c = w.router; r.ldc = R;
+        r.m = T; r.n = R; r.k = h;
+        MR_TRY(launch_gemm(s, GEMM_STORE, r));
+        MoeRowsArgs mr_;
+        MoeArgs &e = mr_.a;
+        e.router = w.router;
+        e.coarse_bias = L.router_coarse_bias.f(); e.group_bias = L.group_bias.f();
+        e.fine_bias = L.router_fine_bias.f(); e.expert_bias = L.expert_bias.f();
+        e.x = w.xn; e.dtype = L.experts[0].gate.dtype;
+        e.ids = w.ids; e.weights = w.mw; e.active = w.active;
+        e.choice = choice; e.choice_stride = choice_stride;
+        e.experts = E; e.groups = d.router_groups; e.kmin = d.router_top_k_min; e.kmax = kmax;
+        e.shared = S; e.ffn = ffn; e.h = h;
+        e.inv_temperature_div = d.router_temperature;
+        e.log_experts = std::max((float)std::log((double)E), 1.0f);
+        e.shared_scale = d.heavy_shared_scale; e.scale = d.heavy_step_scale;
+        mr_.rows = T; mr_.p0 = p0;
+        mr_.counts = w.counts; mr_.offsets = w.offsets; mr_.fill = w.fill; mr_.map = w.map; mr_.xg = w.xg;
+        MR_TRY(launch_moe_route_rows(s, mr_));
+        GemmGroups gg;
+        gg.offset = w.offsets; gg.count = w.counts; gg.groups = groups; gg.max_rows = T;
+        gg.w = L.expert_tab; gg.w2 = L.expert_tab + groups;
+        GemmArgs gu;
+        gu.a = w.xg; gu.lda = h; gu.dtype = e.dtype; gu.c = w.act; gu.ldc = ffn; gu.n = ffn; gu.k = h;
+        MR_TRY(launch_gemm_grouped(s, GEMM_SWIGLU, gu, gg));
+        gg.w = L.expert_tab + 2 * groups;
+        gg.w2 = nullptr;
+        GemmArgs dn;
+        dn.a = w.act; dn.lda = ffn; dn.dtype = e.dtype; dn.c = w.y; dn.ldc = h; dn.n = h; dn.k = ffn;
+        MR_TRY(launch_gemm_grouped(s, GEMM_STORE, dn, gg));
+        MR_TRY(launch_moe_combine_rows(s, mr_, w.y, w.x));
+    }
+    return MR_OK;
+}
+
+// One flashlighting-2.0 layer over the chunk's rows (model.py:146-190,
+// 271-279).  The queries, the new latent rows and their keys and values come
+// from GEMMs; logical row 0 of every step that sees it as an extra row comes
+// from the merge recurrence, with its keys and values by a GEMM at its
+// planned positions; the attention is the windowed one over the original
+// rows (the ring caches for rows before the chunk) with the extra row's
+// partial; the FFN branch and the gated residual follow; last, the chunk's
+// rows and the planned state go to the token step's ring.
+int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan &pl, int p0, int T) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, lat = d.latent_dim;
+    const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
+    MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    GemmArgs q;   // the Q rows of the packed [Wq; Wlatent]
+    q.a = w.xn; q.lda = h; q.w = L.qkv.ptr; q.dtype = L.qkv.dtype; q.c = w.qkv; q.ldc = ld;
+    q.m = T; q.n = qd; q.k = h;
+    MR_TRY(launch_gemm(s, GEMM_STORE, q));
+    GemmArgs lt = q;   // its latent rows, then RMSNorm with latent_norm in place
+    lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
+    lt.n = lat;
+    MR_TRY(launch_gemm(s, GEMM_STORE, lt));
+    MR_TRY(launch_rms_rows(s, w.lat, lat, L.latent_norm.f(), d.norm_eps, lat, w.lat, lat, T));
+    GemmArgs kv;   // [Wk; Wv] . latent beside the queries
+    kv.a = w.lat; kv.lda = lat; kv.w = L.kv_up.ptr; kv.dtype = L.kv_up.dtype; kv.c = w.qkv + qd; kv.ldc = ld;
+    kv.m = T; kv.n = 2 * kvw; kv.k = lat;
+    MR_TRY(launch_gemm(s, GEMM_STORE, kv));
+    MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd, L.q_norm.f(), L.k_norm.f(), d.norm_eps,
+                          1, m->rope, d.split_half_rope));
+    LightRowsArgs r;
+    r.lat = w.lat; r.arena = L.arena; r.positions = L.positions; r.counts = L.counts;
+    r.slot0 = w.slot0; r.slot0_final = w.slot0_final; r.flags = w.flags; r.extra_index = w.extra_index;
+    r.merge_count = w.merge_count; r.merge_row = w.merge_row; r.init_from_arena = pl.init_from_arena;
+    r.init_slot = pl.init_slot; r.p0 = p0; r.rows = T; r.latent = lat; r.cap = L.light_cap;
+    if (d.memory_slots > 0) MR_TRY(launch_light_slot0(s, r));   // reads the ring before this chunk writes it
+    if (pl.extra > 0) {
+        GemmArgs k0 = kv;   // logical row 0's keys and values
+        k0.a = w.slot0; k0.c = w.kv0; k0.ldc = 2 * kvw; k0.m = pl.extra;
+        MR_TRY(launch_gemm(s, GEMM_STORE, k0));
+        MR_TRY(launch_k_rows_at(s, w.kv0, 2 * kvw, pl.extra, w.extra_pos, L.kv_heads, hd, L.k_norm.f(), d.norm_eps,
+                                m->rope, d.split_half_rope));
+        MR_TRY(launch_light_extra(s, w.qkv, ld, w.kv0, w.extra_index, w.ext, T, d.query_heads, L.kv_heads, hd));
+    }
+    PrefillAttnArgs a;
+    a.qkv = w.qkv; a.ld = ld; a.ring_k = L.kcache; a.ring_v = L.vcache; a.cap = L.light_cap;
+    a.window = pl.window; a.hole = pl.hole; a.ext = pl.extra > 0 ? w.ext : nullptr;
+    a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
+    a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+    MR_TRY(launch_prefill_attention(s, a));
+    GemmArgs o;
+    o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.obuf; o.ldc = h; o.m = T; o.n = h; o.k = qd;
+    MR_TRY(launch_gemm(s, GEMM_STORE, o));
+    GemmArgs gu;   // the FFN branch reads the same normalized input
+    gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
+    gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
+    MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
+    GemmArgs dn;
+    dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.fbuf; dn.ldc = h;
+    dn.m = T; dn.n = h; dn.k = ffn;
+    MR_TRY(launch_gemm(s, GEMM_STORE, dn));
+    MR_TRY(launch_light_residual(s, w.x, w.obuf, w.fbuf, L.attention_gate.f(), L.ffn_gate.f(), d.residual_scale,
+                                 T * h, nullptr));
+    MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.kcache, L.vcache, L.light_cap, p0, T));
+    MR_TRY(launch_light_store_rows(s, r));
+    return launch_light_finish(s, r, L.light, pl.fin, pl.write_slot0, pl.slot0_position, pl.slot0_count);
+}
+
+// Whether a prompt of this model can take the batched path: its family, and
+// the widths the GEMM tiles and row kernels take (other geometries, such as
+// the reference's micro test models, take the token loop).
+bool batched_prefill_ok(const mr_model *m) {
+    const mr_model_desc &d = m->d;
+    if (!batched_prefill_family(d.family)) return false;
+    const int hd = d.head_dim, qd = d.query_heads * hd;
+    if (d.hidden_size % 8 || d.ffn_dim % 8 || qd % 8 || hd % 4 || hd > 128) return false;
+    if (d.family == MR_FAMILY_HEAVY_MEDIUM_20)
+        return (hd == 32 || hd == 64 || hd == 128) && d.latent_dim % 8 == 0 && d.shared_experts <= 8 &&
+               d.global_slots <= 32 && ceil_div(d.context_length, d.global_block_size) * 8 + hd * 4 <= 64 * 1024;
+    if (d.family == MR_FAMILY_FLASHLIGHTING_20) return d.latent_dim % 8 == 0;
+    return true;
+}
+
 int prefill_batched(mr_model *m, int n, bool all, float *logits) {
     const mr_model_desc &d = m->d;
     hipStream_t s = m->ctx->stream;
-    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, V = d.vocab_size;
-    MR_REQUIRE(h % 8 == 0 && ffn % 8 == 0 && qd % 8 == 0 && hd % 4 == 0 && hd <= 128,
-               "batched prefill: hidden, ffn and query widths must be multiples of 8 and head_dim a multiple of 4 "
-               "up to 128");
+    const bool heavy = d.family == MR_FAMILY_HEAVY_MEDIUM_20, light = d.family == MR_FAMILY_FLASHLIGHTING_20;
+    const int h = d.hidden_size, V = d.vocab_size;
     const int chunk = std::min(n, kPrefillRows);
     PrefillWs w;
     MR_TRY(prefill_workspace(m, chunk, all, &w));
@@ -1375,35 +1699,28 @@ int prefill_batched(mr_model *m, int n, bool all, float *logits) {
     for (int start = 0; start < n; start += chunk) {
         const int T = std::min(chunk, n - start), p0 = m->position + start;
         MR_TRY(launch_embed_rows(s, m->embed.ptr, m->embed.dtype, m->ids_dev, p0, T, w.x, h));
-        for (Layer &L : m->layers) {
-            const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
-            MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
-            GemmArgs g;
-            g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
-            g.m = T; g.n = ld; g.k = h;
-            MR_TRY(launch_gemm(s, GEMM_STORE, g));
-            MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
-                                  d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
-                                  d.norm_eps, d.qk_norm, m->rope, d.split_half_rope));
-            PrefillAttnArgs a;
-            a.qkv = w.qkv; a.ld = ld; a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.cap = L.capacity;
-            a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
-            a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
-            MR_TRY(launch_prefill_attention(s, a));
-            MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
-            GemmArgs o;
-            o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
-            o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale;
-            MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
-            MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
-            GemmArgs gu;
-            gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
-            gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
-            MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
-            GemmArgs dn;
-            dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;
-            dn.m = T; dn.n = h; dn.k = ffn; dn.scale = d.residual_scale;
-            MR_TRY(launch_gemm(s, GEMM_RESIDUAL, dn));
+        LightPlan plan;
+        if (light) {   // one plan serves every layer (the bookkeeping depends only on positions)
+            plan = LightPlan();
+            plan_light_chunk(d, m->layers[0].light_cap, p0, T, plan);
+            MR_HIP(hipMemcpyAsync(w.flags, plan.flags.data(), T * sizeof(int), hipMemcpyHostToDevice, s), "upload plan");
+            MR_HIP(hipMemcpyAsync(w.extra_index, plan.extra_index.data(), T * sizeof(int), hipMemcpyHostToDevice, s),
+                   "upload plan");
+            MR_HIP(hipMemcpyAsync(w.merge_row, plan.merge_row.data(), T * sizeof(int), hipMemcpyHostToDevice, s),
+                   "upload plan");
+            MR_HIP(hipMemcpyAsync(w.merge_count, plan.merge_count.data(), T * sizeof(float), hipMemcpyHostToDevice, s),
+                   "upload plan");
+            if (plan.extra)
+                MR_HIP(hipMemcpyAsync(w.extra_pos, plan.extra_pos.data(), plan.extra * sizeof(int),
+                                      hipMemcpyHostToDevice, s),
+                       "upload plan");
+            MR_HIP(hipStreamSynchronize(s), "upload plan");   // the host vectors go out of scope
+        }
+        for (int li = 0; li < d.layers; ++li) {
+            Layer &L = m->layers[li];
+            MR_TRY(heavy   ? heavy_layer_rows(m, L, li, w, p0, T)
+                   : light ? light_layer_rows(m, L, w, plan, p0, T)
+                           : gqa_layer_rows(m, L, w, p0, T));
         }
         if (all) {
             MR_TRY(launch_rms_rows(s, w.x, h, m->norm.f(), d.norm_eps, h, w.xn, h, T));
@@ -1452,7 +1769,7 @@ int mr_model_forward(mr_model *m, const int32_t *ids, int n, int flags, float *l
            "upload token ids");
     MR_HIP(hipMemsetAsync(m->done_dev, 0, sizeof(int), s), "clear stop flag");
     const bool all = (flags & MR_FWD_RETURN_ALL) != 0;
-    if ((flags & MR_FWD_BATCHED) && n > 1 && batched_prefill_family(d.family)) return prefill_batched(m, n, all, logits);
+    if ((flags & MR_FWD_BATCHED) && n > 1 && batched_prefill_ok(m)) return prefill_batched(m, n, all, logits);
     for (int i = 0; i < n; ++i) {
         const bool want = all || i == n - 1;
         MR_TRY(run_step(m, want ? STEP_LOGITS : STEP_PLAIN));

@@ -34,4 +34,18 @@ struct GemmArgs {
 // Requires k % 8 == 0, lda % 4 == 0 and 16-byte aligned a and weight rows.
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g);
 
+// Groups of rows with their own weights (the experts of a batched MoE), one
+// launch: group z multiplies rows offset[z] .. offset[z] + count[z] of g.a by
+// w[z] (and w2[z]) into the same rows of g.c; g.w, g.w2 and g.m are unused.
+// Weight rows must be 16-byte aligned.  STORE and SWIGLU epilogues.
+struct GemmGroups {
+    const int *offset = nullptr;     // [groups] device
+    const int *count = nullptr;      // [groups] device
+    void *const *w = nullptr;        // [groups] device table of weight pointers
+    void *const *w2 = nullptr;       // [groups] SWIGLU up rows
+    int groups = 0;
+    int max_rows = 0;                // bound on every count (sizes the grid)
+};
+int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const GemmGroups &gg);
+
 }  // namespace mr

@@ -180,8 +180,9 @@ __device__ __forceinline__ f32x4 mfma(const bf16x8 &a, const bf16x8 &b, const f3
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// One 128 x 128 output tile (rows m0.., columns n0..) of g.
 template <int DT, int EPI>
-__global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0) {
     constexpr int PB = planes<DT>();
     __shared__ __attribute__((aligned(16))) __bf16 as[3][kBM][kPitch];
     __shared__ __attribute__((aligned(16))) __bf16 bs[PB][kBN][kPitch];
@@ -189,8 +190,6 @@ __global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 15, lk = (lane >> 4) * 8;
-    const int m0 = blockIdx.y * kBM;
-    const int n0 = blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN);
     const int nk = (g.k + kBK - 1) / kBK;
 
     f32x4 acc[4][4];
@@ -273,6 +272,39 @@ __global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
     }
 }
 
+template <int DT, int EPI>
+__global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
+    gemm_tile<DT, EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
+}
+
+// grid (column tiles, row tiles of the largest group, groups): group z is
+// rows offset[z] .. + count[z] of a and c with its own weight rows.
+template <int DT, int EPI>
+__global__ void __launch_bounds__(kThreads) k_gemm_grouped(GemmArgs g, GemmGroups gg) {
+    const int z = blockIdx.z, m0 = blockIdx.y * kBM, rows = gg.count[z];
+    if (m0 >= rows) return;
+    const int64_t first = gg.offset[z];
+    g.a += first * g.lda;
+    g.c += first * g.ldc;
+    g.m = rows;
+    g.w = gg.w[z];
+    if (EPI == GEMM_SWIGLU) g.w2 = gg.w2[z];
+    gemm_tile<DT, EPI>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
+}
+
+template <int DT>
+int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroups &gg) {
+    const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
+    const dim3 grid(ceil_div(g.n, cols), ceil_div(gg.max_rows, kBM), gg.groups);
+    switch (epi) {
+        case GEMM_STORE: k_gemm_grouped<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(g, gg); break;
+        case GEMM_SWIGLU: k_gemm_grouped<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(g, gg); break;
+        default: return fail(MR_ERR_INVALID, "grouped gemm: epilogue must be STORE or SWIGLU");
+    }
+    MR_LAUNCHED("enqueue grouped MFMA GEMM");
+    return MR_OK;
+}
+
 template <int DT>
 int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
     const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
@@ -288,6 +320,21 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
 }
 
 }  // namespace
+
+int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const GemmGroups &gg) {
+    MR_REQUIRE(g.a && g.c && g.n > 0 && g.k > 0 && gg.offset && gg.count && gg.w && gg.groups > 0 &&
+                   gg.groups <= 65535 && gg.max_rows > 0 && (epilogue != GEMM_SWIGLU || gg.w2),
+               "grouped gemm: bad arguments");
+    MR_REQUIRE(g.k % 8 == 0 && g.lda % 4 == 0 && g.lda >= g.k && g.ldc >= g.n && ((uintptr_t)g.a & 15) == 0,
+               "grouped gemm: k must be a multiple of 8 and rows 16-byte aligned");
+    MR_REQUIRE(ceil_div(gg.max_rows, kBM) <= 65535, "grouped gemm: too many rows");
+    switch (g.dtype) {
+        case MR_BF16: return launch_grouped_dt<MR_BF16>(s, epilogue, g, gg);
+        case MR_F16: return launch_grouped_dt<MR_F16>(s, epilogue, g, gg);
+        case MR_F32: return launch_grouped_dt<MR_F32>(s, epilogue, g, gg);
+    }
+    return fail(MR_ERR_INVALID, "grouped gemm: unknown weight dtype");
+}
 
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
     MR_REQUIRE(g.a && g.w && g.c && g.m > 0 && g.n > 0 && g.k > 0, "gemm: bad arguments");

@@ -51,7 +51,8 @@ struct MoeArgs {
     void *const *down = nullptr;
     int dtype = MR_BF16;
     const int *done = nullptr;
-    const int *pos = nullptr;
+    const int *pos = nullptr;        // position of the token (or null: `position`)
+    int position = 0;
     int *ids = nullptr;              // [kmax] chosen experts, descending probability
     float *weights = nullptr;        // [kmax] renormalized weights (0 beyond active)
     int *active = nullptr;           // adaptive width
@@ -67,5 +68,54 @@ struct MoeArgs {
 };
 
 int launch_moe(hipStream_t s, const MoeArgs &a);
+
+// ---- batched prefill of a chunk of rows (positions p0 .. p0 + rows - 1) ----
+
+// Block sums of one inner-loop pass after its ring holds the chunk's keys and
+// values: for every row, the running sum of its block up to the row (keys then
+// values, [rows][2 kv_heads d]), in row order from the block's running sum
+// before the chunk, as the token step adds them; bsum_k / bsum_v end holding
+// the running sums after the chunk.
+struct HeavyScanArgs {
+    const float *ring_k = nullptr, *ring_v = nullptr;   // [context, kvw], rows p0 .. p0 + rows - 1 stored
+    float *bsum_k = nullptr, *bsum_v = nullptr;         // [blocks, kvw]
+    float *sums = nullptr;                              // [rows][2 kvw]
+    int p0 = 0, rows = 0, kvw = 0, block = 0;
+};
+int launch_heavy_scan(hipStream_t s, const HeavyScanArgs &a);
+
+// Per row and query head: the block columns scored as the token step scores
+// them (block-sum quotients, sequential dot product, distance penalty), the
+// stable top-k, the choice record, and the chosen blocks' softmax partial
+// ext[row][head] = (m, l, -, -, o[d]) for launch_prefill_attention.
+struct HeavySelectArgs {
+    const float *qkv = nullptr;      // [rows, ld]: normalized, rotated queries at column 0
+    int ld = 0;
+    const float *bsum_k = nullptr, *bsum_v = nullptr;   // after the scan
+    const float *sums = nullptr;     // [rows][2 kvw] from the scan
+    float *ext = nullptr;            // [rows][heads][d + 4]
+    int *choice = nullptr;           // choice record of this layer/loop at position 0 (or null)
+    int choice_stride = 0, choice_blocks = 0;
+    int p0 = 0, rows = 0, heads = 0, kv_heads = 0, d = 0, block = 0, slots = 0, context = 0;
+    float slope = 0.0f;
+};
+int launch_heavy_select(hipStream_t s, const HeavySelectArgs &a);
+
+// Routing of every row (the token step's arithmetic), then the expert-major
+// gather: rows of expert e at offsets[e] .. + counts[e] of xg (routed experts,
+// then one group of all rows per shared expert), map[row][slot] = gathered row.
+// `a` is set up as for launch_moe with router = [rows][groups + experts]
+// logits, ids / weights [rows][kmax], active [rows], x = [rows][h] input.
+struct MoeRowsArgs {
+    MoeArgs a;
+    int rows = 0, p0 = 0;
+    int *counts = nullptr, *offsets = nullptr, *fill = nullptr;   // [experts + shared]
+    int *map = nullptr;              // [rows][kmax]
+    float *xg = nullptr;             // [rows (kmax + shared)][h]
+};
+int launch_moe_route_rows(hipStream_t s, const MoeRowsArgs &m);
+// x[row] += scale * (sum of the routed experts' outputs by weight in chosen
+// order, then the shared ones by shared_scale), y the grouped down outputs.
+int launch_moe_combine_rows(hipStream_t s, const MoeRowsArgs &m, const float *y, float *x);
 
 }  // namespace mr

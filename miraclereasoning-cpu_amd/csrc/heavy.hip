@@ -632,7 +632,7 @@ __device__ __forceinline__ void route_wave(const MoeArgs &a, RouteLds &r, bool p
         }
         if (lane == 0) *a.active = active;
         if (a.choice) {
-            int *rec = a.choice + (int64_t)(*a.pos) * a.choice_stride;
+            int *rec = a.choice + (int64_t)(a.pos ? *a.pos : a.position) * a.choice_stride;
             if (lane == 0) rec[0] = active;
             if (lane < a.kmax) rec[1 + lane] = lane < active ? r.chosen[lane] : -1;
         }
@@ -897,6 +897,165 @@ __global__ void __launch_bounds__(kMoeThreads) k_moe_down_bf16(MoeArgs a) {
     if (lane == 0) a.hidden[row] = a.hidden[row] + a.scale * total;
 }
 
+// ------------------------------------------------------------------ batched prefill
+// grid (blocks the chunk touches, ceil(2 kvw / 256)): one thread per column.
+__global__ void __launch_bounds__(256) k_heavy_scan(HeavyScanArgs a) {
+    const int c = blockIdx.y * 256 + threadIdx.x;
+    if (c >= 2 * a.kvw) return;
+    const bool isk = c < a.kvw;
+    const int j = isk ? c : c - a.kvw;
+    const float *ring = isk ? a.ring_k : a.ring_v;
+    float *bsum = isk ? a.bsum_k : a.bsum_v;
+    const int b = a.p0 / a.block + blockIdx.x, bstart = b * a.block;
+    const int r0 = max(bstart, a.p0), r1 = min(bstart + a.block, a.p0 + a.rows);
+    float v = bstart < a.p0 ? bsum[(int64_t)b * a.kvw + j] : 0.0f;
+    for (int r = r0; r < r1; ++r) {
+        v = v + ring[(int64_t)r * a.kvw + j];
+        a.sums[(int64_t)(r - a.p0) * 2 * a.kvw + c] = v;
+    }
+    bsum[(int64_t)b * a.kvw + j] = v;
+}
+
+// grid (rows, heads), kSelThreads.  LDS: query, block scores, keep flags.
+constexpr int kSelThreads = 128;
+
+template <int D>
+__global__ void __launch_bounds__(kSelThreads) k_heavy_select(HeavySelectArgs a) {
+    extern __shared__ float sh[];
+    __shared__ int chosen[kHeavyMaxChosen];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int pos = a.p0 + t, count = pos + 1, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
+    const int blocks = (count + a.block - 1) / a.block, bt = pos / a.block;
+    float *qs = sh, *sc = qs + D;
+    int *keep_flag = (int *)(sc + blocks);
+    for (int j = tid; j < D; j += kSelThreads) qs[j] = a.qkv[(int64_t)t * a.ld + (int64_t)h * D + j];
+    __syncthreads();
+    const float root = sqrtf((float)D);
+    const float *row_sums = a.sums + (int64_t)t * 2 * kvw;
+    for (int b = tid; b < blocks; b += kSelThreads) {   // the token step's quotients and dot order
+        const float *ks = b < bt ? a.bsum_k + (int64_t)b * kvw + (int64_t)kh * D : row_sums + (int64_t)kh * D;
+        const float n = (float)min(a.block, count - b * a.block);
+        float v = 0.0f;
+        for (int j = 0; j < D; ++j) v += qs[j] * (ks[j] / n);
+        const int end = min((b + 1) * a.block - 1, pos);
+        sc[b] = v / root - a.slope * log1pf((float)(pos - end));
+    }
+    __syncthreads();
+    const int keep = min(a.slots, blocks);
+    for (int b = tid; b < blocks; b += kSelThreads) {   // stable top-k (model.py:220-226)
+        const float sv = sc[b];
+        int rank = 0;
+        for (int c = 0; c < blocks; ++c) {
+            const float o = sc[c];
+            rank += o > sv || (o == sv && c < b);
+        }
+        keep_flag[b] = rank < keep;
+    }
+    __syncthreads();
+    for (int b = tid; b < blocks; b += kSelThreads)
+        if (keep_flag[b]) {
+            int at = 0;
+            for (int c = 0; c < b; ++c) at += keep_flag[c];
+            chosen[at] = b;
+        }
+    __syncthreads();
+    if (a.choice) {
+        int *rec = a.choice + (int64_t)pos * a.choice_stride + a.choice_blocks + h * a.slots;
+        for (int i = tid; i < a.slots; i += kSelThreads) rec[i] = i < keep ? chosen[i] : -1;
+    }
+    float m = -INFINITY;
+    for (int i = 0; i < keep; ++i) m = fmaxf(m, sc[chosen[i]]);
+    float *out = a.ext + ((int64_t)t * a.heads + h) * (D + 4);
+    for (int j = tid; j < D; j += kSelThreads) {
+        float o = 0.0f, l = 0.0f;
+        for (int i = 0; i < keep; ++i) {
+            const int b = chosen[i];
+            const float *vs = b < bt ? a.bsum_v + (int64_t)b * kvw : row_sums + kvw;
+            const float p = __expf(sc[b] - m);
+            const float n = (float)min(a.block, count - b * a.block);
+            o = fmaf(p, vs[(int64_t)kh * D + j] / n, o);
+            l += p;
+        }
+        out[4 + j] = o;
+        if (j == 0) {
+            out[0] = m;
+            out[1] = l;
+            out[2] = out[3] = 0.0f;
+        }
+    }
+}
+
+// grid rows, one wave: route_wave with this row's logits, publishing its
+// experts, weights, width and choice record; then its routed slots counted.
+__global__ void __launch_bounds__(kWave) k_moe_route_rows(MoeRowsArgs m) {
+    __shared__ RouteLds r;
+    const int t = blockIdx.x;
+    MoeArgs a = m.a;
+    a.router += (int64_t)t * (a.groups + a.experts);
+    a.ids += (int64_t)t * a.kmax;
+    a.weights += (int64_t)t * a.kmax;
+    a.active += t;
+    a.pos = nullptr;
+    a.position = m.p0 + t;
+    route_wave(a, r, true);
+    const int lane = threadIdx.x;
+    if (lane < r.active) atomicAdd(&m.counts[r.chosen[lane]], 1);
+}
+
+__global__ void k_moe_zero(int *counts, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) counts[i] = 0;
+}
+
+// one thread: group offsets (routed experts in expert order, then one group
+// of every row per shared expert) and cleared fill cursors
+__global__ void k_moe_offsets(MoeRowsArgs m) {
+    const int E = m.a.experts, S = m.a.shared;
+    int at = 0;
+    for (int e = 0; e < E + S; ++e) {
+        if (e >= E) m.counts[e] = m.rows;
+        m.offsets[e] = at;
+        at += m.counts[e];
+        m.fill[e] = 0;
+    }
+}
+
+// grid rows, 256 threads: copy the row into each of its groups
+__global__ void __launch_bounds__(256) k_moe_gather(MoeRowsArgs m) {
+    __shared__ int dst[kMaxTopK + 8];
+    const int t = blockIdx.x, E = m.a.experts, S = m.a.shared, kmax = m.a.kmax, h = m.a.h;
+    const int active = m.a.active[t];
+    if ((int)threadIdx.x < active) {
+        const int e = m.a.ids[(int64_t)t * kmax + threadIdx.x];
+        const int row = m.offsets[e] + atomicAdd(&m.fill[e], 1);
+        dst[threadIdx.x] = row;
+        m.map[(int64_t)t * kmax + threadIdx.x] = row;
+    } else if ((int)threadIdx.x >= kmax && (int)threadIdx.x < kmax + S) {
+        dst[threadIdx.x - kmax + active] = m.offsets[E + threadIdx.x - kmax] + t;
+    }
+    __syncthreads();
+    const float *x = m.a.x + (int64_t)t * h;
+    for (int i = 0; i < active + S; ++i) {
+        float *y = m.xg + (int64_t)dst[i] * h;
+        for (int j = threadIdx.x * 4; j < h; j += 256 * 4) *(float4 *)(y + j) = load_f4(x + j);
+    }
+}
+
+// grid rows, 256 threads: k_moe_down's accumulation order per element
+__global__ void __launch_bounds__(256) k_moe_combine(MoeRowsArgs m, const float *y, float *x) {
+    const int t = blockIdx.x, E = m.a.experts, S = m.a.shared, kmax = m.a.kmax, h = m.a.h;
+    const int active = m.a.active[t];
+    float *xr = x + (int64_t)t * h;
+    for (int j = threadIdx.x; j < h; j += 256) {
+        float total = 0.0f;
+        for (int i = 0; i < active; ++i)
+            total = total + m.a.weights[(int64_t)t * kmax + i] * y[(int64_t)m.map[(int64_t)t * kmax + i] * h + j];
+        for (int e = 0; e < S; ++e) total = total + m.a.shared_scale * y[(int64_t)(m.offsets[E + e] + t) * h + j];
+        xr[j] = xr[j] + m.a.scale * total;
+    }
+}
+
+
 }  // namespace
 
 bool heavy_kv_fused(int dtype, int latent) {
@@ -986,6 +1145,57 @@ int launch_moe(hipStream_t s, const MoeArgs &a) {
     else
         k_moe_down<<<ceil_div(a.h, kMoeRows), kMoeThreads, lds, s>>>(a);
     MR_LAUNCHED("enqueue moe down");
+    return MR_OK;
+}
+
+int launch_heavy_scan(hipStream_t s, const HeavyScanArgs &a) {
+    MR_REQUIRE(a.ring_k && a.ring_v && a.bsum_k && a.bsum_v && a.sums && a.rows > 0 && a.kvw > 0 && a.block > 0,
+               "heavy scan: bad arguments");
+    const int first = a.p0 / a.block, last = (a.p0 + a.rows - 1) / a.block;
+    k_heavy_scan<<<dim3(last - first + 1, ceil_div(2 * a.kvw, 256)), 256, 0, s>>>(a);
+    MR_LAUNCHED("enqueue heavy block scan");
+    return MR_OK;
+}
+
+int launch_heavy_select(hipStream_t s, const HeavySelectArgs &a) {
+    MR_REQUIRE(a.qkv && a.bsum_k && a.bsum_v && a.sums && a.ext && a.rows > 0 && a.slots <= kHeavyMaxChosen &&
+                   a.kv_heads > 0 && a.heads % a.kv_heads == 0,
+               "heavy select: bad arguments");
+    const int blocks = ceil_div(a.p0 + a.rows, a.block);
+    const size_t lds = (size_t)(a.d + blocks) * sizeof(float) + (size_t)blocks * sizeof(int);
+    MR_REQUIRE(lds <= 64 * 1024, "heavy select: too many blocks for shared memory");
+    const dim3 grid(a.rows, a.heads);
+    switch (a.d) {
+        case 128: k_heavy_select<128><<<grid, kSelThreads, lds, s>>>(a); break;
+        case 64: k_heavy_select<64><<<grid, kSelThreads, lds, s>>>(a); break;
+        case 32: k_heavy_select<32><<<grid, kSelThreads, lds, s>>>(a); break;
+        default: return fail(MR_ERR_INVALID, "heavy select: head_dim must be 32, 64 or 128");
+    }
+    MR_LAUNCHED("enqueue heavy block selection");
+    return MR_OK;
+}
+
+int launch_moe_route_rows(hipStream_t s, const MoeRowsArgs &m) {
+    const MoeArgs &a = m.a;
+    MR_REQUIRE(a.experts >= 1 && a.experts <= kMaxExperts && a.groups >= 1 && a.groups <= a.experts &&
+                   a.kmin >= 1 && a.kmin <= a.kmax && a.kmax <= std::min(a.experts, kMaxTopK) && a.shared <= 8 &&
+                   m.rows > 0 && a.h % 4 == 0,
+               "moe rows: routing geometry out of range");
+    const int groups = a.experts + a.shared;
+    k_moe_zero<<<ceil_div(groups, 256), 256, 0, s>>>(m.counts, groups);
+    MR_LAUNCHED("enqueue moe count clear");
+    k_moe_route_rows<<<m.rows, kWave, 0, s>>>(m);
+    MR_LAUNCHED("enqueue moe row routing");
+    k_moe_offsets<<<1, 1, 0, s>>>(m);
+    MR_LAUNCHED("enqueue moe group offsets");
+    k_moe_gather<<<m.rows, 256, 0, s>>>(m);
+    MR_LAUNCHED("enqueue moe gather");
+    return MR_OK;
+}
+
+int launch_moe_combine_rows(hipStream_t s, const MoeRowsArgs &m, const float *y, float *x) {
+    k_moe_combine<<<m.rows, 256, 0, s>>>(m, y, x);
+    MR_LAUNCHED("enqueue moe combine");
     return MR_OK;
 }
 

@@ -80,6 +80,39 @@ bool light_down_in_attend(LightArgs &a, const GemvArgs &g, int dtype);
 // lat_new and clears skip_merged when a merge happened).
 int launch_light_attend(hipStream_t s, const LightArgs &a);
 
+// ---- batched prefill of a chunk of rows (positions p0 .. p0 + rows - 1) ----
+//
+// Every query of the chunk sees a window of original rows (W + M positions
+// ending at its own, the row at distance W masked as latent_mask does) plus,
+// once the two oldest rows start folding, one extra row: logical row 0, the
+// running merge.  The bookkeeping depends only on positions and is planned on
+// the host; the merged row's latent follows the recurrence below.
+struct LightRowsArgs {
+    const float *lat = nullptr;         // [rows, latent] the chunk's normalized latents
+    float *arena = nullptr, *positions = nullptr, *counts = nullptr;   // the token step's ring state
+    float *slot0 = nullptr;             // [extra rows, latent] logical row 0 at each step that sees it as extra
+    float *slot0_final = nullptr;       // [latent] logical row 0 after the chunk
+    const int *flags = nullptr;         // [rows] 1: the step sees row 0 as extra (index extra_index[t]); 2: merge after it
+    const int *extra_index = nullptr;   // [rows]
+    const float *merge_count = nullptr; // [rows] count of row 0 before the step's merge
+    const int *merge_row = nullptr;     // [rows] position of the row folded in (logical row 1)
+    int init_from_arena = 0, init_slot = 0;   // row 0 before the chunk: arena slot, or the chunk's first row
+    int p0 = 0, rows = 0, latent = 0, cap = 0;
+};
+// Logical row 0's latent through the chunk: kernels.cl merge_rows
+// (a x0 + b x1) / (a + b) with b = 1 at every merge, in step order.
+int launch_light_slot0(hipStream_t s, const LightRowsArgs &a);
+// ext[t][h] = (q . k0 / sqrt(d), 1, -, -, v0) for steps with an extra row,
+// (-inf, 0, -, -, 0) otherwise; kv0 = [extra rows][k | v] (keys normed, rotated).
+int launch_light_extra(hipStream_t s, const float *qkv, int ld, const float *kv0, const int *extra_index, float *ext,
+                       int rows, int heads, int kv_heads, int d);
+// The chunk's rows into the ring state (latent, position, count 1) for
+// positions max(p0, p0 + rows - cap) .. p0 + rows - 1.
+int launch_light_store_rows(hipStream_t s, const LightRowsArgs &a);
+// Logical row 0 after the chunk (when it is a merged row) and the state.
+int launch_light_finish(hipStream_t s, const LightRowsArgs &a, LightState *st, const LightState &fin, int write_slot0,
+                        float slot0_position, float slot0_count);
+
 // hidden += rs * ((0 + ag * o) + fg * f)  (model.py:171-176 parallel gated residual)
 int launch_light_residual(hipStream_t s, float *hidden, const float *o, const float *f, const float *attention_gate,
                           const float *ffn_gate, float rs, int n, const int *done);

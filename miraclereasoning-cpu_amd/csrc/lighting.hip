@@ -391,6 +391,77 @@ __global__ void k_light_residual(float *hidden, const float *o, const float *f, 
     hidden[j] = hidden[j] + rs * branch;
 }
 
+// ------------------------------------------------------------------ batched prefill
+// one thread per latent column: the running logical row 0 through the chunk
+__global__ void __launch_bounds__(256) k_light_slot0(LightRowsArgs a) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= a.latent) return;
+    float v = a.init_from_arena ? a.arena[(int64_t)a.init_slot * a.latent + j] : a.lat[j];
+    for (int t = 0; t < a.rows; ++t) {
+        const int f = a.flags[t];
+        if (f & 1) a.slot0[(int64_t)a.extra_index[t] * a.latent + j] = v;
+        if (f & 2) {
+            const int r = a.merge_row[t];
+            const float x = r >= a.p0 ? a.lat[(int64_t)(r - a.p0) * a.latent + j]
+                                      : a.arena[(int64_t)(r % a.cap) * a.latent + j];
+            const float c = a.merge_count[t];
+            v = (c * v + 1.0f * x) / (c + 1.0f);
+        }
+    }
+    a.slot0_final[j] = v;
+}
+
+// grid (rows, heads), 64 threads
+__global__ void __launch_bounds__(64) k_light_extra(const float *qkv, int ld, const float *kv0, const int *extra_index,
+                                                    float *ext, int heads, int kv_heads, int d) {
+    const int t = blockIdx.x, h = blockIdx.y, kh = h / (heads / kv_heads), kvw = kv_heads * d;
+    float *out = ext + ((int64_t)t * heads + h) * (d + 4);
+    const int e = extra_index[t];
+    if (e < 0) {
+        for (int j = threadIdx.x; j < d; j += 64) out[4 + j] = 0.0f;
+        if (threadIdx.x == 0) {
+            out[0] = -INFINITY;
+            out[1] = out[2] = out[3] = 0.0f;
+        }
+        return;
+    }
+    const float *q = qkv + (int64_t)t * ld + (int64_t)h * d, *k = kv0 + (int64_t)e * 2 * kvw + (int64_t)kh * d;
+    float dot = 0.0f;
+    for (int j = threadIdx.x; j < d; j += 64) dot = fmaf(q[j], k[j], dot);
+    dot = wave_sum(dot);
+    const float *v = k + kvw;
+    for (int j = threadIdx.x; j < d; j += 64) out[4 + j] = v[j];
+    if (threadIdx.x == 0) {
+        out[0] = dot / sqrtf((float)d);
+        out[1] = 1.0f;
+        out[2] = out[3] = 0.0f;
+    }
+}
+
+// grid rows stored, 256 threads
+__global__ void __launch_bounds__(256) k_light_store_rows(LightRowsArgs a, int first) {
+    const int r = first + blockIdx.x, slot = r % a.cap;
+    const float *src = a.lat + (int64_t)(r - a.p0) * a.latent;
+    for (int j = threadIdx.x; j < a.latent; j += 256) a.arena[(int64_t)slot * a.latent + j] = src[j];
+    if (threadIdx.x == 0) {
+        a.positions[slot] = (float)r;
+        a.counts[slot] = 1.0f;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_light_finish(LightRowsArgs a, LightState *st, LightState fin, int write_slot0,
+                                                      float slot0_position, float slot0_count) {
+    if (write_slot0) {
+        for (int j = threadIdx.x; j < a.latent; j += 256)
+            a.arena[(int64_t)fin.start * a.latent + j] = a.slot0_final[j];
+        if (threadIdx.x == 0) {
+            a.positions[fin.start] = slot0_position;
+            a.counts[fin.start] = slot0_count;
+        }
+    }
+    if (threadIdx.x == 0) *st = fin;
+}
+
 }  // namespace
 
 int launch_light_prep(hipStream_t s, const LightArgs &a) {
@@ -502,6 +573,37 @@ int launch_light_residual(hipStream_t s, float *hidden, const float *o, const fl
                           const float *ffn_gate, float rs, int n, const int *done) {
     k_light_residual<<<ceil_div(n, 256), 256, 0, s>>>(hidden, o, f, attention_gate, ffn_gate, rs, n, done);
     MR_LAUNCHED("enqueue gated residual");
+    return MR_OK;
+}
+
+int launch_light_slot0(hipStream_t s, const LightRowsArgs &a) {
+    MR_REQUIRE(a.lat && a.arena && a.slot0 && a.slot0_final && a.flags && a.extra_index && a.merge_count &&
+                   a.merge_row && a.rows > 0 && a.latent > 0 && a.cap > 0,
+               "latent rows: bad arguments");
+    k_light_slot0<<<ceil_div(a.latent, 256), 256, 0, s>>>(a);
+    MR_LAUNCHED("enqueue latent row 0 recurrence");
+    return MR_OK;
+}
+
+int launch_light_extra(hipStream_t s, const float *qkv, int ld, const float *kv0, const int *extra_index, float *ext,
+                       int rows, int heads, int kv_heads, int d) {
+    MR_REQUIRE(qkv && extra_index && ext && rows > 0 && kv_heads > 0 && heads % kv_heads == 0, "latent extra: bad arguments");
+    k_light_extra<<<dim3(rows, heads), 64, 0, s>>>(qkv, ld, kv0, extra_index, ext, heads, kv_heads, d);
+    MR_LAUNCHED("enqueue latent extra row");
+    return MR_OK;
+}
+
+int launch_light_store_rows(hipStream_t s, const LightRowsArgs &a) {
+    const int first = std::max(a.p0, a.p0 + a.rows - a.cap);
+    k_light_store_rows<<<a.p0 + a.rows - first, 256, 0, s>>>(a, first);
+    MR_LAUNCHED("enqueue latent rows");
+    return MR_OK;
+}
+
+int launch_light_finish(hipStream_t s, const LightRowsArgs &a, LightState *st, const LightState &fin, int write_slot0,
+                        float slot0_position, float slot0_count) {
+    k_light_finish<<<1, 256, 0, s>>>(a, st, fin, write_slot0, slot0_position, slot0_count);
+    MR_LAUNCHED("enqueue latent state");
     return MR_OK;
 }
 

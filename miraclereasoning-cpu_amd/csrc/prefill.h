@@ -18,10 +18,15 @@ struct PrefillAttnArgs {
     int p0 = 0, rows = 0;           // position of row 0, rows in the chunk
     int heads = 0, kv_heads = 0, d = 0;
     float inv_root = 1.0f;          // 1 / sqrt(d)
+    int window = 0;                 // keys a query sees (0: cap)
+    int hole = 0;                   // > 0: the key at position p - hole is not seen (latent memory)
+    const float *ext = nullptr;     // [rows][heads][d + 4]: m, l, 2 unused, o[d] of extra columns, merged at the end
 };
 
 // out = softmax(q . k / sqrt(d)) . v per query head over the keys at
-// positions max(0, p - cap + 1) .. p of each query position p.
+// positions max(0, p - window + 1) .. p of each query position p (but
+// p - hole), keys before the chunk read from the ring at slot position % cap;
+// with ext, the extra columns' partial joins the softmax.
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a);
 
 // y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * gain (gain may be null).
@@ -32,6 +37,11 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
 // the q and k heads of each qkv row, in place (model.py:100-103).
 int launch_qk_rows(hipStream_t s, float *qkv, int ld, int rows, int p0, int heads, int kv_heads, int d,
                    const float *q_gain, const float *k_gain, float eps, int norm, const float *rope, int split_half);
+
+// Key heads only (RMSNorm with k_gain, RoPE) of rows whose positions are
+// positions[r] (rows of width ld, keys at column 0).
+int launch_k_rows_at(hipStream_t s, float *k, int ld, int rows, const int *positions, int kv_heads, int d,
+                     const float *k_gain, float eps, const float *rope, int split_half);
 
 // Ring rows of the chunk's last min(rows, cap) positions (model.py:21-25).
 int launch_ring_store(hipStream_t s, const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,

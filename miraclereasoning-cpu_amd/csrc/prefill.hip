@@ -57,8 +57,9 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
         q[g] = qvalid && dim < d ? load_f4(a.qkv + (int64_t)tq * a.ld + h * d + dim) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
+    const int win = a.window ? a.window : a.cap;
     const int last = min(t0 + tile_rows, a.rows) - 1;
-    const int klo = max(0, a.p0 + t0 - a.cap + 1), khi = a.p0 + last;
+    const int klo = max(0, a.p0 + t0 - win + 1), khi = a.p0 + last;
     const int ntiles = (khi - klo) / kKeys + 1;
 
     float4 kr[NL], vr[NL];
@@ -130,7 +131,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int kp = kb + t * 16 + 4 * lq + j;
-                const bool ok = qvalid && kp <= qp && kp > qp - a.cap;
+                const bool ok = qvalid && kp <= qp && kp > qp - win && (a.hole == 0 || kp != qp - a.hole);
                 const float v = ok ? sc[t][j] * a.inv_root : -INFINITY;
                 sc[t][j] = v;
                 tmax = fmaxf(tmax, v);
@@ -167,13 +168,28 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
             }
     }
     if (!qvalid) return;
+    float wo = 1.0f, we = 0.0f;   // weights of the window's and the extra columns' partials
+    const float *ext = nullptr;
+    if (a.ext) {   // the extra partial (m, l, o) joins the softmax
+        ext = a.ext + ((int64_t)tq * a.heads + h) * (d + 4);
+        const float m_e = ext[0], m = fmaxf(m_run, m_e);
+        wo = m_run == -INFINITY ? 0.0f : expf(m_run - m);
+        we = m_e == -INFINITY ? 0.0f : expf(m_e - m);
+        l_run = l_run * wo + ext[1] * we;
+    }
     const float inv = 1.0f / l_run;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         const int dim = g * 16 + 4 * lq;
-        if (dim < d)
-            *(float4 *)(a.out + (int64_t)tq * a.ldo + h * d + dim) =
-                make_float4(o[g][0] * inv, o[g][1] * inv, o[g][2] * inv, o[g][3] * inv);
+        if (dim < d) {
+            float4 r = make_float4(o[g][0] * wo, o[g][1] * wo, o[g][2] * wo, o[g][3] * wo);
+            if (ext) {
+                const float4 e = load_f4(ext + 4 + dim);
+                r = make_float4(r.x + e.x * we, r.y + e.y * we, r.z + e.z * we, r.w + e.w * we);
+            }
+            *(float4 *)(a.out + (int64_t)tq * a.ldo + h * d + dim) = make_float4(r.x * inv, r.y * inv, r.z * inv,
+                                                                               r.w * inv);
+        }
     }
 }
 
@@ -192,7 +208,7 @@ __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const
 // grid (rows, ceil((heads + kv_heads) / 4)), 256 threads: one wave per head.
 __global__ void __launch_bounds__(256) k_qk_rows(float *qkv, int ld, int p0, int heads, int kv_heads, int d,
                                                  const float *q_gain, const float *k_gain, float eps, int norm,
-                                                 const float *rope, int split_half) {
+                                                 const float *rope, int split_half, const int *positions) {
     const int lane = threadIdx.x & 63, hh = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (hh >= heads + kv_heads) return;
     float *row = qkv + (int64_t)blockIdx.x * ld + (int64_t)hh * d;   // k heads follow the q heads
@@ -204,7 +220,8 @@ __global__ void __launch_bounds__(256) k_qk_rows(float *qkv, int ld, int p0, int
         scale = 1.0f / sqrtf(wave_sum(ss) / (float)d + eps);
     }
     const int half = d / 2;
-    const float *cs = rope + (int64_t)(p0 + (int)blockIdx.x) * half * 2;
+    const int p = positions ? positions[blockIdx.x] : p0 + (int)blockIdx.x;
+    const float *cs = rope + (int64_t)p * half * 2;
     for (int i = lane; i < half; i += kWave) {
         const int j = split_half ? i : 2 * i, k = split_half ? i + half : 2 * i + 1;
         float u = row[j], v = row[k];
@@ -267,8 +284,16 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
 int launch_qk_rows(hipStream_t s, float *qkv, int ld, int rows, int p0, int heads, int kv_heads, int d,
                    const float *q_gain, const float *k_gain, float eps, int norm, const float *rope, int split_half) {
     k_qk_rows<<<dim3(rows, ceil_div(heads + kv_heads, 4)), 256, 0, s>>>(qkv, ld, p0, heads, kv_heads, d, q_gain,
-                                                                       k_gain, eps, norm, rope, split_half);
+                                                                       k_gain, eps, norm, rope, split_half, nullptr);
     MR_LAUNCHED("enqueue q/k norm and RoPE");
+    return MR_OK;
+}
+
+int launch_k_rows_at(hipStream_t s, float *k, int ld, int rows, const int *positions, int kv_heads, int d,
+                     const float *k_gain, float eps, const float *rope, int split_half) {
+    k_qk_rows<<<dim3(rows, ceil_div(kv_heads, 4)), 256, 0, s>>>(k, ld, 0, 0, kv_heads, d, nullptr, k_gain, eps, 1,
+                                                               rope, split_half, positions);
+    MR_LAUNCHED("enqueue key norm and RoPE at row positions");
     return MR_OK;
 }
 

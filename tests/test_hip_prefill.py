@@ -97,3 +97,110 @@ def test_batched_full_prompt_matches_token_loop(backend):
     assert model.position == len(ids)
     np.testing.assert_allclose(batched, exact, rtol=1e-3, atol=1e-4)
     assert model.generate(list(ids), max_new_tokens=8) == exact_stream
+
+
+def _heavy_against_oracle(model, cfg, config, weights, ids, context, parts=None):
+    """Device first (its logits, greedy stream and recorded choices), then the
+    oracle following the device's choices within its near-tie band."""
+    from oracle.model import OracleModel
+    if parts:
+        got = np.concatenate([model.prefill(ids[a:b], return_all=True) for a, b in parts])
+    else:
+        got = model.prefill(ids, return_all=True)
+    stream = model.generate(list(ids), max_new_tokens=6)
+    choices = model.engine.choices()
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=context, follow=choices)
+    want = ref.prefill(ids, return_all=True)
+    tok, want_stream = int(np.argmax(want[-1])), []
+    for i in range(6):
+        want_stream.append(tok)
+        if tok == cfg.eos_token_id or i == 5:
+            break
+        tok = int(np.argmax(ref.decode(tok)))
+    print("near-ties adopted", ref.adopted, "mismatches", ref.mismatches, flush=True)
+    assert ref.mismatches == [] and len(ref.adopted) <= 2
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
+    assert stream == want_stream
+
+
+@pytest.mark.parametrize("parts", [None, [(0, 37), (37, 100)]])
+def test_batched_heavy_geometry_matches_oracle(backend, parts):
+    """heavy-medium-2.0 batched (BF16, head dim 64, 16 experts in 4 groups with
+    adaptive width 2..4, blocks of 16 with 3 kept, window 32) over 100 tokens,
+    whole and in two chunks (the second reads the first's rings and block
+    sums): logits of every position, the greedy stream, and every block and
+    expert choice against the oracle."""
+    from test_hip_model import HEAVY_MID
+    weights = synthetic.synthetic_weights(HEAVY_MID, 11, "bf16")
+    ids = synthetic.prompt_ids(HEAVY_MID["vocab_size"], 100, 11)
+    cfg = ModelConfig.from_dict(HEAVY_MID)
+    print("case heavy batched", parts, flush=True)
+    with MiracleModel(cfg, weights, backend=backend, context_length=160, prefill_mode="batched") as model:
+        _heavy_against_oracle(model, cfg, HEAVY_MID, weights, ids, 160, parts)
+
+
+def test_batched_heavy_micro_takes_token_loop(backend, golden_dir):
+    """The reference's micro heavy model (head dim 4) is outside the batched
+    kernels' geometry: under prefill_mode="batched" it takes the token loop and
+    matches the reference's fixture."""
+    from test_oracle_model import _load
+    z, bundle, weights = _load(golden_dir, "heavy-medium-2.0")
+    with MiracleModel(ModelConfig.from_dict(bundle), weights, backend=backend, context_length=32,
+                      prefill_mode="batched") as model:
+        np.testing.assert_allclose(model.prefill(z["ids"], return_all=True), z["logits"], atol=2e-5, rtol=2e-4)
+
+
+@pytest.mark.parametrize("slots,parts", [(4, None), (4, [(0, 20), (20, 31), (31, 90)]), (0, None),
+                                         (0, [(0, 30), (30, 90)])])
+def test_batched_lighting_geometry_matches_oracle(backend, slots, parts):
+    """flashlighting-2.0 batched (BF16, YaRN, window 24 with 4 memory slots or
+    none) over 90 tokens: whole, and in chunks that begin before, at and after
+    the first merge (or drop); logits of every position and the greedy stream
+    against the oracle."""
+    from oracle.model import OracleModel
+    from test_hip_model import LIGHT_MID
+    config = dict(LIGHT_MID, memory_slots=slots)
+    weights = synthetic.synthetic_weights(config, 13, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 90, 13)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=128)
+    want = ref.prefill(ids, return_all=True)
+    stream = ref.generate(list(ids), max_new_tokens=8)
+    print("case lighting batched", slots, parts, flush=True)
+    with MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=128,
+                      prefill_mode="batched") as model:
+        if parts:
+            got = np.concatenate([model.prefill(ids[a:b], return_all=True) for a, b in parts])
+        else:
+            got = model.prefill(ids, return_all=True)
+        np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
+        assert model.generate(list(ids), max_new_tokens=8) == stream
+
+
+def test_batched_lighting_full_prompt_matches_token_loop(backend):
+    """flashlighting-2.0's full 8192-token prompt in two chunks (the second
+    starts before the first merge at 4608 and ends 3584 merges later) batched
+    against the exact token loop: every 64th row of logits, the decode step
+    that follows (it reads the latent memory the batched path left, with a
+    merged row pending), then the greedy continuation.  (heavy-medium-2.0 has
+    no such check: its routing has near-ties, where two exact FP32 orders may
+    choose differently and the paths then part; its batched prompts are
+    checked against the oracle following the device's choices.)"""
+    name = "flashlighting-2.0"
+    wl = presets.workload(name)
+    cfg = ModelConfig.from_dict(wl["config"])
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    ids = synthetic.prompt_ids(cfg.vocab_size, wl["prompt"], wl["seed"])
+    print("case", name, "prompt", len(ids), flush=True)
+    with MiracleModel(cfg, weights, backend=backend, context_length=wl["context"]) as model:
+        exact = model.prefill(ids, return_all=True)[::64].copy()
+        exact_last = model.prefill([int(np.argmax(exact[-1]))])   # position len(ids)
+        exact_stream = model.generate(list(ids), max_new_tokens=6)
+        model.reset()
+        model.prefill_mode = "batched"
+        batched = model.prefill(ids, return_all=True)[::64].copy()
+        assert model.position == len(ids)
+        np.testing.assert_allclose(batched, exact, rtol=1e-3, atol=1e-4)
+        np.testing.assert_allclose(model.prefill([int(np.argmax(exact[-1]))]), exact_last, rtol=1e-3, atol=1e-4)
+        assert model.generate(list(ids), max_new_tokens=6) == exact_stream

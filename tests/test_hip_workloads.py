@@ -88,7 +88,8 @@ def test_long_prompt_matches_oracle(backend, name, prompt, mode):
     assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
-def test_heavy_workload_matches_oracle(backend, record_property):
+@pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
+def test_heavy_workload_matches_oracle(backend, record_property, prefill_mode):
     """The device runs first and records its choices; the oracle then follows
     them wherever they agree with its own values to within its near-tie band
     (a relative 1e-4: two exact FP32 evaluations in different summation orders
@@ -101,7 +102,7 @@ def test_heavy_workload_matches_oracle(backend, record_property):
     cfg = ModelConfig.from_dict(wl["config"])
     weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
     ids = synthetic.prompt_ids(cfg.vocab_size, prompt, wl["seed"])
-    model = MiracleModel(cfg, weights, backend=backend, context_length=wl["context"])
+    model = MiracleModel(cfg, weights, backend=backend, context_length=wl["context"], prefill_mode=prefill_mode)
     got = model.prefill(ids, return_all=True)
     stream = model.generate(list(ids), max_new_tokens=6)
     choices = model.engine.choices()
@@ -114,14 +115,15 @@ def test_heavy_workload_matches_oracle(backend, record_property):
     experts = [r for r in trace if r[0] == "experts"]
     real = [r[4] for r in blocks if math.isfinite(r[4])]
     block_margin, router_margin = min(real), min(r[5] for r in experts)
-    print(f"case {name} {prompt}: {len(blocks)} block choices ({len(real)} with more blocks than slots), smallest "
+    print(f"case {name} {prompt} {prefill_mode}: {len(blocks)} block choices ({len(real)} with more blocks than slots), smallest "
           f"block-score gap {block_margin:.3e}; {len(experts)} routings, smallest probability gap "
           f"{router_margin:.3e}; near-ties adopted {ref.adopted}; mismatches {ref.mismatches}", flush=True)
     record_property("block_score_margin", block_margin)
     record_property("router_probability_margin", router_margin)
     record_property("near_ties_adopted", len(ref.adopted))
     assert ref.mismatches == []
-    assert len(ref.adopted) <= 4, ref.adopted    # rare, or the two paths are not the same arithmetic
+    # rare (at most one per thousand decisions), or the two paths are not the same arithmetic
+    assert len(ref.adopted) <= max(4, (len(blocks) + len(experts)) // 1000), ref.adopted
     # where nothing was adopted, the device's record is the oracle's own choice
     own = follow_record(trace, cfg, prompt + len(want_stream) - 1)
     differ = {(int(p), int(l), int(i)) for p, l, i in zip(*np.nonzero((own != choices).any(axis=3)))}
@@ -134,8 +136,9 @@ LIGHT_SPLIT = dict(presets.workload("flashlighting-2.0")["config"], layers=2, wi
                    max_positions=4096)
 
 
+@pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
 @pytest.mark.parametrize("variant", ["workload", "window150"])
-def test_lighting_workload_matches_oracle(backend, variant):
+def test_lighting_workload_matches_oracle(backend, variant, prefill_mode):
     if variant == "workload":
         wl = presets.workload("flashlighting-2.0")
         config, seed, prompt, context = wl["config"], wl["seed"], 128, wl["context"]
@@ -144,8 +147,13 @@ def test_lighting_workload_matches_oracle(backend, variant):
         config, seed, prompt, context = LIGHT_SPLIT, 29, 230, 256
         weights = synthetic.synthetic_weights(config, seed, "bf16")
     ids = synthetic.prompt_ids(config["vocab_size"], prompt, seed)
-    want, stream = _oracle_run(config, weights, ids, context)
-    print("case flashlighting-2.0", variant, prompt, flush=True)
-    model = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=context)
-    np.testing.assert_allclose(model.prefill(ids, return_all=True), want, **TOL)
-    assert model.generate(list(ids), max_new_tokens=6) == stream
+    key = ("lighting", variant, prompt)
+    if key not in _CACHE:
+        _CACHE.clear()
+        _CACHE[key] = _oracle_run(config, weights, ids, context)
+    want, stream = _CACHE[key]
+    print("case flashlighting-2.0", variant, prompt, prefill_mode, flush=True)
+    with MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=context,
+                      prefill_mode=prefill_mode) as model:
+        np.testing.assert_allclose(model.prefill(ids, return_all=True), want, **TOL)
+        assert model.generate(list(ids), max_new_tokens=6) == stream
