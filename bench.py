@@ -173,6 +173,53 @@ def summarize_trace(path, steps):
     return 0
 
 
+def trace_summary(model, cfg, steps, dump=None):
+    """Per-phase anatomy of `steps` persistent decode steps (mr_model_trace_step)
+    from the model's current position, as a markdown table: for each phase kind
+    of local and of global layers, the mean time from the previous phase's last
+    workgroup to store its outputs to this phase's last ("phase"), and from that
+    same instant to the median workgroup having its input staged ("input") and
+    the median first stream wave having stored its rows ("rows")."""
+    kinds = ("qkv", "attention", "o", "gate_up", "down")
+    acc = {}
+    first_pos = model.engine.position()
+    raw = []
+    for _ in range(steps):
+        t = model.engine.trace_step()          # [phases, grid, 5]
+        raw.append(t)
+        ends = np.nanmax(t[:, :, 2], axis=1)
+        total = ends[-1] - np.nanmin(t[0, :, 0])
+        acc.setdefault(("step", "-"), []).append((total, np.nan, np.nan))
+        for p in range(1, t.shape[0]):
+            if p == t.shape[0] - 1:
+                key = ("head", "-")
+            else:
+                layer, k = divmod(p - 1, 5)
+                key = (kinds[k], "global" if cfg.layer_window(layer) is None else "local")
+            prev = ends[p - 1]
+            ready = np.nanmedian(t[p, :, 1]) - prev
+            rows = np.nanmedian(t[p, :, 3]) - prev if np.any(np.isfinite(t[p, :, 3])) else np.nan
+            acc.setdefault(key, []).append((ends[p] - prev, ready, rows))
+    print(f"persistent decode step anatomy: {steps} steps from position {first_pos}, "
+          f"{cfg.layers} layers ({sum(cfg.layer_window(i) is None for i in range(cfg.layers))} global)")
+    print("| Phase | Layers | Phase µs (mean) | Input staged µs (median WG) | Rows stored µs (median first stream "
+          "wave) | Count |")
+    print("|---|---|---|---|---|---|")
+    order = [(k, s) for k in kinds for s in ("local", "global")] + [("head", "-"), ("step", "-")]
+
+    def fmt(col):
+        return "" if np.all(np.isnan(col)) else f"{np.nanmean(col):.2f}"
+
+    for key in order:
+        if key not in acc:
+            continue
+        v = np.array(acc[key])
+        print(f"| {key[0]} | {key[1]} | {v[:, 0].mean():.2f} | {fmt(v[:, 1])} | {fmt(v[:, 2])} | {len(v)} |")
+    if dump:
+        np.save(dump, np.stack(raw))
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,6 +242,12 @@ def main():
     ap.add_argument("--summarize-trace", metavar="CSV", default=None,
                     help="print the per-kernel summary of the last --steps decode steps in a rocprofv3 kernel "
                          "trace of this bench and exit")
+    ap.add_argument("--trace-steps", type=int, default=0,
+                    help="after the prefill, trace this many persistent decode steps phase by phase, print the "
+                         "per-phase anatomy (markdown) and exit")
+    ap.add_argument("--trace-dump", metavar="NPY", default=None,
+                    help="with --trace-steps: also save the raw timestamps [steps, phases, workgroups, (entry, "
+                         "input staged, exit)] in µs")
     args = ap.parse_args()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace, args.steps)
@@ -239,6 +292,9 @@ def main():
     pf_flops = prefill_flops(cfg, wl["context"], prompt_len) if gqa else None
     log(f"prefill {prompt_len / prefill_s:.1f} tok/s" +
         (f", {pf_flops / prefill_s / 1e12:.1f} TFLOP/s algorithmic" if pf_flops else ""))
+    if args.trace_steps:
+        eng.generate_greedy(args.warmup + 1, -1)    # first launches outside the traced steps
+        return trace_summary(model, cfg, args.trace_steps, args.trace_dump)
 
     if args.traffic_probe:
         n = 64 * 1024 * 1024

@@ -711,6 +711,7 @@ std::vector<Phase> build_program(mr_model *m, bool head) {
         o.w = L.o.ptr; o.x = m->c_attn; o.x_phase = attn_at; o.y = m->c_hidden; o.res_phase = hidden_at;
         o.ready = a.heads_done; o.nready = L.kv_heads * L.step_head_groups;
         o.scale = d.residual_scale;
+        step_attention_mergers(a.at.s, m->grid, o.skip);
         prog.push_back(o);
         hidden_at = last();
         Phase gu;
@@ -1880,7 +1881,7 @@ int mr_model_trace_step(mr_model *m, uint64_t *out, int64_t capacity, int *phase
     if (!m->persistent_ok || m->mode != MR_STEP_PERSISTENT)
         return fail(MR_ERR_STATE, "trace_step: the model does not run the persistent step kernel");
     MR_REQUIRE(m->position >= 1 && m->position < m->d.context_length, "trace_step: call forward first");
-    const size_t n = (size_t)m->n_head * m->grid * 3;
+    const size_t n = (size_t)m->n_head * m->grid * kTraceFields;
     MR_REQUIRE((int64_t)n <= capacity, "trace_step: output too small");
     *phases = m->n_head;
     *grid = m->grid;

@@ -38,7 +38,13 @@ struct Phase {
     // PH_ATTN: at.s.q / k_new / v_new / out point at cells; x_phase = Q/K/V phase
     unsigned *heads_done = nullptr;   // [kv_heads] progress words of the merged heads
     att::Args at{};
+    // Workgroups that take no rows of this GEMV phase (bit b of word b / 32;
+    // grids of up to kSkipBits workgroups): the rows go to the others in
+    // order.  The O projection skips the workgroups that merged attention
+    // heads, which finish the attention phase last.
+    unsigned skip[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 };
+constexpr int kSkipBits = 256;
 
 // Per-launch arguments (all pointers into the model's device state).
 struct StepArgs {
@@ -58,8 +64,13 @@ struct StepArgs {
     int embed_dtype = MR_F32;
     const void *dummy = nullptr;        // 16 readable bytes: target of loads past a matrix's end
     int xbuf = 0;                       // floats of one GEMV input staging buffer (two in LDS)
-    unsigned long long *trace = nullptr;   // optional [nphases][grid][3]: entry, inputs staged, outputs stored
+    unsigned long long *trace = nullptr;   // optional [nphases][grid][kTraceFields]
 };
+
+// Trace record of one (phase, workgroup): wall clock (100 MHz) at the phase's
+// entry, when its input was staged, when its last stream wave stored its
+// outputs and when its first stream wave did; the fifth field is unused.
+constexpr int kTraceFields = 5;
 
 // Waves 0..kControlWaves-1 of a workgroup wait for and stage phase inputs; the
 // other (stream) waves load weights, compute and store outputs.
@@ -80,6 +91,9 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
 // Attention splits per KV head in the step kernel: enough units that each
 // covers its keys in one round of its waves' loads, at most cus / kv_heads.
 int step_attention_splits(int max_total, int kv_heads, int dim, int cus);
+// Workgroups that merge attention heads in the step kernel (the split-0 unit
+// of each (KV head, query-head group)), as a skip mask for the next phase.
+void step_attention_mergers(const AttnStepArgs &a, int grid, unsigned *mask);
 // Groups the query heads of a KV head are split into (AttnStepArgs::head_groups)
 // so that the (KV head, group, split) units fill up to `cus` workgroups.
 int step_attention_head_groups(int heads, int kv_heads, int splits, int cus);

@@ -81,11 +81,36 @@ constexpr int NS = kStreamWaves;
 // channels queues behind them: fewer, rarer polls keep the streams fast.
 __shared__ unsigned finished_waves;
 
-__device__ __forceinline__ void wg_mark(const StepArgs &s, unsigned ep) {
+__device__ __forceinline__ bool wg_mark(const StepArgs &s, unsigned ep) {
     const unsigned old = atomicAdd(&finished_waves, 1u);
-    if ((old + 1) % NS == 0)
+    if ((old + 1) % NS != 0) return false;
 #pragma unroll
-        for (int c = 0; c < kWordCopies; ++c) ll::mark(s.progress + c * kWordCopyStride + blockIdx.x, ep);
+    for (int c = 0; c < kWordCopies; ++c) ll::mark(s.progress + c * kWordCopyStride + blockIdx.x, ep);
+    return true;
+}
+
+// Rows [r0, r1) of this workgroup in a phase of n rows: equal blocks in
+// workgroup order, over the workgroups the phase does not skip.
+__device__ __forceinline__ void wg_rows(const Phase &ph, int &r0, int &r1) {
+    const int n = ph.n, b = blockIdx.x;
+    int workers = gridDim.x, rank = b;
+    bool skipped = false;
+    if (gridDim.x <= kSkipBits) {
+        int total = 0, below = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned m = ph.skip[i];
+            total += __builtin_popcount(m);
+            if (32 * i + 32 <= b) below += __builtin_popcount(m);
+            else if (32 * i <= b) below += __builtin_popcount(m & ((1u << (b - 32 * i)) - 1u));
+        }
+        skipped = (ph.skip[b >> 5] >> (b & 31)) & 1u;
+        workers -= total;
+        rank -= below;
+    }
+    const int rpw = (n + workers - 1) / workers;
+    r0 = skipped ? n : min(rank * rpw, n);
+    r1 = skipped ? n : min(r0 + rpw, n);
 }
 constexpr int kVC = 4;
 constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
@@ -111,9 +136,7 @@ __device__ __forceinline__ GemvGeo gemv_geo(const Phase &ph) {
     g.slots = kWave / g.lpr;
     const int vpl = (g.nvec + g.lpr - 1) / g.lpr;
     g.cpr = (vpl + kVC - 1) / kVC;
-    const int rpw = (ph.n + gridDim.x - 1) / gridDim.x;
-    g.r0 = min((int)blockIdx.x * rpw, ph.n);
-    g.r1 = min(g.r0 + rpw, ph.n);
+    wg_rows(ph, g.r0, g.r1);
     const int ngroups = (g.r1 - g.r0 + g.slots - 1) / g.slots;
     const int sw = (int)(threadIdx.x >> 6) - NC;
     g.groups = sw >= 0 && ngroups > sw ? (ngroups - sw + NS - 1) / NS : 0;
@@ -389,8 +412,8 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
                 else ll::put(ph.y + row, outs[row - g.r0], ep_y);
             }
         }
-        if (!HEAD && lane == 0) wg_mark(s, ep_y);
-        if (tr && tid == NC * kWave) tr[2] = wall_clock64();   // first stream wave done
+        if (!HEAD && lane == 0 && wg_mark(s, ep_y) && tr) tr[2] = wall_clock64();   // last stream wave done
+        if (tr && tid == NC * kWave) tr[3] = wall_clock64();   // first stream wave done
     }
     if (HEAD) {   // per-workgroup greedy partial
         __shared__ float bv[NW];
@@ -416,6 +439,7 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
             stc(s.best_val + blockIdx.x, r.v);
             stci(s.best_idx + blockIdx.x, r.i);
             stci(s.bad + blockIdx.x, r.bad);
+            if (tr) tr[2] = wall_clock64();
         }
     }
     return true;
@@ -539,7 +563,7 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
     int gemvs = 0;   // GEMV phases so far: their inputs alternate between two LDS buffers
     for (int p = 0; p < s.nphases; ++p) {
         const Phase &ph = *(const Phase *)(prog + p);
-        unsigned long long *tr = s.trace ? s.trace + ((size_t)p * gridDim.x + blockIdx.x) * 3 : nullptr;
+        unsigned long long *tr = s.trace ? s.trace + ((size_t)p * gridDim.x + blockIdx.x) * kTraceFields : nullptr;
         stamp(tr, 0);
         const unsigned ep_y = epoch(s, pos, p);
         const unsigned ep_x = epoch(s, pos, ph.x_phase), ep_res = epoch(s, pos, ph.res_phase);
@@ -600,7 +624,11 @@ int step_xbuf_floats(const std::vector<Phase> &program, int grid) {
     int need = 0;
     for (const Phase &ph : program)
         if (ph.kind == PH_GEMV || ph.kind == PH_HEAD) {
-            const int rpw = (ph.n + grid - 1) / grid;
+            int skipped = 0;
+            if (grid <= kSkipBits)
+                for (unsigned m : ph.skip) skipped += __builtin_popcount(m);
+            const int workers = std::max(1, grid - skipped);
+            const int rpw = (ph.n + workers - 1) / workers;
             need = std::max(need, ((ph.k + 3) & ~3) + 2 * ((rpw + 3) & ~3) + ((NC + 3) & ~3));
         }
     return (need + 3) & ~3;
@@ -644,6 +672,18 @@ const void *step_kernel(int dtype, int dim) {
 }
 
 }  // namespace
+
+void step_attention_mergers(const AttnStepArgs &a, int grid, unsigned *mask) {
+    // the unit -> (pair, split) deal of attn_phase; with one unit per
+    // workgroup, the unit of split 0 of each (KV head, group) merges it
+    const int splits = a.splits, hg = a.head_groups, pairs = a.kv_heads * splits, units = pairs * hg;
+    if (units > grid || grid > kSkipBits) return;
+    const bool xcd_map = hg > 1 && pairs % kXcds == 0;
+    for (int u = 0; u < units; ++u) {
+        const int pair = xcd_map ? u % kXcds + kXcds * (u / kXcds / hg) : u / hg;
+        if (pair % splits == 0) mask[u >> 5] |= 1u << (u & 31);
+    }
+}
 
 int step_attention_splits(int max_total, int kv_heads, int dim, int cus) {
     const int per_unit = (NT / kWave) * (dim == 128   ? keys_per_wave_round<128>()

@@ -177,18 +177,25 @@ class Engine:
         _check(self.lib.mr_model_get_step_mode(self.handle, C.byref(mode)), "get_step_mode")
         return {v: k for k, v in self.STEP_MODES.items()}[mode.value]
 
+    TRACE_FIELDS = 5
+
     def trace_step(self):
-        """Per-phase, per-workgroup timestamps (µs, relative to the step start) of
-        one persistent greedy decode step: array [phases, grid, 3] of (phase
-        entry, inputs ready, phase exit); NaN where a workgroup had no work."""
-        cap = 4 * 1024 * 1024
+        """Per-phase, per-workgroup record of one persistent greedy decode step:
+        array [phases, grid, 5] of (phase entry, input staged, outputs stored
+        by the last stream wave, outputs stored by the first stream wave) in µs
+        relative to the step start (NaN where not recorded), and a fifth field
+        the kernel leaves at zero."""
+        cap = 8 * 1024 * 1024
         buf = np.zeros(cap, np.uint64)
         phases, grid = C.c_int(), C.c_int()
         _check(self.lib.mr_model_trace_step(self.handle, buf.ctypes.data, cap, C.byref(phases), C.byref(grid)),
                "trace step")
-        t = buf[:phases.value * grid.value * 3].reshape(phases.value, grid.value, 3).astype(np.int64)
-        t0 = t[0, :, 0].min()
-        return np.where(t > 0, (t - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
+        n = self.TRACE_FIELDS
+        t = buf[:phases.value * grid.value * n].reshape(phases.value, grid.value, n).astype(np.int64)
+        clock = t[:, :, :4]
+        t0 = clock[0, :, 0].min()
+        out = np.where(clock > 0, (clock - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
+        return np.concatenate([out, t[:, :, 4:].astype(np.float64)], axis=2)
 
     def choices(self):
         """Routing decisions of every position so far (heavy-medium-2.0):
