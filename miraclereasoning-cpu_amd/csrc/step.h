@@ -91,7 +91,7 @@ size_t step_lds_bytes(const std::vector<Phase> &program, int grid);
 // Attention splits per KV head in the step kernel: enough units that each
 // covers its keys in one round of its waves' loads, at most cus / kv_heads.
 int step_attention_splits(int max_total, int kv_heads, int dim, int cus);
-// Workgroups that merge attention heads in the step kernel (the split-0 unit
+// Workgroups that merge attention heads in the step kernel (the merging unit
 // of each (KV head, query-head group)), as a skip mask for the next phase.
 void step_attention_mergers(const AttnStepArgs &a, int grid, unsigned *mask);
 // Groups the query heads of a KV head are split into (AttnStepArgs::head_groups)

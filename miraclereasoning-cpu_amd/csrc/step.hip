@@ -14,7 +14,7 @@
 //
 // No grid barriers: activations travel as flag-in-data cells (ll.h), and a
 // workgroup waits only for the cells it reads.  The split merge of a group of
-// query heads is done by its split-0 unit, which polls the other splits'
+// query heads is done by one of its units (merger_split), which polls the other splits'
 // partial cells (by the last unit to count itself when units outnumber the
 // workgroups), and the step's closing work (greedy choice, position) by the
 // last workgroup to leave the launch.  Every wait is bounded (ll.h).
@@ -114,6 +114,14 @@ __device__ __forceinline__ void wg_rows(const Phase &ph, int &r0, int &r1) {
 }
 constexpr int kVC = 4;
 constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
+#ifndef MR_STEP_ENTRY_DEPTH
+#define MR_STEP_ENTRY_DEPTH 2
+#endif
+// Of them, the jobs issued before the phase's input is staged: the rest go
+// out once it is (a CU returns loads in issue order, so the control waves'
+// polls wait behind whatever the stream waves have in flight; two of four
+// measured fastest, none much slower).
+constexpr int kEntryDepth = MR_STEP_ENTRY_DEPTH;
 
 struct GemvGeo {
     int r0, r1;      // rows of this workgroup
@@ -346,6 +354,7 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
     } else {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
+            if (d >= kEntryDepth) break;
             issue<M>(buf[d], is, w0, w1, g, s.dummy);
             advance(is, g.cpr);
         }
@@ -354,6 +363,14 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
 #pragma unroll
     for (int i = 0; i < NC; ++i)
         if (status[i] == ~0u) return false;
+    if (!ctl) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            if (d < kEntryDepth) continue;
+            issue<M>(buf[d], is, w0, w1, g, s.dummy);
+            advance(is, g.cpr);
+        }
+    }
     float scale = 1.0f;
     if (mine && ph.pro == PRO_RMS) {
         float ss = red[0];
@@ -472,6 +489,11 @@ __device__ __forceinline__ void embed_phase(const Phase &ph, const StepArgs &s, 
     if ((threadIdx.x & 63) == 0) wg_mark(s, ep_y);
 }
 
+// The split whose unit merges unit group v (KV head, query-head group).
+// Split 0 for every group puts a layer's mergers on one XCD; spreading them
+// (split v % splits, two per XCD) measured 4 % slower per step.
+__host__ __device__ __forceinline__ int merger_split(int, int) { return 0; }
+
 // Attention units (kv head, group of its query heads, split) dealt to the
 // workgroups write their partials; one unit per group merges the group's
 // splits (kernels.cl:58-107) and reports it in the group's progress word.
@@ -507,7 +529,7 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
                             ? attn_unit_waves<D, NT>(ph.at, g, kh, hs, split, lds, io)
                             : attn_unit<D, true, NT>(ph.at, g, kh, split, lds, io);
         if (!ok) return false;
-        // One unit per workgroup: the unit of split 0 merges its group,
+        // One unit per workgroup: the unit of split merger_split merges its group,
         // polling the other splits' partial cells as they land (no counter,
         // and no unit waits for its stores to be acknowledged).  With more
         // units than workgroups a workgroup runs several units in turn, and a
@@ -515,7 +537,7 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
         // unit to count itself merges.  (Written as below, this measured 2 %
         // faster than with the test hoisted out of the loop.)
         if (units <= (int)gridDim.x) {
-            if (split == 0) {
+            if (split == merger_split(v, splits)) {
                 // the unit's LDS reads fed its stores, so its LDS is free once
                 // every wave is here; the fence keeps the merge's LDS accesses
                 // below the barrier
@@ -675,13 +697,16 @@ const void *step_kernel(int dtype, int dim) {
 
 void step_attention_mergers(const AttnStepArgs &a, int grid, unsigned *mask) {
     // the unit -> (pair, split) deal of attn_phase; with one unit per
-    // workgroup, the unit of split 0 of each (KV head, group) merges it
+    // workgroup, the unit of split merger_split of each (KV head, group)
+    // merges it
     const int splits = a.splits, hg = a.head_groups, pairs = a.kv_heads * splits, units = pairs * hg;
     if (units > grid || grid > kSkipBits) return;
     const bool xcd_map = hg > 1 && pairs % kXcds == 0;
     for (int u = 0; u < units; ++u) {
         const int pair = xcd_map ? u % kXcds + kXcds * (u / kXcds / hg) : u / hg;
-        if (pair % splits == 0) mask[u >> 5] |= 1u << (u & 31);
+        const int hs = xcd_map ? (u / kXcds) % hg : u % hg;
+        const int kh = pair / splits, split = pair % splits;
+        if (split == merger_split(kh * hg + hs, splits)) mask[u >> 5] |= 1u << (u & 31);
     }
 }
 
