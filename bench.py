@@ -242,6 +242,8 @@ def main():
     ap.add_argument("--summarize-trace", metavar="CSV", default=None,
                     help="print the per-kernel summary of the last --steps decode steps in a rocprofv3 kernel "
                          "trace of this bench and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time the prompt's prefill only, print its JSON summary and exit (for counter profiles)")
     ap.add_argument("--trace-steps", type=int, default=0,
                     help="after the prefill, trace this many persistent decode steps phase by phase, print the "
                          "per-phase anatomy (markdown) and exit")
@@ -292,6 +294,13 @@ def main():
     pf_flops = prefill_flops(cfg, wl["context"], prompt_len) if gqa else None
     log(f"prefill {prompt_len / prefill_s:.1f} tok/s" +
         (f", {pf_flops / prefill_s / 1e12:.1f} TFLOP/s algorithmic" if pf_flops else ""))
+    if args.prefill_only:
+        print(json.dumps({"workload": name, "prompt": prompt_len, "mode": prefill_mode,
+                          "tok_s": round(prompt_len / prefill_s, 1), "seconds": round(prefill_s, 4),
+                          "algorithmic_tflop": round(pf_flops / 1e12, 3) if pf_flops else None,
+                          "achieved_tflops": round(pf_flops / prefill_s / 1e12, 1) if pf_flops else None}),
+              flush=True)
+        return 0
     if args.trace_steps:
         eng.generate_greedy(args.warmup + 1, -1)    # first launches outside the traced steps
         return trace_summary(model, cfg, args.trace_steps, args.trace_dump)
