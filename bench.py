@@ -17,11 +17,14 @@ token, algorithmic bytes B(P) averaged over the decode positions); in the graph
 and eager modes the fused RMSNorm + gate/up GEMV + SwiGLU (46.2 MB per launch).
 `cpu_baseline` times the oracle (a C restatement of the
 reference's OpenCL kernels, FP32 weights resident, the reference's token loop)
-on this host's cores for a bounded sample.
+on this host's cores for a bounded sample of steps at the GPU's decode positions
+(the oracle's K/V rings seated with synthetic rows up to the prompt length), with
+the host's CPU model.
 """
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -124,21 +127,45 @@ def gate_up_bytes(cfg):
     return 2 * f * h * 2 + h * 4 + h * 4 + f * 4   # weights + hidden + gain + activations out
 
 
-def cpu_baseline(name, wl, weights, budget_s):
-    """Oracle token steps on the host (FP32 weights resident, all affine cores)."""
+def host_cpu():
+    """Model name of the host CPU (the first `model name` of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(name, wl, weights, budget_s, position):
+    """Oracle token steps on the host (FP32 weights resident, all affine cores),
+    at the GPU's decode positions: the oracle is seated at `position` with
+    synthetic K/V rows in every ring (GQA families), so each step attends over
+    the same row counts as the GPU's decode step there."""
     from oracle import kernels as K
     from oracle.model import OracleModel
     widened = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
     model = OracleModel(wl["config"], widened, context_length=wl["context"])
     ids = synthetic.prompt_ids(wl["config"]["vocab_size"], 256, wl["seed"])
+    try:
+        model.seat(position, seed=wl["seed"])
+        seated = True
+    except ValueError:
+        seated = False
+    start = model.position
     model.step(int(ids[0]))          # first touch of every page of the weights
     n, t0 = 0, time.perf_counter()
     while n < 255 and (n < 4 or time.perf_counter() - t0 < budget_s):
         model.step(int(ids[n + 1]))
         n += 1
     elapsed = time.perf_counter() - t0
+    where = (f"positions {start + 1}..{start + n}, rings seated with synthetic K/V rows" if seated
+             else f"positions {start + 1}..{start + n}")
     return {"value": round(n / elapsed, 3), "unit": "tok/s", "cores": K.threads(), "kind": "port",
-            "sample": f"{n} token steps (positions 1..{n}) of {name} through the oracle's C restatement of "
+            "cpu": host_cpu(),
+            "sample": f"{n} token steps ({where}) of {name} through the oracle's C restatement of "
                       f"the reference kernels, FP32 weights resident, the reference's token-by-token loop; "
                       f"{elapsed:.1f} s"}
 
@@ -382,7 +409,7 @@ def main():
     }
     if args.cpu_seconds > 0:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(name, wl, weights, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(name, wl, weights, args.cpu_seconds, prompt_len)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -246,10 +246,13 @@ MR_API int mr_model_choices(mr_model *model, int32_t *out, int64_t capacity, int
 /* Phase timeline of the persistent step kernel (diagnostics; no counterpart in
  * the reference).  Runs one greedy decode step at the current position with
  * timestamps (100 MHz device wall clock) written per phase and workgroup:
- * out[(phase * grid + wg) * 3 + {0: phase start, 1: inputs ready,
- * 2: phase exit}].  `capacity` is the number of uint64 in `out`;
- * *phases and *grid receive the program size.  The step advances the sequence
- * like any decode step. */
+ * out[(phase * grid + wg) * 5 + {0: phase entry, 1: input staged, 2: outputs
+ * stored by the last stream wave, 3: by the first stream wave, 4: unused}]
+ * (0 where not stamped); in attention phases 1 is the unit's Q/K/V cells
+ * staged, 2 the workgroup's end of the phase, 3 the unit's partial stored and
+ * 4 a merging unit's first partial cells seen.
+ * `capacity` is the number of uint64 in `out`; *phases and *grid receive the
+ * program size.  The step advances the sequence like any decode step. */
 MR_API int mr_model_trace_step(mr_model *model, uint64_t *out, int64_t capacity, int *phases, int *grid);
 
 /* Device milliseconds of the last mr_model_generate_greedy call (HIP events

@@ -465,7 +465,8 @@ __host__ __device__ constexpr int combine_lds_floats(int G, int splits) {
 // finished costs one round trip.  Writes out[(v*G + g)*D + j] as cells.
 // Returns false (block-uniform) when a wait gave up.
 template <int D, int NT>
-__device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int active, float *lds, const Io &io) {
+__device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int active, float *lds, const Io &io,
+                                              unsigned long long *seen = nullptr) {
     constexpr int C4 = D / 4;
     constexpr int kChunk = 8;
     const int tid = threadIdx.x;
@@ -483,28 +484,38 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int 
     // Loads of splits past `active` (and of non-owner threads) fall outside
     // the head's partials and read zero without touching memory.
     const int limit = active * G * (D + 2);
-    // Round 1: the first chunk of o and this thread's (m, l) pair.
+    auto arrived = [&](const ll::u64x2 (&p)[2]) {
+        return (unsigned)(p[0].x >> 32) == io.ep_out && (unsigned)(p[0].y >> 32) == io.ep_out &&
+               (unsigned)(p[1].x >> 32) == io.ep_out && (unsigned)(p[1].y >> 32) == io.ep_out;
+    };
+    // Round 1: the first chunk of o and this thread's (m, l) pair.  Cells that
+    // arrived are kept: a poll round re-reads only what is still missing.
     {
         const int i = tid < active * G ? tid : active * G;
-        ll::u64x2 ml;
-        bool ready;
-        do {
+        ll::u64x2 ml{0ull, 0ull};
+        unsigned pending = tid < active * G ? 1u << kChunk : 0u;   // bit q: chunk q, bit kChunk: (m, l)
 #pragma unroll
-            for (int q = 0; q < kChunk; ++q) {
-                const int s = owner ? sg + q * SG : active;
-                const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
-                c[q][0] = ll::peek2(base, off, limit);
-                c[q][1] = ll::peek2(base, off + 2, limit);
-            }
-            ml = ll::peek2(base, i * (D + 2), limit);
-            ready = tid >= active * G ||
-                    ((unsigned)(ml.x >> 32) == io.ep_out && (unsigned)(ml.y >> 32) == io.ep_out);
+        for (int q = 0; q < kChunk; ++q) {
+            c[q][0] = c[q][1] = ll::u64x2{0ull, 0ull};
+            if (owner && sg + q * SG < active) pending |= 1u << q;
+        }
+        for (;;) {
 #pragma unroll
             for (int q = 0; q < kChunk; ++q)
-                ready &= !owner || sg + q * SG >= active ||
-                         ((unsigned)(c[q][0].x >> 32) == io.ep_out && (unsigned)(c[q][0].y >> 32) == io.ep_out &&
-                          (unsigned)(c[q][1].x >> 32) == io.ep_out && (unsigned)(c[q][1].y >> 32) == io.ep_out);
-        } while (!ready && ll::backoff(wt));
+                if (pending & (1u << q)) {
+                    const int off = ((sg + q * SG) * G + gh) * (D + 2) + 2 + 4 * j4;
+                    c[q][0] = ll::peek2(base, off, limit);
+                    c[q][1] = ll::peek2(base, off + 2, limit);
+                }
+            if (pending & (1u << kChunk)) ml = ll::peek2(base, i * (D + 2), limit);
+#pragma unroll
+            for (int q = 0; q < kChunk; ++q)
+                if (arrived(c[q])) pending &= ~(1u << q);
+            if ((unsigned)(ml.x >> 32) == io.ep_out && (unsigned)(ml.y >> 32) == io.ep_out)
+                pending &= ~(1u << kChunk);
+            if (!pending || !ll::backoff(wt)) break;
+        }
+        if (seen && tid == 0) *seen = wall_clock64();   // trace: thread 0's first cells in
         if (tid < active * G) {
             w[tid] = __uint_as_float((unsigned)ml.x);
             lv[tid] = __uint_as_float((unsigned)ml.y);
@@ -520,22 +531,25 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = 0; s0 < active; s0 += kChunk * SG) {
         if (s0 > 0) {   // further chunks (more than kChunk splits per thread)
-            bool ready;
-            do {
+            unsigned pending = 0;
 #pragma unroll
-                for (int q = 0; q < kChunk; ++q) {
-                    const int s = owner ? s0 + sg + q * SG : active;
-                    const int off = (s * G + gh) * (D + 2) + 2 + 4 * j4;
-                    c[q][0] = ll::peek2(base, off, limit);
-                    c[q][1] = ll::peek2(base, off + 2, limit);
-                }
-                ready = true;
+            for (int q = 0; q < kChunk; ++q) {
+                c[q][0] = c[q][1] = ll::u64x2{0ull, 0ull};
+                if (owner && s0 + sg + q * SG < active) pending |= 1u << q;
+            }
+            for (;;) {
 #pragma unroll
                 for (int q = 0; q < kChunk; ++q)
-                    ready &= !owner || s0 + sg + q * SG >= active ||
-                             ((unsigned)(c[q][0].x >> 32) == io.ep_out && (unsigned)(c[q][0].y >> 32) == io.ep_out &&
-                              (unsigned)(c[q][1].x >> 32) == io.ep_out && (unsigned)(c[q][1].y >> 32) == io.ep_out);
-            } while (!ready && ll::backoff(wt));
+                    if (pending & (1u << q)) {
+                        const int off = ((s0 + sg + q * SG) * G + gh) * (D + 2) + 2 + 4 * j4;
+                        c[q][0] = ll::peek2(base, off, limit);
+                        c[q][1] = ll::peek2(base, off + 2, limit);
+                    }
+#pragma unroll
+                for (int q = 0; q < kChunk; ++q)
+                    if (arrived(c[q])) pending &= ~(1u << q);
+                if (!pending || !ll::backoff(wt)) break;
+            }
         }
 #pragma unroll
         for (int q = 0; q < kChunk; ++q) {
@@ -628,7 +642,7 @@ __device__ __forceinline__ float keygroups_max(float v) {
 
 template <int D, int NT>
 __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, int kh, int hs, int split, float *lds,
-                                                const Io &io) {
+                                                const Io &io, unsigned long long *staged = nullptr) {
     const AttnStepArgs &a = ka.s;
     constexpr int LPK = D / (4 * kWaveVec);   // lanes per key: 8, 4, 2
     constexpr int KPI = kWave / LPK;          // keys side by side in a wave
@@ -646,38 +660,42 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
     float *wl = wm + NWV * G;         // [NWV][G] per-wave sum
     float *wo = wl + NWV * G;         // [NWV][G][D] per-wave weighted values
     const int newest = g.length - 1;
-    const int d0 = sub * 4 * kWaveVec;   // this lane's first dim
+    // The lane's float4 c holds dims 4 (sub + LPK c) .. + 3: the LPK lanes of a
+    // key read one contiguous 16 LPK-byte span of its row per load.
+    auto dim = [&](int c) { return 4 * (sub + LPK * c); };
 
-    float4 kr[kWaveKeys][kWaveVec], vr[kWaveKeys][kWaveVec];
+    typedef float4 KeyRegs[kWaveKeys][kWaveVec];
+    KeyRegs kr, vr;
     auto key_of = [&](int round, int i) { return t0 + (round * NWV + wave) * RK + i * KPI + kg; };
-    auto fetch = [&](int round) {
+    auto fetch = [&](int round, KeyRegs &kd, KeyRegs &vd) {
 #pragma unroll
         for (int i = 0; i < kWaveKeys; ++i) {
             const int t = key_of(round, i);
             const float *kb = nullptr, *vb = nullptr;
             if (t < t1 && t != newest) {
                 if (t < g.length) {
-                    const int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D + d0;
+                    const int64_t off = (int64_t)((g.start + t) % a.capacity) * kvw + (int64_t)kh * D;
                     kb = a.ring_k + off;
                     vb = a.ring_v + off;
                 } else {
-                    const int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D + d0;
+                    const int64_t off = (int64_t)(t - g.length) * kvw + (int64_t)kh * D;
                     kb = a.extra_k + off;
                     vb = a.extra_v + off;
                 }
             }
 #pragma unroll
             for (int c = 0; c < kWaveVec; ++c) {
-                kr[i][c] = kb ? load_f4(kb + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-                vr[i][c] = vb ? load_f4(vb + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                kd[i][c] = kb ? load_f4(kb + dim(c)) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vd[i][c] = vb ? load_f4(vb + dim(c)) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
     };
     if (t0 >= t1) return true;   // no keys at this position (the newest key is in another split)
     const int per_round = NWV * RK;
     const int rounds = (t1 - t0 + per_round - 1) / per_round;
-    fetch(0);
+    fetch(0, kr, vr);
     if (!prepare<true, NT>(ka, g, kh, G, D, qs, kn, vn, t0, t1, io, hs)) return false;
+    if (staged && tid == 0) *staged = wall_clock64();   // trace: Q/K/V cells in
 
     // scores carry the 1/sqrt(D) of kernels.cl:72 through the queries
     const float inv_root = 1.0f / sqrtf((float)D);
@@ -691,14 +709,14 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
         for (int c = 0; c < kWaveVec; ++c) acc[h][c] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int round = 0; round < rounds; ++round) {
-        if (round > 0) fetch(round);
+        if (round > 0) fetch(round, kr, vr);
 #pragma unroll
         for (int i = 0; i < kWaveKeys; ++i)
             if (key_of(round, i) == newest)
 #pragma unroll
                 for (int c = 0; c < kWaveVec; ++c) {
-                    kr[i][c] = *(const float4 *)(kn + d0 + 4 * c);
-                    vr[i][c] = *(const float4 *)(vn + d0 + 4 * c);
+                    kr[i][c] = *(const float4 *)(kn + dim(c));
+                    vr[i][c] = *(const float4 *)(vn + dim(c));
                 }
 #pragma unroll
         for (int h = 0; h < kWaveUnitMaxG; ++h) {
@@ -706,7 +724,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
             float4 q[kWaveVec];
 #pragma unroll
             for (int c = 0; c < kWaveVec; ++c) {
-                const float4 t = *(const float4 *)(qs + h * D + d0 + 4 * c);
+                const float4 t = *(const float4 *)(qs + h * D + dim(c));
                 q[c] = make_float4(t.x * inv_root, t.y * inv_root, t.z * inv_root, t.w * inv_root);
             }
             float sc[kWaveKeys];
@@ -728,7 +746,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
             mx = keygroups_max<LPK>(mx);
             const float m_new = fmaxf(m_run[h], mx);   // -inf while this wave has seen no key
             const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = m_run[h] == -INFINITY ? 0.0f : __expf(m_run[h] - m_ref);
+            const float alpha = m_run[h] == -INFINITY ? 0.0f : expf(m_run[h] - m_ref);
             float sum = 0.0f;
 #pragma unroll
             for (int c = 0; c < kWaveVec; ++c)
@@ -736,7 +754,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
                                         acc[h][c].w * alpha);
 #pragma unroll
             for (int i = 0; i < kWaveKeys; ++i) {
-                const float p = __expf(sc[i] - m_ref);
+                const float p = expf(sc[i] - m_ref);
                 sum += p;
 #pragma unroll
                 for (int c = 0; c < kWaveVec; ++c) {
@@ -763,7 +781,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
             o.y = keygroups_sum_lanes<LPK>(o.y);
             o.z = keygroups_sum_lanes<LPK>(o.z);
             o.w = keygroups_sum_lanes<LPK>(o.w);
-            if (kg == 0) *(float4 *)(wo + (wave * G + h) * D + d0 + 4 * c) = o;
+            if (kg == 0) *(float4 *)(wo + (wave * G + h) * D + dim(c)) = o;
         }
         if (lane == 0) {
             wm[wave * G + h] = m_run[h];
@@ -781,7 +799,7 @@ __device__ __forceinline__ bool attn_unit_waves(const Args &ka, const Geo &g, in
 #pragma unroll
         for (int w = 0; w < NWV; ++w) {
             const float m = wm[w * G + h];
-            const float f = m == -INFINITY ? 0.0f : __expf(m - M);
+            const float f = m == -INFINITY ? 0.0f : expf(m - M);
             L = fmaf(wl[w * G + h], f, L);
             O = fmaf(wo[(w * G + h) * D + j], f, O);
         }

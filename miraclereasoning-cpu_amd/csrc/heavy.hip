@@ -499,7 +499,7 @@ __global__ void __launch_bounds__(split::kThreads) k_heavy_attn_split(HeavyAttnA
             for (int i = 0; i < kChosenBatch; ++i) {
                 if (i0 + i < keep) {
                     const int b = chosen[i0 + i];
-                    const float p = __expf(sc[b] - m);
+                    const float p = expf(sc[b] - m);
                     const float n = (float)min(a.block, count - b * a.block);
                     o = fmaf(p, vals[i] / n, o);
                     l += p;
@@ -971,7 +971,7 @@ __global__ void __launch_bounds__(kSelThreads) k_heavy_select(HeavySelectArgs a)
         for (int i = 0; i < keep; ++i) {
             const int b = chosen[i];
             const float *vs = b < bt ? a.bsum_v + (int64_t)b * kvw : row_sums + kvw;
-            const float p = __expf(sc[b] - m);
+            const float p = expf(sc[b] - m);
             const float n = (float)min(a.block, count - b * a.block);
             o = fmaf(p, vs[(int64_t)kh * D + j] / n, o);
             l += p;

@@ -64,8 +64,8 @@ __device__ __forceinline__ void partial(const float *q_head, int t0, int t1, Row
         s = att::lanes_sum<LPK>(s == -INFINITY ? 0.0f : s) + (s == -INFINITY ? -INFINITY : 0.0f);
         const float m_new = fmaxf(m, s);
         if (m_new != -INFINITY) {
-            const float alpha = m == -INFINITY ? 0.0f : __expf(m - m_new);
-            const float p = s == -INFINITY ? 0.0f : __expf(s - m_new);
+            const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+            const float p = s == -INFINITY ? 0.0f : expf(s - m_new);
             l = l * alpha + p;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -79,7 +79,7 @@ __device__ __forceinline__ void partial(const float *q_head, int t0, int t1, Row
     }
     // fold the wave's row groups: common max, rescale, sum
     const float M = att::keygroups_max<LPK>(m);
-    const float f = m == -INFINITY ? 0.0f : __expf(m - M);
+    const float f = m == -INFINITY ? 0.0f : expf(m - M);
     const float L = att::keygroups_sum<LPK>(l * f);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -101,14 +101,14 @@ __device__ __forceinline__ void partial(const float *q_head, int t0, int t1, Row
         float o = 0.0f;
 #pragma unroll
         for (int w = 0; w < NWV; ++w)
-            if (wm[w] != -INFINITY) o = fmaf(wo[w][j], __expf(wm[w] - Mb), o);
+            if (wm[w] != -INFINITY) o = fmaf(wo[w][j], expf(wm[w] - Mb), o);
         part[2 + j] = o;
     }
     if (threadIdx.x == 0) {
         float Lb = 0.0f;
 #pragma unroll
         for (int w = 0; w < NWV; ++w)
-            if (wm[w] != -INFINITY) Lb = fmaf(wl[w], __expf(wm[w] - Mb), Lb);
+            if (wm[w] != -INFINITY) Lb = fmaf(wl[w], expf(wm[w] - Mb), Lb);
         part[0] = Mb;
         part[1] = Lb;
     }
@@ -147,7 +147,7 @@ __device__ __forceinline__ void merge(const float *part, int n, int extra, float
         mx = fmaxf(mx, ms);
     }
     const float M = block_max(mx, red);
-    for (int s = tid; s < total; s += kThreads) e[s] = e[s] == -INFINITY ? 0.0f : __expf(e[s] - M);
+    for (int s = tid; s < total; s += kThreads) e[s] = e[s] == -INFINITY ? 0.0f : expf(e[s] - M);
     __syncthreads();
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     float l = 0.0f;

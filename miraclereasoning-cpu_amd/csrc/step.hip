@@ -296,26 +296,36 @@ __device__ __forceinline__ void stage_input(const Phase &ph, const GemvGeo &g, c
             const int gi = 2 * min(base + i * lanes, n2 - 1);
             gv[i] = gain ? make_float2(gmem(gain)[gi], gmem(gain)[gi + 1]) : make_float2(1.0f, 1.0f);
         }
-        ll::u64x2 c[B];
-        bool ready;
-        do {
+        // A poll round re-reads only the pairs still missing (late rounds carry
+        // few bytes and return quickly); an arrived pair goes to xs as read,
+        // and the sum of squares and gains follow in a fixed order.
+        unsigned pending = 0;
 #pragma unroll
-            for (int i = 0; i < B; ++i) c[i] = ll::peek2(ph.x, 2 * (base + i * lanes), 2 * n2);
-            ready = true;
+        for (int i = 0; i < B; ++i)
+            if (base + i * lanes < n2) pending |= 1u << i;
+        for (;;) {
+            ll::u64x2 c[B];
 #pragma unroll
             for (int i = 0; i < B; ++i)
-                ready &= base + i * lanes >= n2 ||
-                         ((unsigned)(c[i].x >> 32) == ep_x && (unsigned)(c[i].y >> 32) == ep_x);
-        } while (!ready && ll::backoff(w));
+                c[i] = pending & (1u << i) ? ll::peek2(ph.x, 2 * (base + i * lanes), 2 * n2) : ll::u64x2{0ull, 0ull};
+#pragma unroll
+            for (int i = 0; i < B; ++i)
+                if ((pending & (1u << i)) && (unsigned)(c[i].x >> 32) == ep_x && (unsigned)(c[i].y >> 32) == ep_x) {
+                    const int idx = base + i * lanes;
+                    *(float2 *)(xs + 2 * idx) =
+                        make_float2(__uint_as_float((unsigned)c[i].x), __uint_as_float((unsigned)c[i].y));
+                    pending &= ~(1u << i);
+                }
+            if (!pending || !ll::backoff(w)) break;
+        }
 #pragma unroll
         for (int i = 0; i < B; ++i) {
             const int idx = base + i * lanes;
             if (idx < n2) {
-                const float a = __uint_as_float((unsigned)c[i].x), b = __uint_as_float((unsigned)c[i].y);
-                ss = fmaf(a, a, ss);
-                ss = fmaf(b, b, ss);
-                xs[2 * idx] = a * gv[i].x;
-                xs[2 * idx + 1] = b * gv[i].y;
+                const float2 v = *(const float2 *)(xs + 2 * idx);
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                *(float2 *)(xs + 2 * idx) = make_float2(v.x * gv[i].x, v.y * gv[i].y);
             }
         }
     }
@@ -505,7 +515,7 @@ __host__ __device__ __forceinline__ int merger_split(int, int) { return 0; }
 // cells' epochs).
 template <int D>
 __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, int pos, unsigned ep_in,
-                                           unsigned ep_out, float *lds) {
+                                           unsigned ep_out, float *lds, unsigned long long *tr) {
     const AttnStepArgs &a = ph.at.s;
     const int splits = a.splits, hg = a.head_groups, pairs = a.kv_heads * splits, units = pairs * hg;
     if ((int)blockIdx.x >= units) return true;
@@ -526,9 +536,10 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
         const int kh = pair / splits, split = pair % splits, v = kh * hg + hs;
         // head_groups > 1 is set only where a group fits the wave unit
         const bool ok = a.heads / (a.kv_heads * hg) <= kWaveUnitMaxG
-                            ? attn_unit_waves<D, NT>(ph.at, g, kh, hs, split, lds, io)
+                            ? attn_unit_waves<D, NT>(ph.at, g, kh, hs, split, lds, io, tr ? tr + 1 : nullptr)
                             : attn_unit<D, true, NT>(ph.at, g, kh, split, lds, io);
         if (!ok) return false;
+        stamp(tr, 3);   // the unit's partial is stored
         // One unit per workgroup: the unit of split merger_split merges its group,
         // polling the other splits' partial cells as they land (no counter,
         // and no unit waits for its stores to be acknowledged).  With more
@@ -543,7 +554,7 @@ __device__ __forceinline__ bool attn_phase(const Phase &ph, const StepArgs &s, i
                 // below the barrier
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-                if (!combine_cells<D, NT>(a, v, active, lds, io)) return false;
+                if (!combine_cells<D, NT>(a, v, active, lds, io, tr ? tr + 4 : nullptr)) return false;
                 // the word is a hint (readers check the cells' epochs): it
                 // need not wait for the merged cells' stores
                 if (threadIdx.x == 0) ll::mark(ph.heads_done + v, ep_out);
@@ -605,8 +616,7 @@ __global__ void __launch_bounds__(NT) k_step(StepArgs s) {
                 ++gemvs;
                 break;
             case PH_ATTN:
-                stamp(tr, 1);
-                ok = attn_phase<D>(ph, s, pos, ep_x, ep_y, lds);
+                ok = attn_phase<D>(ph, s, pos, ep_x, ep_y, lds, tr);
                 break;
         }
         if (!ok) return;

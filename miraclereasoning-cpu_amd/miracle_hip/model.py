@@ -184,7 +184,10 @@ class Engine:
         array [phases, grid, 5] of (phase entry, input staged, outputs stored
         by the last stream wave, outputs stored by the first stream wave) in µs
         relative to the step start (NaN where not recorded), and a fifth field
-        the kernel leaves at zero."""
+        unused there.  In attention phases the fields are (entry, the unit's
+        Q/K/V cells staged, the workgroup's end of the phase (after its merge,
+        for a merging unit), the unit's partial stored, a merging unit's first
+        partial cells seen)."""
         cap = 8 * 1024 * 1024
         buf = np.zeros(cap, np.uint64)
         phases, grid = C.c_int(), C.c_int()
@@ -192,10 +195,8 @@ class Engine:
                "trace step")
         n = self.TRACE_FIELDS
         t = buf[:phases.value * grid.value * n].reshape(phases.value, grid.value, n).astype(np.int64)
-        clock = t[:, :, :4]
-        t0 = clock[0, :, 0].min()
-        out = np.where(clock > 0, (clock - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
-        return np.concatenate([out, t[:, :, 4:].astype(np.float64)], axis=2)
+        t0 = t[0, :, 0].min()
+        return np.where(t > 0, (t - t0) / 100.0, np.nan)   # 100 MHz clock -> µs
 
     def choices(self):
         """Routing decisions of every position so far (heavy-medium-2.0):

@@ -100,6 +100,28 @@ class OracleModel:
         self.failed = False
         self.layers = [dict() for _ in range(self.cfg.layers)]
 
+    def seat(self, position, seed=0):
+        """Place a GQA model (flashnano-1.5 / 1.7 / lite) at `position` with
+        synthetic standard-normal K/V rows in every layer's ring, as if
+        `position` tokens had been pushed: the next step then attends over the
+        same row counts as a decode step at that position.  For timing only;
+        the rows stand for no token sequence."""
+        c = self.cfg
+        if c.family in ("flashnano-1.6", "heavy-medium-2.0", "flashlighting-2.0"):
+            raise ValueError(f"seat: {c.family} keeps state beyond the K/V rings")
+        if not 0 <= position < self.ctx:
+            raise ValueError("seat: position outside the context")
+        rng = np.random.default_rng(seed)
+        self.reset()
+        for layer, state in enumerate(self.layers):
+            ring = state["ring"] = _Ring(min(c.window_of(layer) or self.ctx, self.ctx),
+                                         c.kv_heads_of(layer) * c.head_dim)
+            rows = min(position, ring.capacity)
+            ring.k[:rows] = rng.standard_normal((rows, ring.k.shape[1]), np.float32)
+            ring.v[:rows] = rng.standard_normal((rows, ring.v.shape[1]), np.float32)
+            ring.count = position
+        self.position = position
+
     def _rms(self, x, name, width=None, eps=None):
         c = self.cfg
         return K.rms(x, self.w[name] if name else None, width or c.hidden_size,

@@ -181,6 +181,30 @@ def test_persistent_decode_equals_prefill(backend):
     np.testing.assert_array_equal(np.stack([model.decode(int(i)) for i in ids]), whole)
 
 
+def test_traced_persistent_step_changes_nothing(backend):
+    """A step run with the phase timeline (mr_model_trace_step) decodes like an
+    untraced one: the greedy stream through it equals the untraced stream, and
+    every workgroup stamps every phase's entry."""
+    config = SPLIT_MID
+    weights = synthetic.synthetic_weights(config, 31, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 300, 31)
+    plain = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=1024)
+    plain.prefill(ids)
+    want = plain.engine.generate_greedy(6, -1)
+    traced = MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=1024)
+    assert traced.engine.step_mode() == "persistent"
+    traced.prefill(ids)
+    head = traced.engine.generate_greedy(2, -1)
+    t = traced.engine.trace_step()
+    tail = traced.engine.generate_greedy(3, -1)
+    assert list(head) == list(want[:2]) and list(tail) == list(want[3:6])
+    assert t.ndim == 3 and t.shape[2] == 5
+    assert np.all(np.isfinite(t[:, :, 0]))                # every workgroup enters every phase
+    assert np.all(np.isfinite(t[:, :, 1]).any(axis=1))   # every phase stages inputs on some workgroup
+    assert np.all(np.isfinite(t[:, :, 2]).any(axis=1))   # and ends on some workgroup
+    assert np.all(np.nanmax(t[:, :, 2], axis=1) >= np.nanmin(t[:, :, 0], axis=1))
+
+
 def _heavy_variants():
     from conftest import GOLDEN
     return sorted(p.stem[len("micro_"):] for p in GOLDEN.glob("micro_heavy-medium-2.0*.npz"))

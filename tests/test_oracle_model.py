@@ -117,6 +117,33 @@ def test_oracle_invariants_cache_bounds_and_decode_equals_prefill():
         assert model.position == 0
 
 
+def test_oracle_seat_matches_a_prefilled_model():
+    # seat() stands a model at a position without running the prompt (timing of
+    # decode steps at long positions); with the rings' rows replaced by those a
+    # real prefill left, the next decode must be the prefilled model's, bit for
+    # bit (ring count, start and position agree, also for a wrapped local ring).
+    bundle = presets.micro("flashnano-1.5")
+    weights = synthetic.micro_weights(bundle)
+    ids = [1, 3, 5, 8, 2, 9, 11, 10, 9]
+    real = OracleModel(bundle, weights, context_length=12)
+    real.prefill(ids[:8])
+    seated = OracleModel(bundle, weights, context_length=12)
+    seated.seat(8, seed=3)
+    assert seated.position == 8
+    for a, b in zip(real.layers, seated.layers):
+        assert (a["ring"].count, a["ring"].length, a["ring"].start) == (b["ring"].count, b["ring"].length,
+                                                                        b["ring"].start)
+        assert np.all(b["ring"].k[:b["ring"].length] != 0)
+        b["ring"].k[:] = a["ring"].k
+        b["ring"].v[:] = a["ring"].v
+    np.testing.assert_array_equal(seated.decode(ids[8]), real.decode(ids[8]))
+    with pytest.raises(ValueError):
+        seated.seat(12)
+    latent = presets.micro("flashnano-1.6")
+    with pytest.raises(ValueError, match="beyond the K/V rings"):
+        OracleModel(latent, synthetic.micro_weights(latent), context_length=12).seat(4)
+
+
 def test_oracle_workload_tiny(golden_dir):
     z = np.load(golden_dir / "workload_flashnano-1.5-tiny.npz")
     wl = presets.workload("flashnano-1.5-tiny")
