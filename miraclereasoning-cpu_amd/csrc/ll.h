@@ -148,8 +148,9 @@ __device__ __forceinline__ unsigned word(const unsigned *p) {
 
 // Wait until at least n - slack of words[0..n) reach ep.  Only the first wave
 // of the caller polls (lane `me` < 64 takes words me, me+64, ...; 16 each in
-// flight per round) and it pauses between rounds: every workgroup polls the
-// same few lines, so the poll rate is kept low.
+// flight per round) and it pauses briefly between rounds (64-cycle pauses
+// measured faster than longer ones; the step kernel spreads the workgroups'
+// polls over several copies of its words).
 __device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigned ep, int me, int slack, Wait &w) {
     constexpr int B = 16;
     if (me >= kWave) return;
@@ -166,7 +167,7 @@ __device__ __forceinline__ void wait_words(const unsigned *words, int n, unsigne
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) ready += __shfl_xor(ready, off);
         done = ready >= n - slack;
-        if (!done) __builtin_amdgcn_s_sleep(16);
+        if (!done) __builtin_amdgcn_s_sleep(1);
     } while (!done && backoff(w));
 }
 
