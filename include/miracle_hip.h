@@ -283,6 +283,14 @@ MR_API int mr_debug_fail_next(mr_ctx *ctx);
  * function. */
 MR_API int mr_debug_step_timeout(mr_model *model);
 
+/* Test hook: c[m, n] = a[m, k] . w[n, k]^T (device FP32 a and c, device BF16
+ * w) through the batched-prefill MFMA GEMM in the BF16-term scheme
+ * (scheme 0) or the FP16-term scheme (scheme 1, with the matrix's FP16 scale
+ * computed here; `ascale` is a device workspace of m floats).  Synchronizes.
+ * k must be a multiple of 8.  Not a counterpart of any reference function. */
+MR_API int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *ascale, int m, int n, int k,
+                         int scheme);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,9 @@ struct Weight {
     int dtype = MR_F32;
     int64_t rows = 0, cols = 0;
     bool owned = true;
+    // batched prefill GEMMs: power-of-two scale into FP16 range (0: the BF16
+    // term scheme is used for this matrix)
+    float f16_scale = 0.0f;
     explicit operator bool() const { return ptr != nullptr; }
     const float *f() const { return (const float *)ptr; }
 };

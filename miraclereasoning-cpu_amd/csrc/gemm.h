@@ -1,13 +1,17 @@
 // MFMA GEMM for batched prefill: C[m, n] = A[m, k] . W[n, k]^T with FP32
 // activations, BF16/F16/FP32 weights and FP32-faithful products.
 //
-// The matrix cores multiply BF16 operands exactly into FP32 accumulators.  An
-// FP32 activation is carried as the sum of three BF16 terms (hi + mid + lo,
-// each rounded to nearest even from the remainder of the previous), which
-// leaves about 2^-27 of its value behind; weights are BF16 (one term), F16
-// (two terms, exact: 11 significant bits fit in hi + lo) or FP32 (three
-// terms).  Products of terms whose orders sum to at most 2 are accumulated
-// (3, 5 or 6 MFMAs per tile step), so the result carries FP32-level error.
+// The matrix cores multiply BF16 or FP16 operands exactly into FP32
+// accumulators.  BF16 scheme: an FP32 activation is carried as the sum of
+// three BF16 terms (hi + mid + lo, each rounded to nearest even from the
+// remainder of the previous), which leaves about 2^-27 of its value behind;
+// weights are BF16 (one term), F16 (two terms, exact: 11 significant bits fit
+// in hi + lo) or FP32 (three terms).  Products of terms whose orders sum to
+// at most 2 are accumulated (3, 5 or 6 MFMAs per tile step), so the result
+// carries FP32-level error.  FP16 scheme (BF16 weights): each activation row
+// is scaled by a power of two into FP16 range and carried as hi + lo FP16
+// terms (about 2^-23 of its value left behind), the weights scaled by a power
+// of two are exact in FP16, and two MFMAs per tile step carry the product.
 #pragma once
 
 #include "common.h"
@@ -26,6 +30,12 @@ struct GemmArgs {
     int ldc = 0;
     int m = 0, n = 0, k = 0;     // GEMM_SWIGLU: n = output columns (FFN width)
     float scale = 1.0f;          // GEMM_RESIDUAL: c += scale * (A . W^T)
+    // FP16 terms (BF16 weights only): wscale > 0 is the weights' power-of-two
+    // scale into FP16 range (gemm_f16_weight_scale) and ascale a device
+    // workspace of m floats that receives A's row scales; otherwise (wscale
+    // 0) the BF16 scheme runs.
+    float wscale = 0.0f;
+    float *ascale = nullptr;
 };
 
 // STORE:    c = A . W^T
@@ -33,6 +43,12 @@ struct GemmArgs {
 // SWIGLU:   c = silu(A . Wg^T) * (A . Wu^T), silu(g) = g / (1 + exp(-g))
 // Requires k % 8 == 0, lda % 4 == 0 and 16-byte aligned a and weight rows.
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g);
+
+// The power of two 2^s that puts max |w| of a BF16 matrix of `count` values
+// in [2^13, 2^14) (1 for an all-zero matrix), so that w 2^s is exact in FP16
+// for every |w| >= 2^-31 max |w|; 0 for a matrix holding a non-finite value or
+// another dtype (the FP16 scheme is then not used).  Synchronizes the stream.
+int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count, float *scale);
 
 // Groups of rows with their own weights (the experts of a batched MoE), one
 // launch: group z multiplies rows offset[z] .. offset[z] + count[z] of g.a by

@@ -1,10 +1,16 @@
-// MFMA GEMM with FP32-faithful BF16 term products (batched prefill projections).
+// MFMA GEMM with FP32-faithful term products (batched prefill projections).
 //
 // Workgroup tile 128 x 128 outputs, k-steps of 32, four waves each owning a
-// 64 x 64 quadrant as 4 x 4 tiles of v_mfma_f32_16x16x32_bf16.  Each k-step the
-// workgroup loads its A rows (FP32) and W rows (BF16/F16/FP32) into registers,
-// splits them into BF16 terms while writing LDS, and prefetches the next
+// 64 x 64 quadrant as 4 x 4 tiles of v_mfma_f32_16x16x32_{bf16,f16}.  Each
+// k-step the workgroup loads its A rows (FP32) and W rows (BF16/F16/FP32) into
+// registers, splits them into terms while writing LDS, and prefetches the next
 // k-step's rows while the matrix cores work on this one.
+//
+// Two term schemes.  BF16 terms: A as hi + mid + lo (three MFMAs against BF16
+// weights).  FP16 terms (BF16 weights with a scale, gemm.h): A row r scaled by
+// a power of two 2^t_r into FP16 range is hi + lo (11 + 11 significant bits),
+// the weights scaled by 2^s are exact in FP16, so two MFMAs per tile step
+// carry the product; the epilogue multiplies by 2^-t_r 2^-s (exact).
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (wave64): lane l supplies
 // A[l % 16][8 (l / 16) + i] and B[8 (l / 16) + i][l % 16] for i < 8, and holds
@@ -13,6 +19,9 @@
 // bytes of one LDS row.
 #include "gemm.h"
 
+#include <algorithm>
+#include <cstring>
+
 namespace mr {
 namespace {
 
@@ -20,6 +29,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
@@ -129,6 +139,50 @@ __device__ __forceinline__ void store_a(__bf16 (*as)[kBM][kPitch], const ARegs &
     }
 }
 
+// x (already scaled into FP16 range) = hi + lo; x - hi is exact in FP32.
+__device__ __forceinline__ void split2h(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// FP16-term layout: A rows scaled by their row scale (rs[i] for row
+// tid / 8 + 32 i), two planes.
+__device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][kPitch], const ARegs &r, const float (&rs)[4]) {
+    const int tid = threadIdx.x;
+    const int col = (tid & 7) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = (tid >> 3) + 32 * i;
+        const float x[4] = {r.v[i].x * rs[i], r.v[i].y * rs[i], r.v[i].z * rs[i], r.v[i].w * rs[i]};
+        f16x4 h, l;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            _Float16 th, tl;
+            split2h(x[e], th, tl);
+            h[e] = th;
+            l[e] = tl;
+        }
+        *(f16x4 *)&as[0][row][col] = h;
+        *(f16x4 *)&as[1][row][col] = l;
+    }
+}
+
+// BF16 weights times the matrix scale, exact in FP16.
+__device__ __forceinline__ void store_w_h(_Float16 (*bs)[kPitch], const WRegs<MR_BF16> &r, float ws) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int idx = tid + kThreads * i;
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const unsigned bits = (r.v[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            h[e] = (_Float16)(__uint_as_float(bits << 16) * ws);
+        }
+        *(f16x8 *)&bs[idx >> 2][(idx & 3) * 8] = h;
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ void store_w(__bf16 (*bs)[kBN][kPitch], const WRegs<DT> &r) {
     const int tid = threadIdx.x;
@@ -178,6 +232,47 @@ __device__ __forceinline__ void store_w(__bf16 (*bs)[kBN][kPitch], const WRegs<D
 
 __device__ __forceinline__ f32x4 mfma(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// The epilogue of both schemes: rows m0.., columns n0.. of the tile from the
+// accumulators times `unscale` (per output row; 1 for the BF16 scheme).
+template <int EPI, typename Unscale>
+__device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, const f32x4 (&acc)[4][4],
+                                           Unscale unscale) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 15;
+    // C[4 (lane / 16) + j][lane % 16] of each 16 x 16 tile
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = m0 + wm * 64 + mi * 16 + (lane >> 4) * 4 + j;
+            if (row >= g.m) continue;
+            const float u = unscale(row);
+            float *crow = g.c + (int64_t)row * g.ldc;
+            if constexpr (EPI == GEMM_SWIGLU) {
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    const int f = n0 + wn * 32 + ni * 16 + lr;
+                    if (f >= g.n) continue;
+                    const float gt = acc[mi][ni][j] * u, up = acc[mi][ni + 2][j] * u;
+                    crow[f] = (gt / (1.0f + expf(-gt))) * up;
+                }
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const int col = n0 + wn * 64 + ni * 16 + lr;
+                    if (col >= g.n) continue;
+                    const float v = acc[mi][ni][j] * u;
+                    if constexpr (EPI == GEMM_RESIDUAL) crow[col] = crow[col] + g.scale * v;
+                    else crow[col] = v;
+                }
+            }
+        }
+    }
 }
 
 // One 128 x 128 output tile (rows m0.., columns n0..) of g.
@@ -243,33 +338,99 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0) {
         }
     }
 
-    // C[4 (lane / 16) + j][lane % 16] of each 16 x 16 tile
+    gemm_store<EPI>(g, m0, n0, acc, [](int) { return 1.0f; });
+}
+
+// One 128 x 128 output tile in FP16 terms (BF16 weights, g.wscale > 0,
+// g.ascale holding the row scales).
+template <int EPI>
+__device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
+    __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][kPitch];
+    __shared__ __attribute__((aligned(16))) _Float16 bs[kBN][kPitch];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 15, lk = (lane >> 4) * 8;
+    const int nk = (g.k + kBK - 1) / kBK;
+    float rs[4];   // scales of this thread's A rows
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + (tid >> 3) + 32 * i;
+        rs[i] = row < g.m ? g.ascale[row] : 1.0f;
+    }
+
+    f32x4 acc[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = m0 + wm * 64 + mi * 16 + (lane >> 4) * 4 + j;
-            if (row >= g.m) continue;
-            float *crow = g.c + (int64_t)row * g.ldc;
-            if constexpr (EPI == GEMM_SWIGLU) {
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    const int f = n0 + wn * 32 + ni * 16 + lr;
-                    if (f >= g.n) continue;
-                    const float gt = acc[mi][ni][j], up = acc[mi][ni + 2][j];
-                    crow[f] = (gt / (1.0f + expf(-gt))) * up;
-                }
-            } else {
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    ARegs ar;
+    WRegs<MR_BF16> wr;
+    load_a(g, m0, 0, ar);
+    load_w<MR_BF16, EPI>(g, n0, 0, wr);
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
+        store_a_h(as, ar, rs);
+        store_w_h(bs, wr, g.wscale);
+        lds_barrier();
+        if (kt + 1 < nk) {
+            load_a(g, m0, (kt + 1) * kBK, ar);
+            load_w<MR_BF16, EPI>(g, n0, (kt + 1) * kBK, wr);
+        }
+        f16x8 bf[4];
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    const int col = n0 + wn * 64 + ni * 16 + lr;
-                    if (col >= g.n) continue;
-                    if constexpr (EPI == GEMM_RESIDUAL) crow[col] = crow[col] + g.scale * acc[mi][ni][j];
-                    else crow[col] = acc[mi][ni][j];
-                }
-            }
+        for (int ni = 0; ni < 4; ++ni) bf[ni] = *(const f16x8 *)&bs[wn * 64 + ni * 16 + lr][lk];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            const f16x8 lo = *(const f16x8 *)&as[1][wm * 64 + mi * 16 + lr][lk];
+            const f16x8 hi = *(const f16x8 *)&as[0][wm * 64 + mi * 16 + lr][lk];
+            // the smaller term first
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
         }
     }
+    const float inv_w = 1.0f / g.wscale;
+    gemm_store<EPI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
+}
+
+template <int DT, int EPI>
+__global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
+    gemm_tile_h<EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
+}
+
+// Row scales of A for the FP16 terms: 2^t with max_k |a[r][k]| 2^t in
+// [2^13, 2^14) (1 for an all-zero or non-finite row).  One wave per row.
+__global__ void __launch_bounds__(256) k_row_scale(const float *a, int lda, int m, int k, float *scale) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float *r = a + (int64_t)row * lda;
+    float mx = 0.0f;
+    for (int c = 4 * lane; c < k; c += 4 * kWave) {
+        const float4 v = load_f4(r + c);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) {
+        int e = 0;
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            frexpf(mx, &e);                     // mx = f 2^e, f in [0.5, 1)
+            e = min(max(14 - e, -126), 126);    // mx 2^(14 - e) in [2^13, 2^14)
+        }
+        scale[row] = ldexpf(1.0f, e);
+    }
+}
+
+// max |w| over a BF16 array as the bits of a non-negative float (atomic max
+// on the bit patterns, which order like the values).
+__global__ void __launch_bounds__(256) k_abs_max_bf16(const uint16_t *w, int64_t count, unsigned *out) {
+    unsigned mx = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        mx = max(mx, (unsigned)(w[i] & 0x7fffu) << 16);
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, off));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, mx);
 }
 
 template <int DT, int EPI>
@@ -309,6 +470,17 @@ template <int DT>
 int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
     const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
     const dim3 grid(ceil_div(g.n, cols), ceil_div(g.m, kBM));
+    if (DT == MR_BF16 && g.wscale > 0.0f) {
+        k_row_scale<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale);
+        switch (epi) {
+            case GEMM_STORE: k_gemm_h<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(g); break;
+            case GEMM_RESIDUAL: k_gemm_h<DT, GEMM_RESIDUAL><<<grid, kThreads, 0, s>>>(g); break;
+            case GEMM_SWIGLU: k_gemm_h<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(g); break;
+            default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
+        }
+        MR_LAUNCHED("enqueue MFMA GEMM (FP16 terms)");
+        return MR_OK;
+    }
     switch (epi) {
         case GEMM_STORE: k_gemm<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(g); break;
         case GEMM_RESIDUAL: k_gemm<DT, GEMM_RESIDUAL><<<grid, kThreads, 0, s>>>(g); break;
@@ -336,6 +508,35 @@ int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const Ge
     return fail(MR_ERR_INVALID, "grouped gemm: unknown weight dtype");
 }
 
+int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count, float *scale) {
+    MR_REQUIRE(scale && (w || count == 0) && count >= 0, "f16 weight scale: bad arguments");
+    *scale = 0.0f;
+    if (dtype != MR_BF16 || count == 0) return MR_OK;
+    unsigned *dev = nullptr;
+    MR_HIP(hipMalloc((void **)&dev, sizeof(unsigned)), "f16 weight scale");
+    unsigned bits = 0;
+    hipError_t e = hipMemsetAsync(dev, 0, sizeof(unsigned), s);
+    if (e == hipSuccess) {
+        const int64_t blocks = std::min<int64_t>(ceil_div(count, (int64_t)256 * 16), 4096);
+        k_abs_max_bf16<<<(int)std::max<int64_t>(blocks, 1), 256, 0, s>>>((const uint16_t *)w, count, dev);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(&bits, dev, sizeof(unsigned), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(dev);
+    MR_HIP(e, "f16 weight scale");
+    float mx;
+    memcpy(&mx, &bits, sizeof(mx));
+    if (!(mx <= 3.0e38f)) return MR_OK;   // inf or NaN: not eligible
+    int ex = 0;
+    if (mx > 0.0f) {
+        frexpf(mx, &ex);
+        ex = std::min(std::max(14 - ex, -126), 126);
+    }
+    *scale = ldexpf(1.0f, ex);
+    return MR_OK;
+}
+
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
     MR_REQUIRE(g.a && g.w && g.c && g.m > 0 && g.n > 0 && g.k > 0, "gemm: bad arguments");
     MR_REQUIRE(epilogue != GEMM_SWIGLU || g.w2, "gemm: SwiGLU needs gate and up weights");
@@ -343,6 +544,7 @@ int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
     MR_REQUIRE(((uintptr_t)g.a & 15) == 0 && ((uintptr_t)g.w & 15) == 0 && ((uintptr_t)g.w2 & 15) == 0,
                "gemm: operands must be 16-byte aligned");
     MR_REQUIRE(g.ldc >= g.n, "gemm: output rows too short");
+    MR_REQUIRE(g.wscale <= 0.0f || (g.dtype == MR_BF16 && g.ascale), "gemm: FP16 terms need BF16 weights and a row-scale workspace");
     MR_REQUIRE(ceil_div(g.m, kBM) <= 65535, "gemm: too many rows");
     switch (g.dtype) {
         case MR_BF16: return launch_dt<MR_BF16>(s, epilogue, g);

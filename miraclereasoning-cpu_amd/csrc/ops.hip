@@ -2,6 +2,7 @@
 // reference's argument lists.  These serve HIPBackend's op surface (the drop-in
 // for OpenCLBackend); the fused decode step lives in engine.hip.
 #include "attention.h"
+#include "gemm.h"
 #include "linear.h"
 
 namespace mr {
@@ -307,6 +308,23 @@ int mr_attention_noalloc(mr_ctx *ctx, const float *q, const float *k, const floa
     pr.heads = heads; pr.kv_heads = kv_heads; pr.dim = dim; pr.capacity = capacity;
     pr.start = start; pr.length = length; pr.extra_length = extra_length; pr.out = y;
     return launch_attention_op_noalloc(ctx, pr);
+}
+
+int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *ascale, int m, int n, int k,
+                  int scheme) {
+    OP_BEGIN("debug gemm");
+    MR_REQUIRE(a && w && c && m > 0 && n > 0 && k > 0 && k % 8 == 0 && (scheme == 0 || (scheme == 1 && ascale)),
+               "debug gemm: bad arguments");
+    GemmArgs g;
+    g.a = a; g.lda = k; g.w = w; g.dtype = MR_BF16; g.c = c; g.ldc = n; g.m = m; g.n = n; g.k = k;
+    if (scheme == 1) {
+        MR_TRY(gemm_f16_weight_scale(s, w, MR_BF16, (int64_t)n * k, &g.wscale));
+        MR_REQUIRE(g.wscale > 0.0f, "debug gemm: weights not eligible for FP16 terms");
+        g.ascale = ascale;
+    }
+    MR_TRY(launch_gemm(s, GEMM_STORE, g));
+    MR_HIP(hipStreamSynchronize(s), "debug gemm");
+    return MR_OK;
 }
 
 }  // extern "C"

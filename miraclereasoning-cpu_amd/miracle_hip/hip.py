@@ -101,6 +101,7 @@ _SIGNATURES = {
     "mr_model_time_kernel": [_P, _i, _i, C.POINTER(C.c_float)],
     "mr_debug_fail_next": [_P],
     "mr_debug_step_timeout": [_P],
+    "mr_debug_gemm": [_P, _P, _P, _P, _P, _i, _i, _i, _i],
 }
 
 _lib = None
@@ -396,6 +397,19 @@ class HIPBackend:
         _check(self.lib.mr_mix(self.ctx, probs.handle, values.handle,
                                extra_values.handle if extra_values is not None else values.handle, out.handle,
                                heads, kv_heads, dim, values.shape[0], start, length, extra_length), "enqueue mix")
+        return out
+
+    def debug_gemm(self, a, weight, scheme):
+        """a . weight^T through the batched-prefill MFMA GEMM (test hook):
+        scheme 0 = BF16 terms, 1 = FP16 terms; ``weight`` a BF16 tensor."""
+        self._owns(a, weight)
+        if weight.dtype != "bf16" or len(a.shape) != 2 or len(weight.shape) != 2 or a.shape[1] != weight.shape[1]:
+            raise ValueError("debug_gemm needs a[m,k] and a BF16 weight[n,k]")
+        m, k = a.shape
+        n = weight.shape[0]
+        out, ws = self.empty((m, n)), self.empty((m,))
+        _check(self.lib.mr_debug_gemm(self.ctx, a.handle, weight.handle, out.handle, ws.handle, m, n, k, scheme),
+               "debug gemm")
         return out
 
     def fail_next(self):

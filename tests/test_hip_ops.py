@@ -188,3 +188,35 @@ def test_copy_bounds_and_ownership(backend):
         b.copy(src, dst, source_offset=3, count=7, target_offset=1)
     with pytest.raises(ValueError):
         b.empty((0, 3))
+
+
+def test_prefill_gemm_term_schemes(backend):
+    """The batched-prefill MFMA GEMM in both term schemes against a float64
+    product, on rows that stress FP16's range: ordinary values, a row far above
+    FP16's maximum (6.5e4), a row of tiny values (1e-20), a zero row and a row
+    mixing magnitudes 1e4 .. 1e-4; BF16 weights of magnitudes 2^-20 .. 8 with
+    a few zeros.  Bound per element: 2^-20 * sum_k |a| |w| (FP32 accumulation
+    of k = 1000 products of operands carried to 2^-22 or better); the FP16
+    scheme's row and matrix scales are powers of two, so they add no error."""
+    from miracle_hip.weights import BF16Array, bf16_bits
+    b, rng = backend, np.random.default_rng(21)
+    m, n, k = 200, 300, 1000
+    a = rng.normal(size=(m, k)).astype(np.float32)
+    a[1] *= 3.0e6
+    a[2] *= 1.0e-20
+    a[3] = 0.0
+    a[4] *= np.exp(rng.uniform(np.log(1e-4), np.log(1e4), size=k)).astype(np.float32)
+    w = rng.normal(size=(n, k)) * np.exp2(rng.integers(-20, 4, size=(n, k)))
+    w[rng.random(size=(n, k)) < 0.01] = 0.0
+    bits = bf16_bits(w.astype(np.float32))
+    wf = BF16Array(bits)[:].astype(np.float64)
+    want = a.astype(np.float64) @ wf.T
+    bound = 2.0 ** -20 * (np.abs(a).astype(np.float64) @ np.abs(wf).T) + 1e-38
+    dev_a, dev_w = b.upload(a), b.upload_weight(BF16Array(bits))
+    for scheme in (0, 1):
+        got = b.read(b.debug_gemm(dev_a, dev_w, scheme)).astype(np.float64)
+        assert np.all(np.isfinite(got)), scheme
+        assert np.all(got[3] == 0.0), scheme
+        worst = np.max(np.abs(got - want) / bound)
+        print("scheme", scheme, "worst error / bound", worst, flush=True)
+        assert worst <= 1.0, scheme
