@@ -21,6 +21,7 @@ struct Weight {
     // batched prefill GEMMs: power-of-two scale into FP16 range (0: the BF16
     // term scheme is used for this matrix)
     float f16_scale = 0.0f;
+    void *f16 = nullptr;   // the matrix times f16_scale in FP16 (owned)
     explicit operator bool() const { return ptr != nullptr; }
     const float *f() const { return (const float *)ptr; }
 };

@@ -335,7 +335,9 @@ Weight *weight_slot(mr_model *m, int kind, int layer, int expert) {
 
 void free_weight(Weight &w) {
     if (w.ptr && w.owned) hipFree(w.ptr);
+    if (w.f16) hipFree(w.f16);
     w.ptr = nullptr;
+    w.f16 = nullptr;
 }
 
 // The five fused kernels of one GQA layer (plus the flashnano-1.6 CBR kernels,
@@ -1152,8 +1154,16 @@ int mr_model_finalize(mr_model *m) {
         MR_TRY(need(L.ffn.up, "ffn.up", i));
         MR_TRY(need(L.ffn.down, "ffn.down", i));
         MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
+        // FP16 copies of the projections for the batched prefill's FP16-term
+        // GEMMs (gate and up share the smaller scale: one per tile)
         for (Weight *w : {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down})
             MR_TRY(gemm_f16_weight_scale(m->ctx->stream, w->ptr, w->dtype, w->rows * w->cols, &w->f16_scale));
+        L.ffn.gate.f16_scale = L.ffn.up.f16_scale = std::min(L.ffn.gate.f16_scale, L.ffn.up.f16_scale);
+        for (Weight *w : {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down})
+            if (w->f16_scale > 0.0f) {
+                MR_TRY(device_alloc(m, (size_t)w->rows * w->cols * 2, &w->f16));
+                MR_TRY(gemm_f16_weight_copy(m->ctx->stream, w->ptr, w->rows * w->cols, w->f16_scale, w->f16));
+            }
         const int kvw = L.kv_heads * hd;
         max_kvw = std::max(max_kvw, kvw);
         max_kvh = std::max(max_kvh, L.kv_heads);
@@ -1343,6 +1353,7 @@ struct PrefillWs {
           *merge_count = nullptr;
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
+    _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
 };
 
 int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
@@ -1372,7 +1383,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->fbuf, light ? r * h : 0}, {(void **)&w->merge_count, light ? r : 0},
         {(void **)&w->flags, light ? r : 0}, {(void **)&w->extra_index, light ? r : 0},
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
-        {(void **)&w->rowscale, r}};
+        {(void **)&w->rowscale, r}, {(void **)&w->planes, r * std::max({h, qd, (size_t)d.ffn_dim})}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
     size_t total = 0;
     for (const Piece &pc : pieces) total += up(pc.floats);
@@ -1490,7 +1501,7 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
     GemmArgs g;
     g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
-    g.m = T; g.n = ld; g.k = h; g.wscale = L.qkv.f16_scale; g.ascale = w.rowscale;
+    g.m = T; g.n = ld; g.k = h; g.wscale = L.qkv.f16_scale; g.wh = L.qkv.f16; g.ascale = w.rowscale; g.ahl_ws = w.planes;
     MR_TRY(launch_gemm(s, GEMM_STORE, g));
     MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
                           d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
@@ -1503,19 +1514,20 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
     GemmArgs o;
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
-    o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale; o.wscale = L.o.f16_scale; o.ascale = w.rowscale;
+    o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale; o.wscale = L.o.f16_scale; o.wh = L.o.f16; o.ascale = w.rowscale; o.ahl_ws = w.planes;
     MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
     MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
     GemmArgs gu;
     gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
     gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
-    // one scale for the gate and up rows of a tile: the smaller keeps both in range
-    gu.wscale = std::min(L.ffn.gate.f16_scale, L.ffn.up.f16_scale); gu.ascale = w.rowscale;
+    gu.wscale = L.ffn.gate.f16_scale; gu.wh = L.ffn.gate.f16; gu.wh2 = L.ffn.up.f16; gu.ascale = w.rowscale;
+    gu.ahl_ws = w.planes;
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;
     dn.m = T; dn.n = h; dn.k = ffn; dn.scale = d.residual_scale; dn.wscale = L.ffn.down.f16_scale;
-    dn.ascale = w.rowscale;
+    dn.wh = L.ffn.down.f16;
+    dn.ascale = w.rowscale; dn.ahl_ws = w.planes;
     return launch_gemm(s, GEMM_RESIDUAL, dn);
 }
 

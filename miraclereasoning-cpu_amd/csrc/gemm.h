@@ -31,11 +31,15 @@ struct GemmArgs {
     int m = 0, n = 0, k = 0;     // GEMM_SWIGLU: n = output columns (FFN width)
     float scale = 1.0f;          // GEMM_RESIDUAL: c += scale * (A . W^T)
     // FP16 terms (BF16 weights only): wscale > 0 is the weights' power-of-two
-    // scale into FP16 range (gemm_f16_weight_scale) and ascale a device
-    // workspace of m floats that receives A's row scales; otherwise (wscale
-    // 0) the BF16 scheme runs.
+    // scale into FP16 range (gemm_f16_weight_scale) and wh (wh2: SwiGLU up
+    // rows) the weights converted with it; ascale (m floats) and ahl_ws
+    // (2 m k halves) are device workspaces that receive A's row scales and its
+    // hi and lo planes.  Otherwise (wscale 0) the BF16 scheme runs.
     float wscale = 0.0f;
+    const void *wh = nullptr, *wh2 = nullptr;   // the weights times wscale in FP16 (gemm_f16_weight_copy)
     float *ascale = nullptr;
+    _Float16 *ahl_ws = nullptr;
+    const _Float16 *ahl = nullptr;   // set by launch_gemm for the kernel
 };
 
 // STORE:    c = A . W^T
@@ -49,6 +53,10 @@ int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g);
 // for every |w| >= 2^-31 max |w|; 0 for a matrix holding a non-finite value or
 // another dtype (the FP16 scheme is then not used).  Synchronizes the stream.
 int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count, float *scale);
+
+// dst[i] = FP16(w[i] * scale) for `count` BF16 values (exact for a scale from
+// gemm_f16_weight_scale, or a smaller power of two).
+int gemm_f16_weight_copy(hipStream_t s, const void *w, int64_t count, float scale, void *dst);
 
 // Groups of rows with their own weights (the experts of a batched MoE), one
 // launch: group z multiplies rows offset[z] .. offset[z] + count[z] of g.a by

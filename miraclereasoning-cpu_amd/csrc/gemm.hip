@@ -145,41 +145,13 @@ __device__ __forceinline__ void split2h(float x, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
-// FP16-term layout: A rows scaled by their row scale (rs[i] for row
-// tid / 8 + 32 i), two planes.
-__device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][kPitch], const ARegs &r, const float (&rs)[4]) {
-    const int tid = threadIdx.x;
-    const int col = (tid & 7) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = (tid >> 3) + 32 * i;
-        const float x[4] = {r.v[i].x * rs[i], r.v[i].y * rs[i], r.v[i].z * rs[i], r.v[i].w * rs[i]};
-        f16x4 h, l;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            _Float16 th, tl;
-            split2h(x[e], th, tl);
-            h[e] = th;
-            l[e] = tl;
-        }
-        *(f16x4 *)&as[0][row][col] = h;
-        *(f16x4 *)&as[1][row][col] = l;
-    }
-}
-
-// BF16 weights times the matrix scale, exact in FP16.
-__device__ __forceinline__ void store_w_h(_Float16 (*bs)[kPitch], const WRegs<MR_BF16> &r, float ws) {
+// FP16 weight rows (converted once, gemm_f16_weight_copy) as loaded.
+__device__ __forceinline__ void store_w_h(_Float16 (*bs)[kPitch], const WRegs<MR_BF16> &r) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int idx = tid + kThreads * i;
-        f16x8 h;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const unsigned bits = (r.v[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-            h[e] = (_Float16)(__uint_as_float(bits << 16) * ws);
-        }
-        *(f16x8 *)&bs[idx >> 2][(idx & 3) * 8] = h;
+        *(u32x4 *)&bs[idx >> 2][(idx & 3) * 8] = r.v[i];
     }
 }
 
@@ -341,8 +313,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0) {
     gemm_store<EPI>(g, m0, n0, acc, [](int) { return 1.0f; });
 }
 
-// One 128 x 128 output tile in FP16 terms (BF16 weights, g.wscale > 0,
-// g.ascale holding the row scales).
+// A's FP16 planes of a k-step: thread t holds 16 bytes of plane i / 2, rows
+// (t / 4) + 64 (i % 2), halves 8 (t % 4) .. + 7.
+struct AHRegs {
+    u32x4 v[4];
+};
+
+__device__ __forceinline__ void load_a_h(const GemmArgs &g, int m0, int k0, AHRegs &r) {
+    const int tid = threadIdx.x;
+    const int col = k0 + (tid & 3) * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + (tid >> 2) + 64 * (i & 1);
+        const _Float16 *plane = g.ahl + (int64_t)(i >> 1) * g.m * g.k;
+        if (row < g.m && col < g.k) r.v[i] = *gmem((const u32x4 *)(plane + (int64_t)row * g.k + col));
+        else r.v[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+__device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][kPitch], const AHRegs &r) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(u32x4 *)&as[i >> 1][(tid >> 2) + 64 * (i & 1)][(tid & 3) * 8] = r.v[i];
+}
+
+// One 128 x 128 output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
+// planes and row scales from k_row_split, the weights' FP16 copy).  (Two LDS
+// stages with one barrier per k-step measured slower: 60 KB of LDS per
+// workgroup halves the workgroups per CU.)
 template <int EPI>
 __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][kPitch];
@@ -352,12 +350,6 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 15, lk = (lane >> 4) * 8;
     const int nk = (g.k + kBK - 1) / kBK;
-    float rs[4];   // scales of this thread's A rows
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = m0 + (tid >> 3) + 32 * i;
-        rs[i] = row < g.m ? g.ascale[row] : 1.0f;
-    }
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -365,17 +357,17 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    ARegs ar;
+    AHRegs ar;
     WRegs<MR_BF16> wr;
-    load_a(g, m0, 0, ar);
+    load_a_h(g, m0, 0, ar);
     load_w<MR_BF16, EPI>(g, n0, 0, wr);
     for (int kt = 0; kt < nk; ++kt) {
         if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
-        store_a_h(as, ar, rs);
-        store_w_h(bs, wr, g.wscale);
+        store_a_h(as, ar);
+        store_w_h(bs, wr);
         lds_barrier();
         if (kt + 1 < nk) {
-            load_a(g, m0, (kt + 1) * kBK, ar);
+            load_a_h(g, m0, (kt + 1) * kBK, ar);
             load_w<MR_BF16, EPI>(g, n0, (kt + 1) * kBK, wr);
         }
         f16x8 bf[4];
@@ -401,9 +393,12 @@ __global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
     gemm_tile_h<EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
 }
 
-// Row scales of A for the FP16 terms: 2^t with max_k |a[r][k]| 2^t in
-// [2^13, 2^14) (1 for an all-zero or non-finite row).  One wave per row.
-__global__ void __launch_bounds__(256) k_row_scale(const float *a, int lda, int m, int k, float *scale) {
+// A in FP16 terms, once per GEMM: row r's scale 2^t (max_k |a[r][k]| 2^t in
+// [2^13, 2^14); 1 for an all-zero or non-finite row) into scale[r], and
+// a[r][k] 2^t = hi + lo into planes hl[0][r][k], hl[1][r][k].  One wave per
+// row (k a multiple of 4).
+__global__ void __launch_bounds__(256) k_row_split(const float *a, int lda, int m, int k, float *scale,
+                                                   _Float16 *hl) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= m) return;
     const float *r = a + (int64_t)row * lda;
@@ -413,14 +408,33 @@ __global__ void __launch_bounds__(256) k_row_scale(const float *a, int lda, int 
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     mx = wave_max(mx);
-    if (lane == 0) {
-        int e = 0;
-        if (mx > 0.0f && mx <= 3.0e38f) {
-            frexpf(mx, &e);                     // mx = f 2^e, f in [0.5, 1)
-            e = min(max(14 - e, -126), 126);    // mx 2^(14 - e) in [2^13, 2^14)
-        }
-        scale[row] = ldexpf(1.0f, e);
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) {
+        frexpf(mx, &e);                     // mx = f 2^e, f in [0.5, 1)
+        e = min(max(14 - e, -126), 126);    // mx 2^(14 - e) in [2^13, 2^14)
     }
+    const float sc = ldexpf(1.0f, e);
+    if (lane == 0) scale[row] = sc;
+    _Float16 *hi = hl + (int64_t)row * k, *lo = hl + (int64_t)m * k + (int64_t)row * k;
+    for (int c = 4 * lane; c < k; c += 4 * kWave) {
+        const float4 v = load_f4(r + c);
+        const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        f16x4 h, l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            _Float16 th, tl;
+            split2h(x[i], th, tl);
+            h[i] = th;
+            l[i] = tl;
+        }
+        *(f16x4 *)(hi + c) = h;
+        *(f16x4 *)(lo + c) = l;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_bf16_to_f16(const uint16_t *w, int64_t count, float scale, _Float16 *dst) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = (_Float16)(__uint_as_float((unsigned)w[i] << 16) * scale);
 }
 
 // max |w| over a BF16 array as the bits of a non-negative float (atomic max
@@ -471,11 +485,15 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
     const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
     const dim3 grid(ceil_div(g.n, cols), ceil_div(g.m, kBM));
     if (DT == MR_BF16 && g.wscale > 0.0f) {
-        k_row_scale<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale);
+        GemmArgs h = g;
+        h.ahl = g.ahl_ws;
+        h.w = g.wh;   // 16-bit rows: the BF16 loaders read them as they are
+        h.w2 = g.wh2;
+        k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         switch (epi) {
-            case GEMM_STORE: k_gemm_h<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(g); break;
-            case GEMM_RESIDUAL: k_gemm_h<DT, GEMM_RESIDUAL><<<grid, kThreads, 0, s>>>(g); break;
-            case GEMM_SWIGLU: k_gemm_h<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(g); break;
+            case GEMM_STORE: k_gemm_h<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_RESIDUAL: k_gemm_h<DT, GEMM_RESIDUAL><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_SWIGLU: k_gemm_h<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(h); break;
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
         }
         MR_LAUNCHED("enqueue MFMA GEMM (FP16 terms)");
@@ -537,6 +555,14 @@ int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count
     return MR_OK;
 }
 
+int gemm_f16_weight_copy(hipStream_t s, const void *w, int64_t count, float scale, void *dst) {
+    MR_REQUIRE(w && dst && count > 0 && scale > 0.0f, "f16 weight copy: bad arguments");
+    const int64_t blocks = std::min<int64_t>(ceil_div(count, (int64_t)256 * 8), 8192);
+    k_bf16_to_f16<<<(int)blocks, 256, 0, s>>>((const uint16_t *)w, count, scale, (_Float16 *)dst);
+    MR_LAUNCHED("enqueue f16 weight copy");
+    return MR_OK;
+}
+
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
     MR_REQUIRE(g.a && g.w && g.c && g.m > 0 && g.n > 0 && g.k > 0, "gemm: bad arguments");
     MR_REQUIRE(epilogue != GEMM_SWIGLU || g.w2, "gemm: SwiGLU needs gate and up weights");
@@ -544,7 +570,10 @@ int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
     MR_REQUIRE(((uintptr_t)g.a & 15) == 0 && ((uintptr_t)g.w & 15) == 0 && ((uintptr_t)g.w2 & 15) == 0,
                "gemm: operands must be 16-byte aligned");
     MR_REQUIRE(g.ldc >= g.n, "gemm: output rows too short");
-    MR_REQUIRE(g.wscale <= 0.0f || (g.dtype == MR_BF16 && g.ascale), "gemm: FP16 terms need BF16 weights and a row-scale workspace");
+    MR_REQUIRE(g.wscale <= 0.0f || (g.dtype == MR_BF16 && g.ascale && g.ahl_ws && g.wh &&
+                                     (epilogue != GEMM_SWIGLU || g.wh2) && ((uintptr_t)g.wh & 15) == 0 &&
+                                     ((uintptr_t)g.wh2 & 15) == 0),
+               "gemm: FP16 terms need BF16 weights, their FP16 copies and the row-scale and plane workspaces");
     MR_REQUIRE(ceil_div(g.m, kBM) <= 65535, "gemm: too many rows");
     switch (g.dtype) {
         case MR_BF16: return launch_dt<MR_BF16>(s, epilogue, g);

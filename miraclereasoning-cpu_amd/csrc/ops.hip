@@ -321,9 +321,27 @@ int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *a
         MR_TRY(gemm_f16_weight_scale(s, w, MR_BF16, (int64_t)n * k, &g.wscale));
         MR_REQUIRE(g.wscale > 0.0f, "debug gemm: weights not eligible for FP16 terms");
         g.ascale = ascale;
+        MR_HIP(hipMalloc((void **)&g.ahl_ws, (size_t)2 * m * k * sizeof(_Float16)), "debug gemm workspace");
+        void *wh = nullptr;
+        const hipError_t ea = hipMalloc(&wh, (size_t)n * k * 2);
+        if (ea != hipSuccess) {
+            (void)hipFree(g.ahl_ws);
+            MR_HIP(ea, "debug gemm workspace");
+        }
+        g.wh = wh;
+        const int rc = gemm_f16_weight_copy(s, w, (int64_t)n * k, g.wscale, wh);
+        if (rc != MR_OK) {
+            (void)hipFree(g.ahl_ws);
+            (void)hipFree(wh);
+            return rc;
+        }
     }
-    MR_TRY(launch_gemm(s, GEMM_STORE, g));
-    MR_HIP(hipStreamSynchronize(s), "debug gemm");
+    int rc = launch_gemm(s, GEMM_STORE, g);
+    const hipError_t e = hipStreamSynchronize(s);
+    if (g.ahl_ws) (void)hipFree(g.ahl_ws);
+    if (g.wh) (void)hipFree(const_cast<void *>(g.wh));
+    MR_TRY(rc);
+    MR_HIP(e, "debug gemm");
     return MR_OK;
 }
 
