@@ -291,6 +291,17 @@ MR_API int mr_debug_step_timeout(mr_model *model);
 MR_API int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *ascale, int m, int n, int k,
                          int scheme);
 
+/* Test hook: the batched-prefill attention over device FP32 buffers.  qkv
+ * [rows, heads*d + 2*kv_heads*d] holds each row's (normalized, rotated)
+ * query, key and value at positions p0 .. p0 + rows - 1; ring_k/ring_v
+ * [cap, kv_heads*d] hold the keys and values of positions p < p0 at slot
+ * p % cap; out [rows, heads*d] receives softmax(q.k / sqrt(d)).v over the
+ * keys at positions max(0, p - window + 1) .. p (window 0: cap).
+ * Synchronizes.  Not a counterpart of any reference function. */
+MR_API int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_k, const float *ring_v,
+                                      float *out, int rows, int p0, int heads, int kv_heads, int d, int cap,
+                                      int window);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,7 @@
 #include "attention.h"
 #include "gemm.h"
 #include "linear.h"
+#include "prefill.h"
 
 namespace mr {
 namespace {
@@ -342,6 +343,21 @@ int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *a
     if (g.wh) (void)hipFree(const_cast<void *>(g.wh));
     MR_TRY(rc);
     MR_HIP(e, "debug gemm");
+    return MR_OK;
+}
+
+int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_k, const float *ring_v, float *out,
+                               int rows, int p0, int heads, int kv_heads, int d, int cap, int window) {
+    OP_BEGIN("debug prefill attention");
+    MR_REQUIRE(qkv && ring_k && ring_v && out && rows > 0 && p0 >= 0 && heads > 0 && kv_heads > 0 && d > 0 &&
+                   cap > 0 && window >= 0,
+               "debug prefill attention: bad arguments");
+    PrefillAttnArgs a;
+    a.qkv = qkv; a.ld = (heads + 2 * kv_heads) * d; a.ring_k = ring_k; a.ring_v = ring_v; a.cap = cap;
+    a.out = out; a.ldo = heads * d; a.p0 = p0; a.rows = rows; a.heads = heads; a.kv_heads = kv_heads; a.d = d;
+    a.inv_root = 1.0f / sqrtf((float)d); a.window = window;
+    MR_TRY(launch_prefill_attention(s, a));
+    MR_HIP(hipStreamSynchronize(s), "debug prefill attention");
     return MR_OK;
 }
 

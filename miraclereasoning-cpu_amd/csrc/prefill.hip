@@ -27,6 +27,28 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// x = hi + lo in FP16 (x within FP16 range); x - hi is exact in FP32.
+__device__ __forceinline__ void split2h(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// The power of two 2^t with mx 2^t in [2^13, 2^14) (1 for 0 or a non-finite mx).
+__device__ __forceinline__ float f16_range_scale(float mx) {
+    if (!(mx > 0.0f) || !(mx <= 3.0e38f)) return 1.0f;
+    int e;
+    frexpf(mx, &e);
+    return ldexpf(1.0f, min(max(14 - e, -126), 126));
+}
+
 // grid (ceil(rows / (64 / gb)), kv_heads * G / gb), 256 threads.  A workgroup
 // serves gb query heads of one KV group (gb = 4, 2 or 1) on 64 / gb query
 // rows: wave w takes head (w % gb) and rows 16 (w / gb) .. +15.
@@ -193,6 +215,272 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
     }
 }
 
+// FP16-term form of k_attn_prefill for d = D in {32, 64, 128}, on
+// v_mfma_f32_16x16x32_f16 (lane l supplies A[l % 16][8 (l / 16) + i] and
+// B[8 (l / 16) + i][l % 16], i < 8, and holds C[4 (l / 16) + j][l % 16]).
+// Every operand is scaled by a power of two into FP16 range and carried as
+// hi + lo FP16 terms (11 + 11 significant bits); a product takes the three
+// term products hi hi + hi lo + lo hi, and the scales are undone exactly in
+// FP32: the queries per row, the keys and the values per 32-key tile (a
+// workgroup-wide maximum).  Softmax weights in [0, 1] need no scale.
+//   S^T = K . Q^T: A = key rows (16 keys x 32 dims), B = the lane's query
+//                  dims, so lane l again holds the scores of query l % 16
+//                  against keys 4 (l / 16) + j of each 16-key tile.
+//   O^T += V^T . P^T: the 32 keys of a tile enter the contraction in the
+//                  order that puts k-slot 8 g + i of lane group g on key
+//                  4 g + i (i < 4) or 16 + 4 g + i - 4 (i >= 4), the keys whose
+//                  weights the lane already holds; A reads V^T (values stored
+//                  transposed in LDS) at those keys.
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb) {
+    constexpr int NC = D / 32;            // 32-dim chunks (QK contraction steps)
+    constexpr int ND = D / 16;            // 16-dim output tiles
+    constexpr int KP = D + 8;             // LDS pitch of key rows (halves; rows stay 16-byte aligned)
+    constexpr int VP = kKeys + 8;         // LDS pitch of transposed value rows (halves)
+    constexpr int NL = kKeys * (D / 4) / kAttnThreads;   // float4 of K (and of V) per thread per tile
+    static_assert(NL >= 1 && NL <= 4 && kKeys * (D / 4) % kAttnThreads == 0, "tile split");
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kKeys * KP];   // [term][key][dim]
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * VP];       // [term][dim][key]
+    __shared__ float tile_max[2][kAttnThreads / kWave];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 / gb;
+    const int kh = blockIdx.y / sub_groups, hsub = blockIdx.y % sub_groups;
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * tile_rows;   // latest rows (most keys) first
+    const int h = kh * G + hsub * gb + wave % gb;
+    const int tq = t0 + (wave / gb) * 16 + lr;                  // this lane's query row
+    const bool qvalid = tq < a.rows;
+    const int qp = a.p0 + tq;
+    const int kvw = a.kv_heads * D, qd = a.heads * D;
+
+    // The lane's query dims 32 c + 8 lq .. + 7, scaled by the row's power of
+    // two (the row's maximum over the four lane groups that hold it).
+    float qf[NC][8];
+    float qmax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
+        if (qvalid) {
+            const float *src = a.qkv + (int64_t)tq * a.ld + h * D + 32 * c + 8 * lq;
+            u = load_f4(src);
+            v = load_f4(src + 4);
+        }
+        const float t[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qf[c][i] = t[i];
+            qmax = fmaxf(qmax, fabsf(t[i]));
+        }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, kWave));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, kWave));
+    const float sq = f16_range_scale(qmax);
+    f16x8 qh[NC], ql[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 th, tl;
+            split2h(qf[c][i] * sq, th, tl);
+            qh[c][i] = th;
+            ql[c][i] = tl;
+        }
+
+    const int win = a.window ? a.window : a.cap;
+    const int last = min(t0 + tile_rows, a.rows) - 1;
+    const int klo = max(0, a.p0 + t0 - win + 1), khi = a.p0 + last;
+    const int ntiles = (khi - klo) / kKeys + 1;
+
+    // Thread e loads keys NL kg .. + NL - 1 (kg = e / (D / 4)) at dims c4 .. + 3.
+    const int kg = tid / (D / 4), c4 = (tid % (D / 4)) * 4;
+    float4 kr[NL], vr[NL];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            const int kp = kb + NL * kg + u;
+            if (kp <= khi) {
+                const float *kbase, *vbase;
+                if (kp >= a.p0) {
+                    kbase = a.qkv + (int64_t)(kp - a.p0) * a.ld + qd + kh * D;
+                    vbase = kbase + kvw;
+                } else {
+                    const int64_t slot = kp % a.cap;
+                    kbase = a.ring_k + slot * kvw + kh * D;
+                    vbase = a.ring_v + slot * kvw + kh * D;
+                }
+                kr[u] = load_f4(kbase + c4);
+                vr[u] = load_f4(vbase + c4);
+            }
+        }
+    };
+    // Tile scales (workgroup maxima of |K| and |V|) and the split into LDS.
+    auto stash = [&](float &sk, float &sv) {
+        float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            mk = fmaxf(mk, fmaxf(fmaxf(fabsf(kr[u].x), fabsf(kr[u].y)), fmaxf(fabsf(kr[u].z), fabsf(kr[u].w))));
+            mv = fmaxf(mv, fmaxf(fmaxf(fabsf(vr[u].x), fabsf(vr[u].y)), fmaxf(fabsf(vr[u].z), fabsf(vr[u].w))));
+        }
+        mk = wave_max(mk);
+        mv = wave_max(mv);
+        if (lane == 0) {
+            tile_max[0][wave] = mk;
+            tile_max[1][wave] = mv;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int w = 0; w < kAttnThreads / kWave; ++w) {
+            mk = fmaxf(mk, tile_max[0][w]);
+            mv = fmaxf(mv, tile_max[1][w]);
+        }
+        sk = f16_range_scale(mk);
+        sv = f16_range_scale(mv);
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int r = NL * kg + u;
+            const float x[4] = {kr[u].x * sk, kr[u].y * sk, kr[u].z * sk, kr[u].w * sk};
+            f16x4 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                _Float16 th, tl;
+                split2h(x[i], th, tl);
+                hi[i] = th;
+                lo[i] = tl;
+            }
+            *(f16x4 *)&ks[0][r * KP + c4] = hi;
+            *(f16x4 *)&ks[1][r * KP + c4] = lo;
+        }
+        // values transposed: dim c4 + i of keys NL kg .. + NL - 1
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            _Float16 hv[NL], lv[NL];
+#pragma unroll
+            for (int u = 0; u < NL; ++u) {
+                const float x = (i == 0 ? vr[u].x : i == 1 ? vr[u].y : i == 2 ? vr[u].z : vr[u].w) * sv;
+                split2h(x, hv[u], lv[u]);
+            }
+            const int at = (c4 + i) * VP + NL * kg;   // NL consecutive keys: 2 NL bytes, aligned to them
+            if constexpr (NL == 4) {
+                *(f16x4 *)&vt[0][at] = f16x4{hv[0], hv[1], hv[2], hv[3]};
+                *(f16x4 *)&vt[1][at] = f16x4{lv[0], lv[1], lv[2], lv[3]};
+            } else if constexpr (NL == 2) {
+                *(f16x2 *)&vt[0][at] = f16x2{hv[0], hv[1]};
+                *(f16x2 *)&vt[1][at] = f16x2{lv[0], lv[1]};
+            } else {
+                vt[0][at] = hv[0];
+                vt[1][at] = lv[0];
+            }
+        }
+    };
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 o[ND];
+#pragma unroll
+    for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    fetch(klo);
+    for (int it = 0; it < ntiles; ++it) {
+        const int kb = klo + it * kKeys;
+        if (it) lds_barrier();
+        float sk, sv;
+        stash(sk, sv);
+        lds_barrier();
+        if (it + 1 < ntiles) fetch(kb + kKeys);
+
+        f32x4 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            sc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int off = (t * 16 + lr) * KP + 32 * c + 8 * lq;
+                const f16x8 kl = *(const f16x8 *)&ks[1][off];
+                const f16x8 khh = *(const f16x8 *)&ks[0][off];
+                sc[t] = mfma16(kl, qh[c], sc[t]);
+                sc[t] = mfma16(khh, ql[c], sc[t]);
+                sc[t] = mfma16(khh, qh[c], sc[t]);
+            }
+        }
+        const float unscale = a.inv_root / (sq * sk);
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int kp = kb + t * 16 + 4 * lq + j;
+                const bool ok = qvalid && kp <= qp && kp > qp - win && (a.hole == 0 || kp != qp - a.hole);
+                const float v = ok ? sc[t][j] * unscale : -INFINITY;
+                sc[t][j] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = expf(m_run - m_ref);
+        float psum = 0.0f;
+        f16x8 ph, pl;   // the lane's 8 weights in contraction order: tile 0's j, then tile 1's j
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p = expf(sc[t][j] - m_ref);
+                psum += p;
+                _Float16 hh, ll;
+                split2h(p, hh, ll);
+                ph[4 * t + j] = hh;
+                pl[4 * t + j] = ll;
+            }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        const float vun = 1.0f / sv;
+#pragma unroll
+        for (int t = 0; t < ND; ++t) {
+            const int row = (t * 16 + lr) * VP;
+            f16x8 vh, vl;
+            const f16x4 h0 = *(const f16x4 *)&vt[0][row + 4 * lq], h1 = *(const f16x4 *)&vt[0][row + 16 + 4 * lq];
+            const f16x4 l0 = *(const f16x4 *)&vt[1][row + 4 * lq], l1 = *(const f16x4 *)&vt[1][row + 16 + 4 * lq];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vh[i] = h0[i];
+                vh[4 + i] = h1[i];
+                vl[i] = l0[i];
+                vl[4 + i] = l1[i];
+            }
+            f32x4 pv = mfma16(vl, ph, f32x4{0.f, 0.f, 0.f, 0.f});
+            pv = mfma16(vh, pl, pv);
+            pv = mfma16(vh, ph, pv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[t][j] = fmaf(pv[j], vun, o[t][j] * alpha);
+        }
+    }
+    if (!qvalid) return;
+    float wo = 1.0f, we = 0.0f;   // weights of the window's and the extra columns' partials
+    const float *ext = nullptr;
+    if (a.ext) {   // the extra partial (m, l, o) joins the softmax
+        ext = a.ext + ((int64_t)tq * a.heads + h) * (D + 4);
+        const float m_e = ext[0], m = fmaxf(m_run, m_e);
+        wo = m_run == -INFINITY ? 0.0f : expf(m_run - m);
+        we = m_e == -INFINITY ? 0.0f : expf(m_e - m);
+        l_run = l_run * wo + ext[1] * we;
+    }
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+        const int dim = t * 16 + 4 * lq;
+        float4 r = make_float4(o[t][0] * wo, o[t][1] * wo, o[t][2] * wo, o[t][3] * wo);
+        if (ext) {
+            const float4 e = load_f4(ext + 4 + dim);
+            r = make_float4(r.x + e.x * we, r.y + e.y * we, r.z + e.z * we, r.w + e.w * we);
+        }
+        *(float4 *)(a.out + (int64_t)tq * a.ldo + h * D + dim) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+    }
+}
+
 __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const float *gain, float eps, int width,
                                                   float *y, int ldy) {
     __shared__ float red[4];
@@ -266,7 +554,10 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     const int G = a.heads / a.kv_heads;
     const int gb = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
     const dim3 grid(ceil_div(a.rows, 64 / gb), a.kv_heads * (G / gb));
-    if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    if (a.d == 128) k_attn_prefill_h<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else if (a.d == 64) k_attn_prefill_h<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else if (a.d == 32) k_attn_prefill_h<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    else if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 32) k_attn_prefill<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 64) k_attn_prefill<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else k_attn_prefill<128><<<grid, kAttnThreads, 0, s>>>(a, gb);

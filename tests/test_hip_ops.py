@@ -220,3 +220,45 @@ def test_prefill_gemm_term_schemes(backend):
         worst = np.max(np.abs(got - want) / bound)
         print("scheme", scheme, "worst error / bound", worst, flush=True)
         assert worst <= 1.0, scheme
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128])
+def test_prefill_attention_term_scaling(backend, dim):
+    """The batched-prefill attention (FP16-term matrix-core form for head dims
+    32/64/128) against float64 on inputs outside FP16's range: values of
+    kv head 0 up to ~1e6, keys of kv head 1 times 1e6 with their queries times
+    1e-6 (moderate scores), and queries of head 0 times 1e-20 (uniform
+    weights).  70 rows from position 50, the earlier keys from the ring, a
+    64-key window, 4 query heads over 2 kv heads.  Bound per element:
+    2e-5 max |v| of the row's kv head (the terms carry 22 significant bits)."""
+    b, rng = backend, np.random.default_rng(dim)
+    heads, kvh, rows, p0, win = 4, 2, 70, 50, 64
+    cap = win
+
+    def fill(n):
+        x = rng.normal(size=(n, heads + 2 * kvh, dim))
+        x[:, heads + kvh + 0] *= np.where(rng.random(size=dim) < 0.5, 3e5, 1.0)   # values, kv head 0
+        x[:, heads + 1] *= 1e6                                                     # keys, kv head 1
+        x[:, 2:4] *= 1e-6                                                          # its queries
+        x[:, 0] *= 1e-20                                                           # queries of head 0
+        return x.astype(np.float32)
+
+    chunk, old = fill(rows), fill(cap)
+    ring_k = old[:, heads:heads + kvh].reshape(cap, kvh * dim)
+    ring_v = old[:, heads + kvh:].reshape(cap, kvh * dim)
+    got = b.read(b.debug_prefill_attention(b.upload(chunk.reshape(rows, -1)), b.upload(ring_k), b.upload(ring_v),
+                                           p0=p0, heads=heads, kv_heads=kvh, dim=dim, window=win))
+    got = got.reshape(rows, heads, dim).astype(np.float64)
+    for t in range(rows):
+        p = p0 + t
+        pos = np.arange(max(0, p - win + 1), p + 1)
+        src = [old[q % cap] if q < p0 else chunk[q - p0] for q in pos]
+        keys = np.stack([s[heads:heads + kvh] for s in src]).astype(np.float64)
+        vals = np.stack([s[heads + kvh:] for s in src]).astype(np.float64)
+        for h in range(heads):
+            kv = h // (heads // kvh)
+            s = keys[:, kv] @ chunk[t, h].astype(np.float64) / np.sqrt(dim)
+            w = np.exp(s - s.max())
+            want = (w / w.sum()) @ vals[:, kv]
+            bound = 2e-5 * np.abs(vals[:, kv]).max()
+            assert np.all(np.abs(got[t, h] - want) <= bound), (t, h, np.abs(got[t, h] - want).max() / bound)
