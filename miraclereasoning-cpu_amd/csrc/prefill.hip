@@ -41,6 +41,12 @@ __device__ __forceinline__ void split2h(float x, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x by the hardware's exp2 (v_exp_f32, about 1 ulp; results below the
+// normal range flush to 0, which a softmax weight that small is anyway).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // The power of two 2^t with mx 2^t in [2^13, 2^14) (1 for 0 or a non-finite mx).
 __device__ __forceinline__ float f16_range_scale(float mx) {
     if (!(mx > 0.0f) || !(mx <= 3.0e38f)) return 1.0f;
@@ -296,6 +302,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     const int kg = tid / (D / 4), c4 = (tid % (D / 4)) * 4;
     float4 kr[NL], vr[NL];
     auto fetch = [&](int kb) {
+        const int kb_slot = kb < a.p0 ? kb % a.cap : 0;   // ring slot of the tile's first key (uniform)
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
             kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -306,9 +313,10 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                     kbase = a.qkv + (int64_t)(kp - a.p0) * a.ld + qd + kh * D;
                     vbase = kbase + kvw;
                 } else {
-                    const int64_t slot = kp % a.cap;
-                    kbase = a.ring_k + slot * kvw + kh * D;
-                    vbase = a.ring_v + slot * kvw + kh * D;
+                    int slot = kb_slot + NL * kg + u;
+                    while (slot >= a.cap) slot -= a.cap;
+                    kbase = a.ring_k + (int64_t)slot * kvw + kh * D;
+                    vbase = a.ring_v + (int64_t)slot * kvw + kh * D;
                 }
                 kr[u] = load_f4(kbase + c4);
                 vr[u] = load_f4(vbase + c4);
@@ -403,15 +411,22 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                 sc[t] = mfma16(khh, qh[c], sc[t]);
             }
         }
-        const float unscale = a.inv_root / (sq * sk);
+        // scores in base-2 units: e^(s - m) = 2^(s log2 e - m log2 e), with
+        // log2 e folded into the unscale product (one rounding, as for s)
+        const float unscale = a.inv_root * kLog2e / (sq * sk);
+        // a tile inside every row's window (and no hole) needs no mask
+        const bool full = a.hole == 0 && kb + kKeys - 1 <= a.p0 + t0 && kb > a.p0 + last - win;
         float tmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int kp = kb + t * 16 + 4 * lq + j;
-                const bool ok = qvalid && kp <= qp && kp > qp - win && (a.hole == 0 || kp != qp - a.hole);
-                const float v = ok ? sc[t][j] * unscale : -INFINITY;
+                float v = sc[t][j] * unscale;
+                if (!full) {
+                    const int kp = kb + t * 16 + 4 * lq + j;
+                    const bool ok = qvalid && kp <= qp && kp > qp - win && (a.hole == 0 || kp != qp - a.hole);
+                    v = ok ? v : -INFINITY;
+                }
                 sc[t][j] = v;
                 tmax = fmaxf(tmax, v);
             }
@@ -419,14 +434,14 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
         const float m_new = fmaxf(m_run, tmax);
         const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = expf(m_run - m_ref);
+        const float alpha = exp2_hw(m_run - m_ref);
         float psum = 0.0f;
         f16x8 ph, pl;   // the lane's 8 weights in contraction order: tile 0's j, then tile 1's j
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float p = expf(sc[t][j] - m_ref);
+                const float p = exp2_hw(sc[t][j] - m_ref);
                 psum += p;
                 _Float16 hh, ll;
                 split2h(p, hh, ll);
@@ -461,11 +476,11 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     if (!qvalid) return;
     float wo = 1.0f, we = 0.0f;   // weights of the window's and the extra columns' partials
     const float *ext = nullptr;
-    if (a.ext) {   // the extra partial (m, l, o) joins the softmax
+    if (a.ext) {   // the extra partial (m, l, o; m in natural units) joins the softmax
         ext = a.ext + ((int64_t)tq * a.heads + h) * (D + 4);
-        const float m_e = ext[0], m = fmaxf(m_run, m_e);
-        wo = m_run == -INFINITY ? 0.0f : expf(m_run - m);
-        we = m_e == -INFINITY ? 0.0f : expf(m_e - m);
+        const float m_e = ext[0] * kLog2e, m = fmaxf(m_run, m_e);
+        wo = m_run == -INFINITY ? 0.0f : exp2_hw(m_run - m);
+        we = m_e == -INFINITY ? 0.0f : exp2_hw(m_e - m);
         l_run = l_run * wo + ext[1] * we;
     }
     const float inv = 1.0f / l_run;
