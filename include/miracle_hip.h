@@ -296,11 +296,13 @@ MR_API int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, f
  * query, key and value at positions p0 .. p0 + rows - 1; ring_k/ring_v
  * [cap, kv_heads*d] hold the keys and values of positions p < p0 at slot
  * p % cap; out [rows, heads*d] receives softmax(q.k / sqrt(d)).v over the
- * keys at positions max(0, p - window + 1) .. p (window 0: cap).
+ * keys at positions max(0, p - window + 1) .. p (window 0: cap).  presplit
+ * 1 splits the attended keys and values into FP16 terms once beforehand
+ * (workspace allocated here), 0 lets every workgroup split its tiles.
  * Synchronizes.  Not a counterpart of any reference function. */
 MR_API int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_k, const float *ring_v,
                                       float *out, int rows, int p0, int heads, int kv_heads, int d, int cap,
-                                      int window);
+                                      int window, int presplit);
 
 #ifdef __cplusplus
 }

@@ -1354,6 +1354,10 @@ struct PrefillWs {
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
+    _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
+    int kv16_rows = 0;
+    float *kv16_scale = nullptr;
+    unsigned *kv16_max = nullptr;
 };
 
 int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
@@ -1366,6 +1370,11 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     const size_t groups = heavy ? (size_t)d.routed_experts + d.shared_experts : 0;
     const size_t kmax = heavy ? d.router_top_k_max : 0, lat = heavy || light ? d.latent_dim : 0;
     const size_t ext = heavy || light ? r * d.query_heads * (d.head_dim + 4) : 0;
+    int max_cap = 0;
+    for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
+    const bool gqa = !heavy && !light && d.family != MR_FAMILY_FLASHNANO_16;
+    w->kv16_rows = gqa ? rows + max_cap : 0;
+    const size_t kv16 = gqa ? (size_t)w->kv16_rows * kvw * 2 : 0;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
     const Piece pieces[] = {
         {(void **)&w->x, r * h}, {(void **)&w->xn, r * h}, {(void **)&w->qkv, r * (qd + 2 * kvw)},
@@ -1383,7 +1392,9 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->fbuf, light ? r * h : 0}, {(void **)&w->merge_count, light ? r : 0},
         {(void **)&w->flags, light ? r : 0}, {(void **)&w->extra_index, light ? r : 0},
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
-        {(void **)&w->rowscale, r}, {(void **)&w->planes, r * std::max({h, qd, (size_t)d.ffn_dim})}};
+        {(void **)&w->rowscale, r}, {(void **)&w->planes, r * std::max({h, qd, (size_t)d.ffn_dim})},
+        {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, gqa ? 2 * kvw : 0},
+        {(void **)&w->kv16_max, gqa ? 2 * kvw : 0}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
     size_t total = 0;
     for (const Piece &pc : pieces) total += up(pc.floats);
@@ -1510,6 +1521,7 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     a.qkv = w.qkv; a.ld = ld; a.ring_k = L.ring_k; a.ring_v = L.ring_v; a.cap = L.capacity;
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+    a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
     MR_TRY(launch_prefill_attention(s, a));
     MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
     GemmArgs o;

@@ -1,6 +1,8 @@
 // Op-level ABI: one entry point per reference kernel (kernels.cl), with the
 // reference's argument lists.  These serve HIPBackend's op surface (the drop-in
 // for OpenCLBackend); the fused decode step lives in engine.hip.
+#include <algorithm>
+
 #include "attention.h"
 #include "gemm.h"
 #include "linear.h"
@@ -347,7 +349,7 @@ int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *a
 }
 
 int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_k, const float *ring_v, float *out,
-                               int rows, int p0, int heads, int kv_heads, int d, int cap, int window) {
+                               int rows, int p0, int heads, int kv_heads, int d, int cap, int window, int presplit) {
     OP_BEGIN("debug prefill attention");
     MR_REQUIRE(qkv && ring_k && ring_v && out && rows > 0 && p0 >= 0 && heads > 0 && kv_heads > 0 && d > 0 &&
                    cap > 0 && window >= 0,
@@ -356,8 +358,21 @@ int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_
     a.qkv = qkv; a.ld = (heads + 2 * kv_heads) * d; a.ring_k = ring_k; a.ring_v = ring_v; a.cap = cap;
     a.out = out; a.ldo = heads * d; a.p0 = p0; a.rows = rows; a.heads = heads; a.kv_heads = kv_heads; a.d = d;
     a.inv_root = 1.0f / sqrtf((float)d); a.window = window;
-    MR_TRY(launch_prefill_attention(s, a));
-    MR_HIP(hipStreamSynchronize(s), "debug prefill attention");
+    void *ws = nullptr;
+    if (presplit) {
+        const int n = rows + std::min(p0, (window ? window : cap) - 1);
+        const size_t planes = (size_t)4 * n * kv_heads * d * sizeof(_Float16);
+        MR_HIP(hipMalloc(&ws, planes + 4 * kv_heads * sizeof(float)), "debug prefill attention workspace");
+        a.kv16 = (_Float16 *)ws;
+        a.kv16_rows = n;
+        a.kv16_scale = (float *)((char *)ws + planes);
+        a.kv16_max = (unsigned *)(a.kv16_scale + 2 * kv_heads);
+    }
+    const int rc = launch_prefill_attention(s, a);
+    const hipError_t e = hipStreamSynchronize(s);
+    if (ws) (void)hipFree(ws);
+    MR_TRY(rc);
+    MR_HIP(e, "debug prefill attention");
     return MR_OK;
 }
 

@@ -21,6 +21,15 @@ struct PrefillAttnArgs {
     int window = 0;                 // keys a query sees (0: cap)
     int hole = 0;                   // > 0: the key at position p - hole is not seen (latent memory)
     const float *ext = nullptr;     // [rows][heads][d + 4]: m, l, 2 unused, o[d] of extra columns, merged at the end
+    // Optional workspace (head dims 32/64/128): the keys and values of the
+    // positions the chunk attends to, split once into FP16 terms (4 planes of
+    // kv16_rows x kv_heads*d halves) with per-KV-head scales (kv16_scale,
+    // 2 kv_heads floats; kv16_max, 2 kv_heads words); without it (or with too
+    // few rows) every workgroup splits its tiles itself.
+    _Float16 *kv16 = nullptr;
+    int kv16_rows = 0;
+    float *kv16_scale = nullptr;
+    unsigned *kv16_max = nullptr;
 };
 
 // out = softmax(q . k / sqrt(d)) . v per query head over the keys at

@@ -30,6 +30,7 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4 &c) {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -237,8 +238,8 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
 //                  4 g + i (i < 4) or 16 + 4 g + i - 4 (i >= 4), the keys whose
 //                  weights the lane already holds; A reads V^T (values stored
 //                  transposed in LDS) at those keys.
-template <int D>
-__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb) {
+template <int D, bool P>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb, int first) {
     constexpr int NC = D / 32;            // 32-dim chunks (QK contraction steps)
     constexpr int ND = D / 16;            // 16-dim output tiles
     constexpr int KP = D + 8;             // LDS pitch of key rows (halves; rows stay 16-byte aligned)
@@ -301,6 +302,23 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     // Thread e loads keys NL kg .. + NL - 1 (kg = e / (D / 4)) at dims c4 .. + 3.
     const int kg = tid / (D / 4), c4 = (tid % (D / 4)) * 4;
     float4 kr[NL], vr[NL];
+    u32x2 kq[NL][2], vq[NL][2];   // P: the keys' and values' FP16 terms (hi, lo) at dims c4 .. + 3
+    const int64_t plane = (int64_t)a.kv16_rows * kvw;
+    auto fetch_p = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int kp = kb + NL * kg + u;
+            const _Float16 *src = a.kv16 + (int64_t)(kp - first) * kvw + kh * D + c4;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                kq[u][t] = vq[u][t] = u32x2{0u, 0u};
+                if (kp <= khi) {
+                    kq[u][t] = *gmem((const u32x2 *)(src + t * plane));
+                    vq[u][t] = *gmem((const u32x2 *)(src + (2 + t) * plane));
+                }
+            }
+        }
+    };
     auto fetch = [&](int kb) {
         const int kb_slot = kb < a.p0 ? kb % a.cap : 0;   // ring slot of the tile's first key (uniform)
 #pragma unroll
@@ -383,19 +401,52 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
         }
     };
 
+    // P: the terms as split once per chunk; the values go in transposed.
+    auto stash_p = [&]() {
+#pragma unroll
+        for (int u = 0; u < NL; ++u)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) *(u32x2 *)&ks[t][(NL * kg + u) * KP + c4] = kq[u][t];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                _Float16 x[NL];
+#pragma unroll
+                for (int u = 0; u < NL; ++u) {
+                    const unsigned w = i < 2 ? vq[u][t].x : vq[u][t].y;
+                    x[u] = __builtin_bit_cast(_Float16, (unsigned short)(w >> (16 * (i & 1))));
+                }
+                const int at = (c4 + i) * VP + NL * kg;
+                if constexpr (NL == 4) *(f16x4 *)&vt[t][at] = f16x4{x[0], x[1], x[2], x[3]};
+                else if constexpr (NL == 2) *(f16x2 *)&vt[t][at] = f16x2{x[0], x[1]};
+                else vt[t][at] = x[0];
+            }
+    };
+
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 o[ND];
 #pragma unroll
     for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    fetch(klo);
+    float sk = 1.0f, sv = 1.0f;
+    if constexpr (P) {
+        sk = a.kv16_scale[kh];
+        sv = a.kv16_scale[a.kv_heads + kh];
+        fetch_p(klo);
+    } else {
+        fetch(klo);
+    }
     for (int it = 0; it < ntiles; ++it) {
         const int kb = klo + it * kKeys;
         if (it) lds_barrier();
-        float sk, sv;
-        stash(sk, sv);
+        if constexpr (P) stash_p();
+        else stash(sk, sv);
         lds_barrier();
-        if (it + 1 < ntiles) fetch(kb + kKeys);
+        if (it + 1 < ntiles) {
+            if constexpr (P) fetch_p(kb + kKeys);
+            else fetch(kb + kKeys);
+        }
 
         f32x4 sc[2];
 #pragma unroll
@@ -466,12 +517,24 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                 vl[i] = l0[i];
                 vl[4 + i] = l1[i];
             }
-            f32x4 pv = mfma16(vl, ph, f32x4{0.f, 0.f, 0.f, 0.f});
-            pv = mfma16(vh, pl, pv);
-            pv = mfma16(vh, ph, pv);
+            if constexpr (P) {   // one value scale for the chunk: undone at the end
+                o[t] *= alpha;
+                o[t] = mfma16(vl, ph, o[t]);
+                o[t] = mfma16(vh, pl, o[t]);
+                o[t] = mfma16(vh, ph, o[t]);
+            } else {
+                f32x4 pv = mfma16(vl, ph, f32x4{0.f, 0.f, 0.f, 0.f});
+                pv = mfma16(vh, pl, pv);
+                pv = mfma16(vh, ph, pv);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[t][j] = fmaf(pv[j], vun, o[t][j] * alpha);
+                for (int j = 0; j < 4; ++j) o[t][j] = fmaf(pv[j], vun, o[t][j] * alpha);
+            }
         }
+    }
+    if constexpr (P) {
+        const float vun = 1.0f / sv;
+#pragma unroll
+        for (int t = 0; t < ND; ++t) o[t] *= vun;
     }
     if (!qvalid) return;
     float wo = 1.0f, we = 0.0f;   // weights of the window's and the extra columns' partials
@@ -494,6 +557,74 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
         }
         *(float4 *)(a.out + (int64_t)tq * a.ldo + h * D + dim) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
     }
+}
+
+// The keys and values of positions first .. first + n - 1 (ring slot p % cap
+// before p0, chunk row p - p0 after): per-KV-head maxima of |K| and |V| into
+// mx[2][kv_heads] (bit patterns of non-negative floats, which order like the
+// values; zeroed before).  A block takes kMaxRows positions, a thread 4 dims;
+// the D / 4 threads of a head combine their maxima before one atomic each.
+constexpr int kMaxRows = 32;
+
+__global__ void k_kv_max(PrefillAttnArgs a, int first, int n) {
+    const int kvw = a.kv_heads * a.d, qd = a.heads * a.d, c4 = 4 * threadIdx.x;
+    const bool on = c4 < kvw;
+    float mk = 0.0f, mv = 0.0f;
+    for (int i = 0; i < kMaxRows && on; ++i) {
+        const int p = first + blockIdx.x * kMaxRows + i;
+        if (p >= first + n) break;
+        const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
+        const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
+        const float4 x = load_f4(k + c4), y = load_f4(v + c4);
+        mk = fmaxf(mk, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+        mv = fmaxf(mv, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+    }
+    // the head's threads are a run of D / 4 <= 32 lanes starting at a multiple of D / 4
+    for (int off = 1; off < a.d / 4; off <<= 1) {
+        mk = fmaxf(mk, __shfl_xor(mk, off, kWave));
+        mv = fmaxf(mv, __shfl_xor(mv, off, kWave));
+    }
+    if (on && c4 % a.d == 0) {
+        const int head = c4 / a.d;
+        atomicMax(a.kv16_max + head, __float_as_uint(mk));
+        atomicMax(a.kv16_max + a.kv_heads + head, __float_as_uint(mv));
+    }
+}
+
+// The same positions split into FP16 terms with the per-head scales:
+// kv16 planes [K hi, K lo, V hi, V lo][n][kv_heads d]; block 0 also stores
+// the scales for the attention kernel.
+__global__ void k_kv_split(PrefillAttnArgs a, int first, int n) {
+    const int kvw = a.kv_heads * a.d, qd = a.heads * a.d, c4 = 4 * threadIdx.x;
+    const int p = first + blockIdx.x;
+    if (c4 >= kvw) return;
+    const int head = c4 / a.d;
+    const float sk = f16_range_scale(__uint_as_float(a.kv16_max[head]));
+    const float sv = f16_range_scale(__uint_as_float(a.kv16_max[a.kv_heads + head]));
+    if (blockIdx.x == 0 && c4 % a.d == 0) {
+        a.kv16_scale[head] = sk;
+        a.kv16_scale[a.kv_heads + head] = sv;
+    }
+    const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
+    const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
+    const float4 x = load_f4(k + c4), y = load_f4(v + c4);
+    const float xs[4] = {x.x * sk, x.y * sk, x.z * sk, x.w * sk}, ys[4] = {y.x * sv, y.y * sv, y.z * sv, y.w * sv};
+    f16x4 kh4, kl4, vh4, vl4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        _Float16 h, l;
+        split2h(xs[i], h, l);
+        kh4[i] = h;
+        kl4[i] = l;
+        split2h(ys[i], h, l);
+        vh4[i] = h;
+        vl4[i] = l;
+    }
+    const int64_t plane = (int64_t)a.kv16_rows * kvw, at = (int64_t)blockIdx.x * kvw + c4;
+    *(f16x4 *)(a.kv16 + at) = kh4;
+    *(f16x4 *)(a.kv16 + plane + at) = kl4;
+    *(f16x4 *)(a.kv16 + 2 * plane + at) = vh4;
+    *(f16x4 *)(a.kv16 + 3 * plane + at) = vl4;
 }
 
 __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const float *gain, float eps, int width,
@@ -569,10 +700,26 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     const int G = a.heads / a.kv_heads;
     const int gb = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
     const dim3 grid(ceil_div(a.rows, 64 / gb), a.kv_heads * (G / gb));
-    if (a.d == 128) k_attn_prefill_h<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
-    else if (a.d == 64) k_attn_prefill_h<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
-    else if (a.d == 32) k_attn_prefill_h<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
-    else if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
+    const int win = a.window ? a.window : a.cap;
+    const int first = std::max(0, a.p0 - win + 1), n = a.p0 + a.rows - first;
+    const bool h = a.d == 128 || a.d == 64 || a.d == 32;
+    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n <= a.kv16_rows && a.kv_heads * a.d <= 1024;
+    if (planes) {   // split the attended keys and values once
+        MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
+        const int threads = ceil_div(a.kv_heads * a.d / 4, kWave) * kWave;
+        k_kv_max<<<ceil_div(n, kMaxRows), threads, 0, s>>>(a, first, n);
+        k_kv_split<<<n, threads, 0, s>>>(a, first, n);
+    }
+    if (a.d == 128) {
+        if (planes) k_attn_prefill_h<128, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<128, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+    } else if (a.d == 64) {
+        if (planes) k_attn_prefill_h<64, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<64, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+    } else if (a.d == 32) {
+        if (planes) k_attn_prefill_h<32, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<32, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+    } else if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 32) k_attn_prefill<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 64) k_attn_prefill<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else k_attn_prefill<128><<<grid, kAttnThreads, 0, s>>>(a, gb);

@@ -102,7 +102,7 @@ _SIGNATURES = {
     "mr_debug_fail_next": [_P],
     "mr_debug_step_timeout": [_P],
     "mr_debug_gemm": [_P, _P, _P, _P, _P, _i, _i, _i, _i],
-    "mr_debug_prefill_attention": [_P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i],
+    "mr_debug_prefill_attention": [_P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i, _i],
 }
 
 _lib = None
@@ -413,7 +413,7 @@ class HIPBackend:
                "debug gemm")
         return out
 
-    def debug_prefill_attention(self, qkv, ring_k, ring_v, *, p0, heads, kv_heads, dim, window=0):
+    def debug_prefill_attention(self, qkv, ring_k, ring_v, *, p0, heads, kv_heads, dim, window=0, presplit=False):
         """The batched-prefill attention kernel on device buffers (test hook):
         qkv [rows, (heads + 2 kv_heads) dim], ring_k/ring_v [cap, kv_heads dim]."""
         self._owns(qkv, ring_k, ring_v)
@@ -423,7 +423,7 @@ class HIPBackend:
             raise ValueError("debug_prefill_attention: shapes do not match the head geometry")
         out = self.empty((rows, heads * dim))
         _check(self.lib.mr_debug_prefill_attention(self.ctx, qkv.handle, ring_k.handle, ring_v.handle, out.handle,
-                                                   rows, p0, heads, kv_heads, dim, cap, window),
+                                                   rows, p0, heads, kv_heads, dim, cap, window, int(presplit)),
                "debug prefill attention")
         return out
 

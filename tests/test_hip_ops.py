@@ -222,15 +222,18 @@ def test_prefill_gemm_term_schemes(backend):
         assert worst <= 1.0, scheme
 
 
+@pytest.mark.parametrize("presplit", [False, True])
 @pytest.mark.parametrize("dim", [32, 64, 128])
-def test_prefill_attention_term_scaling(backend, dim):
+def test_prefill_attention_term_scaling(backend, dim, presplit):
     """The batched-prefill attention (FP16-term matrix-core form for head dims
     32/64/128) against float64 on inputs outside FP16's range: values of
     kv head 0 up to ~1e6, keys of kv head 1 times 1e6 with their queries times
     1e-6 (moderate scores), and queries of head 0 times 1e-20 (uniform
     weights).  70 rows from position 50, the earlier keys from the ring, a
-    64-key window, 4 query heads over 2 kv heads.  Bound per element:
-    2e-5 max |v| of the row's kv head (the terms carry 22 significant bits)."""
+    64-key window, 4 query heads over 2 kv heads; the keys and values split
+    per tile by the workgroups or once beforehand (per-head scales).  Bound
+    per element: 2e-5 max |v| of the kv head over the rows attended (the terms
+    carry 22 significant bits of the scale's range)."""
     b, rng = backend, np.random.default_rng(dim)
     heads, kvh, rows, p0, win = 4, 2, 70, 50, 64
     cap = win
@@ -247,7 +250,8 @@ def test_prefill_attention_term_scaling(backend, dim):
     ring_k = old[:, heads:heads + kvh].reshape(cap, kvh * dim)
     ring_v = old[:, heads + kvh:].reshape(cap, kvh * dim)
     got = b.read(b.debug_prefill_attention(b.upload(chunk.reshape(rows, -1)), b.upload(ring_k), b.upload(ring_v),
-                                           p0=p0, heads=heads, kv_heads=kvh, dim=dim, window=win))
+                                           p0=p0, heads=heads, kv_heads=kvh, dim=dim, window=win,
+                                           presplit=presplit))
     got = got.reshape(rows, heads, dim).astype(np.float64)
     for t in range(rows):
         p = p0 + t
