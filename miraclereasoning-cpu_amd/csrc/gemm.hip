@@ -35,6 +35,10 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBM = 128, kBN = 128, kBK = 32;
 constexpr int kPitch = kBK + 8;   // BF16 elements per LDS row (80 bytes: rows stay 16-byte aligned)
 constexpr int kThreads = 256;
+#ifndef MR_GEMM_SWIGLU_NI
+#define MR_GEMM_SWIGLU_NI 4
+#endif
+constexpr int kSwigluNI = MR_GEMM_SWIGLU_NI;   // 16-column MFMA tiles per wave in the SwiGLU FP16-term GEMM
 
 template <int DT>
 constexpr int planes() {
@@ -145,16 +149,6 @@ __device__ __forceinline__ void split2h(float x, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
-// FP16 weight rows (converted once, gemm_f16_weight_copy) as loaded.
-__device__ __forceinline__ void store_w_h(_Float16 (*bs)[kPitch], const WRegs<MR_BF16> &r) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int idx = tid + kThreads * i;
-        *(u32x4 *)&bs[idx >> 2][(idx & 3) * 8] = r.v[i];
-    }
-}
-
 template <int DT>
 __device__ __forceinline__ void store_w(__bf16 (*bs)[kBN][kPitch], const WRegs<DT> &r) {
     const int tid = threadIdx.x;
@@ -210,9 +204,11 @@ __device__ __forceinline__ f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x
 }
 
 // The epilogue of both schemes: rows m0.., columns n0.. of the tile from the
-// accumulators times `unscale` (per output row; 1 for the BF16 scheme).
-template <int EPI, typename Unscale>
-__device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, const f32x4 (&acc)[4][4],
+// accumulators times `unscale` (per output row; 1 for the BF16 scheme).  A
+// wave holds NI 16-column tiles; with SwiGLU the first NI / 2 are gate
+// columns and the others the up columns of the same FFN columns.
+template <int EPI, int NI = 4, typename Unscale>
+__device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, const f32x4 (&acc)[4][NI],
                                            Unscale unscale) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 15;
@@ -227,16 +223,16 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, co
             float *crow = g.c + (int64_t)row * g.ldc;
             if constexpr (EPI == GEMM_SWIGLU) {
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    const int f = n0 + wn * 32 + ni * 16 + lr;
+                for (int ni = 0; ni < NI / 2; ++ni) {
+                    const int f = n0 + wn * 8 * NI + ni * 16 + lr;
                     if (f >= g.n) continue;
-                    const float gt = acc[mi][ni][j] * u, up = acc[mi][ni + 2][j] * u;
+                    const float gt = acc[mi][ni][j] * u, up = acc[mi][ni + NI / 2][j] * u;
                     crow[f] = (gt / (1.0f + expf(-gt))) * up;
                 }
             } else {
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    const int col = n0 + wn * 64 + ni * 16 + lr;
+                for (int ni = 0; ni < NI; ++ni) {
+                    const int col = n0 + wn * 16 * NI + ni * 16 + lr;
                     if (col >= g.n) continue;
                     const float v = acc[mi][ni][j] * u;
                     if constexpr (EPI == GEMM_RESIDUAL) crow[col] = crow[col] + g.scale * v;
@@ -337,60 +333,97 @@ __device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][kPitch], const AHR
     for (int i = 0; i < 4; ++i) *(u32x4 *)&as[i >> 1][(tid >> 2) + 64 * (i & 1)][(tid & 3) * 8] = r.v[i];
 }
 
-// One 128 x 128 output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
-// planes and row scales from k_row_split, the weights' FP16 copy).  (Two LDS
-// stages with one barrier per k-step measured slower: 60 KB of LDS per
-// workgroup halves the workgroups per CU.)
-template <int EPI>
+// Weight row r of an FP16-term tile of 32 NI rows: two halves of 16 NI rows
+// (one per wave column); with SwiGLU the first 8 NI rows of a half are gate
+// rows and the rest the up rows of the same FFN columns.
+template <int EPI, int NI>
+__device__ __forceinline__ const char *w_row_h(const GemmArgs &g, int n0, int r, bool &ok) {
+    int f;
+    const void *base = g.w;
+    if constexpr (EPI == GEMM_SWIGLU) {
+        const int half = r / (16 * NI), q = r % (16 * NI);
+        f = n0 + half * 8 * NI + q % (8 * NI);
+        if (q >= 8 * NI) base = g.w2;
+    } else {
+        f = n0 + r;
+    }
+    ok = f < g.n;
+    return (const char *)base + (int64_t)(ok ? f : 0) * g.k * 2;
+}
+
+// The FP16 weight rows of a k-step: NI / 2 chunks of 16 bytes per thread.
+template <int EPI, int NI>
+__device__ __forceinline__ void load_w_h(const GemmArgs &g, int n0, int k0, u32x4 (&r)[NI / 2]) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NI / 2; ++i) {
+        const int idx = tid + kThreads * i;
+        const int col = k0 + (idx & 3) * 8;
+        bool ok;
+        const char *row = w_row_h<EPI, NI>(g, n0, idx >> 2, ok);
+        if (ok && col < g.k) r[i] = *gmem((const u32x4 *)(row + (int64_t)col * 2));
+        else r[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+// One 128 x 32 NI output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
+// planes and row scales from k_row_split, the weights' FP16 copy); each wave
+// owns 64 x 16 NI outputs.  (Two LDS stages with one barrier per k-step
+// measured slower: the LDS per workgroup halves the workgroups per CU.)
+template <int EPI, int NI>
 __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][kPitch];
-    __shared__ __attribute__((aligned(16))) _Float16 bs[kBN][kPitch];
+    __shared__ __attribute__((aligned(16))) _Float16 bs[32 * NI][kPitch];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 15, lk = (lane >> 4) * 8;
     const int nk = (g.k + kBK - 1) / kBK;
 
-    f32x4 acc[4][4];
+    f32x4 acc[4][NI];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     AHRegs ar;
-    WRegs<MR_BF16> wr;
+    u32x4 wr[NI / 2];
     load_a_h(g, m0, 0, ar);
-    load_w<MR_BF16, EPI>(g, n0, 0, wr);
+    load_w_h<EPI, NI>(g, n0, 0, wr);
     for (int kt = 0; kt < nk; ++kt) {
         if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
         store_a_h(as, ar);
-        store_w_h(bs, wr);
+#pragma unroll
+        for (int i = 0; i < NI / 2; ++i) {
+            const int idx = tid + kThreads * i;
+            *(u32x4 *)&bs[idx >> 2][(idx & 3) * 8] = wr[i];
+        }
         lds_barrier();
         if (kt + 1 < nk) {
             load_a_h(g, m0, (kt + 1) * kBK, ar);
-            load_w<MR_BF16, EPI>(g, n0, (kt + 1) * kBK, wr);
+            load_w_h<EPI, NI>(g, n0, (kt + 1) * kBK, wr);
         }
-        f16x8 bf[4];
+        f16x8 bf[NI];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) bf[ni] = *(const f16x8 *)&bs[wn * 64 + ni * 16 + lr][lk];
+        for (int ni = 0; ni < NI; ++ni) bf[ni] = *(const f16x8 *)&bs[wn * 16 * NI + ni * 16 + lr][lk];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             const f16x8 lo = *(const f16x8 *)&as[1][wm * 64 + mi * 16 + lr][lk];
             const f16x8 hi = *(const f16x8 *)&as[0][wm * 64 + mi * 16 + lr][lk];
             // the smaller term first
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
         }
     }
     const float inv_w = 1.0f / g.wscale;
-    gemm_store<EPI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
+    gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
 }
 
-template <int DT, int EPI>
+template <int EPI, int NI>
 __global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
-    gemm_tile_h<EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
+    gemm_tile_h<EPI, NI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 // A in FP16 terms, once per GEMM: row r's scale 2^t (max_k |a[r][k]| 2^t in
@@ -490,10 +523,14 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         h.w = g.wh;   // 16-bit rows: the BF16 loaders read them as they are
         h.w2 = g.wh2;
         k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        // 128 x 128 tiles (wider SwiGLU tiles, 192 or 256 columns, measured
+        // slower: the accumulators leave one or two waves per SIMD)
         switch (epi) {
-            case GEMM_STORE: k_gemm_h<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(h); break;
-            case GEMM_RESIDUAL: k_gemm_h<DT, GEMM_RESIDUAL><<<grid, kThreads, 0, s>>>(h); break;
-            case GEMM_SWIGLU: k_gemm_h<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_STORE: k_gemm_h<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_RESIDUAL: k_gemm_h<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_SWIGLU:
+                k_gemm_h<GEMM_SWIGLU, kSwigluNI><<<dim3(ceil_div(g.n, 16 * kSwigluNI), grid.y), kThreads, 0, s>>>(h);
+                break;
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
         }
         MR_LAUNCHED("enqueue MFMA GEMM (FP16 terms)");
