@@ -238,6 +238,11 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
 //                  4 g + i (i < 4) or 16 + 4 g + i - 4 (i >= 4), the keys whose
 //                  weights the lane already holds; A reads V^T (values stored
 //                  transposed in LDS) at those keys.
+// Slot of key k (< 32) of a tile in the value contraction: lane group g's
+// slots 8 g .. 8 g + 7 hold keys 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3
+// (the keys whose weights the group's lanes hold); runs of 4 keys stay runs.
+__device__ __forceinline__ int vslot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
+
 template <int D, bool P>
 __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb, int first) {
     constexpr int NC = D / 32;            // 32-dim chunks (QK contraction steps)
@@ -387,7 +392,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                 const float x = (i == 0 ? vr[u].x : i == 1 ? vr[u].y : i == 2 ? vr[u].z : vr[u].w) * sv;
                 split2h(x, hv[u], lv[u]);
             }
-            const int at = (c4 + i) * VP + NL * kg;   // NL consecutive keys: 2 NL bytes, aligned to them
+            const int at = (c4 + i) * VP + vslot(NL * kg);   // NL consecutive keys and slots
             if constexpr (NL == 4) {
                 *(f16x4 *)&vt[0][at] = f16x4{hv[0], hv[1], hv[2], hv[3]};
                 *(f16x4 *)&vt[1][at] = f16x4{lv[0], lv[1], lv[2], lv[3]};
@@ -417,7 +422,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                     const unsigned w = i < 2 ? vq[u][t].x : vq[u][t].y;
                     x[u] = __builtin_bit_cast(_Float16, (unsigned short)(w >> (16 * (i & 1))));
                 }
-                const int at = (c4 + i) * VP + NL * kg;
+                const int at = (c4 + i) * VP + vslot(NL * kg);
                 if constexpr (NL == 4) *(f16x4 *)&vt[t][at] = f16x4{x[0], x[1], x[2], x[3]};
                 else if constexpr (NL == 2) *(f16x2 *)&vt[t][at] = f16x2{x[0], x[1]};
                 else vt[t][at] = x[0];
@@ -506,17 +511,9 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
         const float vun = 1.0f / sv;
 #pragma unroll
         for (int t = 0; t < ND; ++t) {
-            const int row = (t * 16 + lr) * VP;
-            f16x8 vh, vl;
-            const f16x4 h0 = *(const f16x4 *)&vt[0][row + 4 * lq], h1 = *(const f16x4 *)&vt[0][row + 16 + 4 * lq];
-            const f16x4 l0 = *(const f16x4 *)&vt[1][row + 4 * lq], l1 = *(const f16x4 *)&vt[1][row + 16 + 4 * lq];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                vh[i] = h0[i];
-                vh[4 + i] = h1[i];
-                vl[i] = l0[i];
-                vl[4 + i] = l1[i];
-            }
+            // the lane group's 8 slots, stored in contraction order by the stash
+            const int row = (t * 16 + lr) * VP + 8 * lq;
+            const f16x8 vh = *(const f16x8 *)&vt[0][row], vl = *(const f16x8 *)&vt[1][row];
             if constexpr (P) {   // one value scale for the chunk: undone at the end
                 o[t] *= alpha;
                 o[t] = mfma16(vl, ph, o[t]);
