@@ -1509,10 +1509,13 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     hipStream_t s = m->ctx->stream;
     const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim;
     const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
-    MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
     GemmArgs g;
     g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
     g.m = T; g.n = ld; g.k = h; g.wscale = L.qkv.f16_scale; g.wh = L.qkv.f16; g.ascale = w.rowscale; g.ahl_ws = w.planes;
+    // the normalized rows go straight into the FP16-term GEMM's A workspace
+    g.a_split = g.wscale > 0.0f;
+    if (g.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
+    else MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
     MR_TRY(launch_gemm(s, GEMM_STORE, g));
     MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
                           d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
@@ -1528,12 +1531,14 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
     o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale; o.wscale = L.o.f16_scale; o.wh = L.o.f16; o.ascale = w.rowscale; o.ahl_ws = w.planes;
     MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
-    MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
     GemmArgs gu;
     gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
     gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
     gu.wscale = L.ffn.gate.f16_scale; gu.wh = L.ffn.gate.f16; gu.wh2 = L.ffn.up.f16; gu.ascale = w.rowscale;
     gu.ahl_ws = w.planes;
+    gu.a_split = gu.wscale > 0.0f;
+    if (gu.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
+    else MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;

@@ -39,6 +39,7 @@ struct GemmArgs {
     const void *wh = nullptr, *wh2 = nullptr;   // the weights times wscale in FP16 (gemm_f16_weight_copy)
     float *ascale = nullptr;
     _Float16 *ahl_ws = nullptr;
+    bool a_split = false;            // FP16 terms: ascale and ahl_ws already hold A (a unused)
     const _Float16 *ahl = nullptr;   // set by launch_gemm for the kernel
 };
 

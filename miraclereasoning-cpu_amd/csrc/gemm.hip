@@ -522,7 +522,7 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         h.ahl = g.ahl_ws;
         h.w = g.wh;   // 16-bit rows: the BF16 loaders read them as they are
         h.w2 = g.wh2;
-        k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        if (!g.a_split) k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // 128 x 128 tiles (wider SwiGLU tiles, 192 or 256 columns, measured
         // slower: the accumulators leave one or two waves per SIMD)
         switch (epi) {
@@ -601,7 +601,8 @@ int gemm_f16_weight_copy(hipStream_t s, const void *w, int64_t count, float scal
 }
 
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
-    MR_REQUIRE(g.a && g.w && g.c && g.m > 0 && g.n > 0 && g.k > 0, "gemm: bad arguments");
+    MR_REQUIRE((g.a || (g.a_split && g.wscale > 0.0f)) && g.w && g.c && g.m > 0 && g.n > 0 && g.k > 0,
+               "gemm: bad arguments");
     MR_REQUIRE(epilogue != GEMM_SWIGLU || g.w2, "gemm: SwiGLU needs gate and up weights");
     MR_REQUIRE(g.k % 8 == 0 && g.lda % 4 == 0 && g.lda >= g.k, "gemm: k must be a multiple of 8");
     MR_REQUIRE(((uintptr_t)g.a & 15) == 0 && ((uintptr_t)g.w & 15) == 0 && ((uintptr_t)g.w2 & 15) == 0,

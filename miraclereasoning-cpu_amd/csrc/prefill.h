@@ -39,6 +39,10 @@ struct PrefillAttnArgs {
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a);
 
 // y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * gain (gain may be null).
+// k_rms_rows straight into an FP16-term GEMM's A workspace (row scales and
+// hi / lo planes, see gemm.h): the GEMM then runs with a_split.
+int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
+                          float *scale, _Float16 *planes, int rows);
 int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width, float *y,
                     int ldy, int rows);
 

@@ -636,6 +636,33 @@ __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const
     for (int j = threadIdx.x; j < width; j += blockDim.x) yr[j] = xr[j] * scale * (gain ? gain[j] : 1.0f);
 }
 
+// k_rms_rows feeding an FP16-term GEMM directly: y = RMSNorm(x) gain (the
+// same arithmetic), then y's row scale 2^t (max |y| 2^t in [2^13, 2^14)) into
+// scale[row] and y 2^t = hi + lo into planes hl[0][row][.], hl[1][row][.]
+// (rows of `width` halves; `rows` planes apart), as the GEMM's own split
+// would write them.
+__global__ void __launch_bounds__(256) k_rms_rows_split(const float *x, int ldx, const float *gain, float eps,
+                                                        int width, float *scale, _Float16 *hl, int rows) {
+    __shared__ float red[4];
+    const float *xr = x + (int64_t)blockIdx.x * ldx;
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) ss += xr[j] * xr[j];
+    ss = block_sum(ss, red);
+    const float rs = 1.0f / sqrtf(ss / (float)width + eps);
+    float mx = 0.0f;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) mx = fmaxf(mx, fabsf(xr[j] * rs * (gain ? gain[j] : 1.0f)));
+    mx = block_max(mx, red);
+    const float sc = f16_range_scale(mx);
+    if (threadIdx.x == 0) scale[blockIdx.x] = sc;
+    _Float16 *hi = hl + (int64_t)blockIdx.x * width, *lo = hl + (int64_t)rows * width + (int64_t)blockIdx.x * width;
+    for (int j = threadIdx.x; j < width; j += blockDim.x) {
+        _Float16 h, l;
+        split2h(xr[j] * rs * (gain ? gain[j] : 1.0f) * sc, h, l);
+        hi[j] = h;
+        lo[j] = l;
+    }
+}
+
 // grid (rows, ceil((heads + kv_heads) / 4)), 256 threads: one wave per head.
 __global__ void __launch_bounds__(256) k_qk_rows(float *qkv, int ld, int p0, int heads, int kv_heads, int d,
                                                  const float *q_gain, const float *k_gain, float eps, int norm,
@@ -728,6 +755,13 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
                     int ldy, int rows) {
     k_rms_rows<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, y, ldy);
     MR_LAUNCHED("enqueue row RMSNorm");
+    return MR_OK;
+}
+
+int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
+                          float *scale, _Float16 *planes, int rows) {
+    k_rms_rows_split<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
+    MR_LAUNCHED("enqueue row RMSNorm into FP16 terms");
     return MR_OK;
 }
 
