@@ -38,7 +38,11 @@ constexpr int kThreads = 256;
 #ifndef MR_GEMM_SWIGLU_NI
 #define MR_GEMM_SWIGLU_NI 4
 #endif
-constexpr int kSwigluNI = MR_GEMM_SWIGLU_NI;   // 16-column MFMA tiles per wave in the SwiGLU FP16-term GEMM
+constexpr int kSwigluNI = MR_GEMM_SWIGLU_NI;
+#ifndef MR_GEMM_KBH
+#define MR_GEMM_KBH 64
+#endif
+constexpr int kKBH = MR_GEMM_KBH;   // k-step of the FP16-term GEMM (halves)   // 16-column MFMA tiles per wave in the SwiGLU FP16-term GEMM
 
 template <int DT>
 constexpr int planes() {
@@ -309,28 +313,40 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, int m0, int n0) {
     gemm_store<EPI>(g, m0, n0, acc, [](int) { return 1.0f; });
 }
 
-// A's FP16 planes of a k-step: thread t holds 16 bytes of plane i / 2, rows
-// (t / 4) + 64 (i % 2), halves 8 (t % 4) .. + 7.
+// A's FP16 planes of a k-step of KB halves: per plane 128 rows of KB / 8
+// chunks of 16 bytes; thread t holds chunks t + 256 j of each plane (row
+// (t + 256 j) / (KB / 8), halves 8 ((t + 256 j) % (KB / 8)) .. + 7).
+template <int KB>
 struct AHRegs {
-    u32x4 v[4];
+    u32x4 v[2][KB / 16];
 };
 
-__device__ __forceinline__ void load_a_h(const GemmArgs &g, int m0, int k0, AHRegs &r) {
+template <int KB>
+__device__ __forceinline__ void load_a_h(const GemmArgs &g, int m0, int k0, AHRegs<KB> &r) {
+    constexpr int CPR = KB / 8;
     const int tid = threadIdx.x;
-    const int col = k0 + (tid & 3) * 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = m0 + (tid >> 2) + 64 * (i & 1);
-        const _Float16 *plane = g.ahl + (int64_t)(i >> 1) * g.m * g.k;
-        if (row < g.m && col < g.k) r.v[i] = *gmem((const u32x4 *)(plane + (int64_t)row * g.k + col));
-        else r.v[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < KB / 16; ++j) {
+            const int q = tid + kThreads * j, row = m0 + q / CPR, col = k0 + (q % CPR) * 8;
+            const _Float16 *plane = g.ahl + (int64_t)p * g.m * g.k;
+            if (row < g.m && col < g.k) r.v[p][j] = *gmem((const u32x4 *)(plane + (int64_t)row * g.k + col));
+            else r.v[p][j] = u32x4{0u, 0u, 0u, 0u};
+        }
 }
 
-__device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][kPitch], const AHRegs &r) {
+template <int KB>
+__device__ __forceinline__ void store_a_h(_Float16 (*as)[kBM][KB + 8], const AHRegs<KB> &r) {
+    constexpr int CPR = KB / 8;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4 *)&as[i >> 1][(tid >> 2) + 64 * (i & 1)][(tid & 3) * 8] = r.v[i];
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < KB / 16; ++j) {
+            const int q = tid + kThreads * j;
+            *(u32x4 *)&as[p][q / CPR][(q % CPR) * 8] = r.v[p][j];
+        }
 }
 
 // Weight row r of an FP16-term tile of 32 NI rows: two halves of 16 NI rows
@@ -351,34 +367,38 @@ __device__ __forceinline__ const char *w_row_h(const GemmArgs &g, int n0, int r,
     return (const char *)base + (int64_t)(ok ? f : 0) * g.k * 2;
 }
 
-// The FP16 weight rows of a k-step: NI / 2 chunks of 16 bytes per thread.
-template <int EPI, int NI>
-__device__ __forceinline__ void load_w_h(const GemmArgs &g, int n0, int k0, u32x4 (&r)[NI / 2]) {
+// The FP16 weight rows of a k-step: 32 NI rows of KB / 8 chunks of 16 bytes,
+// NI KB / 64 chunks per thread (row q / (KB / 8), halves 8 (q % (KB / 8))).
+template <int EPI, int NI, int KB>
+__device__ __forceinline__ void load_w_h(const GemmArgs &g, int n0, int k0, u32x4 (&r)[NI * KB / 64]) {
+    constexpr int CPR = KB / 8;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < NI / 2; ++i) {
-        const int idx = tid + kThreads * i;
-        const int col = k0 + (idx & 3) * 8;
+    for (int i = 0; i < NI * KB / 64; ++i) {
+        const int q = tid + kThreads * i;
+        const int col = k0 + (q % CPR) * 8;
         bool ok;
-        const char *row = w_row_h<EPI, NI>(g, n0, idx >> 2, ok);
+        const char *row = w_row_h<EPI, NI>(g, n0, q / CPR, ok);
         if (ok && col < g.k) r[i] = *gmem((const u32x4 *)(row + (int64_t)col * 2));
         else r[i] = u32x4{0u, 0u, 0u, 0u};
     }
 }
 
 // One 128 x 32 NI output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
-// planes and row scales from k_row_split, the weights' FP16 copy); each wave
-// owns 64 x 16 NI outputs.  (Two LDS stages with one barrier per k-step
-// measured slower: the LDS per workgroup halves the workgroups per CU.)
-template <int EPI, int NI>
+// planes and row scales from k_row_split, the weights' FP16 copy), k-steps
+// of KB halves; each wave owns 64 x 16 NI outputs.  (Two LDS stages with one
+// barrier per k-step measured slower: the LDS per workgroup halves the
+// workgroups per CU.)
+template <int EPI, int NI, int KB>
 __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
-    __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][kPitch];
-    __shared__ __attribute__((aligned(16))) _Float16 bs[32 * NI][kPitch];
+    constexpr int CPR = KB / 8;
+    __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][KB + 8];
+    __shared__ __attribute__((aligned(16))) _Float16 bs[32 * NI][KB + 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 15, lk = (lane >> 4) * 8;
-    const int nk = (g.k + kBK - 1) / kBK;
+    const int nk = (g.k + KB - 1) / KB;
 
     f32x4 acc[4][NI];
 #pragma unroll
@@ -386,35 +406,38 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    AHRegs ar;
-    u32x4 wr[NI / 2];
-    load_a_h(g, m0, 0, ar);
-    load_w_h<EPI, NI>(g, n0, 0, wr);
+    AHRegs<KB> ar;
+    u32x4 wr[NI * KB / 64];
+    load_a_h<KB>(g, m0, 0, ar);
+    load_w_h<EPI, NI, KB>(g, n0, 0, wr);
     for (int kt = 0; kt < nk; ++kt) {
         if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
-        store_a_h(as, ar);
+        store_a_h<KB>(as, ar);
 #pragma unroll
-        for (int i = 0; i < NI / 2; ++i) {
-            const int idx = tid + kThreads * i;
-            *(u32x4 *)&bs[idx >> 2][(idx & 3) * 8] = wr[i];
+        for (int i = 0; i < NI * KB / 64; ++i) {
+            const int q = tid + kThreads * i;
+            *(u32x4 *)&bs[q / CPR][(q % CPR) * 8] = wr[i];
         }
         lds_barrier();
         if (kt + 1 < nk) {
-            load_a_h(g, m0, (kt + 1) * kBK, ar);
-            load_w_h<EPI, NI>(g, n0, (kt + 1) * kBK, wr);
+            load_a_h<KB>(g, m0, (kt + 1) * KB, ar);
+            load_w_h<EPI, NI, KB>(g, n0, (kt + 1) * KB, wr);
         }
-        f16x8 bf[NI];
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) bf[ni] = *(const f16x8 *)&bs[wn * 16 * NI + ni * 16 + lr][lk];
+        for (int kk = 0; kk < KB / 32; ++kk) {
+            f16x8 bf[NI];
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-            const f16x8 lo = *(const f16x8 *)&as[1][wm * 64 + mi * 16 + lr][lk];
-            const f16x8 hi = *(const f16x8 *)&as[0][wm * 64 + mi * 16 + lr][lk];
-            // the smaller term first
+            for (int ni = 0; ni < NI; ++ni) bf[ni] = *(const f16x8 *)&bs[wn * 16 * NI + ni * 16 + lr][32 * kk + lk];
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
+            for (int mi = 0; mi < 4; ++mi) {
+                const f16x8 lo = *(const f16x8 *)&as[1][wm * 64 + mi * 16 + lr][32 * kk + lk];
+                const f16x8 hi = *(const f16x8 *)&as[0][wm * 64 + mi * 16 + lr][32 * kk + lk];
+                // the smaller term first
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
+                for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
+            }
         }
     }
     const float inv_w = 1.0f / g.wscale;
@@ -423,7 +446,7 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 
 template <int EPI, int NI>
 __global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
-    gemm_tile_h<EPI, NI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    gemm_tile_h<EPI, NI, kKBH>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 // A in FP16 terms, once per GEMM: row r's scale 2^t (max_k |a[r][k]| 2^t in
