@@ -14,6 +14,7 @@
 // captured once in a hipGraph and replayed for every token.
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 
 #include "engine.h"
 
@@ -841,6 +842,23 @@ int setup_persistent(mr_model *m) {
 
 // heavy-medium-2.0 layer: packed projections present, experts complete,
 // per-inner-loop rings (capacity = context) and block sums, expert table.
+// FP16 copies of projection matrices for the batched prefill's FP16-term
+// GEMMs (gemm.h), each with its power-of-two scale; the matrices in `shared`
+// (a SwiGLU pair, one tile holds rows of both) take their smaller scale.
+int f16_copies(mr_model *m, std::initializer_list<Weight *> ws, std::initializer_list<Weight *> shared) {
+    for (Weight *w : ws)
+        MR_TRY(gemm_f16_weight_scale(m->ctx->stream, w->ptr, w->dtype, w->rows * w->cols, &w->f16_scale));
+    float common = INFINITY;
+    for (Weight *w : shared) common = std::min(common, w->f16_scale);
+    for (Weight *w : shared) w->f16_scale = common;
+    for (Weight *w : ws)
+        if (w->f16_scale > 0.0f) {
+            MR_TRY(device_alloc(m, (size_t)w->rows * w->cols * 2, &w->f16));
+            MR_TRY(gemm_f16_weight_copy(m->ctx->stream, w->ptr, w->rows * w->cols, w->f16_scale, w->f16));
+        }
+    return MR_OK;
+}
+
 int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     const mr_model_desc &d = m->d;
     const int hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
@@ -896,6 +914,7 @@ int finalize_light_layer(mr_model *m, Layer &L, int i) {
     if (L.kv_up.rows != 3) return fail(MR_ERR_STATE, "missing k/v weight" + at);
     L.kv_up.rows = 2 * kvw;
     MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
+    MR_TRY(f16_copies(m, {&L.qkv, &L.kv_up, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
     L.light_cap = d.window + d.memory_slots + 1;
     const size_t cap = L.light_cap;
     MR_TRY(device_alloc(m, cap * d.latent_dim * sizeof(float), (void **)&L.arena));
@@ -1154,16 +1173,7 @@ int mr_model_finalize(mr_model *m) {
         MR_TRY(need(L.ffn.up, "ffn.up", i));
         MR_TRY(need(L.ffn.down, "ffn.down", i));
         MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
-        // FP16 copies of the projections for the batched prefill's FP16-term
-        // GEMMs (gate and up share the smaller scale: one per tile)
-        for (Weight *w : {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down})
-            MR_TRY(gemm_f16_weight_scale(m->ctx->stream, w->ptr, w->dtype, w->rows * w->cols, &w->f16_scale));
-        L.ffn.gate.f16_scale = L.ffn.up.f16_scale = std::min(L.ffn.gate.f16_scale, L.ffn.up.f16_scale);
-        for (Weight *w : {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down})
-            if (w->f16_scale > 0.0f) {
-                MR_TRY(device_alloc(m, (size_t)w->rows * w->cols * 2, &w->f16));
-                MR_TRY(gemm_f16_weight_copy(m->ctx->stream, w->ptr, w->rows * w->cols, w->f16_scale, w->f16));
-            }
+        MR_TRY(f16_copies(m, {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
         const int kvw = L.kv_heads * hd;
         max_kvw = std::max(max_kvw, kvw);
         max_kvh = std::max(max_kvh, L.kv_heads);
@@ -1372,7 +1382,8 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     const size_t ext = heavy || light ? r * d.query_heads * (d.head_dim + 4) : 0;
     int max_cap = 0;
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
-    const bool gqa = !heavy && !light && d.family != MR_FAMILY_FLASHNANO_16;
+    for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.light_cap);
+    const bool gqa = !heavy && d.family != MR_FAMILY_FLASHNANO_16;   // with flashlighting-2.0
     w->kv16_rows = gqa ? rows + max_cap : 0;
     const size_t kv16 = gqa ? (size_t)w->kv16_rows * kvw * 2 : 0;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
@@ -1656,18 +1667,28 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, lat = d.latent_dim;
     const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
     MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    // FP16-term GEMMs where the weights have FP16 copies (BF16 weights)
+    auto f16 = [&](GemmArgs &g, const Weight &wt, size_t row0 = 0) {
+        g.wscale = wt.f16_scale;
+        g.wh = wt.f16 ? (const void *)((const _Float16 *)wt.f16 + row0 * wt.cols) : nullptr;
+        g.ascale = w.rowscale;
+        g.ahl_ws = w.planes;
+    };
     GemmArgs q;   // the Q rows of the packed [Wq; Wlatent]
     q.a = w.xn; q.lda = h; q.w = L.qkv.ptr; q.dtype = L.qkv.dtype; q.c = w.qkv; q.ldc = ld;
     q.m = T; q.n = qd; q.k = h;
+    f16(q, L.qkv);
     MR_TRY(launch_gemm(s, GEMM_STORE, q));
     GemmArgs lt = q;   // its latent rows, then RMSNorm with latent_norm in place
     lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
     lt.n = lat;
+    f16(lt, L.qkv, qd);
     MR_TRY(launch_gemm(s, GEMM_STORE, lt));
     MR_TRY(launch_rms_rows(s, w.lat, lat, L.latent_norm.f(), d.norm_eps, lat, w.lat, lat, T));
     GemmArgs kv;   // [Wk; Wv] . latent beside the queries
     kv.a = w.lat; kv.lda = lat; kv.w = L.kv_up.ptr; kv.dtype = L.kv_up.dtype; kv.c = w.qkv + qd; kv.ldc = ld;
     kv.m = T; kv.n = 2 * kvw; kv.k = lat;
+    f16(kv, L.kv_up);
     MR_TRY(launch_gemm(s, GEMM_STORE, kv));
     MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd, L.q_norm.f(), L.k_norm.f(), d.norm_eps,
                           1, m->rope, d.split_half_rope));
@@ -1690,17 +1711,22 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     a.window = pl.window; a.hole = pl.hole; a.ext = pl.extra > 0 ? w.ext : nullptr;
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+    a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
     MR_TRY(launch_prefill_attention(s, a));
     GemmArgs o;
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.obuf; o.ldc = h; o.m = T; o.n = h; o.k = qd;
+    f16(o, L.o);
     MR_TRY(launch_gemm(s, GEMM_STORE, o));
     GemmArgs gu;   // the FFN branch reads the same normalized input
     gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
     gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
+    f16(gu, L.ffn.gate);
+    gu.wh2 = L.ffn.up.f16;
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.fbuf; dn.ldc = h;
     dn.m = T; dn.n = h; dn.k = ffn;
+    f16(dn, L.ffn.down);
     MR_TRY(launch_gemm(s, GEMM_STORE, dn));
     MR_TRY(launch_light_residual(s, w.x, w.obuf, w.fbuf, L.attention_gate.f(), L.ffn_gate.f(), d.residual_scale,
                                  T * h, nullptr));

@@ -727,7 +727,7 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     const int win = a.window ? a.window : a.cap;
     const int first = std::max(0, a.p0 - win + 1), n = a.p0 + a.rows - first;
     const bool h = a.d == 128 || a.d == 64 || a.d == 32;
-    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n <= a.kv16_rows && a.kv_heads * a.d <= 1024;
+    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n <= a.kv16_rows && a.kv_heads * a.d <= 4096;
     if (planes) {   // split the attended keys and values once
         MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
         const int threads = ceil_div(a.kv_heads * a.d / 4, kWave) * kWave;
