@@ -28,14 +28,13 @@ bool is_gqa(int family) {
            family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20;
 }
 
-// Families whose prompt can run as whole-chunk kernels: the GQA families whose
-// attention state is the ring alone, heavy-medium-2.0, whose block sums and
-// block choices are rebuilt per row from a scan of the chunk, and
-// flashlighting-2.0, whose latent memory is planned per step (flashnano-1.6's
-// relay rows take the token loop).
+// Families whose prompt can run as whole-chunk kernels: the GQA families
+// (flashnano-1.6 with the relay rows of every CBR chunk that ends inside the
+// prompt chunk built before its attention), heavy-medium-2.0, whose block sums
+// and block choices are rebuilt per row from a scan of the chunk, and
+// flashlighting-2.0, whose latent memory is planned per step.
 bool batched_prefill_family(int family) {
-    return family == MR_FAMILY_FLASHNANO_15 || family == MR_FAMILY_FLASHNANO_17 || family == MR_FAMILY_FLASHLITE_20 ||
-           family == MR_FAMILY_HEAVY_MEDIUM_20 || family == MR_FAMILY_FLASHLIGHTING_20;
+    return is_gqa(family) || family == MR_FAMILY_HEAVY_MEDIUM_20 || family == MR_FAMILY_FLASHLIGHTING_20;
 }
 
 int dtype_bytes(int dt) { return dt == MR_F32 ? 4 : 2; }
@@ -112,25 +111,14 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *logits, int n, int
 }
 
 // ---- flashnano-1.6 CBR (model.py:118-144) -----------------------------------
-// Stores this step's normalized input in the pending chunk; at a chunk end pools
-// it into `slots` rows with learned queries (kernels.cl:110-130).  Block m pools
-// slot m.
-__global__ void __launch_bounds__(256) k_cbr_pool(const float *xnorm, float *pending, const float *queries,
-                                                  float *pooled, float *anchors, int *skip_flag, const int *pos_p,
-                                                  const int *done, int chunk, int h) {
-    extern __shared__ float sp[];   // [chunk] probabilities, then reduction scratch
+// Pools one chunk (row(t), t < chunk, at positions start_position + t) into one
+// slot with its learned query q: scores u . q / sqrt(h), softmax over the
+// chunk, the probability-weighted row and the rounded probability-weighted
+// position as its anchor (kernels.cl:110-130).  sp holds chunk + 8 floats.
+template <typename RowFn>
+__device__ void cbr_pool_slot(RowFn row, const float *q, int chunk, int h, int start_position, float *sp,
+                              float *pooled, float *anchor) {
     float *red = sp + chunk;
-    const int pos = *pos_p;
-    const bool skip = *done || (pos % chunk != chunk - 1);
-    if (blockIdx.x == 0) {
-        if (threadIdx.x == 0) *skip_flag = skip ? 1 : 0;
-        if (!*done)
-            for (int j = threadIdx.x; j < h; j += blockDim.x) pending[(int64_t)(pos % chunk) * h + j] = xnorm[j];
-    }
-    if (skip) return;
-    const int m = blockIdx.x;
-    const float *q = queries + (int64_t)m * h;
-    auto row = [&](int t) -> const float * { return t == chunk - 1 ? xnorm : pending + (int64_t)t * h; };
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int t = wave; t < chunk; t += blockDim.x / 64) {
         const float *u = row(t);
@@ -149,17 +137,65 @@ __global__ void __launch_bounds__(256) k_cbr_pool(const float *xnorm, float *pen
     __syncthreads();
     for (int t = threadIdx.x; t < chunk; t += blockDim.x) sp[t] = expf(sp[t] - mx) / den;
     __syncthreads();
-    const int start_position = pos + 1 - chunk;
     for (int j = threadIdx.x; j < h; j += blockDim.x) {
         float v = 0.0f;
         for (int t = 0; t < chunk; ++t) v = fmaf(sp[t], row(t)[j], v);
-        pooled[(int64_t)m * h + j] = v;
+        pooled[j] = v;
     }
     if (threadIdx.x == 0) {
         float ps = 0.0f;
         for (int t = 0; t < chunk; ++t) ps = fmaf(sp[t], (float)(start_position + t), ps);
-        anchors[m] = rintf(ps);
+        *anchor = rintf(ps);
     }
+}
+
+// Token step: stores this step's normalized input in the pending chunk; at a
+// chunk end pools it into `slots` rows.  Block m pools slot m.
+__global__ void __launch_bounds__(256) k_cbr_pool(const float *xnorm, float *pending, const float *queries,
+                                                  float *pooled, float *anchors, int *skip_flag, const int *pos_p,
+                                                  const int *done, int chunk, int h) {
+    extern __shared__ float sp[];   // [chunk] probabilities, then reduction scratch
+    const int pos = *pos_p;
+    const bool skip = *done || (pos % chunk != chunk - 1);
+    if (blockIdx.x == 0) {
+        if (threadIdx.x == 0) *skip_flag = skip ? 1 : 0;
+        if (!*done)
+            for (int j = threadIdx.x; j < h; j += blockDim.x) pending[(int64_t)(pos % chunk) * h + j] = xnorm[j];
+    }
+    if (skip) return;
+    const int m = blockIdx.x;
+    auto row = [&](int t) -> const float * { return t == chunk - 1 ? xnorm : pending + (int64_t)t * h; };
+    cbr_pool_slot(row, queries + (int64_t)m * h, chunk, h, pos + 1 - chunk, sp, pooled + (int64_t)m * h,
+                  anchors + m);
+}
+
+// Batched prefill: pools the chunks first_chunk .. first_chunk + gridDim.y - 1,
+// which end inside the prompt rows at positions p0 .. (block (m, c): slot m
+// of chunk first_chunk + c, into pooled row c * slots + m).  Positions before
+// p0 read the pending buffer (row position % chunk), the others row
+// position - p0 of xn.
+__global__ void __launch_bounds__(256) k_cbr_pool_rows(const float *xn, int ldx, const float *pending,
+                                                       const float *queries, float *pooled, float *anchors, int p0,
+                                                       int first_chunk, int chunk, int h) {
+    extern __shared__ float sp[];
+    const int m = blockIdx.x, r = blockIdx.y * gridDim.x + m;
+    const int start = (first_chunk + blockIdx.y) * chunk;
+    auto row = [&](int t) -> const float * {
+        const int p = start + t;
+        return p < p0 ? pending + (int64_t)(p % chunk) * h : xn + (int64_t)(p - p0) * ldx;
+    };
+    cbr_pool_slot(row, queries + (int64_t)m * h, chunk, h, start, sp, pooled + (int64_t)r * h, anchors + r);
+}
+
+// Batched prefill: the pending buffer as the token loop leaves it after the
+// rows at positions p0 .. p0 + rows - 1 (row position % chunk holds the
+// latest position of that residue); block b stores row rows - gridDim.x + b.
+__global__ void __launch_bounds__(256) k_cbr_pending_rows(const float *xn, int ldx, float *pending, int p0, int rows,
+                                                          int chunk, int h) {
+    const int t = rows - gridDim.x + blockIdx.x;
+    const float *src = xn + (int64_t)t * ldx;
+    float *dst = pending + (int64_t)((p0 + t) % chunk) * h;
+    for (int j = threadIdx.x; j < h; j += blockDim.x) dst[j] = src[j];
 }
 
 // Pooled rows through Wk and Wv (model.py:135): one wave per output value.
@@ -176,15 +212,12 @@ __global__ void __launch_bounds__(256) k_cbr_project(const float *pooled, const 
     if (lane == 0) out[(int64_t)m * kvw2 + o] = acc;
 }
 
-// K-norm + RoPE at the pooled anchors, then relay append (model.py:136-144).
-__global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float *anchors, const float *k_gain,
-                                                    float eps, const float *rope, int split_half, float *relay_k,
-                                                    float *relay_v, const int *skip_flag, const int *pos_p,
-                                                    int chunk, int slots, int kv_heads, int d) {
-    extern __shared__ float kr[];
-    if (*skip_flag) return;
-    const int m = blockIdx.x, kvw = kv_heads * d;
-    const float *src = kv + (int64_t)m * 2 * kvw;
+// K-norm + RoPE at the pooled anchor of one pooled [K | V] row, then its relay
+// row dst (model.py:136-144).  kr holds kv_heads * d floats.
+__device__ void cbr_finish_row(const float *src, float anchor, const float *k_gain, float eps, const float *rope,
+                               int split_half, float *relay_k, float *relay_v, int64_t dst, int kv_heads, int d,
+                               float *kr) {
+    const int kvw = kv_heads * d;
     for (int j = threadIdx.x; j < kvw; j += blockDim.x) kr[j] = src[j];
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -198,23 +231,45 @@ __global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float
     }
     __syncthreads();
     const int half = d / 2;
+    // anchors are rounded positions inside the chunk, so they index the table
+    const float *cs = rope + (int64_t)anchor * half * 2;
     for (int i = threadIdx.x; i < kv_heads * half; i += blockDim.x) {
         int hh = i / half, p = i % half;
         float *row = kr + hh * d;
         int j = split_half ? p : 2 * p, k = split_half ? p + half : 2 * p + 1;
         float u = row[j], v = row[k];
-        // anchors are rounded positions inside the chunk, so they index the table
-        const float *cs = rope + (int64_t)anchors[m] * half * 2;
         rope_rotate(u, v, cs[2 * p], cs[2 * p + 1]);
         row[j] = u;
         row[k] = v;
     }
     __syncthreads();
-    const int64_t dst = ((int64_t)(*pos_p / chunk) * slots + m) * kvw;
     for (int j = threadIdx.x; j < kvw; j += blockDim.x) {
-        relay_k[dst + j] = kr[j];
-        relay_v[dst + j] = src[kvw + j];
+        relay_k[dst * kvw + j] = kr[j];
+        relay_v[dst * kvw + j] = src[kvw + j];
     }
+}
+
+// Token step: block m finishes slot m of the chunk that ends at this position.
+__global__ void __launch_bounds__(256) k_cbr_finish(const float *kv, const float *anchors, const float *k_gain,
+                                                    float eps, const float *rope, int split_half, float *relay_k,
+                                                    float *relay_v, const int *skip_flag, const int *pos_p,
+                                                    int chunk, int slots, int kv_heads, int d) {
+    extern __shared__ float kr[];
+    if (*skip_flag) return;
+    const int m = blockIdx.x;
+    cbr_finish_row(kv + (int64_t)m * 2 * kv_heads * d, anchors[m], k_gain, eps, rope, split_half, relay_k, relay_v,
+                   (int64_t)(*pos_p / chunk) * slots + m, kv_heads, d, kr);
+}
+
+// Batched prefill: block r finishes pooled row r (relay row first_chunk * slots + r).
+__global__ void __launch_bounds__(256) k_cbr_finish_rows(const float *kv, const float *anchors, const float *k_gain,
+                                                         float eps, const float *rope, int split_half, float *relay_k,
+                                                         float *relay_v, int first_chunk, int slots, int kv_heads,
+                                                         int d) {
+    extern __shared__ float kr[];
+    const int r = blockIdx.x;
+    cbr_finish_row(kv + (int64_t)r * 2 * kv_heads * d, anchors[r], k_gain, eps, rope, split_half, relay_k, relay_v,
+                   (int64_t)first_chunk * slots + r, kv_heads, d, kr);
 }
 
 // Non-affine RMSNorm of the learned CBR queries, once per model (model.py:126-127).
@@ -1353,7 +1408,9 @@ constexpr int kPrefillRows = 4096;   // prompt rows per batched prefill chunk
 // for heavy-medium-2.0 also the latent rows, the block scan, the block
 // partials, the router logits, the routing and the expert-major gather; for
 // flashlighting-2.0 the latent rows, logical row 0 of each step, its keys and
-// values and partials, both branches' outputs and the chunk's plan.
+// values and partials, both branches' outputs and the chunk's plan; for
+// flashnano-1.6 the pooled CBR rows, their anchors and [K | V] projections,
+// and the relay partials.
 struct PrefillWs {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *lg = nullptr;
     float *lat = nullptr, *sums = nullptr, *ext = nullptr, *router = nullptr, *mw = nullptr, *xg = nullptr,
@@ -1362,6 +1419,7 @@ struct PrefillWs {
     float *slot0 = nullptr, *slot0_final = nullptr, *kv0 = nullptr, *obuf = nullptr, *fbuf = nullptr,
           *merge_count = nullptr;
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
+    float *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;   // flashnano-1.6 pooled rows
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
@@ -1379,11 +1437,14 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     const size_t slots = heavy ? (size_t)d.router_top_k_max + d.shared_experts : 1;
     const size_t groups = heavy ? (size_t)d.routed_experts + d.shared_experts : 0;
     const size_t kmax = heavy ? d.router_top_k_max : 0, lat = heavy || light ? d.latent_dim : 0;
-    const size_t ext = heavy || light ? r * d.query_heads * (d.head_dim + 4) : 0;
+    const bool cbr = d.family == MR_FAMILY_FLASHNANO_16;
+    // pooled rows: cbr_slots per CBR chunk ending inside the rows
+    const size_t pr = cbr ? (size_t)(rows / d.cbr_chunk_size + 1) * d.cbr_slots : 0;
+    const size_t ext = heavy || light || cbr ? r * d.query_heads * (d.head_dim + 4) : 0;
     int max_cap = 0;
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.light_cap);
-    const bool gqa = !heavy && d.family != MR_FAMILY_FLASHNANO_16;   // with flashlighting-2.0
+    const bool gqa = !heavy;   // with flashlighting-2.0
     w->kv16_rows = gqa ? rows + max_cap : 0;
     const size_t kv16 = gqa ? (size_t)w->kv16_rows * kvw * 2 : 0;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
@@ -1403,7 +1464,10 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->fbuf, light ? r * h : 0}, {(void **)&w->merge_count, light ? r : 0},
         {(void **)&w->flags, light ? r : 0}, {(void **)&w->extra_index, light ? r : 0},
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
-        {(void **)&w->rowscale, r}, {(void **)&w->planes, r * std::max({h, qd, (size_t)d.ffn_dim})},
+        // flashnano-1.6
+        {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
+        {(void **)&w->rowscale, std::max(r, pr)},
+        {(void **)&w->planes, std::max(r, pr) * std::max({h, qd, (size_t)d.ffn_dim})},
         {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, gqa ? 2 * kvw : 0},
         {(void **)&w->kv16_max, gqa ? 2 * kvw : 0}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
@@ -1514,6 +1578,38 @@ void plan_light_chunk(const mr_model_desc &d, int cap, int p0, int rows, LightPl
     pl.slot0_count = C0;
 }
 
+// flashnano-1.6 over the chunk's rows (model.py:118-144): the relay rows of
+// every CBR chunk that ends at a position p0 .. p0 + T - 1, all at once (a
+// chunk's pooled rows depend only on its normalized layer inputs, w.xn here
+// and the pending buffer before p0), then the pending buffer as the token
+// loop leaves it.
+int cbr_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
+    const mr_model_desc &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
+    const int chunk = d.cbr_chunk_size, slots = d.cbr_slots;
+    const int first = p0 / chunk, nc = (p0 + T) / chunk - first;   // chunk c ends at (c + 1) * chunk - 1
+    if (nc > 0) {
+        k_cbr_pool_rows<<<dim3(slots, nc), 256, (size_t)(chunk + 8) * sizeof(float), s>>>(
+            w.xn, h, L.pending, L.cbr_queries, w.cbr_pooled, w.cbr_anchor, p0, first, chunk, h);
+        MR_LAUNCHED("enqueue cbr pool rows");
+        GemmArgs kv;   // pooled rows through [Wk; Wv], the rows after Wq of the fused projection
+        kv.a = w.cbr_pooled; kv.lda = h; kv.dtype = L.qkv.dtype;
+        kv.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype);
+        kv.c = w.cbr_kv; kv.ldc = 2 * kvw; kv.m = nc * slots; kv.n = 2 * kvw; kv.k = h;
+        kv.wscale = L.qkv.f16_scale; kv.ascale = w.rowscale; kv.ahl_ws = w.planes;
+        if (L.qkv.f16) kv.wh = (const _Float16 *)L.qkv.f16 + (size_t)qd * h;
+        MR_TRY(launch_gemm(s, GEMM_STORE, kv));
+        k_cbr_finish_rows<<<nc * slots, 256, (size_t)kvw * sizeof(float), s>>>(
+            w.cbr_kv, w.cbr_anchor, L.k_norm.f(), d.norm_eps, m->rope, d.split_half_rope, L.relay_k, L.relay_v,
+            first, slots, L.kv_heads, hd);
+        MR_LAUNCHED("enqueue cbr finish rows");
+    }
+    k_cbr_pending_rows<<<std::min(T, chunk), 256, 0, s>>>(w.xn, h, L.pending, p0, T, chunk, h);
+    MR_LAUNCHED("enqueue cbr pending rows");
+    return MR_OK;
+}
+
 // One GQA layer over the chunk's rows (model.py:95-116, 264-266).
 int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     const mr_model_desc &d = m->d;
@@ -1524,9 +1620,12 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     g.a = w.xn; g.lda = h; g.w = L.qkv.ptr; g.dtype = L.qkv.dtype; g.c = w.qkv; g.ldc = ld;
     g.m = T; g.n = ld; g.k = h; g.wscale = L.qkv.f16_scale; g.wh = L.qkv.f16; g.ascale = w.rowscale; g.ahl_ws = w.planes;
     // the normalized rows go straight into the FP16-term GEMM's A workspace
-    g.a_split = g.wscale > 0.0f;
+    // (flashnano-1.6 pools them in FP32 first)
+    const bool cbr = d.family == MR_FAMILY_FLASHNANO_16;
+    g.a_split = g.wscale > 0.0f && !cbr;
     if (g.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
     else MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    if (cbr) MR_TRY(cbr_layer_rows(m, L, w, p0, T));
     MR_TRY(launch_gemm(s, GEMM_STORE, g));
     MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd,
                           d.qk_norm ? L.q_norm.f() : nullptr, d.qk_norm ? L.k_norm.f() : nullptr,
@@ -1536,6 +1635,14 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
     a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
+    if (cbr) {   // the relay rows join every row's softmax as its extra partial
+        RelayPartialArgs r;
+        r.qkv = w.qkv; r.ld = ld; r.relay_k = L.relay_k; r.relay_v = L.relay_v; r.ext = w.ext;
+        r.p0 = p0; r.rows = T; r.heads = d.query_heads; r.kv_heads = L.kv_heads; r.d = hd;
+        r.chunk = d.cbr_chunk_size; r.slots = d.cbr_slots; r.inv_root = a.inv_root;
+        MR_TRY(launch_relay_partial(s, r));
+        a.ext = w.ext;
+    }
     MR_TRY(launch_prefill_attention(s, a));
     MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
     GemmArgs o;

@@ -38,6 +38,19 @@ struct PrefillAttnArgs {
 // with ext, the extra columns' partial joins the softmax.
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a);
 
+// flashnano-1.6's relay rows (keys pooled from completed chunks) as the
+// attention's extra partial: ext[t][head] = (m, l, 0, 0, o[d]) over the first
+// ((p0 + t) / chunk) * slots relay rows (d a multiple of 4, at most 128).
+struct RelayPartialArgs {
+    const float *qkv = nullptr;   // [rows, ld]: normalized, rotated queries at column 0
+    int ld = 0;
+    const float *relay_k = nullptr, *relay_v = nullptr;   // [relay rows, kv_heads * d]
+    float *ext = nullptr;         // [rows][heads][d + 4]
+    int p0 = 0, rows = 0, heads = 0, kv_heads = 0, d = 0, chunk = 0, slots = 0;
+    float inv_root = 1.0f;
+};
+int launch_relay_partial(hipStream_t s, const RelayPartialArgs &a);
+
 // y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * gain (gain may be null).
 // k_rms_rows straight into an FP16-term GEMM's A workspace (row scales and
 // hi / lo planes, see gemm.h): the GEMM then runs with a_split.

@@ -714,6 +714,58 @@ __global__ void k_embed_rows(const void *table, int dt, const int *ids, int p0, 
     }
 }
 
+// The relay columns of flashnano-1.6 (attention's extra keys, model.py:104-110)
+// as a partial per row and query head, for the attention's ext input: row t
+// (position p0 + t) sees the first (position / chunk) * slots relay rows, those
+// of the chunks completed before it; m = the largest score (natural units),
+// l = sum of exp(score - m), o = the exp-weighted sum of values (no relay
+// row: m = -inf, l = 0, o = 0).  Wave w of block (t, y) takes query head
+// 4y + w; its lanes score 64 relay rows at a time, then take the dims.
+__global__ void __launch_bounds__(256) k_relay_partial(RelayPartialArgs a) {
+    const int t = blockIdx.x, lane = threadIdx.x & 63;
+    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (h >= a.heads) return;
+    const int G = a.heads / a.kv_heads, d = a.d, kvw = a.kv_heads * d;
+    const int n = ((a.p0 + t) / a.chunk) * a.slots;
+    const float *q = a.qkv + (int64_t)t * a.ld + h * d;
+    const float *kb = a.relay_k + (h / G) * d, *vb = a.relay_v + (h / G) * d;
+    float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int base = 0; base < n; base += kWave) {
+        const int j = base + lane;
+        float s = -INFINITY;
+        if (j < n) {
+            const float *k = kb + (int64_t)j * kvw;
+            float acc = 0.0f;
+            for (int i = 0; i < d; i += 4) {
+                const float4 kk = load_f4(k + i), qq = load_f4(q + i);
+                acc = fmaf(qq.x, kk.x, acc);
+                acc = fmaf(qq.y, kk.y, acc);
+                acc = fmaf(qq.z, kk.z, acc);
+                acc = fmaf(qq.w, kk.w, acc);
+            }
+            s = acc * a.inv_root;
+        }
+        const float mn = fmaxf(m, wave_max(s));   // finite: row base is scored
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+        const float p = j < n ? expf(s - mn) : 0.0f;
+        l = l * alpha + wave_sum(p);
+        o0 *= alpha;
+        o1 *= alpha;
+        const int cnt = min(kWave, n - base);
+        for (int jj = 0; jj < cnt; ++jj) {
+            const float pj = __shfl(p, jj, kWave);
+            const float *v = vb + (int64_t)(base + jj) * kvw;
+            if (lane < d) o0 = fmaf(pj, v[lane], o0);
+            if (lane + kWave < d) o1 = fmaf(pj, v[lane + kWave], o1);
+        }
+        m = mn;
+    }
+    float *out = a.ext + ((int64_t)t * a.heads + h) * (d + 4);
+    if (lane == 0) *(float4 *)out = make_float4(m, l, 0.0f, 0.0f);
+    if (lane < d) out[4 + lane] = o0;
+    if (lane + kWave < d) out[4 + lane + kWave] = o1;
+}
+
 }  // namespace
 
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
@@ -748,6 +800,16 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     else if (a.d <= 64) k_attn_prefill<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else k_attn_prefill<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
     MR_LAUNCHED("enqueue prefill attention");
+    return MR_OK;
+}
+
+int launch_relay_partial(hipStream_t s, const RelayPartialArgs &a) {
+    MR_REQUIRE(a.qkv && a.relay_k && a.relay_v && a.ext && a.rows > 0 && a.chunk > 0 && a.slots > 0,
+               "relay partial: bad arguments");
+    MR_REQUIRE(a.kv_heads > 0 && a.heads % a.kv_heads == 0 && a.d % 4 == 0 && a.d <= 2 * kWave && a.ld % 4 == 0,
+               "relay partial: unsupported geometry");
+    k_relay_partial<<<dim3(a.rows, ceil_div(a.heads, 4)), 256, 0, s>>>(a);
+    MR_LAUNCHED("enqueue relay partial");
     return MR_OK;
 }
 

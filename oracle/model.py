@@ -169,7 +169,9 @@ class OracleModel:
         state["pending"][row] = x.reshape(-1)
         if row != chunk - 1:
             return
-        queries = K.rms(self.w[p + "cbr"], None, h, c.cbr_norm_eps)
+        # the learned queries as FP32 values (the reference reads them widened,
+        # model.py:126); BF16 ones are held as bits like every matrix here
+        queries = K.rms(_widen(self.w[p + "cbr"]), None, h, c.cbr_norm_eps)
         probs = K.softmax(K.pool_scores(state["pending"], queries, chunk, slots, h))
         pooled, anchors = K.pool_mix(state["pending"], probs, chunk, slots, h, self.position + 1 - chunk)
         key = K.linear(pooled, self.w[p + "k"])

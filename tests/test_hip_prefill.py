@@ -17,7 +17,7 @@ from miracle_hip import MiracleModel, ModelConfig, presets, synthetic
 
 pytestmark = pytest.mark.gpu
 
-BATCHED = ("flashnano-1.5", "flashnano-1.7", "flashlite-2.0")
+BATCHED = ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
 
 
 def _variants():
@@ -98,6 +98,60 @@ def test_batched_full_prompt_matches_token_loop(backend):
     np.testing.assert_allclose(batched, exact, rtol=1e-3, atol=1e-4)
     assert model.generate(list(ids), max_new_tokens=8) == exact_stream
 
+
+
+# flashnano-1.6 with CBR chunks of 16 rows pooled into 4 relay rows each, a
+# 64-key local window and one global layer.
+CBR_MID = {"family": "flashnano-1.6", "cbr_chunk_size": 16, "cbr_slots": 4, "vocab_size": 1000, "hidden_size": 512,
+           "layers": 3, "query_heads": 8, "kv_heads": 2, "head_dim": 64, "ffn_dim": 1024, "max_positions": 2048,
+           "window": 64, "global_layers": [3], "rope_theta": 10000.0, "backend_format": 1}
+
+
+@pytest.mark.parametrize("dim,parts", [(64, None), (128, [(0, 37), (37, 150), (150, 300)])])
+def test_batched_cbr_geometry_matches_oracle(backend, dim, parts):
+    """flashnano-1.6 batched (BF16) over 300 tokens, whole and in chunks that
+    start and end inside CBR chunks (their pooling reads the pending rows of
+    the previous call): logits of every position against the oracle, then the
+    greedy stream, whose decode steps pool and read the relay the batched path
+    left."""
+    from oracle.model import OracleModel
+    config = dict(CBR_MID, head_dim=dim, query_heads=CBR_MID["hidden_size"] // dim)
+    weights = synthetic.synthetic_weights(config, 17, "bf16")
+    ids = synthetic.prompt_ids(config["vocab_size"], 300, 17)
+    ref = OracleModel(config, {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()},
+                      context_length=512)
+    want = ref.prefill(ids, return_all=True)
+    stream = ref.generate(list(ids), max_new_tokens=8)
+    print("case cbr batched", dim, parts, flush=True)
+    with MiracleModel(ModelConfig.from_dict(config), weights, backend=backend, context_length=512,
+                      prefill_mode="batched") as model:
+        if parts:
+            got = np.concatenate([model.prefill(ids[a:b], return_all=True) for a, b in parts])
+        else:
+            got = model.prefill(ids, return_all=True)
+        np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
+        assert model.generate(list(ids), max_new_tokens=8) == stream
+
+
+def test_batched_cbr_long_prompt_matches_token_loop(backend):
+    """flashnano-1.6 over a 2000-token prompt (124 CBR chunks, so up to 496
+    relay rows join each row's softmax): batched against the exact token loop,
+    every 16th row of logits, the decode step that follows, then the greedy
+    continuation."""
+    weights = synthetic.synthetic_weights(CBR_MID, 19, "bf16")
+    ids = synthetic.prompt_ids(CBR_MID["vocab_size"], 2000, 19)
+    print("case cbr long prompt", len(ids), flush=True)
+    with MiracleModel(ModelConfig.from_dict(CBR_MID), weights, backend=backend, context_length=2048) as model:
+        exact = model.prefill(ids, return_all=True)[::16].copy()
+        exact_last = model.prefill([int(np.argmax(exact[-1]))])
+        exact_stream = model.generate(list(ids), max_new_tokens=6)
+        model.reset()
+        model.prefill_mode = "batched"
+        batched = model.prefill(ids, return_all=True)[::16].copy()
+        assert model.position == len(ids)
+        np.testing.assert_allclose(batched, exact, rtol=1e-3, atol=1e-4)
+        np.testing.assert_allclose(model.prefill([int(np.argmax(exact[-1]))]), exact_last, rtol=1e-3, atol=1e-4)
+        assert model.generate(list(ids), max_new_tokens=6) == exact_stream
 
 def _heavy_against_oracle(model, cfg, config, weights, ids, context, parts=None):
     """Device first (its logits, greedy stream and recorded choices), then the

@@ -144,6 +144,29 @@ def test_oracle_seat_matches_a_prefilled_model():
         OracleModel(latent, synthetic.micro_weights(latent), context_length=12).seat(4)
 
 
+
+@pytest.mark.parametrize("family", ["flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlighting-2.0"])
+def test_oracle_bf16_bits_equal_widened_weights(family):
+    """The oracle holds BF16 matrices as bits and widens them where it uses
+    them; given the same weights already widened to FP32 it must compute the
+    same logits.  (flashnano-1.6 reads its learned CBR queries through an
+    RMSNorm rather than a projection: unwidened bits there are integers and
+    the relay rows come out wrong.)"""
+    config = dict(presets.micro(family), hidden_size=64, query_heads=4, kv_heads=2, head_dim=16, ffn_dim=96,
+                  vocab_size=64, max_positions=64)
+    if family == "flashnano-1.6":
+        config.update(cbr_chunk_size=4, cbr_slots=2)
+    if family == "flashlighting-2.0":
+        config.update(latent_dim=16)
+    weights = synthetic.synthetic_weights(config, 23, "bf16")
+    bits = {k: (v.bits if hasattr(v, "bits") else v) for k, v in weights.items()}
+    wide = {k: ((v.astype(np.uint32) << 16).view(np.float32) if v.dtype == np.uint16 else v) for k, v in bits.items()}
+    assert any(v.dtype == np.uint16 and v.ndim == 2 for v in bits.values())
+    ids = synthetic.prompt_ids(64, 20, 23)
+    got = OracleModel(config, bits, context_length=32).prefill(ids, return_all=True)
+    want = OracleModel(config, wide, context_length=32).prefill(ids, return_all=True)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
 def test_oracle_workload_tiny(golden_dir):
     z = np.load(golden_dir / "workload_flashnano-1.5-tiny.npz")
     wl = presets.workload("flashnano-1.5-tiny")
