@@ -108,8 +108,9 @@ def decode_bytes(cfg, context, position, dtype_bytes=2):
 def prefill_flops(cfg, context, tokens):
     """Algorithmic FLOPs of a batched prefill of `tokens` from position 0: the
     projections (2 per weight per token), attention scores and mixing
-    (4 * query heads * head_dim per query-key pair inside each layer's window)
-    and the LM head of the last token."""
+    (4 * query heads * head_dim per query-key pair inside each layer's window,
+    and per relay row a query sees in flashnano-1.6) and the LM head of the
+    last token."""
     h, d, hq, f, V = cfg.hidden_size, cfg.head_dim, cfg.query_heads, cfg.ffn_dim, cfg.vocab_size
     proj = attn = 0
     for layer in range(cfg.layers):
@@ -117,6 +118,8 @@ def prefill_flops(cfg, context, tokens):
         proj += h * (hq * d + 2 * kvw) + hq * d * h + 3 * h * f
         cap = min(cfg.layer_window(layer) or context, context)
         keys = sum(min(t + 1, cap) for t in range(tokens))
+        if cfg.family == "flashnano-1.6":
+            keys += sum((t // cfg.cbr_chunk_size) * cfg.cbr_slots for t in range(tokens))
         attn += 4 * hq * d * keys
     return 2 * tokens * proj + attn + 2 * h * V
 
@@ -291,12 +294,9 @@ def main():
     wl = presets.workload(name)
     cfg = ModelConfig.from_dict(wl["config"])
     gqa = cfg.family in ("flashnano-1.5", "flashnano-1.6", "flashnano-1.7", "flashlite-2.0")
-    # batched prefill covers the GQA families without relay rows and heavy-medium-2.0; the others take the
-    # token loop
-    batched_families = ("flashnano-1.5", "flashnano-1.7", "flashlite-2.0", "heavy-medium-2.0", "flashlighting-2.0")
-    prefill_mode = args.prefill_mode if cfg.family in batched_families else "exact"
+    prefill_mode = args.prefill_mode   # every family has the batched path
     prompt_len = args.prompt or wl["prompt"]
-    if prompt_len + args.warmup + args.steps > wl["context"]:
+    if prompt_len + (0 if args.prefill_only else args.warmup + args.steps) > wl["context"]:
         raise SystemExit("prompt + warmup + steps exceed the context")
     log("generating synthetic weights")
     weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])

@@ -169,22 +169,61 @@ __global__ void __launch_bounds__(256) k_cbr_pool(const float *xnorm, float *pen
                   anchors + m);
 }
 
-// Batched prefill: pools the chunks first_chunk .. first_chunk + gridDim.y - 1,
-// which end inside the prompt rows at positions p0 .. (block (m, c): slot m
-// of chunk first_chunk + c, into pooled row c * slots + m).  Positions before
-// p0 read the pending buffer (row position % chunk), the others row
-// position - p0 of xn.
-__global__ void __launch_bounds__(256) k_cbr_pool_rows(const float *xn, int ldx, const float *pending,
-                                                       const float *queries, float *pooled, float *anchors, int p0,
-                                                       int first_chunk, int chunk, int h) {
-    extern __shared__ float sp[];
-    const int m = blockIdx.x, r = blockIdx.y * gridDim.x + m;
-    const int start = (first_chunk + blockIdx.y) * chunk;
-    auto row = [&](int t) -> const float * {
-        const int p = start + t;
-        return p < p0 ? pending + (int64_t)(p % chunk) * h : xn + (int64_t)(p - p0) * ldx;
-    };
-    cbr_pool_slot(row, queries + (int64_t)m * h, chunk, h, start, sp, pooled + (int64_t)r * h, anchors + r);
+// Batched prefill, CBR pooling of the chunks first_chunk .. first_chunk + nc - 1
+// (all ending inside the prompt rows at positions p0 ..): the row of position
+// p is pending row p % chunk before p0, row p - p0 of xn after.
+__device__ __forceinline__ const float *cbr_row(const float *xn, int ldx, const float *pending, int p0, int chunk,
+                                                int h, int p) {
+    return p < p0 ? pending + (int64_t)(p % chunk) * h : xn + (int64_t)(p - p0) * ldx;
+}
+
+// Pooling step 1, one block per row of the chunks: its scores against the
+// learned queries, scores[(c * slots + m) * chunk + t] = u . q_m / sqrt(h),
+// each summed as the token step sums it.
+__global__ void __launch_bounds__(256) k_cbr_scores_rows(const float *xn, int ldx, const float *pending,
+                                                         const float *queries, float *scores, int p0,
+                                                         int first_chunk, int chunk, int slots, int h) {
+    const int c = blockIdx.x / chunk, t = blockIdx.x % chunk;
+    const float *u = cbr_row(xn, ldx, pending, p0, chunk, h, (first_chunk + c) * chunk + t);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int m = wave; m < slots; m += blockDim.x / 64) {
+        const float *q = queries + (int64_t)m * h;
+        float acc = 0.0f;
+        for (int j = lane; j < h; j += 64) acc = fmaf(u[j], q[j], acc);
+        acc = wave_sum(acc);
+        if (lane == 0) scores[((int64_t)c * slots + m) * chunk + t] = acc / sqrtf((float)h);
+    }
+}
+
+// Pooling step 2, block (c, m, b): the softmax of chunk c's scores for slot m
+// (as the token step forms it), then columns 256 b .. 256 b + 255 of pooled
+// row c * slots + m; column block 0 also writes its anchor.
+__global__ void __launch_bounds__(256) k_cbr_mix_rows(const float *xn, int ldx, const float *pending,
+                                                      const float *scores, float *pooled, float *anchors, int p0,
+                                                      int first_chunk, int chunk, int slots, int h) {
+    extern __shared__ float sp[];   // [chunk] probabilities, then reduction scratch
+    float *red = sp + chunk;
+    const int c = blockIdx.x, r = c * slots + blockIdx.y, start = (first_chunk + c) * chunk;
+    const float *s = scores + (int64_t)r * chunk;
+    float mx = -INFINITY;
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) mx = fmaxf(mx, s[t]);
+    mx = block_max(mx, red);
+    float den = 0.0f;
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) den += expf(s[t] - mx);
+    den = block_sum(den, red);
+    for (int t = threadIdx.x; t < chunk; t += blockDim.x) sp[t] = expf(s[t] - mx) / den;
+    __syncthreads();
+    const int j = blockIdx.z * blockDim.x + threadIdx.x;
+    if (j < h) {
+        float v = 0.0f;
+        for (int t = 0; t < chunk; ++t) v = fmaf(sp[t], cbr_row(xn, ldx, pending, p0, chunk, h, start + t)[j], v);
+        pooled[(int64_t)r * h + j] = v;
+    }
+    if (blockIdx.z == 0 && threadIdx.x == 0) {
+        float ps = 0.0f;
+        for (int t = 0; t < chunk; ++t) ps = fmaf(sp[t], (float)(start + t), ps);
+        anchors[r] = rintf(ps);
+    }
 }
 
 // Batched prefill: the pending buffer as the token loop leaves it after the
@@ -1419,7 +1458,7 @@ struct PrefillWs {
     float *slot0 = nullptr, *slot0_final = nullptr, *kv0 = nullptr, *obuf = nullptr, *fbuf = nullptr,
           *merge_count = nullptr;
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
-    float *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;   // flashnano-1.6 pooled rows
+    float *cbr_scores = nullptr, *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;   // flashnano-1.6
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
@@ -1465,7 +1504,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->flags, light ? r : 0}, {(void **)&w->extra_index, light ? r : 0},
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
         // flashnano-1.6
-        {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
+        {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
         {(void **)&w->rowscale, std::max(r, pr)},
         {(void **)&w->planes, std::max(r, pr) * std::max({h, qd, (size_t)d.ffn_dim})},
         {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, gqa ? 2 * kvw : 0},
@@ -1590,9 +1629,12 @@ int cbr_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     const int chunk = d.cbr_chunk_size, slots = d.cbr_slots;
     const int first = p0 / chunk, nc = (p0 + T) / chunk - first;   // chunk c ends at (c + 1) * chunk - 1
     if (nc > 0) {
-        k_cbr_pool_rows<<<dim3(slots, nc), 256, (size_t)(chunk + 8) * sizeof(float), s>>>(
-            w.xn, h, L.pending, L.cbr_queries, w.cbr_pooled, w.cbr_anchor, p0, first, chunk, h);
-        MR_LAUNCHED("enqueue cbr pool rows");
+        k_cbr_scores_rows<<<nc * chunk, 256, 0, s>>>(w.xn, h, L.pending, L.cbr_queries, w.cbr_scores, p0, first,
+                                                      chunk, slots, h);
+        MR_LAUNCHED("enqueue cbr scores");
+        k_cbr_mix_rows<<<dim3(nc, slots, ceil_div(h, 256)), 256, (size_t)(chunk + 8) * sizeof(float), s>>>(
+            w.xn, h, L.pending, w.cbr_scores, w.cbr_pooled, w.cbr_anchor, p0, first, chunk, slots, h);
+        MR_LAUNCHED("enqueue cbr pooling");
         GemmArgs kv;   // pooled rows through [Wk; Wv], the rows after Wq of the fused projection
         kv.a = w.cbr_pooled; kv.lda = h; kv.dtype = L.qkv.dtype;
         kv.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype);

@@ -719,51 +719,113 @@ __global__ void k_embed_rows(const void *table, int dt, const int *ids, int p0, 
 // (position p0 + t) sees the first (position / chunk) * slots relay rows, those
 // of the chunks completed before it; m = the largest score (natural units),
 // l = sum of exp(score - m), o = the exp-weighted sum of values (no relay
-// row: m = -inf, l = 0, o = 0).  Wave w of block (t, y) takes query head
-// 4y + w; its lanes score 64 relay rows at a time, then take the dims.
-__global__ void __launch_bounds__(256) k_relay_partial(RelayPartialArgs a) {
-    const int t = blockIdx.x, lane = threadIdx.x & 63;
-    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (h >= a.heads) return;
-    const int G = a.heads / a.kv_heads, d = a.d, kvw = a.kv_heads * d;
-    const int n = ((a.p0 + t) / a.chunk) * a.slots;
-    const float *q = a.qkv + (int64_t)t * a.ld + h * d;
-    const float *kb = a.relay_k + (h / G) * d, *vb = a.relay_v + (h / G) * d;
-    float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (int base = 0; base < n; base += kWave) {
-        const int j = base + lane;
-        float s = -INFINITY;
-        if (j < n) {
-            const float *k = kb + (int64_t)j * kvw;
-            float acc = 0.0f;
-            for (int i = 0; i < d; i += 4) {
-                const float4 kk = load_f4(k + i), qq = load_f4(q + i);
-                acc = fmaf(qq.x, kk.x, acc);
-                acc = fmaf(qq.y, kk.y, acc);
-                acc = fmaf(qq.z, kk.z, acc);
-                acc = fmaf(qq.w, kk.w, acc);
-            }
-            s = acc * a.inv_root;
-        }
-        const float mn = fmaxf(m, wave_max(s));   // finite: row base is scored
-        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
-        const float p = j < n ? expf(s - mn) : 0.0f;
-        l = l * alpha + wave_sum(p);
-        o0 *= alpha;
-        o1 *= alpha;
-        const int cnt = min(kWave, n - base);
-        for (int jj = 0; jj < cnt; ++jj) {
-            const float pj = __shfl(p, jj, kWave);
-            const float *v = vb + (int64_t)(base + jj) * kvw;
-            if (lane < d) o0 = fmaf(pj, v[lane], o0);
-            if (lane + kWave < d) o1 = fmaf(pj, v[lane + kWave], o1);
-        }
-        m = mn;
+// row: m = -inf, l = 0, o = 0).
+//
+// Block (x, y) takes 32 (row, query head) pairs of KV head y (rows_per_block
+// consecutive rows times its G query heads), 8 per wave, and streams the
+// relay rows it sees through LDS in tiles of TR rows (64 for d <= 64, 32 for
+// d <= 128, so a tile of keys and values stays under 34 KB; the pairs'
+// queries take 16 KB more).  Scores: SPLIT
+// lanes per relay row (lane % TR the row, lane / TR half of the dims), one
+// online-softmax update per pair and tile; values: lanes over dims, the
+// probabilities read lane by lane.
+constexpr int kRelayPairs = 32, kRelayPairsPerWave = kRelayPairs / 4;
+
+template <int SPLIT>
+__global__ void __launch_bounds__(256) k_relay_partial(RelayPartialArgs a, int rows_per_block) {
+    constexpr int TR = kWave / SPLIT;   // relay rows per tile
+    constexpr int DL = SPLIT;           // dims per lane in the value sum (d <= 64 * SPLIT)
+    extern __shared__ __align__(16) float rl[];
+    const int d = a.d, KP = d + 4, kvw = a.kv_heads * d, G = a.heads / a.kv_heads, kvh = blockIdx.y;
+    // [TR][d + 4] keys, [TR][d] values, [kRelayPairs][d] queries
+    float *ks = rl, *vs = rl + TR * KP, *qs = vs + TR * d;
+    const int r0 = blockIdx.x * rows_per_block, nrows = min(rows_per_block, a.rows - r0), pairs = nrows * G;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int jr = lane % TR, part = lane / TR, dp = d / SPLIT;   // score lanes: relay row, dims part
+    const int n_max = ((a.p0 + r0 + nrows - 1) / a.chunk) * a.slots;
+    // pair pi is row r0 + pi / G, query head kvh * G + pi % G; pairs past the
+    // last row repeat the last pair and are not stored
+    for (int i = threadIdx.x; i < kRelayPairs * (d / 4); i += blockDim.x) {
+        const int pi = min(i / (d / 4), pairs - 1), c = (i % (d / 4)) * 4;
+        const float4 q = load_f4(a.qkv + (int64_t)(r0 + pi / G) * a.ld + (kvh * G + pi % G) * d + c);
+        *(float4 *)(qs + (i / (d / 4)) * d + c) = q;
     }
-    float *out = a.ext + ((int64_t)t * a.heads + h) * (d + 4);
-    if (lane == 0) *(float4 *)out = make_float4(m, l, 0.0f, 0.0f);
-    if (lane < d) out[4 + lane] = o0;
-    if (lane + kWave < d) out[4 + lane + kWave] = o1;
+    int seen[kRelayPairsPerWave];   // relay rows each pair sees
+    float m[kRelayPairsPerWave], l[kRelayPairsPerWave], o[kRelayPairsPerWave][DL];
+#pragma unroll
+    for (int k = 0; k < kRelayPairsPerWave; ++k) {
+        const int pi = min(wave * kRelayPairsPerWave + k, pairs - 1);
+        seen[k] = ((a.p0 + r0 + pi / G) / a.chunk) * a.slots;
+        m[k] = -INFINITY;
+        l[k] = 0.0f;
+#pragma unroll
+        for (int x = 0; x < DL; ++x) o[k][x] = 0.0f;
+    }
+    const float *kb = a.relay_k + kvh * d, *vb = a.relay_v + kvh * d;
+    for (int base = 0; base < n_max; base += TR) {
+        const int cnt = min(TR, n_max - base);
+        __syncthreads();   // the previous tile is read (the first: the queries are staged)
+        for (int i = threadIdx.x; i < TR * (d / 4); i += blockDim.x) {   // rows past cnt: zeros
+            const int j = i / (d / 4), c = (i % (d / 4)) * 4;
+            const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            *(float4 *)(ks + j * KP + c) = j < cnt ? load_f4(kb + (int64_t)(base + j) * kvw + c) : z;
+            *(float4 *)(vs + j * d + c) = j < cnt ? load_f4(vb + (int64_t)(base + j) * kvw + c) : z;
+        }
+        __syncthreads();
+        // No branches per pair: a pair that sees none of the tile scores -inf
+        // everywhere and keeps its state (alpha 1, or 0 with nothing summed).
+#pragma unroll
+        for (int k = 0; k < kRelayPairsPerWave; ++k) {
+            const int n = min(seen[k] - base, cnt);   // rows of the tile it sees (may be <= 0)
+            const float *q = qs + (wave * kRelayPairsPerWave + k) * d + part * dp, *kr = ks + jr * KP + part * dp;
+            float s = 0.0f;
+            for (int i = 0; i < dp; i += 4) {
+                const float4 qq = *(const float4 *)(q + i), kk = *(const float4 *)(kr + i);
+                s = fmaf(qq.x, kk.x, s);
+                s = fmaf(qq.y, kk.y, s);
+                s = fmaf(qq.z, kk.z, s);
+                s = fmaf(qq.w, kk.w, s);
+            }
+            if constexpr (SPLIT == 2) s += __shfl_xor(s, TR, kWave);
+            s = jr < n ? s * a.inv_root : -INFINITY;
+            const float mn = fmaxf(m[k], wave_max(s));
+            const float alpha = m[k] == -INFINITY ? 0.0f : expf(m[k] - mn);
+            const float p = jr < n ? expf(s - mn) : 0.0f;
+            l[k] = l[k] * alpha + wave_sum(p) / SPLIT;   // each row's probability sits in SPLIT lanes
+            m[k] = mn;
+#pragma unroll
+            for (int x = 0; x < DL; ++x) o[k][x] *= alpha;
+            // 8 relay rows a round over the staged rows (past n: probability 0;
+            // past cnt: zero values)
+            for (int jj = 0; jj < cnt; jj += 8) {
+                float pj[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) pj[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), jj + u));
+#pragma unroll
+                for (int x = 0; x < DL; ++x) {
+                    const int dim = lane + x * kWave;
+                    if (dim < d) {
+                        float vv[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) vv[u] = vs[(jj + u) * d + dim];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) o[k][x] = fmaf(pj[u], vv[u], o[k][x]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRelayPairsPerWave; ++k) {
+        const int pi = wave * kRelayPairsPerWave + k;
+        if (pi >= pairs) break;
+        const int t = r0 + pi / G, h = kvh * G + pi % G;
+        float *out = a.ext + ((int64_t)t * a.heads + h) * (d + 4);
+        if (lane == 0) *(float4 *)out = make_float4(m[k], l[k], 0.0f, 0.0f);
+#pragma unroll
+        for (int x = 0; x < DL; ++x)
+            if (lane + x * kWave < d) out[4 + lane + x * kWave] = o[k][x];
+    }
 }
 
 }  // namespace
@@ -806,9 +868,17 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
 int launch_relay_partial(hipStream_t s, const RelayPartialArgs &a) {
     MR_REQUIRE(a.qkv && a.relay_k && a.relay_v && a.ext && a.rows > 0 && a.chunk > 0 && a.slots > 0,
                "relay partial: bad arguments");
-    MR_REQUIRE(a.kv_heads > 0 && a.heads % a.kv_heads == 0 && a.d % 4 == 0 && a.d <= 2 * kWave && a.ld % 4 == 0,
+    MR_REQUIRE(a.kv_heads > 0 && a.heads % a.kv_heads == 0 && a.heads / a.kv_heads <= kRelayPairs && a.d % 4 == 0 &&
+                   a.d <= 2 * kWave && (a.d <= kWave || a.d % 8 == 0) && a.ld % 4 == 0,
                "relay partial: unsupported geometry");
-    k_relay_partial<<<dim3(a.rows, ceil_div(a.heads, 4)), 256, 0, s>>>(a);
+    const int G = a.heads / a.kv_heads, rows_per_block = kRelayPairs / G;
+    const dim3 grid(ceil_div(a.rows, rows_per_block), a.kv_heads);
+    const size_t q_lds = (size_t)kRelayPairs * a.d * sizeof(float);
+    if (a.d <= kWave)
+        k_relay_partial<1><<<grid, 256, (size_t)kWave * (2 * a.d + 4) * sizeof(float) + q_lds, s>>>(a, rows_per_block);
+    else
+        k_relay_partial<2><<<grid, 256, (size_t)(kWave / 2) * (2 * a.d + 4) * sizeof(float) + q_lds, s>>>(
+            a, rows_per_block);
     MR_LAUNCHED("enqueue relay partial");
     return MR_OK;
 }

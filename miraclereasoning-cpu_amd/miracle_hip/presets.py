@@ -31,6 +31,13 @@ WORKLOADS = {
                        kv_heads=4, head_dim=64, ffn_dim=2816, max_positions=2048, window=512,
                        global_layers=_every(4, 19), rope_theta=1e4),
         dtype="bf16", seed=1, context=2048, prompt=512, new_tokens=256),
+    # flashnano-1.5-mid's geometry with CBR: chunks of 64 positions pooled into 4 relay
+    # rows per layer; BF16 (seed 1).
+    "flashnano-1.6-mid": dict(
+        config=_bundle(family="flashnano-1.6", vocab_size=32000, hidden_size=1024, layers=19, query_heads=16,
+                       kv_heads=4, head_dim=64, ffn_dim=2816, max_positions=2048, window=512,
+                       global_layers=_every(4, 19), rope_theta=1e4, cbr_chunk_size=64, cbr_slots=4),
+        dtype="bf16", seed=1, context=2048, prompt=1024, new_tokens=256),
     # 24 layers, every 4th global, rest ring window 1024; 4 local / 8 global KV heads;
     # split-half RoPE theta 5e5; BF16 (seed 2).
     "flashnano-1.7": dict(

@@ -5,6 +5,9 @@ lengths that exercise what the short-prompt tests cannot reach.
   persistent step merges many active key splits per KV head (global layers
   about 18); both step modes.
 * flashnano-1.5 mid over 600 tokens: its 512-key local rings wrap.
+* flashnano-1.6 mid (the same geometry with CBR chunks of 64 pooled into 4
+  relay rows) over 600 tokens: 9 chunks pooled, so up to 36 relay rows join
+  each softmax beside a wrapped ring; token loop and batched prefill.
 * heavy-medium-2.0 at its full geometry (64 experts in 8 groups, top-6 + 2
   shared, blocks of 64 with top-8, head dim 128) over 640 tokens: the 512-row
   window overflows and top-8 of 10 blocks is a real choice.  Every expert id
@@ -86,6 +89,16 @@ def test_long_prompt_matches_oracle(backend, name, prompt, mode):
     got = model.prefill(ids, return_all=True)
     np.testing.assert_allclose(got, want, **TOL)
     assert model.generate(list(ids), max_new_tokens=6) == stream
+
+
+@pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
+def test_cbr_workload_matches_oracle(backend, prefill_mode):
+    wl, weights, ids, want, stream = _workload("flashnano-1.6-mid", 600)
+    print("case flashnano-1.6-mid 600", prefill_mode, flush=True)
+    with MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"],
+                      prefill_mode=prefill_mode) as model:
+        np.testing.assert_allclose(model.prefill(ids, return_all=True), want, **TOL)
+        assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
 @pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
