@@ -304,23 +304,27 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     const int klo = max(0, a.p0 + t0 - win + 1), khi = a.p0 + last;
     const int ntiles = (khi - klo) / kKeys + 1;
 
-    // Thread e loads keys NL kg .. + NL - 1 (kg = e / (D / 4)) at dims c4 .. + 3.
+    // Thread e loads keys NL kg .. + NL - 1 (kg = e / (D / 4)) at dims c4 .. + 3,
+    // and values NL kv .. + NL - 1 (kv = e % (kKeys / NL)) at dims v4 .. + 3:
+    // the values go into LDS transposed, and with this mapping the lanes of a
+    // write group store whole rows of V^T (the tile's key groups at one dim),
+    // where the keys' mapping would put every lane on the same two banks.
     const int kg = tid / (D / 4), c4 = (tid % (D / 4)) * 4;
+    const int kv = tid % (kKeys / NL), v4 = (tid / (kKeys / NL)) * 4;
     float4 kr[NL], vr[NL];
     u32x2 kq[NL][2], vq[NL][2];   // P: the keys' and values' FP16 terms (hi, lo) at dims c4 .. + 3
     const int64_t plane = (int64_t)a.kv16_rows * kvw;
     auto fetch_p = [&](int kb) {
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
-            const int kp = kb + NL * kg + u;
-            const _Float16 *src = a.kv16 + (int64_t)(kp - first) * kvw + kh * D + c4;
+            const int kp = kb + NL * kg + u, vp = kb + NL * kv + u;
+            const _Float16 *ksrc = a.kv16 + (int64_t)(kp - first) * kvw + kh * D + c4;
+            const _Float16 *vsrc = a.kv16 + (int64_t)(vp - first) * kvw + kh * D + v4;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 kq[u][t] = vq[u][t] = u32x2{0u, 0u};
-                if (kp <= khi) {
-                    kq[u][t] = *gmem((const u32x2 *)(src + t * plane));
-                    vq[u][t] = *gmem((const u32x2 *)(src + (2 + t) * plane));
-                }
+                if (kp <= khi) kq[u][t] = *gmem((const u32x2 *)(ksrc + t * plane));
+                if (vp <= khi) vq[u][t] = *gmem((const u32x2 *)(vsrc + (2 + t) * plane));
             }
         }
     };
@@ -329,20 +333,21 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
             kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            const int kp = kb + NL * kg + u;
-            if (kp <= khi) {
-                const float *kbase, *vbase;
-                if (kp >= a.p0) {
-                    kbase = a.qkv + (int64_t)(kp - a.p0) * a.ld + qd + kh * D;
-                    vbase = kbase + kvw;
-                } else {
-                    int slot = kb_slot + NL * kg + u;
-                    while (slot >= a.cap) slot -= a.cap;
-                    kbase = a.ring_k + (int64_t)slot * kvw + kh * D;
-                    vbase = a.ring_v + (int64_t)slot * kvw + kh * D;
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {   // the key row, then the value row
+                const int r = NL * (x ? kv : kg) + u, kp = kb + r;
+                if (kp <= khi) {
+                    const float *base;
+                    if (kp >= a.p0) {
+                        base = a.qkv + (int64_t)(kp - a.p0) * a.ld + qd + x * kvw + kh * D;
+                    } else {
+                        int slot = kb_slot + r;
+                        while (slot >= a.cap) slot -= a.cap;
+                        base = (x ? a.ring_v : a.ring_k) + (int64_t)slot * kvw + kh * D;
+                    }
+                    if (x) vr[u] = load_f4(base + v4);
+                    else kr[u] = load_f4(base + c4);
                 }
-                kr[u] = load_f4(kbase + c4);
-                vr[u] = load_f4(vbase + c4);
             }
         }
     };
@@ -383,7 +388,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
             *(f16x4 *)&ks[0][r * KP + c4] = hi;
             *(f16x4 *)&ks[1][r * KP + c4] = lo;
         }
-        // values transposed: dim c4 + i of keys NL kg .. + NL - 1
+        // values transposed: dim v4 + i of keys NL kv .. + NL - 1
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             _Float16 hv[NL], lv[NL];
@@ -392,7 +397,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                 const float x = (i == 0 ? vr[u].x : i == 1 ? vr[u].y : i == 2 ? vr[u].z : vr[u].w) * sv;
                 split2h(x, hv[u], lv[u]);
             }
-            const int at = (c4 + i) * VP + vslot(NL * kg);   // NL consecutive keys and slots
+            const int at = (v4 + i) * VP + vslot(NL * kv);   // NL consecutive keys and slots
             if constexpr (NL == 4) {
                 *(f16x4 *)&vt[0][at] = f16x4{hv[0], hv[1], hv[2], hv[3]};
                 *(f16x4 *)&vt[1][at] = f16x4{lv[0], lv[1], lv[2], lv[3]};
@@ -422,7 +427,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
                     const unsigned w = i < 2 ? vq[u][t].x : vq[u][t].y;
                     x[u] = __builtin_bit_cast(_Float16, (unsigned short)(w >> (16 * (i & 1))));
                 }
-                const int at = (c4 + i) * VP + vslot(NL * kg);
+                const int at = (v4 + i) * VP + vslot(NL * kv);
                 if constexpr (NL == 4) *(f16x4 *)&vt[t][at] = f16x4{x[0], x[1], x[2], x[3]};
                 else if constexpr (NL == 2) *(f16x2 *)&vt[t][at] = f16x2{x[0], x[1]};
                 else vt[t][at] = x[0];
