@@ -384,12 +384,73 @@ __device__ __forceinline__ void load_w_h(const GemmArgs &g, int n0, int k0, u32x
     }
 }
 
+// The buffer form of the two loaders, for K a multiple of KB and matrices
+// under 2^31 bytes: a thread's byte offsets into A's planes and the weight
+// rows are computed once per tile, a k-step only moves the scalar offset,
+// and a row past M or N addresses past its buffer's end, where the bounds
+// check returns zeros (no per-load address arithmetic, no 64-bit pointers).
+constexpr unsigned kPastEnd = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t half_rsrc(const void *p, int64_t halves) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(halves * 2), 0x00020000);
+}
+
+template <int NI, int KB>
+struct TileOffsets {
+    unsigned a[KB / 16];        // the rows of A (chunks t + 256 j)
+    unsigned w[NI * KB / 64];   // the weight rows (chunks t + 256 i)
+};
+
+// Weight load step i of a SwiGLU tile reads up rows (else gate rows): every
+// step covers 256 / (KB / 8) rows, inside one run of 8 NI gate or up rows.
+template <int EPI, int NI, int KB>
+__device__ __forceinline__ constexpr bool w_up(int i) {
+    constexpr int rps = kThreads / (KB / 8);
+    return EPI == GEMM_SWIGLU && (i * rps) % (16 * NI) >= 8 * NI;
+}
+
+template <int EPI, int NI, int KB>
+__device__ __forceinline__ void tile_offsets(const GemmArgs &g, int m0, int n0, TileOffsets<NI, KB> &o) {
+    constexpr int CPR = KB / 8;
+    static_assert(EPI != GEMM_SWIGLU || (8 * NI) % (kThreads / CPR) == 0, "a load step spans gate and up rows");
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < KB / 16; ++j) {
+        const int q = tid + kThreads * j, row = m0 + q / CPR;
+        o.a[j] = row < g.m ? (unsigned)(((int64_t)row * g.k + (q % CPR) * 8) * 2) : kPastEnd;
+    }
+#pragma unroll
+    for (int i = 0; i < NI * KB / 64; ++i) {
+        const int q = tid + kThreads * i, r = q / CPR;
+        int f = n0 + r;
+        if constexpr (EPI == GEMM_SWIGLU) f = n0 + (r / (16 * NI)) * 8 * NI + (r % (16 * NI)) % (8 * NI);
+        o.w[i] = f < g.n ? (unsigned)(((int64_t)f * g.k + (q % CPR) * 8) * 2) : kPastEnd;
+    }
+}
+
+template <int EPI, int NI, int KB>
+__device__ __forceinline__ void load_tile_buf(const GemmArgs &g, const TileOffsets<NI, KB> &o, int k0, AHRegs<KB> &ar,
+                                              u32x4 (&wr)[NI * KB / 64]) {
+    const int64_t mk = (int64_t)g.m * g.k, nk = (int64_t)g.n * g.k;
+    const __amdgpu_buffer_rsrc_t a0 = half_rsrc(g.ahl, mk), a1 = half_rsrc(g.ahl + mk, mk);
+    const __amdgpu_buffer_rsrc_t w0 = half_rsrc(g.w, nk), w1 = half_rsrc(EPI == GEMM_SWIGLU ? g.w2 : g.w, nk);
+    const int so = k0 * 2;
+#pragma unroll
+    for (int j = 0; j < KB / 16; ++j) {
+        ar.v[0][j] = __builtin_amdgcn_raw_buffer_load_b128(a0, o.a[j], so, 0);
+        ar.v[1][j] = __builtin_amdgcn_raw_buffer_load_b128(a1, o.a[j], so, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NI * KB / 64; ++i)
+        wr[i] = __builtin_amdgcn_raw_buffer_load_b128(w_up<EPI, NI, KB>(i) ? w1 : w0, o.w[i], so, 0);
+}
+
 // One 128 x 32 NI output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
 // planes and row scales from k_row_split, the weights' FP16 copy), k-steps
 // of KB halves; each wave owns 64 x 16 NI outputs.  (Two LDS stages with one
 // barrier per k-step measured slower: the LDS per workgroup halves the
 // workgroups per CU.)
-template <int EPI, int NI, int KB>
+template <int EPI, int NI, int KB, bool BUF>
 __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     constexpr int CPR = KB / 8;
     __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][KB + 8];
@@ -408,8 +469,14 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 
     AHRegs<KB> ar;
     u32x4 wr[NI * KB / 64];
-    load_a_h<KB>(g, m0, 0, ar);
-    load_w_h<EPI, NI, KB>(g, n0, 0, wr);
+    TileOffsets<NI, KB> off;
+    if constexpr (BUF) {
+        tile_offsets<EPI, NI, KB>(g, m0, n0, off);
+        load_tile_buf<EPI, NI, KB>(g, off, 0, ar, wr);
+    } else {
+        load_a_h<KB>(g, m0, 0, ar);
+        load_w_h<EPI, NI, KB>(g, n0, 0, wr);
+    }
     for (int kt = 0; kt < nk; ++kt) {
         if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
         store_a_h<KB>(as, ar);
@@ -420,8 +487,12 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
         }
         lds_barrier();
         if (kt + 1 < nk) {
-            load_a_h<KB>(g, m0, (kt + 1) * KB, ar);
-            load_w_h<EPI, NI, KB>(g, n0, (kt + 1) * KB, wr);
+            if constexpr (BUF) {
+                load_tile_buf<EPI, NI, KB>(g, off, (kt + 1) * KB, ar, wr);
+            } else {
+                load_a_h<KB>(g, m0, (kt + 1) * KB, ar);
+                load_w_h<EPI, NI, KB>(g, n0, (kt + 1) * KB, wr);
+            }
         }
 #pragma unroll
         for (int kk = 0; kk < KB / 32; ++kk) {
@@ -444,9 +515,9 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
 }
 
-template <int EPI, int NI>
+template <int EPI, int NI, bool BUF>
 __global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
-    gemm_tile_h<EPI, NI, kKBH>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    gemm_tile_h<EPI, NI, kKBH, BUF>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 // A in FP16 terms, once per GEMM: row r's scale 2^t (max_k |a[r][k]| 2^t in
@@ -548,11 +619,22 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         if (!g.a_split) k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // 128 x 128 tiles (wider SwiGLU tiles, 192 or 256 columns, measured
         // slower: the accumulators leave one or two waves per SIMD)
+        // the buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
+        const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
+                         (int64_t)g.n * g.k * 2 < (1ll << 31);
+        const dim3 sgrid(ceil_div(g.n, 16 * kSwigluNI), grid.y);
         switch (epi) {
-            case GEMM_STORE: k_gemm_h<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h); break;
-            case GEMM_RESIDUAL: k_gemm_h<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h); break;
+            case GEMM_STORE:
+                if (buf) k_gemm_h<GEMM_STORE, 4, true><<<grid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_STORE, 4, false><<<grid, kThreads, 0, s>>>(h);
+                break;
+            case GEMM_RESIDUAL:
+                if (buf) k_gemm_h<GEMM_RESIDUAL, 4, true><<<grid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_RESIDUAL, 4, false><<<grid, kThreads, 0, s>>>(h);
+                break;
             case GEMM_SWIGLU:
-                k_gemm_h<GEMM_SWIGLU, kSwigluNI><<<dim3(ceil_div(g.n, 16 * kSwigluNI), grid.y), kThreads, 0, s>>>(h);
+                if (buf) k_gemm_h<GEMM_SWIGLU, kSwigluNI, true><<<sgrid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_SWIGLU, kSwigluNI, false><<<sgrid, kThreads, 0, s>>>(h);
                 break;
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
         }
