@@ -313,19 +313,30 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     const int kv = tid % (kKeys / NL), v4 = (tid / (kKeys / NL)) * 4;
     float4 kr[NL], vr[NL];
     u32x2 kq[NL][2], vq[NL][2];   // P: the keys' and values' FP16 terms (hi, lo) at dims c4 .. + 3
+    // P: the four planes as buffers of the attended rows first .. khi; a
+    // thread's byte offsets are fixed, a tile adds its first row, and a key
+    // past khi addresses past the buffer's end, where the bounds check
+    // returns zeros.
     const int64_t plane = (int64_t)a.kv16_rows * kvw;
+    const int nbytes = P ? (khi - first + 1) * kvw * 2 : 0;
+    auto plane_rsrc = [&](int t) {
+        return __builtin_amdgcn_make_buffer_rsrc((void *)(a.kv16 + t * plane), (short)0, nbytes, 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t rk0 = plane_rsrc(0), rk1 = plane_rsrc(1), rv0 = plane_rsrc(2), rv1 = plane_rsrc(3);
+    unsigned ko[NL], vo[NL];
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        ko[u] = (unsigned)(((NL * kg + u) * kvw + kh * D + c4) * 2);
+        vo[u] = (unsigned)(((NL * kv + u) * kvw + kh * D + v4) * 2);
+    }
     auto fetch_p = [&](int kb) {
+        const unsigned rel = (unsigned)((kb - first) * kvw * 2);
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
-            const int kp = kb + NL * kg + u, vp = kb + NL * kv + u;
-            const _Float16 *ksrc = a.kv16 + (int64_t)(kp - first) * kvw + kh * D + c4;
-            const _Float16 *vsrc = a.kv16 + (int64_t)(vp - first) * kvw + kh * D + v4;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                kq[u][t] = vq[u][t] = u32x2{0u, 0u};
-                if (kp <= khi) kq[u][t] = *gmem((const u32x2 *)(ksrc + t * plane));
-                if (vp <= khi) vq[u][t] = *gmem((const u32x2 *)(vsrc + (2 + t) * plane));
-            }
+            kq[u][0] = __builtin_amdgcn_raw_buffer_load_b64(rk0, ko[u] + rel, 0, 0);
+            kq[u][1] = __builtin_amdgcn_raw_buffer_load_b64(rk1, ko[u] + rel, 0, 0);
+            vq[u][0] = __builtin_amdgcn_raw_buffer_load_b64(rv0, vo[u] + rel, 0, 0);
+            vq[u][1] = __builtin_amdgcn_raw_buffer_load_b64(rv1, vo[u] + rel, 0, 0);
         }
     };
     auto fetch = [&](int kb) {
