@@ -963,6 +963,9 @@ int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     L.qkv.rows = qd + d.latent_dim;
     if (L.router.rows != 3) return fail(MR_ERR_STATE, "missing router weight" + at);
     L.router.rows = d.router_groups + d.routed_experts;
+    // the batched prefill's FP16-term projections (the router keeps the exact
+    // BF16-term GEMM: its logits choose the experts)
+    MR_TRY(f16_copies(m, {&L.qkv, &L.kv_up, &L.o}, {}));
     const int dt = L.experts[0].gate.dtype;
     std::vector<void *> tab(3 * (size_t)(d.routed_experts + d.shared_experts));
     const size_t n = d.routed_experts + d.shared_experts;
@@ -1728,18 +1731,24 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         float *bsum_k = L.bsum_k + (size_t)loop * blocks * kvw, *bsum_v = L.bsum_v + (size_t)loop * blocks * kvw;
         int *choice = m->choices + ((size_t)li * inner + loop) * m->choice_rec;
         const int choice_stride = d.layers * inner * m->choice_rec;
-        MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
         GemmArgs q;   // the Q rows of the packed [Wq; Wlatent]
         q.a = w.xn; q.lda = h; q.w = L.qkv.ptr; q.dtype = L.qkv.dtype; q.c = w.qkv; q.ldc = ld;
         q.m = T; q.n = qd; q.k = h;
+        q.wscale = L.qkv.f16_scale; q.wh = L.qkv.f16; q.ascale = w.rowscale; q.ahl_ws = w.planes;
+        // the normalized rows go straight into the FP16-term GEMMs' A workspace
+        q.a_split = q.wscale > 0.0f;
+        if (q.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
+        else MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
         MR_TRY(launch_gemm(s, GEMM_STORE, q));
-        GemmArgs lt = q;   // its latent rows
+        GemmArgs lt = q;   // its latent rows (the same A)
         lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
         lt.n = lat;
+        if (L.qkv.f16) lt.wh = (const _Float16 *)L.qkv.f16 + (size_t)qd * h;
         MR_TRY(launch_gemm(s, GEMM_STORE, lt));
         GemmArgs kv;   // latent -> [K | V] beside the queries
         kv.a = w.lat; kv.lda = lat; kv.w = L.kv_up.ptr; kv.dtype = L.kv_up.dtype; kv.c = w.qkv + qd; kv.ldc = ld;
         kv.m = T; kv.n = 2 * kvw; kv.k = lat;
+        kv.wscale = L.kv_up.f16_scale; kv.wh = L.kv_up.f16; kv.ascale = w.rowscale; kv.ahl_ws = w.planes;
         MR_TRY(launch_gemm(s, GEMM_STORE, kv));
         MR_TRY(launch_qk_rows(s, w.qkv, ld, T, p0, d.query_heads, L.kv_heads, hd, nullptr, nullptr, 1e-6f, 1,
                               m->rope, d.split_half_rope));
@@ -1764,6 +1773,7 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         GemmArgs o;   // hidden += step_scale * Wo . attended
         o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
         o.m = T; o.n = h; o.k = qd; o.scale = d.heavy_step_scale;
+        o.wscale = L.o.f16_scale; o.wh = L.o.f16; o.ascale = w.rowscale; o.ahl_ws = w.planes;
         MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
         MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
         GemmArgs r;   // [Wcoarse; Wfine]
