@@ -199,14 +199,14 @@ MR_API int mr_model_position(mr_model *model, int *position);
 /* Append n tokens to the sequence (reference: prefill, model.py:295-312).
  * flags: MR_FWD_RETURN_ALL -> logits for every token ([n, vocab]); otherwise
  * only for the last token ([vocab]).  MR_FWD_BATCHED -> batched prefill for
- * flashnano-1.5/1.7, flashlite-2.0, flashlighting-2.0 and heavy-medium-2.0:
- * each layer runs once per chunk of up to 4096 prompt rows (projections as
- * MFMA GEMMs with FP32-faithful products, windowed attention over the chunk
- * plus the caches; the latent memory's compaction planned per position; block
- * sums scanned per row and blocks chosen per row as the token step chooses
- * them; experts as grouped GEMMs); results agree with the token loop to FP32
- * rounding, not bit for bit.  A single token, flashnano-1.6 (relay rows) and
- * geometries outside the kernels' widths take the token loop.
+ * every family: each layer runs once per chunk of up to 4096 prompt rows
+ * (projections as MFMA GEMMs with FP32-faithful products, windowed attention
+ * over the chunk plus the caches; flashnano-1.6's relay rows pooled for every
+ * CBR chunk that ends in the chunk; the latent memory's compaction planned per
+ * position; block sums scanned per row and blocks chosen per row as the token
+ * step chooses them; experts as grouped GEMMs); results agree with the token
+ * loop to FP32 rounding, not bit for bit.  A single token and geometries
+ * outside the kernels' widths take the token loop.
  * logits may be NULL (no readback; the last token's logits stay on device). */
 enum { MR_FWD_RETURN_ALL = 1, MR_FWD_BATCHED = 2 };
 MR_API int mr_model_forward(mr_model *model, const int32_t *ids, int n, int flags, float *logits);

@@ -223,13 +223,12 @@ class MiracleModel:
     ``prefill_mode="exact"`` (default) appends a prompt token by token through
     the decode step, so ``decode`` and ``prefill`` agree bit for bit as in the
     reference (tests/test_inference.py:63-64 of the reference);
-    ``"batched"`` runs prompts of flashnano-1.5/1.7, flashlite-2.0,
-    flashlighting-2.0 and heavy-medium-2.0 through whole-chunk kernels (MFMA
-    projections, windowed attention with the latent memory's and the block
-    selection's per-position semantics, grouped expert GEMMs), equal to the
-    token loop within FP32 rounding (routing near-ties aside); single tokens,
-    flashnano-1.6 and geometries outside the kernels' widths keep the token
-    loop.
+    ``"batched"`` runs prompts of every family through whole-chunk kernels
+    (MFMA projections, windowed attention with the relay rows', the latent
+    memory's and the block selection's per-position semantics, grouped expert
+    GEMMs), equal to the token loop within FP32 rounding (routing near-ties
+    aside); single tokens and geometries outside the kernels' widths keep the
+    token loop.
     ``weight_cache_bytes`` is accepted and validated for compatibility: every
     weight stays resident in HBM in its stored dtype, so no cache is needed.
     """
