@@ -1667,7 +1667,7 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     // the normalized rows go straight into the FP16-term GEMM's A workspace
     // (flashnano-1.6 pools them in FP32 first)
     const bool cbr = d.family == MR_FAMILY_FLASHNANO_16;
-    g.a_split = g.wscale > 0.0f && !cbr;
+    g.a_split = g.wscale > 0.0f && !cbr && rms_split_fits(h);
     if (g.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
     else MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
     if (cbr) MR_TRY(cbr_layer_rows(m, L, w, p0, T));
@@ -1699,7 +1699,7 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
     gu.wscale = L.ffn.gate.f16_scale; gu.wh = L.ffn.gate.f16; gu.wh2 = L.ffn.up.f16; gu.ascale = w.rowscale;
     gu.ahl_ws = w.planes;
-    gu.a_split = gu.wscale > 0.0f;
+    gu.a_split = gu.wscale > 0.0f && rms_split_fits(h);
     if (gu.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
     else MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
@@ -1736,7 +1736,7 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         q.m = T; q.n = qd; q.k = h;
         q.wscale = L.qkv.f16_scale; q.wh = L.qkv.f16; q.ascale = w.rowscale; q.ahl_ws = w.planes;
         // the normalized rows go straight into the FP16-term GEMMs' A workspace
-        q.a_split = q.wscale > 0.0f;
+        q.a_split = q.wscale > 0.0f && rms_split_fits(h);
         if (q.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
         else MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
         MR_TRY(launch_gemm(s, GEMM_STORE, q));

@@ -56,6 +56,9 @@ int launch_relay_partial(hipStream_t s, const RelayPartialArgs &a);
 // hi / lo planes, see gemm.h): the GEMM then runs with a_split.
 int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
                           float *scale, _Float16 *planes, int rows);
+// The widths launch_rms_rows_split takes: multiples of 8 up to 8192 (wider
+// rows take launch_rms_rows and the GEMM's own split).
+inline bool rms_split_fits(int width) { return width % 8 == 0 && width <= 8192; }
 int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width, float *y,
                     int ldy, int rows);
 

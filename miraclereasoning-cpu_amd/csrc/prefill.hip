@@ -657,25 +657,64 @@ __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const
 // scale[row] and y 2^t = hi + lo into planes hl[0][row][.], hl[1][row][.]
 // (rows of `width` halves; `rows` planes apart), as the GEMM's own split
 // would write them.
+// A thread holds up to kSplitChunks runs of 8 values of its row in registers
+// (width a multiple of 8, at most 256 * 8 * kSplitChunks) through the three
+// passes (sum of squares, maximum, split) and stores 8 halves at a time.
+constexpr int kSplitChunks = 4;
+
 __global__ void __launch_bounds__(256) k_rms_rows_split(const float *x, int ldx, const float *gain, float eps,
                                                         int width, float *scale, _Float16 *hl, int rows) {
     __shared__ float red[4];
     const float *xr = x + (int64_t)blockIdx.x * ldx;
+    const int runs = width / 8;
+    float4 v[kSplitChunks][2];
     float ss = 0.0f;
-    for (int j = threadIdx.x; j < width; j += blockDim.x) ss += xr[j] * xr[j];
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+        const int r = threadIdx.x + c * blockDim.x;
+        v[c][0] = v[c][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < runs) {
+            v[c][0] = load_f4(xr + 8 * r);
+            v[c][1] = load_f4(xr + 8 * r + 4);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            ss += v[c][t].x * v[c][t].x + v[c][t].y * v[c][t].y + v[c][t].z * v[c][t].z + v[c][t].w * v[c][t].w;
+    }
     ss = block_sum(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)width + eps);
     float mx = 0.0f;
-    for (int j = threadIdx.x; j < width; j += blockDim.x) mx = fmaxf(mx, fabsf(xr[j] * rs * (gain ? gain[j] : 1.0f)));
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+        const int r = threadIdx.x + c * blockDim.x;
+        if (r >= runs) continue;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const float4 g = gain ? load_f4(gain + 8 * r + 4 * t) : make_float4(1.f, 1.f, 1.f, 1.f);
+            v[c][t] = make_float4(v[c][t].x * rs * g.x, v[c][t].y * rs * g.y, v[c][t].z * rs * g.z,
+                                  v[c][t].w * rs * g.w);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[c][t].x), fabsf(v[c][t].y)), fmaxf(fabsf(v[c][t].z), fabsf(v[c][t].w))));
+        }
+    }
     mx = block_max(mx, red);
     const float sc = f16_range_scale(mx);
     if (threadIdx.x == 0) scale[blockIdx.x] = sc;
     _Float16 *hi = hl + (int64_t)blockIdx.x * width, *lo = hl + (int64_t)rows * width + (int64_t)blockIdx.x * width;
-    for (int j = threadIdx.x; j < width; j += blockDim.x) {
-        _Float16 h, l;
-        split2h(xr[j] * rs * (gain ? gain[j] : 1.0f) * sc, h, l);
-        hi[j] = h;
-        lo[j] = l;
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+        const int r = threadIdx.x + c * blockDim.x;
+        if (r >= runs) continue;
+        const float y[8] = {v[c][0].x, v[c][0].y, v[c][0].z, v[c][0].w, v[c][1].x, v[c][1].y, v[c][1].z, v[c][1].w};
+        f16x8 h, l;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 th, tl;
+            split2h(y[i] * sc, th, tl);
+            h[i] = th;
+            l[i] = tl;
+        }
+        *(f16x8 *)(hi + 8 * r) = h;
+        *(f16x8 *)(lo + 8 * r) = l;
     }
 }
 
@@ -908,6 +947,9 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
 
 int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
                           float *scale, _Float16 *planes, int rows) {
+    static_assert(256 * 8 * kSplitChunks == 8192, "rms_split_fits");
+    MR_REQUIRE(rms_split_fits(width) && ldx % 4 == 0,
+               "row RMSNorm into FP16 terms: width must be a multiple of 8 and at most 8192");
     k_rms_rows_split<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
     MR_LAUNCHED("enqueue row RMSNorm into FP16 terms");
     return MR_OK;
