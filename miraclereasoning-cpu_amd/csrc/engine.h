@@ -44,6 +44,11 @@ struct Layer {
     Weight kv_up, router, router_coarse_bias, router_fine_bias, group_bias, expert_bias;
     std::vector<Mlp> experts, shared;
     void **expert_tab = nullptr;       // device [3][experts + shared]: gate, up, down pointers
+    // the batched prefill's FP16 copies of the experts (null when an expert has
+    // none): device [3][experts + shared] pointers and their scales (an expert's
+    // gate and up share one)
+    void **expert_tab_h = nullptr;
+    float *expert_scale = nullptr;
     float *bsum_k = nullptr, *bsum_v = nullptr;   // [inner][blocks, kvw] running block sums
     // flashlighting-2.0: qkv packs [Wq; Wlatent], kv_up packs [Wk; Wv]; latent
     // memory ring of light_cap rows with per-row key/value caches

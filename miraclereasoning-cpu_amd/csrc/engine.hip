@@ -980,6 +980,29 @@ int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     }
     MR_TRY(device_alloc(m, tab.size() * sizeof(void *), (void **)&L.expert_tab));
     MR_HIP(hipMemcpy(L.expert_tab, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice), "upload expert table");
+    // FP16 copies for the batched prefill's grouped GEMMs (all experts or none)
+    std::vector<void *> tab_h(tab.size());
+    std::vector<float> scale(tab.size());
+    bool all = true;
+    for (size_t e = 0; e < n && all; ++e) {
+        Mlp &mlp = e < (size_t)d.routed_experts ? L.experts[e] : L.shared[e - d.routed_experts];
+        MR_TRY(f16_copies(m, {&mlp.gate, &mlp.up, &mlp.down}, {&mlp.gate, &mlp.up}));
+        all = mlp.gate.f16 && mlp.up.f16 && mlp.down.f16;
+        tab_h[e] = mlp.gate.f16;
+        tab_h[n + e] = mlp.up.f16;
+        tab_h[2 * n + e] = mlp.down.f16;
+        scale[e] = mlp.gate.f16_scale;
+        scale[n + e] = mlp.up.f16_scale;
+        scale[2 * n + e] = mlp.down.f16_scale;
+    }
+    if (all) {
+        MR_TRY(device_alloc(m, tab_h.size() * sizeof(void *), (void **)&L.expert_tab_h));
+        MR_HIP(hipMemcpy(L.expert_tab_h, tab_h.data(), tab_h.size() * sizeof(void *), hipMemcpyHostToDevice),
+               "upload expert table");
+        MR_TRY(device_alloc(m, scale.size() * sizeof(float), (void **)&L.expert_scale));
+        MR_HIP(hipMemcpy(L.expert_scale, scale.data(), scale.size() * sizeof(float), hipMemcpyHostToDevice),
+               "upload expert scales");
+    }
     const size_t ring = (size_t)d.inner_loop_steps * d.context_length * kvw * sizeof(float);
     const int blocks = ceil_div(d.context_length, d.global_block_size);
     const size_t bsum = (size_t)d.inner_loop_steps * blocks * kvw * sizeof(float);
@@ -1114,6 +1137,8 @@ int mr_model_destroy(mr_model *m) {
             if (p) hipFree(p);
         if (L.light) hipFree(L.light);
         if (L.expert_tab) hipFree(L.expert_tab);
+        if (L.expert_tab_h) hipFree(L.expert_tab_h);
+        if (L.expert_scale) hipFree(L.expert_scale);
     }
     if (m->choices) hipFree(m->choices);
     if (m->freq) hipFree(m->freq);
@@ -1483,6 +1508,9 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     // pooled rows: cbr_slots per CBR chunk ending inside the rows
     const size_t pr = cbr ? (size_t)(rows / d.cbr_chunk_size + 1) * d.cbr_slots : 0;
     const size_t ext = heavy || light || cbr ? r * d.query_heads * (d.head_dim + 4) : 0;
+    // rows split into FP16 terms at once: a chunk, its pooled CBR rows, or its
+    // rows gathered for every expert slot
+    const size_t split_rows = std::max({r, pr, heavy ? r * slots : 0});
     int max_cap = 0;
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.light_cap);
@@ -1508,8 +1536,8 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
         // flashnano-1.6
         {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
-        {(void **)&w->rowscale, std::max(r, pr)},
-        {(void **)&w->planes, std::max(r, pr) * std::max({h, qd, (size_t)d.ffn_dim})},
+        {(void **)&w->rowscale, split_rows},
+        {(void **)&w->planes, split_rows * std::max({h, qd, (size_t)d.ffn_dim})},
         {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, gqa ? 2 * kvw : 0},
         {(void **)&w->kv16_max, gqa ? 2 * kvw : 0}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
@@ -1799,13 +1827,19 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         GemmGroups gg;
         gg.offset = w.offsets; gg.count = w.counts; gg.groups = groups; gg.max_rows = T;
         gg.w = L.expert_tab; gg.w2 = L.expert_tab + groups;
+        const bool f16 = L.expert_tab_h != nullptr;   // FP16 terms: the experts' copies and scales
+        if (f16) { gg.wh = L.expert_tab_h; gg.wh2 = L.expert_tab_h + groups; gg.wscale = L.expert_scale; }
+        const int rows = T * (kmax + S);   // the gathered rows' capacity (routed slots, then shared)
         GemmArgs gu;
         gu.a = w.xg; gu.lda = h; gu.dtype = e.dtype; gu.c = w.act; gu.ldc = ffn; gu.n = ffn; gu.k = h;
+        gu.m = rows; gu.ascale = w.rowscale; gu.ahl_ws = w.planes;
         MR_TRY(launch_gemm_grouped(s, GEMM_SWIGLU, gu, gg));
         gg.w = L.expert_tab + 2 * groups;
         gg.w2 = nullptr;
+        if (f16) { gg.wh = L.expert_tab_h + 2 * groups; gg.wh2 = nullptr; gg.wscale = L.expert_scale + 2 * groups; }
         GemmArgs dn;
         dn.a = w.act; dn.lda = ffn; dn.dtype = e.dtype; dn.c = w.y; dn.ldc = h; dn.n = h; dn.k = ffn;
+        dn.m = rows; dn.ascale = w.rowscale; dn.ahl_ws = w.planes;
         MR_TRY(launch_gemm_grouped(s, GEMM_STORE, dn, gg));
         MR_TRY(launch_moe_combine_rows(s, mr_, w.y, w.x));
     }

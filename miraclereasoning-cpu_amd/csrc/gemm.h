@@ -41,6 +41,7 @@ struct GemmArgs {
     _Float16 *ahl_ws = nullptr;
     bool a_split = false;            // FP16 terms: ascale and ahl_ws already hold A (a unused)
     const _Float16 *ahl = nullptr;   // set by launch_gemm for the kernel
+    int64_t plane_stride = 0;        // halves from A's hi plane to its lo plane (0: m k)
 };
 
 // STORE:    c = A . W^T
@@ -61,13 +62,19 @@ int gemm_f16_weight_copy(hipStream_t s, const void *w, int64_t count, float scal
 
 // Groups of rows with their own weights (the experts of a batched MoE), one
 // launch: group z multiplies rows offset[z] .. offset[z] + count[z] of g.a by
-// w[z] (and w2[z]) into the same rows of g.c; g.w, g.w2 and g.m are unused.
-// Weight rows must be 16-byte aligned.  STORE and SWIGLU epilogues.
+// w[z] (and w2[z]) into the same rows of g.c; g.w and g.w2 are unused.
+// Weight rows must be 16-byte aligned.  STORE and SWIGLU epilogues.  With wh
+// (BF16 weights), the FP16-term scheme: wh[z] (wh2[z]) are the groups' FP16
+// copies with scales wscale[z] (SwiGLU: gate and up share it), and g.m rows
+// of g.a (every row a group may hold) are split into g.ascale and g.ahl_ws
+// first.  Otherwise g.m is unused and the BF16-term scheme runs.
 struct GemmGroups {
     const int *offset = nullptr;     // [groups] device
     const int *count = nullptr;      // [groups] device
     void *const *w = nullptr;        // [groups] device table of weight pointers
     void *const *w2 = nullptr;       // [groups] SWIGLU up rows
+    void *const *wh = nullptr, *const *wh2 = nullptr;   // [groups] FP16 copies
+    const float *wscale = nullptr;   // [groups] their scales
     int groups = 0;
     int max_rows = 0;                // bound on every count (sizes the grid)
 };

@@ -330,7 +330,7 @@ __device__ __forceinline__ void load_a_h(const GemmArgs &g, int m0, int k0, AHRe
 #pragma unroll
         for (int j = 0; j < KB / 16; ++j) {
             const int q = tid + kThreads * j, row = m0 + q / CPR, col = k0 + (q % CPR) * 8;
-            const _Float16 *plane = g.ahl + (int64_t)p * g.m * g.k;
+            const _Float16 *plane = g.ahl + p * (g.plane_stride ? g.plane_stride : (int64_t)g.m * g.k);
             if (row < g.m && col < g.k) r.v[p][j] = *gmem((const u32x4 *)(plane + (int64_t)row * g.k + col));
             else r.v[p][j] = u32x4{0u, 0u, 0u, 0u};
         }
@@ -432,7 +432,8 @@ template <int EPI, int NI, int KB>
 __device__ __forceinline__ void load_tile_buf(const GemmArgs &g, const TileOffsets<NI, KB> &o, int k0, AHRegs<KB> &ar,
                                               u32x4 (&wr)[NI * KB / 64]) {
     const int64_t mk = (int64_t)g.m * g.k, nk = (int64_t)g.n * g.k;
-    const __amdgpu_buffer_rsrc_t a0 = half_rsrc(g.ahl, mk), a1 = half_rsrc(g.ahl + mk, mk);
+    const __amdgpu_buffer_rsrc_t a0 = half_rsrc(g.ahl, mk),
+                                 a1 = half_rsrc(g.ahl + (g.plane_stride ? g.plane_stride : mk), mk);
     const __amdgpu_buffer_rsrc_t w0 = half_rsrc(g.w, nk), w1 = half_rsrc(EPI == GEMM_SWIGLU ? g.w2 : g.w, nk);
     const int so = k0 * 2;
 #pragma unroll
@@ -594,10 +595,55 @@ __global__ void __launch_bounds__(kThreads) k_gemm_grouped(GemmArgs g, GemmGroup
     gemm_tile<DT, EPI>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
 }
 
+// The FP16-term form: group z's rows are rows offset[z] .. of the planes and
+// row scales split for all g.m rows.
+template <int EPI, int NI, bool BUF>
+__global__ void __launch_bounds__(kThreads) k_gemm_grouped_h(GemmArgs g, GemmGroups gg) {
+    const int z = blockIdx.z, m0 = blockIdx.y * kBM, rows = gg.count[z];
+    if (m0 >= rows) return;
+    const int64_t first = gg.offset[z];
+    g.plane_stride = (int64_t)g.m * g.k;
+    g.ahl += first * g.k;
+    g.ascale += first;
+    g.c += first * g.ldc;
+    g.m = rows;
+    g.w = gg.wh[z];
+    if (EPI == GEMM_SWIGLU) g.w2 = gg.wh2[z];
+    g.wscale = gg.wscale[z];
+    gemm_tile_h<EPI, NI, kKBH, BUF>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+}
+
 template <int DT>
 int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroups &gg) {
     const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
     const dim3 grid(ceil_div(g.n, cols), ceil_div(gg.max_rows, kBM), gg.groups);
+    if (DT == MR_BF16 && gg.wh) {
+        MR_REQUIRE(g.m > 0 && g.ascale && g.ahl_ws && gg.wscale && (epi != GEMM_SWIGLU || gg.wh2),
+                   "grouped gemm: FP16 terms need the rows to split, their workspaces and the weights' scales");
+        GemmArgs h = g;
+        h.ahl = g.ahl_ws;
+        k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        // buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
+        const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
+                         (int64_t)g.n * g.k * 2 < (1ll << 31);
+        switch (epi) {
+            case GEMM_STORE: {
+                const dim3 gs(ceil_div(g.n, 32 * 4), ceil_div(gg.max_rows, kBM), gg.groups);
+                if (buf) k_gemm_grouped_h<GEMM_STORE, 4, true><<<gs, kThreads, 0, s>>>(h, gg);
+                else k_gemm_grouped_h<GEMM_STORE, 4, false><<<gs, kThreads, 0, s>>>(h, gg);
+                break;
+            }
+            case GEMM_SWIGLU: {
+                const dim3 gs(ceil_div(g.n, 16 * kSwigluNI), ceil_div(gg.max_rows, kBM), gg.groups);
+                if (buf) k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI, true><<<gs, kThreads, 0, s>>>(h, gg);
+                else k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI, false><<<gs, kThreads, 0, s>>>(h, gg);
+                break;
+            }
+            default: return fail(MR_ERR_INVALID, "grouped gemm: epilogue must be STORE or SWIGLU");
+        }
+        MR_LAUNCHED("enqueue grouped MFMA GEMM (FP16 terms)");
+        return MR_OK;
+    }
     switch (epi) {
         case GEMM_STORE: k_gemm_grouped<DT, GEMM_STORE><<<grid, kThreads, 0, s>>>(g, gg); break;
         case GEMM_SWIGLU: k_gemm_grouped<DT, GEMM_SWIGLU><<<grid, kThreads, 0, s>>>(g, gg); break;
