@@ -208,10 +208,8 @@ def trace_summary(model, cfg, steps, dump=None):
     from the model's current position, as a markdown table: for each phase kind
     of local and of global layers, the mean time from the previous phase's last
     workgroup to store its outputs to this phase's last ("phase"), and from that
-    same instant to the median workgroup having its input staged ("input"),
-    the median first stream wave having consumed its first weight job
-    ("weights"; in attention phases, the median merging unit seeing its first
-    partial cells) and having stored its rows ("rows")."""
+    same instant to the median workgroup having its input staged ("input") and
+    the median first stream wave having stored its rows ("rows")."""
     kinds = ("qkv", "attention", "o", "gate_up", "down")
     acc = {}
     first_pos = model.engine.position()
@@ -221,7 +219,7 @@ def trace_summary(model, cfg, steps, dump=None):
         raw.append(t)
         ends = np.nanmax(t[:, :, 2], axis=1)
         total = ends[-1] - np.nanmin(t[0, :, 0])
-        acc.setdefault(("step", "-"), []).append((total, np.nan, np.nan, np.nan))
+        acc.setdefault(("step", "-"), []).append((total, np.nan, np.nan))
         for p in range(1, t.shape[0]):
             if p == t.shape[0] - 1:
                 key = ("head", "-")
@@ -231,13 +229,12 @@ def trace_summary(model, cfg, steps, dump=None):
             prev = ends[p - 1]
             ready = np.nanmedian(t[p, :, 1]) - prev
             rows = np.nanmedian(t[p, :, 3]) - prev if np.any(np.isfinite(t[p, :, 3])) else np.nan
-            first = np.nanmedian(t[p, :, 4]) - prev if np.any(np.isfinite(t[p, :, 4])) else np.nan
-            acc.setdefault(key, []).append((ends[p] - prev, ready, rows, first))
+            acc.setdefault(key, []).append((ends[p] - prev, ready, rows))
     print(f"persistent decode step anatomy: {steps} steps from position {first_pos}, "
           f"{cfg.layers} layers ({sum(cfg.layer_window(i) is None for i in range(cfg.layers))} global)")
-    print("| Phase | Layers | Phase µs (mean) | Input staged µs (median WG) | First weights consumed µs (median "
-          "first stream wave; attention: merger's first cells) | Rows stored µs (median first stream wave) | Count |")
-    print("|---|---|---|---|---|---|---|")
+    print("| Phase | Layers | Phase µs (mean) | Input staged µs (median WG) | Rows stored µs (median first stream "
+          "wave) | Count |")
+    print("|---|---|---|---|---|---|")
     order = [(k, s) for k in kinds for s in ("local", "global")] + [("head", "-"), ("step", "-")]
 
     def fmt(col):
@@ -247,8 +244,7 @@ def trace_summary(model, cfg, steps, dump=None):
         if key not in acc:
             continue
         v = np.array(acc[key])
-        print(f"| {key[0]} | {key[1]} | {v[:, 0].mean():.2f} | {fmt(v[:, 1])} | {fmt(v[:, 3])} | {fmt(v[:, 2])} "
-              f"| {len(v)} |")
+        print(f"| {key[0]} | {key[1]} | {v[:, 0].mean():.2f} | {fmt(v[:, 1])} | {fmt(v[:, 2])} | {len(v)} |")
     if dump:
         np.save(dump, np.stack(raw))
     return 0

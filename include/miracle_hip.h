@@ -247,8 +247,7 @@ MR_API int mr_model_choices(mr_model *model, int32_t *out, int64_t capacity, int
  * the reference).  Runs one greedy decode step at the current position with
  * timestamps (100 MHz device wall clock) written per phase and workgroup:
  * out[(phase * grid + wg) * 5 + {0: phase entry, 1: input staged, 2: outputs
- * stored by the last stream wave, 3: by the first stream wave, 4: the first
- * stream wave's first weight job consumed}]
+ * stored by the last stream wave, 3: by the first stream wave, 4: unused}]
  * (0 where not stamped); in attention phases 1 is the unit's Q/K/V cells
  * staged, 2 the workgroup's end of the phase, 3 the unit's partial stored and
  * 4 a merging unit's first partial cells seen.

@@ -69,8 +69,7 @@ struct StepArgs {
 
 // Trace record of one (phase, workgroup): wall clock (100 MHz) at the phase's
 // entry, when its input was staged, when its last stream wave stored its
-// outputs, when its first stream wave did, and when that wave had consumed
-// its first weight job (its loads had returned).  In
+// outputs and when its first stream wave did; the fifth field is unused.  In
 // an attention phase: entry, the unit's Q/K/V cells staged, the phase's end
 // for this workgroup (after its merge, for a merging unit), the unit's partial
 // stored and, in a merging unit, its first partial cells seen.

@@ -405,10 +405,6 @@ __device__ __forceinline__ bool gemv_phase(const Phase &ph, const StepArgs &s, u
                 if (t0 + d < g.jobs) {
                     if (g.cpr != 1) load_x<E>(xr, g, xs, cs.c);
                     consume<DT, M, E>(buf[d], cs, g, xr, acc);
-                    if (tr && t0 == 0 && d == 0 && tid == NC * kWave) {   // its first job's weights are in
-                        asm volatile("" ::"v"(acc[0]));
-                        tr[4] = wall_clock64();
-                    }
                     if (cs.c == g.cpr - 1) {   // row group complete
                         const float a0 = scale * group_sum(acc[0], g.lpr);
                         const float a1 = M == 2 ? scale * group_sum(acc[M - 1], g.lpr) : a0;

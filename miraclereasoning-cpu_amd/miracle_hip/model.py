@@ -182,9 +182,9 @@ class Engine:
     def trace_step(self):
         """Per-phase, per-workgroup record of one persistent greedy decode step:
         array [phases, grid, 5] of (phase entry, input staged, outputs stored
-        by the last stream wave, outputs stored by the first stream wave, the
-        first stream wave's first weight job consumed) in µs relative to the
-        step start (NaN where not recorded).  In attention phases the fields are (entry, the unit's
+        by the last stream wave, outputs stored by the first stream wave) in µs
+        relative to the step start (NaN where not recorded), and a fifth field
+        unused there.  In attention phases the fields are (entry, the unit's
         Q/K/V cells staged, the workgroup's end of the phase (after its merge,
         for a merging unit), the unit's partial stored, a merging unit's first
         partial cells seen)."""
