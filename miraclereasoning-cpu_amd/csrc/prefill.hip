@@ -781,9 +781,10 @@ __global__ void k_embed_rows(const void *table, int dt, const int *ids, int p0, 
 // relay rows it sees through LDS in tiles of TR rows (64 for d <= 64, 32 for
 // d <= 128, so a tile of keys and values stays under 34 KB; the pairs'
 // queries take 16 KB more).  Scores: SPLIT
-// lanes per relay row (lane % TR the row, lane / TR half of the dims), one
-// online-softmax update per pair and tile; values: lanes over dims, the
-// probabilities read lane by lane.
+// lanes per relay row (lane % TR the row, lane / TR half of the dims), the
+// lane's part of the key row held in registers across the wave's pairs, one
+// online-softmax update per pair and tile; values: lanes over dims, each value
+// read from LDS once for all the pairs, the probabilities read lane by lane.
 constexpr int kRelayPairs = 32, kRelayPairsPerWave = kRelayPairs / 4;
 
 template <int SPLIT>
@@ -827,47 +828,56 @@ __global__ void __launch_bounds__(256) k_relay_partial(RelayPartialArgs a, int r
             *(float4 *)(vs + j * d + c) = j < cnt ? load_f4(vb + (int64_t)(base + j) * kvw + c) : z;
         }
         __syncthreads();
-        // No branches per pair: a pair that sees none of the tile scores -inf
+        // The lane's key row (its dims part) stays in registers for the
+        // wave's pairs, and each value read from LDS serves all of them.  No
+        // branches per pair: a pair that sees none of the tile scores -inf
         // everywhere and keeps its state (alpha 1, or 0 with nothing summed).
+        float4 kr4[16];   // dp <= 64
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            kr4[i] = 4 * i < dp ? *(const float4 *)(ks + jr * KP + part * dp + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float p[kRelayPairsPerWave];
 #pragma unroll
         for (int k = 0; k < kRelayPairsPerWave; ++k) {
             const int n = min(seen[k] - base, cnt);   // rows of the tile it sees (may be <= 0)
-            const float *q = qs + (wave * kRelayPairsPerWave + k) * d + part * dp, *kr = ks + jr * KP + part * dp;
-            float s = 0.0f;
-            for (int i = 0; i < dp; i += 4) {
-                const float4 qq = *(const float4 *)(q + i), kk = *(const float4 *)(kr + i);
-                s = fmaf(qq.x, kk.x, s);
-                s = fmaf(qq.y, kk.y, s);
-                s = fmaf(qq.z, kk.z, s);
-                s = fmaf(qq.w, kk.w, s);
+            const float *q = qs + (wave * kRelayPairsPerWave + k) * d + part * dp;
+            float sc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (4 * i < dp) {
+                    const float4 qq = *(const float4 *)(q + 4 * i);
+                    sc = fmaf(qq.x, kr4[i].x, sc);
+                    sc = fmaf(qq.y, kr4[i].y, sc);
+                    sc = fmaf(qq.z, kr4[i].z, sc);
+                    sc = fmaf(qq.w, kr4[i].w, sc);
+                }
             }
-            if constexpr (SPLIT == 2) s += __shfl_xor(s, TR, kWave);
-            s = jr < n ? s * a.inv_root : -INFINITY;
-            const float mn = fmaxf(m[k], wave_max(s));
+            if constexpr (SPLIT == 2) sc += __shfl_xor(sc, TR, kWave);
+            sc = jr < n ? sc * a.inv_root : -INFINITY;
+            const float mn = fmaxf(m[k], wave_max(sc));
             const float alpha = m[k] == -INFINITY ? 0.0f : expf(m[k] - mn);
-            const float p = jr < n ? expf(s - mn) : 0.0f;
-            l[k] = l[k] * alpha + wave_sum(p) / SPLIT;   // each row's probability sits in SPLIT lanes
+            p[k] = jr < n ? expf(sc - mn) : 0.0f;
+            l[k] = l[k] * alpha + wave_sum(p[k]) / SPLIT;   // each row's probability sits in SPLIT lanes
             m[k] = mn;
 #pragma unroll
             for (int x = 0; x < DL; ++x) o[k][x] *= alpha;
-            // 8 relay rows a round over the staged rows (past n: probability 0;
-            // past cnt: zero values)
-            for (int jj = 0; jj < cnt; jj += 8) {
-                float pj[8];
+        }
+        // 8 relay rows a round over the staged rows (past a pair's n:
+        // probability 0; past cnt: zero values)
+        for (int jj = 0; jj < cnt; jj += 8) {
+            float vv[8][DL];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) pj[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), jj + u));
+            for (int u = 0; u < 8; ++u)
 #pragma unroll
-                for (int x = 0; x < DL; ++x) {
-                    const int dim = lane + x * kWave;
-                    if (dim < d) {
-                        float vv[8];
+                for (int x = 0; x < DL; ++x) vv[u][x] = lane + x * kWave < d ? vs[(jj + u) * d + lane + x * kWave] : 0.0f;
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) vv[u] = vs[(jj + u) * d + dim];
+            for (int k = 0; k < kRelayPairsPerWave; ++k)
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) o[k][x] = fmaf(pj[u], vv[u], o[k][x]);
-                    }
+                for (int u = 0; u < 8; ++u) {
+                    const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[k]), jj + u));
+#pragma unroll
+                    for (int x = 0; x < DL; ++x) o[k][x] = fmaf(pj, vv[u][x], o[k][x]);
                 }
-            }
         }
     }
 #pragma unroll
