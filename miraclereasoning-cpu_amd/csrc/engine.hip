@@ -1469,6 +1469,7 @@ namespace {
 __global__ void k_set_int(int *p, int v) { *p = v; }
 
 constexpr int kPrefillRows = 4096;   // prompt rows per batched prefill chunk
+constexpr int kRouterSlices = 8;     // K slices of heavy-medium-2.0's router GEMM
 
 // One chunk's activations (FP32, rows of the chunk): hidden, normalized input,
 // q|k|v, attended values, SwiGLU activations and, with return_all, logits;
@@ -1487,6 +1488,7 @@ struct PrefillWs {
           *merge_count = nullptr;
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
     float *cbr_scores = nullptr, *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;   // flashnano-1.6
+    float *router_part = nullptr;   // heavy-medium-2.0: the router GEMM's K slices
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
@@ -1525,6 +1527,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         // heavy-medium-2.0
         {(void **)&w->sums, heavy ? r * 2 * kvw : 0}, {(void **)&w->router, heavy ? r * (d.router_groups + groups) : 0},
         {(void **)&w->mw, r * kmax}, {(void **)&w->xg, heavy ? r * slots * h : 0},
+        {(void **)&w->router_part, heavy ? r * kRouterSlices * (d.router_groups + groups) : 0},
         {(void **)&w->y, heavy ? r * slots * h : 0}, {(void **)&w->ids, r * kmax}, {(void **)&w->active, heavy ? r : 0},
         {(void **)&w->counts, groups}, {(void **)&w->offsets, groups}, {(void **)&w->fill, groups},
         {(void **)&w->map, r * kmax},
@@ -1804,10 +1807,10 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         o.wscale = L.o.f16_scale; o.wh = L.o.f16; o.ascale = w.rowscale; o.ahl_ws = w.planes;
         MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
         MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
-        GemmArgs r;   // [Wcoarse; Wfine]
+        GemmArgs r;   // [Wcoarse; Wfine], K in slices: its R columns fill few tiles
         r.a = w.xn; r.lda = h; r.w = L.router.ptr; r.dtype = L.router.dtype; r.c = w.router; r.ldc = R;
         r.m = T; r.n = R; r.k = h;
-        MR_TRY(launch_gemm(s, GEMM_STORE, r));
+        MR_TRY(launch_gemm_split(s, r, kRouterSlices, w.router_part));
         MoeRowsArgs mr_;
         MoeArgs &e = mr_.a;
         e.router = w.router;

@@ -42,6 +42,7 @@ struct GemmArgs {
     bool a_split = false;            // FP16 terms: ascale and ahl_ws already hold A (a unused)
     const _Float16 *ahl = nullptr;   // set by launch_gemm for the kernel
     int64_t plane_stride = 0;        // halves from A's hi plane to its lo plane (0: m k)
+    int ldw = 0;                     // elements between weight rows (0: k; set by the split GEMM)
 };
 
 // STORE:    c = A . W^T
@@ -49,6 +50,12 @@ struct GemmArgs {
 // SWIGLU:   c = silu(A . Wg^T) * (A . Wu^T), silu(g) = g / (1 + exp(-g))
 // Requires k % 8 == 0, lda % 4 == 0 and 16-byte aligned a and weight rows.
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g);
+
+// c = A . W^T (BF16-term scheme, no FP16 weights) with K cut into `slices`
+// runs of whole k-steps, each its own workgroups' partial product in `part`
+// (slices x m x n floats), then summed slice by slice in order: for a few
+// output columns over many rows, where the plain GEMM has too few tiles.
+int launch_gemm_split(hipStream_t s, const GemmArgs &g, int slices, float *part);
 
 // The power of two 2^s that puts max |w| of a BF16 matrix of `count` values
 // in [2^13, 2^14) (1 for an all-zero matrix), so that w 2^s is exact in FP16

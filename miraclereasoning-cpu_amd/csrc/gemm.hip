@@ -86,7 +86,7 @@ __device__ __forceinline__ const char *w_row(const GemmArgs &g, int n0, int r, i
         f = n0 + r;
     }
     ok = f < g.n;
-    return (const char *)base + (int64_t)(ok ? f : 0) * g.k * esize;
+    return (const char *)base + (int64_t)(ok ? f : 0) * (g.ldw ? g.ldw : g.k) * esize;
 }
 
 __device__ __forceinline__ void load_a(const GemmArgs &g, int m0, int k0, ARegs &r) {
@@ -580,6 +580,32 @@ __global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
     gemm_tile<DT, EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
 }
 
+// grid (column tiles, row tiles, slices): slice z multiplies columns
+// z ks .. of A by the same columns of W into its own partial product
+// part[z] (STORE epilogue, BF16-term scheme), summed by k_sum_slices.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_gemm_split(GemmArgs g, int ks, float *part) {
+    const int z = blockIdx.z, lo = z * ks;
+    const int esize = DT == MR_F32 ? 4 : 2;
+    g.a += lo;
+    g.w = (const char *)g.w + (int64_t)lo * esize;
+    g.ldw = g.k;
+    g.k = min(ks, g.k - lo);
+    g.c = part + (int64_t)z * g.m * g.ldc;
+    gemm_tile<DT, GEMM_STORE>(g, blockIdx.y * kBM, blockIdx.x * kBN);
+}
+
+// c[r][j] = sum over z of part[z][r][j], slices in order.
+__global__ void __launch_bounds__(256) k_sum_slices(const float *part, int slices, int m, int n, int ldp, float *c,
+                                                    int ldc) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)m * n) return;
+    const int r = (int)(i / n), j = (int)(i % n);
+    float v = 0.0f;
+    for (int z = 0; z < slices; ++z) v += part[((int64_t)z * m + r) * ldp + j];
+    c[(int64_t)r * ldc + j] = v;
+}
+
 // grid (column tiles, row tiles of the largest group, groups): group z is
 // rows offset[z] .. + count[z] of a and c with its own weight rows.
 template <int DT, int EPI>
@@ -698,6 +724,29 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
 }
 
 }  // namespace
+
+int launch_gemm_split(hipStream_t s, const GemmArgs &g, int slices, float *part) {
+    MR_REQUIRE(g.a && g.w && g.c && part && g.m > 0 && g.n > 0 && g.k > 0 && slices >= 1 && g.wscale <= 0.0f,
+               "split gemm: bad arguments");
+    MR_REQUIRE(g.k % 8 == 0 && g.lda % 4 == 0 && g.lda >= g.k && g.ldc >= g.n && ((uintptr_t)g.a & 15) == 0 &&
+                   ((uintptr_t)g.w & 15) == 0,
+               "split gemm: k must be a multiple of 8 and rows 16-byte aligned");
+    const int ks = ceil_div(ceil_div(g.k, slices), kBK) * kBK;   // whole k-steps per slice
+    const int n_slices = ceil_div(g.k, ks);
+    GemmArgs h = g;
+    h.ldc = g.n;   // partial products are packed rows of n
+    const dim3 grid(ceil_div(g.n, kBN), ceil_div(g.m, kBM), n_slices);
+    switch (g.dtype) {
+        case MR_BF16: k_gemm_split<MR_BF16><<<grid, kThreads, 0, s>>>(h, ks, part); break;
+        case MR_F16: k_gemm_split<MR_F16><<<grid, kThreads, 0, s>>>(h, ks, part); break;
+        case MR_F32: k_gemm_split<MR_F32><<<grid, kThreads, 0, s>>>(h, ks, part); break;
+        default: return fail(MR_ERR_INVALID, "split gemm: unknown weight dtype");
+    }
+    MR_LAUNCHED("enqueue split MFMA GEMM");
+    k_sum_slices<<<(int)(((int64_t)g.m * g.n + 255) / 256), 256, 0, s>>>(part, n_slices, g.m, g.n, g.n, g.c, g.ldc);
+    MR_LAUNCHED("enqueue split GEMM sum");
+    return MR_OK;
+}
 
 int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const GemmGroups &gg) {
     MR_REQUIRE(g.a && g.c && g.n > 0 && g.k > 0 && gg.offset && gg.count && gg.w && gg.groups > 0 &&
