@@ -917,22 +917,29 @@ __global__ void __launch_bounds__(256) k_heavy_scan(HeavyScanArgs a) {
 }
 
 // grid (rows, heads), kSelThreads.  LDS: query, block scores, keep flags.
-constexpr int kSelThreads = 128;
+constexpr int kSelHeads = 4;   // query heads of one row per workgroup, a wave each
+constexpr int kSelThreads = kSelHeads * kWave;
 
 template <int D>
 __global__ void __launch_bounds__(kSelThreads) k_heavy_select(HeavySelectArgs a) {
     extern __shared__ float sh[];
-    __shared__ int chosen[kHeavyMaxChosen];
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    __shared__ int chosen_all[kSelHeads][kHeavyMaxChosen];
+    // wave w takes head kSelHeads y + w of row x; a wave past the last head
+    // repeats the last head's work (every wave meets the same barriers: the
+    // row's heads see the same blocks) and stores nothing
+    const int t = blockIdx.x, wave = threadIdx.x >> 6, tid = threadIdx.x & 63;
+    const bool live = (int)blockIdx.y * kSelHeads + wave < a.heads;
+    const int h = min((int)blockIdx.y * kSelHeads + wave, a.heads - 1);
     const int pos = a.p0 + t, count = pos + 1, kh = h / (a.heads / a.kv_heads), kvw = a.kv_heads * D;
     const int blocks = (count + a.block - 1) / a.block, bt = pos / a.block;
-    float *qs = sh, *sc = qs + D;
+    float *qs = sh + wave * (D + 2 * blocks), *sc = qs + D;
     int *keep_flag = (int *)(sc + blocks);
-    for (int j = tid; j < D; j += kSelThreads) qs[j] = a.qkv[(int64_t)t * a.ld + (int64_t)h * D + j];
+    int *chosen = chosen_all[wave];
+    for (int j = tid; j < D; j += kWave) qs[j] = a.qkv[(int64_t)t * a.ld + (int64_t)h * D + j];
     __syncthreads();
     const float root = sqrtf((float)D);
     const float *row_sums = a.sums + (int64_t)t * 2 * kvw;
-    for (int b = tid; b < blocks; b += kSelThreads) {   // the token step's quotients and dot order
+    for (int b = tid; b < blocks; b += kWave) {   // the token step's quotients and dot order
         const float *ks = b < bt ? a.bsum_k + (int64_t)b * kvw + (int64_t)kh * D : row_sums + (int64_t)kh * D;
         const float n = (float)min(a.block, count - b * a.block);
         float v = 0.0f;
@@ -942,7 +949,7 @@ __global__ void __launch_bounds__(kSelThreads) k_heavy_select(HeavySelectArgs a)
     }
     __syncthreads();
     const int keep = min(a.slots, blocks);
-    for (int b = tid; b < blocks; b += kSelThreads) {   // stable top-k (model.py:220-226)
+    for (int b = tid; b < blocks; b += kWave) {   // stable top-k (model.py:220-226)
         const float sv = sc[b];
         int rank = 0;
         for (int c = 0; c < blocks; ++c) {
@@ -952,21 +959,22 @@ __global__ void __launch_bounds__(kSelThreads) k_heavy_select(HeavySelectArgs a)
         keep_flag[b] = rank < keep;
     }
     __syncthreads();
-    for (int b = tid; b < blocks; b += kSelThreads)
+    for (int b = tid; b < blocks; b += kWave)
         if (keep_flag[b]) {
             int at = 0;
             for (int c = 0; c < b; ++c) at += keep_flag[c];
             chosen[at] = b;
         }
     __syncthreads();
+    if (!live) return;   // no barrier follows
     if (a.choice) {
         int *rec = a.choice + (int64_t)pos * a.choice_stride + a.choice_blocks + h * a.slots;
-        for (int i = tid; i < a.slots; i += kSelThreads) rec[i] = i < keep ? chosen[i] : -1;
+        for (int i = tid; i < a.slots; i += kWave) rec[i] = i < keep ? chosen[i] : -1;
     }
     float m = -INFINITY;
     for (int i = 0; i < keep; ++i) m = fmaxf(m, sc[chosen[i]]);
     float *out = a.ext + ((int64_t)t * a.heads + h) * (D + 4);
-    for (int j = tid; j < D; j += kSelThreads) {
+    for (int j = tid; j < D; j += kWave) {
         float o = 0.0f, l = 0.0f;
         for (int i = 0; i < keep; ++i) {
             const int b = chosen[i];
@@ -1162,9 +1170,9 @@ int launch_heavy_select(hipStream_t s, const HeavySelectArgs &a) {
                    a.kv_heads > 0 && a.heads % a.kv_heads == 0,
                "heavy select: bad arguments");
     const int blocks = ceil_div(a.p0 + a.rows, a.block);
-    const size_t lds = (size_t)(a.d + blocks) * sizeof(float) + (size_t)blocks * sizeof(int);
+    const size_t lds = (size_t)kSelHeads * (a.d + 2 * blocks) * sizeof(float);   // per wave: q, scores, flags
     MR_REQUIRE(lds <= 64 * 1024, "heavy select: too many blocks for shared memory");
-    const dim3 grid(a.rows, a.heads);
+    const dim3 grid(a.rows, ceil_div(a.heads, kSelHeads));
     switch (a.d) {
         case 128: k_heavy_select<128><<<grid, kSelThreads, lds, s>>>(a); break;
         case 64: k_heavy_select<64><<<grid, kSelThreads, lds, s>>>(a); break;
