@@ -1893,6 +1893,9 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     r.slot0 = w.slot0; r.slot0_final = w.slot0_final; r.flags = w.flags; r.extra_index = w.extra_index;
     r.merge_count = w.merge_count; r.merge_row = w.merge_row; r.init_from_arena = pl.init_from_arena;
     r.init_slot = pl.init_slot; r.p0 = p0; r.rows = T; r.latent = lat; r.cap = L.light_cap;
+    r.merged = w.obuf;   // free until the O projection
+    r.row0_ws = w.fbuf;  // free until the FFN's down projection
+    MR_REQUIRE(light_row0_ws_floats(T, d.latent_dim) <= (size_t)T * h, "latent rows: workspace too small");
     if (d.memory_slots > 0) MR_TRY(launch_light_slot0(s, r));   // reads the ring before this chunk writes it
     if (pl.extra > 0) {
         GemmArgs k0 = kv;   // logical row 0's keys and values

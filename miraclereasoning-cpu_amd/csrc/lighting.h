@@ -97,11 +97,19 @@ struct LightRowsArgs {
     const float *merge_count = nullptr; // [rows] count of row 0 before the step's merge
     const int *merge_row = nullptr;     // [rows] position of the row folded in (logical row 1)
     int init_from_arena = 0, init_slot = 0;   // row 0 before the chunk: arena slot, or the chunk's first row
+    float *merged = nullptr;            // [rows, latent] scratch: the row a step's merge folds in, at its step
+    float *row0_ws = nullptr;           // scratch of light_row0_ws_floats(rows, latent) floats
     int p0 = 0, rows = 0, latent = 0, cap = 0;
 };
 // Logical row 0's latent through the chunk: kernels.cl merge_rows
-// (a x0 + b x1) / (a + b) with b = 1 at every merge, in step order.
+// (a x0 + b x1) / (a + b) with b = 1 at every merge, in step order (with a
+// growing by 1 a merge, evaluated as a running sum over the count: equal to
+// the step-by-step form up to rounding).
 int launch_light_slot0(hipStream_t s, const LightRowsArgs &a);
+inline size_t light_row0_ws_floats(int rows, int latent) {
+    const size_t seg = (size_t)(rows + 127) / 128;   // segments of the recurrence
+    return seg * latent + 4 + 2 * seg;
+}
 // ext[t][h] = (q . k0 / sqrt(d), 1, -, -, v0) for steps with an extra row,
 // (-inf, 0, -, -, 0) otherwise; kv0 = [extra rows][k | v] (keys normed, rotated).
 int launch_light_extra(hipStream_t s, const float *qkv, int ld, const float *kv0, const int *extra_index, float *ext,

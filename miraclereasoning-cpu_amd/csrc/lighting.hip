@@ -393,22 +393,124 @@ __global__ void k_light_residual(float *hidden, const float *o, const float *f, 
 
 // ------------------------------------------------------------------ batched prefill
 // one thread per latent column: the running logical row 0 through the chunk
-__global__ void __launch_bounds__(256) k_light_slot0(LightRowsArgs a) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= a.latent) return;
-    float v = a.init_from_arena ? a.arena[(int64_t)a.init_slot * a.latent + j] : a.lat[j];
-    for (int t = 0; t < a.rows; ++t) {
-        const int f = a.flags[t];
-        if (f & 1) a.slot0[(int64_t)a.extra_index[t] * a.latent + j] = v;
-        if (f & 2) {
-            const int r = a.merge_row[t];
-            const float x = r >= a.p0 ? a.lat[(int64_t)(r - a.p0) * a.latent + j]
-                                      : a.arena[(int64_t)(r % a.cap) * a.latent + j];
-            const float c = a.merge_count[t];
-            v = (c * v + 1.0f * x) / (c + 1.0f);
+// Logical row 0 through the chunk.  Every merge folds one original row
+// (count 1) into row 0 and adds 1 to its count, so row 0 is the running mean
+// of what it folded: with sum = count * row 0 a merge is sum += row, and row 0
+// is sum / count wherever a step reads it (the value merge_rows gives step by
+// step, up to rounding).  The chunk's steps go in segments of kRow0Seg: the
+// merged rows are gathered by step (zeros where a step merges nothing), each
+// segment's sum and merge count formed in parallel, the segments' starting
+// states by one pass over them, and then every segment runs its steps from its
+// starting state, in parallel.
+constexpr int kRow0Seg = 128;
+
+// merged[t] = the row step t's merge folds in, or zeros (one workgroup a step).
+__global__ void __launch_bounds__(kWave) k_light_gather_merged(LightRowsArgs a) {
+    const int t = blockIdx.x;
+    float *dst = a.merged + (int64_t)t * a.latent;
+    if (!(a.flags[t] & 2)) {
+        for (int j = threadIdx.x; j < a.latent; j += kWave) dst[j] = 0.0f;
+        return;
+    }
+    const int r = a.merge_row[t];
+    const float *src = r >= a.p0 ? a.lat + (int64_t)(r - a.p0) * a.latent : a.arena + (int64_t)(r % a.cap) * a.latent;
+    for (int j = threadIdx.x; j < a.latent; j += kWave) dst[j] = src[j];
+}
+
+// grid (segments, latent / 64), one wave: the segment's sum of merged rows
+// (8 rows' loads in flight) and its merge count.
+__global__ void __launch_bounds__(kWave) k_row0_segments(LightRowsArgs a, float *seg_sum, int *seg_cnt) {
+    const int sg = blockIdx.x, lane = threadIdx.x, j = blockIdx.y * kWave + lane;
+    const int t0 = sg * kRow0Seg, t1 = min(t0 + kRow0Seg, a.rows);
+    const int jj = min(j, a.latent - 1);
+    float acc = 0.0f;
+    for (int t = t0; t < t1; t += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = t + u < t1 ? a.merged[(int64_t)(t + u) * a.latent + jj] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += x[u];
+    }
+    if (j < a.latent) seg_sum[(int64_t)sg * a.latent + j] = acc;
+    if (blockIdx.y == 0) {
+        int c = 0;
+        for (int t = t0 + lane; t < t1; t += kWave) c += (a.flags[t] & 2) ? 1 : 0;
+        for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, kWave);
+        if (lane == 0) seg_cnt[sg] = c;
+    }
+}
+
+// grid latent / 64, one wave: segment starting sums (exclusive, in segment
+// order, in place: each workgroup its own dims) and counts (into seg_start,
+// by workgroup 0), row 0's count before the chunk's first merge
+// (first_count[0]) and row 0 after the chunk.
+__global__ void __launch_bounds__(kWave) k_row0_starts(LightRowsArgs a, float *seg_sum, const int *seg_cnt, int nseg,
+                                                       float *first_count, int *seg_start) {
+    const int lane = threadIdx.x, j = blockIdx.x * kWave + lane, jj = min(j, a.latent - 1);
+    const float v0 = a.init_from_arena ? a.arena[(int64_t)a.init_slot * a.latent + jj] : a.lat[jj];
+    float sum = 0.0f;
+    int cnt = 0, first_seg = -1;
+    for (int sg = 0; sg < nseg; ++sg) {
+        const float x = seg_sum[(int64_t)sg * a.latent + jj];
+        const int c = seg_cnt[sg];
+        if (j < a.latent) seg_sum[(int64_t)sg * a.latent + j] = sum;
+        if (blockIdx.x == 0 && lane == 0) seg_start[sg] = cnt;
+        if (first_seg < 0 && c > 0) first_seg = sg;
+        sum += x;
+        cnt += c;
+    }
+    float c0 = 1.0f;
+    if (first_seg >= 0)
+        for (int t = first_seg * kRow0Seg;; ++t)
+            if (a.flags[t] & 2) {
+                c0 = a.merge_count[t];
+                break;
+            }
+    if (blockIdx.x == 0 && lane == 0) first_count[0] = c0;
+    if (j < a.latent) a.slot0_final[j] = cnt > 0 ? (c0 * v0 + sum) / (c0 + (float)cnt) : v0;
+}
+
+// grid (segments, latent / 64), one wave: the segment's steps from its
+// starting state: a step that sees row 0 stores it, a merge adds its row
+// (8 steps' records read ahead, no branches on them).
+__global__ void __launch_bounds__(kWave) k_row0_steps(LightRowsArgs a, const float *seg_sum, const int *seg_cnt,
+                                                      const float *first_count) {
+    __shared__ __align__(16) int fl[kRow0Seg], ex[kRow0Seg];
+    const int sg = blockIdx.x, lane = threadIdx.x, j = blockIdx.y * kWave + lane, jj = min(j, a.latent - 1);
+    const bool on = j < a.latent;
+    const int t0 = sg * kRow0Seg, nt = min(kRow0Seg, a.rows - t0);
+    for (int i = lane; i < kRow0Seg; i += kWave) {
+        fl[i] = i < nt ? a.flags[t0 + i] : 0;
+        ex[i] = i < nt ? a.extra_index[t0 + i] : 0;
+    }
+    __syncthreads();
+    const float v0 = a.init_from_arena ? a.arena[(int64_t)a.init_slot * a.latent + jj] : a.lat[jj];
+    const float c0 = first_count[0];
+    const int before = seg_cnt[sg];
+    bool merged = before > 0;
+    float sum = merged ? c0 * v0 + seg_sum[(int64_t)sg * a.latent + jj] : 0.0f;
+    float count = c0 + (float)before;
+    for (int i0 = 0; i0 < nt; i0 += 8) {
+        int f[8], e[8];
+        float x[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int4 f4 = *(const int4 *)&fl[i0 + 4 * h], e4 = *(const int4 *)&ex[i0 + 4 * h];
+            f[4 * h] = f4.x; f[4 * h + 1] = f4.y; f[4 * h + 2] = f4.z; f[4 * h + 3] = f4.w;
+            e[4 * h] = e4.x; e[4 * h + 1] = e4.y; e[4 * h + 2] = e4.z; e[4 * h + 3] = e4.w;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = i0 + u < nt ? a.merged[(int64_t)(t0 + i0 + u) * a.latent + jj] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if ((f[u] & 1) && on) a.slot0[(int64_t)e[u] * a.latent + j] = merged ? sum / count : v0;
+            const bool m = (f[u] & 2) != 0;
+            sum = m && !merged ? c0 * v0 : sum;
+            merged = merged || m;
+            sum += x[u];   // zeros where the step merges nothing
+            count = m ? count + 1.0f : count;
         }
     }
-    a.slot0_final[j] = v;
 }
 
 // grid (rows, heads), 64 threads
@@ -578,10 +680,19 @@ int launch_light_residual(hipStream_t s, float *hidden, const float *o, const fl
 
 int launch_light_slot0(hipStream_t s, const LightRowsArgs &a) {
     MR_REQUIRE(a.lat && a.arena && a.slot0 && a.slot0_final && a.flags && a.extra_index && a.merge_count &&
-                   a.merge_row && a.rows > 0 && a.latent > 0 && a.cap > 0,
+                   a.merge_row && a.merged && a.row0_ws && a.rows > 0 && a.latent > 0 && a.cap > 0,
                "latent rows: bad arguments");
-    k_light_slot0<<<ceil_div(a.latent, 256), 256, 0, s>>>(a);
-    MR_LAUNCHED("enqueue latent row 0 recurrence");
+    const int nseg = ceil_div(a.rows, kRow0Seg), slices = ceil_div(a.latent, kWave);
+    float *seg_sum = a.row0_ws, *first_count = seg_sum + (size_t)nseg * a.latent;
+    int *seg_cnt = (int *)(first_count + 4), *seg_start = seg_cnt + nseg;
+    k_light_gather_merged<<<a.rows, kWave, 0, s>>>(a);
+    MR_LAUNCHED("enqueue merged-row gather");
+    k_row0_segments<<<dim3(nseg, slices), kWave, 0, s>>>(a, seg_sum, seg_cnt);
+    MR_LAUNCHED("enqueue row 0 segment sums");
+    k_row0_starts<<<slices, kWave, 0, s>>>(a, seg_sum, seg_cnt, nseg, first_count, seg_start);
+    MR_LAUNCHED("enqueue row 0 segment starts");
+    k_row0_steps<<<dim3(nseg, slices), kWave, 0, s>>>(a, seg_sum, seg_start, first_count);
+    MR_LAUNCHED("enqueue row 0 steps");
     return MR_OK;
 }
 
