@@ -1517,7 +1517,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.light_cap);
     const bool gqa = !heavy;   // with flashlighting-2.0
-    w->kv16_rows = gqa ? rows + max_cap : 0;
+    w->kv16_rows = gqa ? ceil_div(rows + max_cap, 32) * 32 : 0;   // whole 32-row tiles
     const size_t kv16 = gqa ? (size_t)w->kv16_rows * kvw * 2 : 0;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
     const Piece pieces[] = {

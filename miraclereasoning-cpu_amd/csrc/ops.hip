@@ -360,7 +360,7 @@ int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_
     a.inv_root = 1.0f / sqrtf((float)d); a.window = window;
     void *ws = nullptr;
     if (presplit) {
-        const int n = rows + std::min(p0, (window ? window : cap) - 1);
+        const int n = ceil_div(rows + std::min(p0, (window ? window : cap) - 1), 32) * 32;   // whole 32-row tiles
         const size_t planes = (size_t)4 * n * kv_heads * d * sizeof(_Float16);
         MR_HIP(hipMalloc(&ws, planes + 4 * kv_heads * sizeof(float)), "debug prefill attention workspace");
         a.kv16 = (_Float16 *)ws;

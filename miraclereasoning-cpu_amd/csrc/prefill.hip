@@ -30,7 +30,6 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, const f32x4 &c) {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -243,8 +242,8 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill(PrefillAttnArgs a
 // (the keys whose weights the group's lanes hold); runs of 4 keys stay runs.
 __device__ __forceinline__ int vslot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
 
-template <int D, bool P>
-__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb, int first) {
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs a, int gb) {
     constexpr int NC = D / 32;            // 32-dim chunks (QK contraction steps)
     constexpr int ND = D / 16;            // 16-dim output tiles
     constexpr int KP = D + 8;             // LDS pitch of key rows (halves; rows stay 16-byte aligned)
@@ -312,33 +311,6 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
     const int kg = tid / (D / 4), c4 = (tid % (D / 4)) * 4;
     const int kv = tid % (kKeys / NL), v4 = (tid / (kKeys / NL)) * 4;
     float4 kr[NL], vr[NL];
-    u32x2 kq[NL][2], vq[NL][2];   // P: the keys' and values' FP16 terms (hi, lo) at dims c4 .. + 3
-    // P: the four planes as buffers of the attended rows first .. khi; a
-    // thread's byte offsets are fixed, a tile adds its first row, and a key
-    // past khi addresses past the buffer's end, where the bounds check
-    // returns zeros.
-    const int64_t plane = (int64_t)a.kv16_rows * kvw;
-    const int nbytes = P ? (khi - first + 1) * kvw * 2 : 0;
-    auto plane_rsrc = [&](int t) {
-        return __builtin_amdgcn_make_buffer_rsrc((void *)(a.kv16 + t * plane), (short)0, nbytes, 0x00020000);
-    };
-    const __amdgpu_buffer_rsrc_t rk0 = plane_rsrc(0), rk1 = plane_rsrc(1), rv0 = plane_rsrc(2), rv1 = plane_rsrc(3);
-    unsigned ko[NL], vo[NL];
-#pragma unroll
-    for (int u = 0; u < NL; ++u) {
-        ko[u] = (unsigned)(((NL * kg + u) * kvw + kh * D + c4) * 2);
-        vo[u] = (unsigned)(((NL * kv + u) * kvw + kh * D + v4) * 2);
-    }
-    auto fetch_p = [&](int kb) {
-        const unsigned rel = (unsigned)((kb - first) * kvw * 2);
-#pragma unroll
-        for (int u = 0; u < NL; ++u) {
-            kq[u][0] = __builtin_amdgcn_raw_buffer_load_b64(rk0, ko[u] + rel, 0, 0);
-            kq[u][1] = __builtin_amdgcn_raw_buffer_load_b64(rk1, ko[u] + rel, 0, 0);
-            vq[u][0] = __builtin_amdgcn_raw_buffer_load_b64(rv0, vo[u] + rel, 0, 0);
-            vq[u][1] = __builtin_amdgcn_raw_buffer_load_b64(rv1, vo[u] + rel, 0, 0);
-        }
-    };
     auto fetch = [&](int kb) {
         const int kb_slot = kb < a.p0 ? kb % a.cap : 0;   // ring slot of the tile's first key (uniform)
 #pragma unroll
@@ -422,52 +394,19 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
         }
     };
 
-    // P: the terms as split once per chunk; the values go in transposed.
-    auto stash_p = [&]() {
-#pragma unroll
-        for (int u = 0; u < NL; ++u)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) *(u32x2 *)&ks[t][(NL * kg + u) * KP + c4] = kq[u][t];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                _Float16 x[NL];
-#pragma unroll
-                for (int u = 0; u < NL; ++u) {
-                    const unsigned w = i < 2 ? vq[u][t].x : vq[u][t].y;
-                    x[u] = __builtin_bit_cast(_Float16, (unsigned short)(w >> (16 * (i & 1))));
-                }
-                const int at = (v4 + i) * VP + vslot(NL * kv);
-                if constexpr (NL == 4) *(f16x4 *)&vt[t][at] = f16x4{x[0], x[1], x[2], x[3]};
-                else if constexpr (NL == 2) *(f16x2 *)&vt[t][at] = f16x2{x[0], x[1]};
-                else vt[t][at] = x[0];
-            }
-    };
-
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 o[ND];
 #pragma unroll
     for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     float sk = 1.0f, sv = 1.0f;
-    if constexpr (P) {
-        sk = a.kv16_scale[kh];
-        sv = a.kv16_scale[a.kv_heads + kh];
-        fetch_p(klo);
-    } else {
-        fetch(klo);
-    }
+    fetch(klo);
     for (int it = 0; it < ntiles; ++it) {
         const int kb = klo + it * kKeys;
         if (it) lds_barrier();
-        if constexpr (P) stash_p();
-        else stash(sk, sv);
+        stash(sk, sv);
         lds_barrier();
-        if (it + 1 < ntiles) {
-            if constexpr (P) fetch_p(kb + kKeys);
-            else fetch(kb + kKeys);
-        }
+        if (it + 1 < ntiles) fetch(kb + kKeys);
 
         f32x4 sc[2];
 #pragma unroll
@@ -530,29 +469,238 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_h(PrefillAttnArgs
             // the lane group's 8 slots, stored in contraction order by the stash
             const int row = (t * 16 + lr) * VP + 8 * lq;
             const f16x8 vh = *(const f16x8 *)&vt[0][row], vl = *(const f16x8 *)&vt[1][row];
-            if constexpr (P) {   // one value scale for the chunk: undone at the end
-                o[t] *= alpha;
-                o[t] = mfma16(vl, ph, o[t]);
-                o[t] = mfma16(vh, pl, o[t]);
-                o[t] = mfma16(vh, ph, o[t]);
-            } else {
-                f32x4 pv = mfma16(vl, ph, f32x4{0.f, 0.f, 0.f, 0.f});
-                pv = mfma16(vh, pl, pv);
-                pv = mfma16(vh, ph, pv);
+            f32x4 pv = mfma16(vl, ph, f32x4{0.f, 0.f, 0.f, 0.f});
+            pv = mfma16(vh, pl, pv);
+            pv = mfma16(vh, ph, pv);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[t][j] = fmaf(pv[j], vun, o[t][j] * alpha);
-            }
+            for (int j = 0; j < 4; ++j) o[t][j] = fmaf(pv[j], vun, o[t][j] * alpha);
         }
-    }
-    if constexpr (P) {
-        const float vun = 1.0f / sv;
-#pragma unroll
-        for (int t = 0; t < ND; ++t) o[t] *= vun;
     }
     if (!qvalid) return;
     float wo = 1.0f, we = 0.0f;   // weights of the window's and the extra columns' partials
     const float *ext = nullptr;
     if (a.ext) {   // the extra partial (m, l, o; m in natural units) joins the softmax
+        ext = a.ext + ((int64_t)tq * a.heads + h) * (D + 4);
+        const float m_e = ext[0] * kLog2e, m = fmaxf(m_run, m_e);
+        wo = m_run == -INFINITY ? 0.0f : exp2_hw(m_run - m);
+        we = m_e == -INFINITY ? 0.0f : exp2_hw(m_e - m);
+        l_run = l_run * wo + ext[1] * we;
+    }
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+        const int dim = t * 16 + 4 * lq;
+        float4 r = make_float4(o[t][0] * wo, o[t][1] * wo, o[t][2] * wo, o[t][3] * wo);
+        if (ext) {
+            const float4 e = load_f4(ext + 4 + dim);
+            r = make_float4(r.x + e.x * we, r.y + e.y * we, r.z + e.z * we, r.w + e.w * we);
+        }
+        *(float4 *)(a.out + (int64_t)tq * a.ldo + h * D + dim) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+    }
+}
+
+// The chunk's presplit form (the kv16 planes in k_kv_split_tiles' layout):
+// the same arithmetic as k_attn_prefill_h with the keys' and values' terms
+// and scales fixed for the chunk, and the tiles copied into LDS by the
+// buffer unit (buffer_load_dwordx4 ... lds) with no register staging.  Two
+// LDS stages: after the barrier that publishes tile it, the copy of tile
+// it + 1 runs while the waves compute on tile it.  A stage is
+// [K hi | K lo | V^T hi | V^T lo], 32 x D halves each, rows unpadded (one DMA
+// instruction fills 1 KB in lane order); the 16-byte chunks of a row sit at
+// swizzled positions so that the operand reads of 8 consecutive rows fall on
+// distinct banks.
+template <int D>
+__device__ __forceinline__ int key_swizzle(int r) { return D / 8 >= 8 ? (r & 7) : ((r >> 1) & 3); }
+__device__ __forceinline__ int vt_swizzle(int r) { return (r >> 1) & 3; }   // V^T rows: 4 chunks of 8 slots
+
+// 16 bytes a lane from the buffer at voff + soff into LDS at lds + 16 lane
+// (lds wave-uniform).
+__device__ __forceinline__ void copy_to_lds16(__amdgpu_buffer_rsrc_t rs, void *lds, unsigned voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+}
+
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs a, int gb, int first) {
+    constexpr int NC = D / 32, ND = D / 16;
+    constexpr int SUB = kKeys * D;                      // halves per sub-tile
+    constexpr int NQ = 4 * SUB * 2 / 1024 / (kAttnThreads / kWave);   // 1 KB copies per wave per tile
+    static_assert(NQ >= 1 && (4 * SUB * 2) % (1024 * (kAttnThreads / kWave)) == 0, "stage split");
+    __shared__ __attribute__((aligned(16))) _Float16 st[2][4 * SUB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 / gb;
+    const int kh = blockIdx.y / sub_groups, hsub = blockIdx.y % sub_groups;
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * tile_rows;   // latest rows (most keys) first
+    const int h = kh * G + hsub * gb + wave % gb;
+    const int tq = t0 + (wave / gb) * 16 + lr;
+    const bool qvalid = tq < a.rows;
+    const int qp = a.p0 + tq;
+    const int kvw = a.kv_heads * D;
+
+    float qf[NC][8];
+    float qmax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
+        if (qvalid) {
+            const float *src = a.qkv + (int64_t)tq * a.ld + h * D + 32 * c + 8 * lq;
+            u = load_f4(src);
+            v = load_f4(src + 4);
+        }
+        const float t[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qf[c][i] = t[i];
+            qmax = fmaxf(qmax, fabsf(t[i]));
+        }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, kWave));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, kWave));
+    const float sq = f16_range_scale(qmax);
+    f16x8 qh[NC], ql[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 th, tl;
+            split2h(qf[c][i] * sq, th, tl);
+            qh[c][i] = th;
+            ql[c][i] = tl;
+        }
+
+    const int win = a.window ? a.window : a.cap;
+    const int last = min(t0 + tile_rows, a.rows) - 1;
+    const int klo = max(0, a.p0 + t0 - win + 1), khi = a.p0 + last;
+    const int j0 = (klo - first) / kKeys;               // the planes' tiles start at position first
+    const int ntiles = (khi - first) / kKeys - j0 + 1;
+
+    // Copy q of a wave (q = wave + 4 i) fills stage chunks 64 q .. 64 q + 63;
+    // lane l's chunk f = 64 q + l reads the plane chunk that belongs there.
+    // Byte offsets within tile 0; tile j adds j * 32 kvw * 2 (a K tile is 32
+    // rows of kvw halves, a V^T tile the kv heads' [dim][slot] blocks).
+    const unsigned plane = (unsigned)a.kv16_rows * (unsigned)kvw * 2u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.kv16, (short)0, (int)(4u * plane), 0x00020000);
+    unsigned voff[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int f = (wave + 4 * i) * kWave + lane, sub = f / (SUB / 8), idx = f % (SUB / 8);
+        if (sub < 2) {
+            const int r = idx / (D / 8), pos = idx % (D / 8);
+            voff[i] = sub * plane + (unsigned)((r * kvw + kh * D) * 2 + (pos ^ key_swizzle<D>(r)) * 16);
+        } else {
+            const int r = idx / 4, pos = idx % 4;
+            voff[i] = sub * plane + (unsigned)(kh * D * kKeys * 2 + r * kKeys * 2 + (pos ^ vt_swizzle(r)) * 16);
+        }
+    }
+    auto issue = [&](int j, int stage) {
+        const int soff = j * kKeys * kvw * 2;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+            copy_to_lds16(rs, &st[stage][(wave + 4 * i) * 512], voff[i], soff);
+    };
+    // the lane's operand chunks (half offsets within a stage)
+    int koff[2][NC], voffl[ND];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int r = t * 16 + lr;
+            koff[t][c] = r * D + ((4 * c + lq) ^ key_swizzle<D>(r)) * 8;
+        }
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+        const int r = t * 16 + lr;
+        voffl[t] = 2 * SUB + r * kKeys + (lq ^ vt_swizzle(r)) * 8;
+    }
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 o[ND];
+#pragma unroll
+    for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float sk = a.kv16_scale[kh], sv = a.kv16_scale[a.kv_heads + kh];
+    const float unscale = a.inv_root * kLog2e / (sq * sk);
+
+    issue(j0, 0);
+    for (int it = 0; it < ntiles; ++it) {
+        const int kb = first + (j0 + it) * kKeys;
+        const _Float16 *cur = st[it & 1];
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's copies of tile it are in LDS
+        lds_barrier();                          // every wave's are; stage (it + 1) & 1 is read
+        if (it + 1 < ntiles) issue(j0 + it + 1, (it + 1) & 1);
+
+        f32x4 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            sc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const f16x8 kl = *(const f16x8 *)&cur[SUB + koff[t][c]];
+                const f16x8 khh = *(const f16x8 *)&cur[koff[t][c]];
+                sc[t] = mfma16(kl, qh[c], sc[t]);
+                sc[t] = mfma16(khh, ql[c], sc[t]);
+                sc[t] = mfma16(khh, qh[c], sc[t]);
+            }
+        }
+        const bool full = a.hole == 0 && kb + kKeys - 1 <= a.p0 + t0 && kb > a.p0 + last - win;
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = sc[t][j] * unscale;
+                if (!full) {
+                    const int kp = kb + t * 16 + 4 * lq + j;
+                    const bool ok = qvalid & (kp <= qp) & (kp > qp - win) & ((a.hole == 0) | (kp != qp - a.hole));
+                    v = ok ? v : -INFINITY;
+                }
+                sc[t][j] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = exp2_hw(m_run - m_ref);
+        float psum = 0.0f;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p = exp2_hw(sc[t][j] - m_ref);
+                psum += p;
+                _Float16 hh, ll;
+                split2h(p, hh, ll);
+                ph[4 * t + j] = hh;
+                pl[4 * t + j] = ll;
+            }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        // o * 1 is o: the rescale only runs while some row's maximum moves
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < ND; ++t) o[t] *= alpha;
+        }
+#pragma unroll
+        for (int t = 0; t < ND; ++t) {
+            const f16x8 vh = *(const f16x8 *)&cur[voffl[t]], vl = *(const f16x8 *)&cur[SUB + voffl[t]];
+            o[t] = mfma16(vl, ph, o[t]);
+            o[t] = mfma16(vh, pl, o[t]);
+            o[t] = mfma16(vh, ph, o[t]);
+        }
+    }
+    {
+        const float vun = 1.0f / sv;
+#pragma unroll
+        for (int t = 0; t < ND; ++t) o[t] *= vun;
+    }
+    if (!qvalid) return;
+    float wo = 1.0f, we = 0.0f;
+    const float *ext = nullptr;
+    if (a.ext) {
         ext = a.ext + ((int64_t)tq * a.heads + h) * (D + 4);
         const float m_e = ext[0] * kLog2e, m = fmaxf(m_run, m_e);
         wo = m_run == -INFINITY ? 0.0f : exp2_hw(m_run - m);
@@ -604,40 +752,60 @@ __global__ void k_kv_max(PrefillAttnArgs a, int first, int n) {
     }
 }
 
-// The same positions split into FP16 terms with the per-head scales:
-// kv16 planes [K hi, K lo, V hi, V lo][n][kv_heads d]; block 0 also stores
-// the scales for the attention kernel.
-__global__ void k_kv_split(PrefillAttnArgs a, int first, int n) {
-    const int kvw = a.kv_heads * a.d, qd = a.heads * a.d, c4 = 4 * threadIdx.x;
-    const int p = first + blockIdx.x;
-    if (c4 >= kvw) return;
-    const int head = c4 / a.d;
+// The same positions split into FP16 terms with the per-head scales, as the
+// kv16 planes [K hi, K lo, V hi, V lo] in 32-row tiles from position first
+// (kv16_rows x kv_heads d halves each): a K tile is its 32 rows as they are;
+// a V tile holds each KV head's block transposed, [head][dim][slot], the key
+// at row k of the tile in slot vslot(k).  Rows at first + n and beyond are
+// zeros.  Grid (tiles, kv_heads), 256 threads; block (0, head) also stores
+// the head's scales for the attention kernel.
+template <int D>
+__global__ void __launch_bounds__(256) k_kv_split_tiles(PrefillAttnArgs a, int first, int n) {
+    constexpr int PER = kKeys * D / 4 / 256;   // float4 of K (and of V) per thread
+    static_assert(PER >= 1 && kKeys * D / 4 % 256 == 0, "tile split");
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * kKeys];
+    const int kvw = a.kv_heads * D, qd = a.heads * D, head = blockIdx.y, j = blockIdx.x;
     const float sk = f16_range_scale(__uint_as_float(a.kv16_max[head]));
     const float sv = f16_range_scale(__uint_as_float(a.kv16_max[a.kv_heads + head]));
-    if (blockIdx.x == 0 && c4 % a.d == 0) {
+    if (j == 0 && threadIdx.x == 0) {
         a.kv16_scale[head] = sk;
         a.kv16_scale[a.kv_heads + head] = sv;
     }
-    const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
-    const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
-    const float4 x = load_f4(k + c4), y = load_f4(v + c4);
-    const float xs[4] = {x.x * sk, x.y * sk, x.z * sk, x.w * sk}, ys[4] = {y.x * sv, y.y * sv, y.z * sv, y.w * sv};
-    f16x4 kh4, kl4, vh4, vl4;
+    const int64_t plane = (int64_t)a.kv16_rows * kvw;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        _Float16 h, l;
-        split2h(xs[i], h, l);
-        kh4[i] = h;
-        kl4[i] = l;
-        split2h(ys[i], h, l);
-        vh4[i] = h;
-        vl4[i] = l;
+    for (int u = 0; u < PER; ++u) {
+        const int e = threadIdx.x + 256 * u, r = e / (D / 4), c4 = (e % (D / 4)) * 4;
+        const int p = first + j * kKeys + r;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+        if (p < first + n) {
+            const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
+            const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
+            x = load_f4(k + head * D + c4);
+            y = load_f4(v + head * D + c4);
+        }
+        const float xs[4] = {x.x * sk, x.y * sk, x.z * sk, x.w * sk}, ys[4] = {y.x * sv, y.y * sv, y.z * sv, y.w * sv};
+        f16x4 kh4, kl4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            _Float16 hi, lo;
+            split2h(xs[i], hi, lo);
+            kh4[i] = hi;
+            kl4[i] = lo;
+            split2h(ys[i], hi, lo);
+            vt[0][(c4 + i) * kKeys + vslot(r)] = hi;
+            vt[1][(c4 + i) * kKeys + vslot(r)] = lo;
+        }
+        const int64_t at = (int64_t)(j * kKeys + r) * kvw + head * D + c4;
+        *(f16x4 *)(a.kv16 + at) = kh4;
+        *(f16x4 *)(a.kv16 + plane + at) = kl4;
     }
-    const int64_t plane = (int64_t)a.kv16_rows * kvw, at = (int64_t)blockIdx.x * kvw + c4;
-    *(f16x4 *)(a.kv16 + at) = kh4;
-    *(f16x4 *)(a.kv16 + plane + at) = kl4;
-    *(f16x4 *)(a.kv16 + 2 * plane + at) = vh4;
-    *(f16x4 *)(a.kv16 + 3 * plane + at) = vl4;
+    __syncthreads();
+    constexpr int CH = D * kKeys / 8;   // 16-byte chunks of a V^T block
+    const int64_t vbase = (int64_t)j * kKeys * kvw + (int64_t)head * D * kKeys;
+    for (int e = threadIdx.x; e < 2 * CH; e += 256) {
+        const int t = e / CH, c = e % CH;
+        *(f16x8 *)(a.kv16 + (2 + t) * plane + vbase + c * 8) = *(const f16x8 *)&vt[t][c * 8];
+    }
 }
 
 __global__ void __launch_bounds__(256) k_rms_rows(const float *x, int ldx, const float *gain, float eps, int width,
@@ -906,22 +1074,27 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     const int win = a.window ? a.window : a.cap;
     const int first = std::max(0, a.p0 - win + 1), n = a.p0 + a.rows - first;
     const bool h = a.d == 128 || a.d == 64 || a.d == 32;
-    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n <= a.kv16_rows && a.kv_heads * a.d <= 4096;
+    const int n_tiles = ceil_div(n, kKeys);
+    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n_tiles * kKeys <= a.kv16_rows &&
+                        a.kv_heads * a.d <= 4096 && (int64_t)4 * a.kv16_rows * a.kv_heads * a.d * 2 < ((int64_t)1 << 31);
     if (planes) {   // split the attended keys and values once
         MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
         const int threads = ceil_div(a.kv_heads * a.d / 4, kWave) * kWave;
         k_kv_max<<<ceil_div(n, kMaxRows), threads, 0, s>>>(a, first, n);
-        k_kv_split<<<n, threads, 0, s>>>(a, first, n);
+        const dim3 tiles(n_tiles, a.kv_heads);
+        if (a.d == 128) k_kv_split_tiles<128><<<tiles, 256, 0, s>>>(a, first, n);
+        else if (a.d == 64) k_kv_split_tiles<64><<<tiles, 256, 0, s>>>(a, first, n);
+        else k_kv_split_tiles<32><<<tiles, 256, 0, s>>>(a, first, n);
     }
     if (a.d == 128) {
-        if (planes) k_attn_prefill_h<128, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
-        else k_attn_prefill_h<128, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes) k_attn_prefill_t<128><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d == 64) {
-        if (planes) k_attn_prefill_h<64, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
-        else k_attn_prefill_h<64, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes) k_attn_prefill_t<64><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d == 32) {
-        if (planes) k_attn_prefill_h<32, true><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
-        else k_attn_prefill_h<32, false><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes) k_attn_prefill_t<32><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        else k_attn_prefill_h<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 32) k_attn_prefill<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 64) k_attn_prefill<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
