@@ -530,8 +530,15 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lq = lane >> 4;
     const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 / gb;
-    const int kh = blockIdx.y / sub_groups, hsub = blockIdx.y % sub_groups;
-    const int t0 = (gridDim.x - 1 - blockIdx.x) * tile_rows;   // latest rows (most keys) first
+    // Workgroups go to the 8 XCDs in turn (linear id mod 8), each XCD with its
+    // own L2.  Neighbouring row blocks of a head read the same key tiles a
+    // couple of iterations apart, so XCD x takes the x-th eighth of the
+    // (head, row block) order, row blocks fastest.
+    const int nwg = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int wg = nwg % 8 == 0 ? (lin % 8) * (nwg / 8) + lin / 8 : lin;
+    const int rb = wg % gridDim.x, by = wg / gridDim.x;
+    const int kh = by / sub_groups, hsub = by % sub_groups;
+    const int t0 = (gridDim.x - 1 - rb) * tile_rows;   // latest rows (most keys) first
     const int h = kh * G + hsub * gb + wave % gb;
     const int tq = t0 + (wave / gb) * 16 + lr;
     const bool qvalid = tq < a.rows;
