@@ -519,7 +519,7 @@ __device__ __forceinline__ void copy_to_lds16(__amdgpu_buffer_rsrc_t rs, void *l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
 }
 
-template <int D>
+template <int D, int R>
 __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs a, int gb, int first) {
     constexpr int NC = D / 32, ND = D / 16;
     constexpr int SUB = kKeys * D;                      // halves per sub-tile
@@ -529,7 +529,9 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lq = lane >> 4;
-    const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 / gb;
+    // A wave takes R sets of 16 query rows: every key and value operand read
+    // from LDS feeds R products.
+    const int G = a.heads / a.kv_heads, sub_groups = G / gb, tile_rows = 64 * R / gb;
     // Workgroups go to the 8 XCDs in turn (linear id mod 8), each XCD with its
     // own L2.  Neighbouring row blocks of a head read the same key tiles a
     // couple of iterations apart, so XCD x takes the x-th eighth of the
@@ -540,41 +542,52 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
     const int kh = by / sub_groups, hsub = by % sub_groups;
     const int t0 = (gridDim.x - 1 - rb) * tile_rows;   // latest rows (most keys) first
     const int h = kh * G + hsub * gb + wave % gb;
-    const int tq = t0 + (wave / gb) * 16 + lr;
-    const bool qvalid = tq < a.rows;
-    const int qp = a.p0 + tq;
+    int tq[R], qp[R];
+    bool qvalid[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        tq[r] = t0 + (wave / gb) * 16 * R + 16 * r + lr;
+        qvalid[r] = tq[r] < a.rows;
+        qp[r] = a.p0 + tq[r];
+    }
     const int kvw = a.kv_heads * D;
 
-    float qf[NC][8];
-    float qmax = 0.0f;
+    // The lane's query dims 32 c + 8 lq .. + 7 per row set, scaled by the
+    // row's power of two.
+    f16x8 qh[R][NC], ql[R][NC];
+    float sq[R];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
-        if (qvalid) {
-            const float *src = a.qkv + (int64_t)tq * a.ld + h * D + 32 * c + 8 * lq;
-            u = load_f4(src);
-            v = load_f4(src + 4);
-        }
-        const float t[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    for (int r = 0; r < R; ++r) {
+        float qf[NC][8];
+        float qmax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            qf[c][i] = t[i];
-            qmax = fmaxf(qmax, fabsf(t[i]));
+        for (int c = 0; c < NC; ++c) {
+            float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
+            if (qvalid[r]) {
+                const float *src = a.qkv + (int64_t)tq[r] * a.ld + h * D + 32 * c + 8 * lq;
+                u = load_f4(src);
+                v = load_f4(src + 4);
+            }
+            const float t[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                qf[c][i] = t[i];
+                qmax = fmaxf(qmax, fabsf(t[i]));
+            }
         }
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 16, kWave));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, kWave));
+        sq[r] = f16_range_scale(qmax);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                _Float16 th, tl;
+                split2h(qf[c][i] * sq[r], th, tl);
+                qh[r][c][i] = th;
+                ql[r][c][i] = tl;
+            }
     }
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, kWave));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, kWave));
-    const float sq = f16_range_scale(qmax);
-    f16x8 qh[NC], ql[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            _Float16 th, tl;
-            split2h(qf[c][i] * sq, th, tl);
-            qh[c][i] = th;
-            ql[c][i] = tl;
-        }
 
     const int win = a.window ? a.window : a.cap;
     const int last = min(t0 + tile_rows, a.rows) - 1;
@@ -603,8 +616,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
     auto issue = [&](int j, int stage) {
         const int soff = j * kKeys * kvw * 2;
 #pragma unroll
-        for (int i = 0; i < NQ; ++i)
-            copy_to_lds16(rs, &st[stage][(wave + 4 * i) * 512], voff[i], soff);
+        for (int i = 0; i < NQ; ++i) copy_to_lds16(rs, &st[stage][(wave + 4 * i) * 512], voff[i], soff);
     };
     // the lane's operand chunks (half offsets within a stage)
     int koff[2][NC], voffl[ND];
@@ -621,12 +633,17 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
         voffl[t] = 2 * SUB + r * kKeys + (lq ^ vt_swizzle(r)) * 8;
     }
 
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x4 o[ND];
-#pragma unroll
-    for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[R], l_run[R], unscale[R];
+    f32x4 o[R][ND];
     const float sk = a.kv16_scale[kh], sv = a.kv16_scale[a.kv_heads + kh];
-    const float unscale = a.inv_root * kLog2e / (sq * sk);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
+        unscale[r] = a.inv_root * kLog2e / (sq[r] * sk);
+#pragma unroll
+        for (int t = 0; t < ND; ++t) o[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
     issue(j0, 0);
     for (int it = 0; it < ntiles; ++it) {
@@ -636,94 +653,111 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
         lds_barrier();                          // every wave's are; stage (it + 1) & 1 is read
         if (it + 1 < ntiles) issue(j0 + it + 1, (it + 1) & 1);
 
-        f32x4 sc[2];
+        f32x4 sc[R][2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            sc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < R; ++r) sc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const f16x8 kl = *(const f16x8 *)&cur[SUB + koff[t][c]];
                 const f16x8 khh = *(const f16x8 *)&cur[koff[t][c]];
-                sc[t] = mfma16(kl, qh[c], sc[t]);
-                sc[t] = mfma16(khh, ql[c], sc[t]);
-                sc[t] = mfma16(khh, qh[c], sc[t]);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    sc[r][t] = mfma16(kl, qh[r][c], sc[r][t]);
+                    sc[r][t] = mfma16(khh, ql[r][c], sc[r][t]);
+                    sc[r][t] = mfma16(khh, qh[r][c], sc[r][t]);
+                }
             }
         }
         const bool full = a.hole == 0 && kb + kKeys - 1 <= a.p0 + t0 && kb > a.p0 + last - win;
-        float tmax = -INFINITY;
+        f16x8 ph[R], pl[R];
+        bool moved = false;
+        float alpha[R];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int r = 0; r < R; ++r) {
+            float tmax = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v = sc[t][j] * unscale;
-                if (!full) {
-                    const int kp = kb + t * 16 + 4 * lq + j;
-                    const bool ok = qvalid & (kp <= qp) & (kp > qp - win) & ((a.hole == 0) | (kp != qp - a.hole));
-                    v = ok ? v : -INFINITY;
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float v = sc[r][t][j] * unscale[r];
+                    if (!full) {
+                        const int kp = kb + t * 16 + 4 * lq + j;
+                        const bool ok = qvalid[r] & (kp <= qp[r]) & (kp > qp[r] - win) &
+                                        ((a.hole == 0) | (kp != qp[r] - a.hole));
+                        v = ok ? v : -INFINITY;
+                    }
+                    sc[r][t][j] = v;
+                    tmax = fmaxf(tmax, v);
                 }
-                sc[t][j] = v;
-                tmax = fmaxf(tmax, v);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2_hw(m_run - m_ref);
-        float psum = 0.0f;
-        f16x8 ph, pl;
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+            const float m_new = fmaxf(m_run[r], tmax);
+            const float m_ref = m_new == -INFINITY ? 0.0f : m_new;
+            alpha[r] = exp2_hw(m_run[r] - m_ref);
+            moved |= alpha[r] != 1.0f;
+            float psum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float p = exp2_hw(sc[t][j] - m_ref);
-                psum += p;
-                _Float16 hh, ll;
-                split2h(p, hh, ll);
-                ph[4 * t + j] = hh;
-                pl[4 * t + j] = ll;
-            }
-        psum += __shfl_xor(psum, 16, kWave);
-        psum += __shfl_xor(psum, 32, kWave);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
+                for (int j = 0; j < 4; ++j) {
+                    const float p = exp2_hw(sc[r][t][j] - m_ref);
+                    psum += p;
+                    _Float16 hh, ll;
+                    split2h(p, hh, ll);
+                    ph[r][4 * t + j] = hh;
+                    pl[r][4 * t + j] = ll;
+                }
+            psum += __shfl_xor(psum, 16, kWave);
+            psum += __shfl_xor(psum, 32, kWave);
+            l_run[r] = l_run[r] * alpha[r] + psum;
+            m_run[r] = m_new;
+        }
         // o * 1 is o: the rescale only runs while some row's maximum moves
-        if (__any(alpha != 1.0f)) {
+        if (__any(moved)) {
 #pragma unroll
-            for (int t = 0; t < ND; ++t) o[t] *= alpha;
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < ND; ++t) o[r][t] *= alpha[r];
         }
 #pragma unroll
         for (int t = 0; t < ND; ++t) {
             const f16x8 vh = *(const f16x8 *)&cur[voffl[t]], vl = *(const f16x8 *)&cur[SUB + voffl[t]];
-            o[t] = mfma16(vl, ph, o[t]);
-            o[t] = mfma16(vh, pl, o[t]);
-            o[t] = mfma16(vh, ph, o[t]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                o[r][t] = mfma16(vl, ph[r], o[r][t]);
+                o[r][t] = mfma16(vh, pl[r], o[r][t]);
+                o[r][t] = mfma16(vh, ph[r], o[r][t]);
+            }
         }
     }
-    {
-        const float vun = 1.0f / sv;
+    const float vun = 1.0f / sv;
 #pragma unroll
-        for (int t = 0; t < ND; ++t) o[t] *= vun;
-    }
-    if (!qvalid) return;
-    float wo = 1.0f, we = 0.0f;
-    const float *ext = nullptr;
-    if (a.ext) {
-        ext = a.ext + ((int64_t)tq * a.heads + h) * (D + 4);
-        const float m_e = ext[0] * kLog2e, m = fmaxf(m_run, m_e);
-        wo = m_run == -INFINITY ? 0.0f : exp2_hw(m_run - m);
-        we = m_e == -INFINITY ? 0.0f : exp2_hw(m_e - m);
-        l_run = l_run * wo + ext[1] * we;
-    }
-    const float inv = 1.0f / l_run;
-#pragma unroll
-    for (int t = 0; t < ND; ++t) {
-        const int dim = t * 16 + 4 * lq;
-        float4 r = make_float4(o[t][0] * wo, o[t][1] * wo, o[t][2] * wo, o[t][3] * wo);
-        if (ext) {
-            const float4 e = load_f4(ext + 4 + dim);
-            r = make_float4(r.x + e.x * we, r.y + e.y * we, r.z + e.z * we, r.w + e.w * we);
+    for (int r = 0; r < R; ++r) {
+        if (!qvalid[r]) continue;
+        float wo = 1.0f, we = 0.0f;
+        const float *ext = nullptr;
+        float l = l_run[r];
+        if (a.ext) {   // the extra partial (m, l, o; m in natural units) joins the softmax
+            ext = a.ext + ((int64_t)tq[r] * a.heads + h) * (D + 4);
+            const float m_e = ext[0] * kLog2e, m = fmaxf(m_run[r], m_e);
+            wo = m_run[r] == -INFINITY ? 0.0f : exp2_hw(m_run[r] - m);
+            we = m_e == -INFINITY ? 0.0f : exp2_hw(m_e - m);
+            l = l * wo + ext[1] * we;
         }
-        *(float4 *)(a.out + (int64_t)tq * a.ldo + h * D + dim) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int t = 0; t < ND; ++t) {
+            const int dim = t * 16 + 4 * lq;
+            const f32x4 ov = o[r][t] * vun;
+            float4 x = make_float4(ov[0] * wo, ov[1] * wo, ov[2] * wo, ov[3] * wo);
+            if (ext) {
+                const float4 e = load_f4(ext + 4 + dim);
+                x = make_float4(x.x + e.x * we, x.y + e.y * we, x.z + e.z * we, x.w + e.w * we);
+            }
+            *(float4 *)(a.out + (int64_t)tq[r] * a.ldo + h * D + dim) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+        }
     }
 }
 
@@ -1093,14 +1127,25 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
         else if (a.d == 64) k_kv_split_tiles<64><<<tiles, 256, 0, s>>>(a, first, n);
         else k_kv_split_tiles<32><<<tiles, 256, 0, s>>>(a, first, n);
     }
+    // Two row sets a wave where that still leaves two workgroups per CU and
+    // the rows' key counts are about even (at most a quarter of the rows see
+    // less than a whole window) or the grid still fills the CUs twice; a
+    // causal chunk keeps the twice as many one-set workgroups, latest rows
+    // first, so that the short ones fill in behind the long ones.
+    const dim3 grid2(ceil_div(a.rows, 128 / gb), a.kv_heads * (G / gb));
+    const int wg2 = grid2.x * grid2.y;
+    const bool two = wg2 >= 512 && (wg2 >= 1024 || (int64_t)(win - a.p0) * 4 <= a.rows);
     if (a.d == 128) {
-        if (planes) k_attn_prefill_t<128><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes && two) k_attn_prefill_t<128, 2><<<grid2, kAttnThreads, 0, s>>>(a, gb, first);
+        else if (planes) k_attn_prefill_t<128, 1><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
         else k_attn_prefill_h<128><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d == 64) {
-        if (planes) k_attn_prefill_t<64><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes && two) k_attn_prefill_t<64, 2><<<grid2, kAttnThreads, 0, s>>>(a, gb, first);
+        else if (planes) k_attn_prefill_t<64, 1><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
         else k_attn_prefill_h<64><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d == 32) {
-        if (planes) k_attn_prefill_t<32><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
+        if (planes && two) k_attn_prefill_t<32, 2><<<grid2, kAttnThreads, 0, s>>>(a, gb, first);
+        else if (planes) k_attn_prefill_t<32, 1><<<grid, kAttnThreads, 0, s>>>(a, gb, first);
         else k_attn_prefill_h<32><<<grid, kAttnThreads, 0, s>>>(a, gb);
     } else if (a.d <= 16) k_attn_prefill<16><<<grid, kAttnThreads, 0, s>>>(a, gb);
     else if (a.d <= 32) k_attn_prefill<32><<<grid, kAttnThreads, 0, s>>>(a, gb);

@@ -266,3 +266,36 @@ def test_prefill_attention_term_scaling(backend, dim, presplit):
             want = (w / w.sum()) @ vals[:, kv]
             bound = 2e-5 * np.abs(vals[:, kv]).max()
             assert np.all(np.abs(got[t, h] - want) <= bound), (t, h, np.abs(got[t, h] - want).max() / bound)
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128])
+def test_prefill_attention_wide_chunk(backend, dim):
+    """The presplit attention on a chunk wide enough for its two-row-set form
+    (each wave two sets of 16 query rows; taken at 512 workgroups or more):
+    2048 rows from position 300, 32 query heads over 8 kv heads, a 256-key
+    window reaching into the ring, against float64.  Bound per element: 2e-5
+    max |v| of the kv head."""
+    b, rng = backend, np.random.default_rng(100 + dim)
+    heads, kvh, rows, p0, win = 32, 8, 2048, 300, 256
+    cap = win
+    chunk = rng.normal(size=(rows, heads + 2 * kvh, dim)).astype(np.float32)
+    old = rng.normal(size=(cap, heads + 2 * kvh, dim)).astype(np.float32)
+    ring_k = old[:, heads:heads + kvh].reshape(cap, kvh * dim)
+    ring_v = old[:, heads + kvh:].reshape(cap, kvh * dim)
+    got = b.read(b.debug_prefill_attention(b.upload(chunk.reshape(rows, -1)), b.upload(ring_k), b.upload(ring_v),
+                                           p0=p0, heads=heads, kv_heads=kvh, dim=dim, window=win, presplit=True))
+    got = got.reshape(rows, heads, dim).astype(np.float64)
+    first = p0 - win + 1
+    pos = np.arange(first, p0 + rows)
+    src = np.stack([old[q % cap] if q < p0 else chunk[q - p0] for q in pos]).astype(np.float64)
+    qpos = p0 + np.arange(rows)
+    seen = (pos[None, :] <= qpos[:, None]) & (pos[None, :] > qpos[:, None] - win)
+    for h in range(heads):
+        kv = h // (heads // kvh)
+        s = chunk[:, h].astype(np.float64) @ src[:, heads + kv].T / np.sqrt(dim)
+        s = np.where(seen, s, -np.inf)
+        w = np.exp(s - s.max(axis=1, keepdims=True))
+        want = (w / w.sum(axis=1, keepdims=True)) @ src[:, heads + kvh + kv]
+        bound = 2e-5 * np.abs(src[:, heads + kvh + kv]).max()
+        err = np.abs(got[:, h] - want)
+        assert np.all(err <= bound), (h, err.max() / bound)
