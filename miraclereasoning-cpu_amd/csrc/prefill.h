@@ -23,9 +23,11 @@ struct PrefillAttnArgs {
     const float *ext = nullptr;     // [rows][heads][d + 4]: m, l, 2 unused, o[d] of extra columns, merged at the end
     // Optional workspace (head dims 32/64/128): the keys and values of the
     // positions the chunk attends to, split once into FP16 terms (4 planes of
-    // kv16_rows x kv_heads*d halves) with per-KV-head scales (kv16_scale,
-    // 2 kv_heads floats; kv16_max, 2 kv_heads words); without it (or with too
-    // few rows) every workgroup splits its tiles itself.
+    // kv16_rows x kv_heads*d halves, in 32-row tiles from the first attended
+    // position, so kv16_rows covers the attended rows rounded up to 32) with
+    // per-KV-head scales (kv16_scale, 2 kv_heads floats; kv16_max, 2 kv_heads
+    // words); without it (or with too few rows) every workgroup splits its
+    // tiles itself.
     _Float16 *kv16 = nullptr;
     int kv16_rows = 0;
     float *kv16_scale = nullptr;
