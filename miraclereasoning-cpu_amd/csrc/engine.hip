@@ -1516,9 +1516,11 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     int max_cap = 0;
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.capacity);
     for (const Layer &L : m->layers) max_cap = std::max(max_cap, L.light_cap);
-    const bool gqa = !heavy;   // with flashlighting-2.0
-    w->kv16_rows = gqa ? ceil_div(rows + max_cap, 32) * 32 : 0;   // whole 32-row tiles
-    const size_t kv16 = gqa ? (size_t)w->kv16_rows * kvw * 2 : 0;   // 4 planes of halves, in floats
+    // the attended keys and values in FP16 terms, whole 32-row tiles: heavy-medium's window
+    // attention sees the window, the others up to the ring
+    const int attend = heavy && d.window > 0 ? d.window : max_cap;
+    w->kv16_rows = ceil_div(rows + attend, 32) * 32;
+    const size_t kv16 = (size_t)w->kv16_rows * kvw * 2;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
     const Piece pieces[] = {
         {(void **)&w->x, r * h}, {(void **)&w->xn, r * h}, {(void **)&w->qkv, r * (qd + 2 * kvw)},
@@ -1541,8 +1543,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
         {(void **)&w->rowscale, split_rows},
         {(void **)&w->planes, split_rows * std::max({h, qd, (size_t)d.ffn_dim})},
-        {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, gqa ? 2 * kvw : 0},
-        {(void **)&w->kv16_max, gqa ? 2 * kvw : 0}};
+        {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, 2 * kvw}, {(void **)&w->kv16_max, 2 * kvw}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
     size_t total = 0;
     for (const Piece &pc : pieces) total += up(pc.floats);
@@ -1800,6 +1801,7 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         a.window = d.window; a.ext = w.ext;
         a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
         a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
+        a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
         MR_TRY(launch_prefill_attention(s, a));
         GemmArgs o;   // hidden += step_scale * Wo . attended
         o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
