@@ -1489,6 +1489,8 @@ struct PrefillWs {
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
     float *cbr_scores = nullptr, *cbr_pooled = nullptr, *cbr_anchor = nullptr, *cbr_kv = nullptr;   // flashnano-1.6
     float *router_part = nullptr;   // heavy-medium-2.0: the router GEMM's K slices
+    float *xn_scale = nullptr;      // heavy-medium-2.0: the normalized rows' FP16 terms, split once
+    _Float16 *xn_planes = nullptr;
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
@@ -1530,6 +1532,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->sums, heavy ? r * 2 * kvw : 0}, {(void **)&w->router, heavy ? r * (d.router_groups + groups) : 0},
         {(void **)&w->mw, r * kmax}, {(void **)&w->xg, heavy ? r * slots * h : 0},
         {(void **)&w->router_part, heavy ? r * kRouterSlices * (d.router_groups + groups) : 0},
+        {(void **)&w->xn_scale, heavy ? r : 0}, {(void **)&w->xn_planes, heavy ? r * h : 0},
         {(void **)&w->y, heavy ? r * slots * h : 0}, {(void **)&w->ids, r * kmax}, {(void **)&w->active, heavy ? r : 0},
         {(void **)&w->counts, groups}, {(void **)&w->offsets, groups}, {(void **)&w->fill, groups},
         {(void **)&w->map, r * kmax},
@@ -1828,16 +1831,23 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         e.shared_scale = d.heavy_shared_scale; e.scale = d.heavy_step_scale;
         mr_.rows = T; mr_.p0 = p0;
         mr_.counts = w.counts; mr_.offsets = w.offsets; mr_.fill = w.fill; mr_.map = w.map; mr_.xg = w.xg;
+        const bool f16 = L.expert_tab_h != nullptr;   // FP16 terms: the experts' copies and scales
+        const int rows = T * (kmax + S);   // the gathered rows' capacity (routed slots, then shared)
+        // FP16 terms: the T rows split once and their terms gathered, not the gathered rows split
+        const bool gsplit = f16 && h % 8 == 0 && w.xn_planes;
+        if (gsplit) {
+            MR_TRY(launch_row_split(s, w.xn, h, T, h, w.xn_scale, w.xn_planes));
+            mr_.x_scale = w.xn_scale; mr_.x_planes = w.xn_planes;
+            mr_.xg_scale = w.rowscale; mr_.xg_planes = w.planes; mr_.capacity = rows;
+        }
         MR_TRY(launch_moe_route_rows(s, mr_));
         GemmGroups gg;
         gg.offset = w.offsets; gg.count = w.counts; gg.groups = groups; gg.max_rows = T;
         gg.w = L.expert_tab; gg.w2 = L.expert_tab + groups;
-        const bool f16 = L.expert_tab_h != nullptr;   // FP16 terms: the experts' copies and scales
         if (f16) { gg.wh = L.expert_tab_h; gg.wh2 = L.expert_tab_h + groups; gg.wscale = L.expert_scale; }
-        const int rows = T * (kmax + S);   // the gathered rows' capacity (routed slots, then shared)
         GemmArgs gu;
         gu.a = w.xg; gu.lda = h; gu.dtype = e.dtype; gu.c = w.act; gu.ldc = ffn; gu.n = ffn; gu.k = h;
-        gu.m = rows; gu.ascale = w.rowscale; gu.ahl_ws = w.planes;
+        gu.m = rows; gu.ascale = w.rowscale; gu.ahl_ws = w.planes; gu.a_split = gsplit;
         MR_TRY(launch_gemm_grouped(s, GEMM_SWIGLU, gu, gg));
         gg.w = L.expert_tab + 2 * groups;
         gg.w2 = nullptr;

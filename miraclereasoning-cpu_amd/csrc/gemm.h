@@ -51,6 +51,10 @@ struct GemmArgs {
 // Requires k % 8 == 0, lda % 4 == 0 and 16-byte aligned a and weight rows.
 int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g);
 
+// A's FP16 terms as the FP16-term GEMMs take them (a_split): row r's scale
+// 2^t into scale[r], a[r][k] 2^t = hi + lo into planes [hi: m x k | lo: m x k].
+int launch_row_split(hipStream_t s, const float *a, int lda, int m, int k, float *scale, _Float16 *planes);
+
 // c = A . W^T (BF16-term scheme, no FP16 weights) with K cut into `slices`
 // runs of whole k-steps, each its own workgroups' partial product in `part`
 // (slices x m x n floats), then summed slice by slice in order: for a few

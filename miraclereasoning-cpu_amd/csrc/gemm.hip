@@ -648,7 +648,7 @@ int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroup
                    "grouped gemm: FP16 terms need the rows to split, their workspaces and the weights' scales");
         GemmArgs h = g;
         h.ahl = g.ahl_ws;
-        k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        if (!g.a_split) k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
         const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
                          (int64_t)g.n * g.k * 2 < (1ll << 31);
@@ -745,6 +745,13 @@ int launch_gemm_split(hipStream_t s, const GemmArgs &g, int slices, float *part)
     MR_LAUNCHED("enqueue split MFMA GEMM");
     k_sum_slices<<<(int)(((int64_t)g.m * g.n + 255) / 256), 256, 0, s>>>(part, n_slices, g.m, g.n, g.n, g.c, g.ldc);
     MR_LAUNCHED("enqueue split GEMM sum");
+    return MR_OK;
+}
+
+int launch_row_split(hipStream_t s, const float *a, int lda, int m, int k, float *scale, _Float16 *planes) {
+    MR_REQUIRE(a && scale && planes && m > 0 && k > 0 && k % 4 == 0 && lda % 4 == 0, "row split: bad arguments");
+    k_row_split<<<ceil_div(m, 4), 256, 0, s>>>(a, lda, m, k, scale, planes);
+    MR_LAUNCHED("enqueue row split");
     return MR_OK;
 }
 

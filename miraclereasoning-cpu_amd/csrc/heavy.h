@@ -112,6 +112,16 @@ struct MoeRowsArgs {
     int *counts = nullptr, *offsets = nullptr, *fill = nullptr;   // [experts + shared]
     int *map = nullptr;              // [rows][kmax]
     float *xg = nullptr;             // [rows (kmax + shared)][h]
+    // FP16 terms (h a multiple of 8): the rows' scales and planes from
+    // launch_row_split over `rows` rows, gathered into the grouped GEMM's
+    // workspace (planes [hi | lo] of capacity rows, one scale a row) in place
+    // of xg: a row's split depends on the row alone, so the gathered split is
+    // the split of the gathered rows.
+    const float *x_scale = nullptr;
+    const _Float16 *x_planes = nullptr;
+    float *xg_scale = nullptr;
+    _Float16 *xg_planes = nullptr;
+    int capacity = 0;
 };
 int launch_moe_route_rows(hipStream_t s, const MoeRowsArgs &m);
 // x[row] += scale * (sum of the routed experts' outputs by weight in chosen

@@ -1042,6 +1042,20 @@ __global__ void __launch_bounds__(256) k_moe_gather(MoeRowsArgs m) {
         dst[threadIdx.x - kmax + active] = m.offsets[E + threadIdx.x - kmax] + t;
     }
     __syncthreads();
+    if (m.x_planes) {
+        const uint4 *hi = (const uint4 *)(m.x_planes + (int64_t)t * h);
+        const uint4 *lo = (const uint4 *)(m.x_planes + ((int64_t)m.rows + t) * h);
+        for (int i = 0; i < active + S; ++i) {
+            const int64_t row = dst[i];
+            if (threadIdx.x == 0) m.xg_scale[row] = m.x_scale[t];
+            uint4 *yh = (uint4 *)(m.xg_planes + row * h), *yl = (uint4 *)(m.xg_planes + ((int64_t)m.capacity + row) * h);
+            for (int j = threadIdx.x; j < h / 8; j += 256) {
+                yh[j] = hi[j];
+                yl[j] = lo[j];
+            }
+        }
+        return;
+    }
     const float *x = m.a.x + (int64_t)t * h;
     for (int i = 0; i < active + S; ++i) {
         float *y = m.xg + (int64_t)dst[i] * h;
