@@ -1891,7 +1891,18 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
     lt.n = lat;
     f16(lt, L.qkv, qd);
+    // the Q projection left the normalized rows' FP16 terms in the workspace when it took them:
+    // the latent rows and the FFN branch (the same input) reuse them before anything else splits
+    const bool xn_split = q.dtype == MR_BF16 && q.wscale > 0.0f;
+    lt.a_split = xn_split;
     MR_TRY(launch_gemm(s, GEMM_STORE, lt));
+    GemmArgs gu;   // the FFN branch reads the same normalized input
+    gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
+    gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
+    f16(gu, L.ffn.gate);
+    gu.wh2 = L.ffn.up.f16;
+    gu.a_split = xn_split && gu.dtype == MR_BF16 && gu.wscale > 0.0f;
+    MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     MR_TRY(launch_rms_rows(s, w.lat, lat, L.latent_norm.f(), d.norm_eps, lat, w.lat, lat, T));
     GemmArgs kv;   // [Wk; Wv] . latent beside the queries
     kv.a = w.lat; kv.lda = lat; kv.w = L.kv_up.ptr; kv.dtype = L.kv_up.dtype; kv.c = w.qkv + qd; kv.ldc = ld;
@@ -1928,12 +1939,6 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.obuf; o.ldc = h; o.m = T; o.n = h; o.k = qd;
     f16(o, L.o);
     MR_TRY(launch_gemm(s, GEMM_STORE, o));
-    GemmArgs gu;   // the FFN branch reads the same normalized input
-    gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;
-    gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
-    f16(gu, L.ffn.gate);
-    gu.wh2 = L.ffn.up.f16;
-    MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.fbuf; dn.ldc = h;
     dn.m = T; dn.n = h; dn.k = ffn;
