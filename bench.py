@@ -278,8 +278,10 @@ def main():
                     help="after the prefill, trace this many persistent decode steps phase by phase, print the "
                          "per-phase anatomy (markdown) and exit")
     ap.add_argument("--trace-dump", metavar="NPY", default=None,
-                    help="with --trace-steps: also save the raw timestamps [steps, phases, workgroups, (entry, "
-                         "input staged, exit)] in µs")
+                    help="with --trace-steps: also save the raw timestamps [steps, phases, workgroups, 5] in µs: "
+                         "GEMV phases (entry, input staged, last stream wave stored, first stream wave stored, "
+                         "unused); attention phases (entry, Q/K/V cells staged, end, partial stored, a merging "
+                         "unit's first partial cells seen)")
     args = ap.parse_args()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace, args.steps)

@@ -712,12 +712,22 @@ void step_attention_mergers(const AttnStepArgs &a, int grid, unsigned *mask) {
     const int splits = a.splits, hg = a.head_groups, pairs = a.kv_heads * splits, units = pairs * hg;
     if (units > grid || grid > kSkipBits) return;
     const bool xcd_map = hg > 1 && pairs % kXcds == 0;
+    unsigned m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int mergers = 0;
     for (int u = 0; u < units; ++u) {
         const int pair = xcd_map ? u % kXcds + kXcds * (u / kXcds / hg) : u / hg;
         const int hs = xcd_map ? (u / kXcds) % hg : u % hg;
         const int kh = pair / splits, split = pair % splits;
-        if (split == merger_split(kh * hg + hs, splits)) mask[u >> 5] |= 1u << (u & 31);
+        if (split == merger_split(kh * hg + hs, splits)) {
+            m[u >> 5] |= 1u << (u & 31);
+            ++mergers;
+        }
     }
+    // Mergers on every workgroup (one split per group and as many groups as
+    // workgroups) would leave the next phase no workers (wg_rows divides its
+    // rows among the workgroups it does not skip): skip none then.
+    if (mergers >= grid) return;
+    for (int i = 0; i < 8; ++i) mask[i] |= m[i];
 }
 
 int step_attention_splits(int max_total, int kv_heads, int dim, int cus) {

@@ -141,14 +141,21 @@ _shut_down = False
 
 
 def close_all():
-    """Release every live model and context now (also run at interpreter exit)."""
-    global _shut_down
+    """Release every live model and context now.  Backends, models and
+    tensors made afterwards work and are released as usual."""
     for backend in list(_backends):
         backend.close()
+
+
+def _at_exit():
+    # The interpreter is ending: release everything, then make the finalizers
+    # that still run during module teardown do nothing.
+    global _shut_down
+    close_all()
     _shut_down = True
 
 
-atexit.register(close_all)
+atexit.register(_at_exit)
 
 
 def _check(code, operation):

@@ -355,7 +355,11 @@ class OracleModel:
         rest = np.setdiff1d(np.arange(E), dev)
         if rest.size:
             gap = min(gap, float(pd[-1] - probs[rest].max()))                  # the cut
-        width_ok = width == active or abs(raw - math.floor(raw) - 0.5) <= self.NEAR_TIE * max(1.0, abs(raw))
+        # a rounding near-tie moves the width only to the other rounding of raw
+        # (floor or floor + 1 around the .5 boundary, clipped like the width)
+        near = abs(raw - math.floor(raw) - 0.5) <= self.NEAR_TIE * max(1.0, abs(raw))
+        roundings = {int(np.clip(kmin + math.floor(raw) + d, kmin, kmax)) for d in (0, 1)}
+        width_ok = width == active or (near and width in roundings)
         if gap >= -tol and width_ok:
             tail = [e for e in np.argsort(-probs, kind="stable") if e not in set(dev.tolist())]
             self.adopted.append(event + (gap,))

@@ -3,6 +3,7 @@
 Run in the build container only (the reference is not present anywhere else):
 
     python tests/golden/make_golden.py [/root/reference]
+    python tests/golden/make_golden.py names     # only native_names.json
 
 It imports the reference package ``miracle_reasoning`` from the given tree and
 drives its own ``MiracleModel`` (model.py), ``ModelConfig`` (config.py) and
@@ -173,11 +174,42 @@ def native_configs():
     }
 
 
+def native_name_cases():
+    """Micro bundles of every family, tied and untied, with and without Q/K
+    norms: the switches the native checkpoint names depend on."""
+    cases = {}
+    for f in sorted(presets.MICRO):
+        for tied in (True, False):
+            for qk in (True, False):
+                cases[f"{f}-{'tied' if tied else 'untied'}-{'qk' if qk else 'noqk'}"] = dict(
+                    presets.micro(f), tie_embeddings=tied, qk_norm=qk)
+    return cases
+
+
+def write_native_names(ref):
+    """native_names.json: the reference's own native checkpoint name table
+    (weights.py:145-208) for each case of native_name_cases()."""
+    from miracle_reasoning.weights import native_names
+    out = {}
+    for name, bundle in native_name_cases().items():
+        try:
+            cfg = ref.ModelConfig.from_dict(bundle)
+        except ValueError:           # a family that requires Q/K norms
+            continue
+        out[name] = {"bundle": bundle, "names": native_names(cfg)}
+    (HERE / "native_names.json").write_text(json.dumps(out, indent=0, sort_keys=True))
+    print("wrote native_names.json", len(out), "cases")
+
+
 def main():
-    ref_root = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    ref_root = Path(sys.argv[1] if len(sys.argv) > 1 and sys.argv[1] != "names" else "/root/reference")
     sys.path.insert(0, str(ref_root))
     import miracle_reasoning as ref
     from miracle_reasoning.weights import expected_shapes
+
+    if "names" in sys.argv[1:]:      # only the native name table
+        write_native_names(ref)
+        return
 
     ids = list(presets.MICRO_IDS)
     variants = {}
@@ -231,6 +263,7 @@ def main():
     for name, data in native_configs().items():
         parsed[name] = {"input": data, "parsed": ref.ModelConfig.from_dict(data).to_dict()}
     (HERE / "configs.json").write_text(json.dumps(parsed, indent=1, sort_keys=True))
+    write_native_names(ref)
     print("done")
 
 

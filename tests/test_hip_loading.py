@@ -105,3 +105,51 @@ def test_native_npz_with_native_config_loads_bit_exact(backend, golden_dir, tmp_
     with MiracleModel.from_pretrained(directory, backend=backend, context_length=16) as loaded:
         assert loaded.config == config
         np.testing.assert_array_equal(loaded.prefill(ids, return_all=True), want)
+
+
+def test_exported_bundles_load_on_the_gpu(backend, tmp_path, mid):
+    """Export (reference export.py:41-80) of the flashnano-1.5 mid workload
+    from a native-name PyTorch BF16 state dict and from a native-name npz: the
+    BF16-keeping bundle loads with from_pretrained into a model whose logits
+    equal the in-memory model's bit for bit; the widened FP32 bundle (the
+    reference's own format) runs the FP32-weight kernels on the same values,
+    so its logits agree within the BF16 tolerance and its greedy stream is the
+    same.  The command line's export writes the same bundle."""
+    torch = pytest.importorskip("torch")
+    from miracle_hip.export import export_checkpoint
+    config, weights = mid
+    with MiracleModel(config, weights, backend=backend, context_length=64) as model:
+        want = model.prefill(IDS, return_all=True)
+        stream = model.generate(IDS, max_new_tokens=4)
+    names = native_names(config)
+    state = {}
+    for key, value in weights.items():
+        if isinstance(value, BF16Array):
+            state[names[key]] = torch.from_numpy(value.bits.view(np.int16)).view(torch.bfloat16)
+        else:
+            state[names[key]] = torch.from_numpy(np.asarray(value, np.float32))
+    torch.save({"model_state_dict": state}, tmp_path / "ckpt.pt")
+    (tmp_path / "config.json").write_text(json.dumps(config.to_dict()))
+    print("case export torch state dict -> BF16 bundle", flush=True)
+    assert export_checkpoint(tmp_path / "ckpt.pt", tmp_path / "config.json", tmp_path / "bf16") == config
+    assert SafeTensors(tmp_path / "bf16" / "model.safetensors").entries["layers.0.q"][1] == "BF16"
+    with MiracleModel.from_pretrained(tmp_path / "bf16", backend=backend, context_length=64) as loaded:
+        np.testing.assert_array_equal(loaded.prefill(IDS, return_all=True), want)
+        assert loaded.generate(IDS, max_new_tokens=4) == stream
+    print("case export widened FP32 bundle (command line)", flush=True)
+    assert main(["export", "--checkpoint", str(tmp_path / "ckpt.pt"), "--config", str(tmp_path / "config.json"),
+                 "--output", str(tmp_path / "f32"), "--fp32"]) == 0
+    assert SafeTensors(tmp_path / "f32" / "model.safetensors").entries["layers.0.q"][1] == "F32"
+    with MiracleModel.from_pretrained(tmp_path / "f32", backend=backend, context_length=64) as loaded:
+        np.testing.assert_allclose(loaded.prefill(IDS, return_all=True), want, rtol=1e-3, atol=1e-4)
+        assert loaded.generate(IDS, max_new_tokens=4) == stream
+    print("case export native npz (FP32 values) -> bundle", flush=True)
+    del state
+    native = tmp_path / "native"
+    native.mkdir()
+    np.savez(native / "model.npz", **{names[k]: np.asarray(v, np.float32) for k, v in weights.items()})
+    assert export_checkpoint(native / "model.npz", tmp_path / "config.json", tmp_path / "npz") == config
+    assert SafeTensors(tmp_path / "npz" / "model.safetensors").entries["layers.0.q"][1] == "F32"
+    with MiracleModel.from_pretrained(tmp_path / "npz", backend=backend, context_length=64) as loaded:
+        np.testing.assert_allclose(loaded.prefill(IDS, return_all=True), want, rtol=1e-3, atol=1e-4)
+        assert loaded.generate(IDS, max_new_tokens=4) == stream

@@ -422,9 +422,8 @@ def test_weight_cache_budget_and_untied_head(backend):
 
 
 def test_close_releases_models_before_their_backend():
-    """Models may outlive or be outlived by their backend in any order (the
-    library keeps a context alive while a model uses it), and closing twice
-    is harmless."""
+    """HIPBackend.close() closes the backend's models first, then its context;
+    closing either twice is harmless, and a backend made afterwards works."""
     from miracle_hip import HIPBackend
     bundle = presets.micro("flashnano-1.7")
     cfg = ModelConfig.from_dict(bundle)
@@ -432,7 +431,8 @@ def test_close_releases_models_before_their_backend():
     b1 = HIPBackend()
     m1 = MiracleModel(cfg, weights, backend=b1, context_length=16)
     want = m1.prefill([1, 2, 3])
-    b1.close()                       # the context goes first; m1 still holds it
+    b1.close()                       # closes m1, then the context
+    assert m1.engine.handle is None
     b1.close()
     m1.close()
     m1.close()
@@ -440,3 +440,23 @@ def test_close_releases_models_before_their_backend():
     with MiracleModel(cfg, weights, backend=b2, context_length=16) as m2:
         np.testing.assert_array_equal(m2.prefill([1, 2, 3]), want)
     b2.close()
+
+
+def test_context_destroyed_under_a_live_model():
+    """Through the C ABI: mr_ctx_destroy while a model still uses the context
+    drops only the caller's reference (the model holds its own), so the model
+    keeps running, and mr_model_destroy then releases the context."""
+    from miracle_hip import HIPBackend
+    bundle = presets.micro("flashnano-1.7")
+    cfg = ModelConfig.from_dict(bundle)
+    weights = synthetic.micro_weights(bundle)
+    backend = HIPBackend()
+    model = MiracleModel(cfg, weights, backend=backend, context_length=16)
+    want = model.prefill([1, 2, 3])
+    lib = backend.lib
+    ctx, backend.ctx = backend.ctx, None      # the caller's reference, taken over here
+    assert lib.mr_ctx_destroy(ctx) == 0
+    model.reset()
+    np.testing.assert_array_equal(model.prefill([1, 2, 3]), want)   # mr_model_forward on the live model
+    handle, model.engine.handle = model.engine.handle, None
+    assert lib.mr_model_destroy(handle) == 0   # the last reference: the context goes with it

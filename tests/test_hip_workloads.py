@@ -78,17 +78,48 @@ def _workload(name, prompt):
     return _CACHE[key]
 
 
-@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("mode,prefill_mode", [("persistent", "exact"), ("graph", "exact"),
+                                               ("persistent", "batched")])
 @pytest.mark.parametrize("name,prompt", [("flashnano-1.7", 1100), ("flashnano-1.5-mid", 600)])
-def test_long_prompt_matches_oracle(backend, name, prompt, mode):
+def test_long_prompt_matches_oracle(backend, name, prompt, mode, prefill_mode):
     wl, weights, ids, want, stream = _workload(name, prompt)
-    print("case", name, prompt, mode, flush=True)
-    model = MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"])
-    model.engine.set_step_mode(mode)
-    assert model.engine.step_mode() == mode
-    got = model.prefill(ids, return_all=True)
-    np.testing.assert_allclose(got, want, **TOL)
-    assert model.generate(list(ids), max_new_tokens=6) == stream
+    print("case", name, prompt, mode, prefill_mode, flush=True)
+    with MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend, context_length=wl["context"],
+                      prefill_mode=prefill_mode) as model:
+        model.engine.set_step_mode(mode)
+        assert model.engine.step_mode() == mode
+        got = model.prefill(ids, return_all=True)
+        np.testing.assert_allclose(got, want, **TOL)
+        assert model.generate(list(ids), max_new_tokens=6) == stream
+
+
+def test_flashnano17_full_prompt_matches_oracle_fixture(backend, golden_dir):
+    """flashnano-1.7 at the bench's own positions: the whole 4096-token prompt,
+    then decoding at 4096..4099 with the 6 global layers attending over ~4100
+    keys in every key split the step runs, against the oracle's fixture
+    (tests/golden/make_workload_golden.py: last prompt row's logits, the next
+    4 positions' logits, an 8-token greedy stream).  Token-loop prefill with
+    the persistent step and with the graph step, and batched prefill then
+    persistent decode (the bench's configuration)."""
+    fx = np.load(golden_dir / "workload_flashnano-1.7-p4096.npz")
+    wl = presets.workload("flashnano-1.7")
+    prompt = int(fx["prompt"])
+    ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
+    assert int(fx["seed"]) == wl["seed"] and int(np.sum(ids, dtype=np.int64)) == int(fx["ids_sum"])
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    stream = [int(t) for t in fx["stream"]]
+    with MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend,
+                      context_length=wl["context"]) as model:
+        for mode, prefill_mode in (("persistent", "batched"), ("persistent", "exact"), ("graph", "exact")):
+            print("case flashnano-1.7 4096", mode, prefill_mode, flush=True)
+            model.reset()
+            model.prefill_mode = prefill_mode
+            model.engine.set_step_mode(mode)
+            assert model.engine.step_mode() == mode
+            np.testing.assert_allclose(model.prefill(ids), fx["last"], **TOL)
+            for i, want in enumerate(fx["decode"]):
+                np.testing.assert_allclose(model.decode(stream[i]), want, **TOL)
+            assert model.generate(list(ids), max_new_tokens=len(stream)) == stream
 
 
 @pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
@@ -101,16 +132,17 @@ def test_cbr_workload_matches_oracle(backend, prefill_mode):
         assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
-@pytest.mark.parametrize("prefill_mode", ["exact", "batched"])
-def test_heavy_workload_matches_oracle(backend, record_property, prefill_mode):
+@pytest.mark.parametrize("prompt,prefill_mode", [(640, "exact"), (640, "batched")])
+def test_heavy_workload_matches_oracle(backend, record_property, parity_note, prompt, prefill_mode):
     """The device runs first and records its choices; the oracle then follows
     them wherever they agree with its own values to within its near-tie band
     (a relative 1e-4: two exact FP32 evaluations in different summation orders
     can rank values that close either way) and logs every other disagreement
     as a mismatch.  No mismatch is allowed; each adopted near-tie is printed
-    with its gap, together with the smallest decision margins the oracle saw."""
+    with its gap, together with the smallest decision margins the oracle saw,
+    and the count goes into the session's closing summary."""
     from test_oracle_model import follow_record
-    name, prompt = "heavy-medium-2.0", 640
+    name = "heavy-medium-2.0"
     wl = presets.workload(name)
     cfg = ModelConfig.from_dict(wl["config"])
     weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
@@ -134,6 +166,9 @@ def test_heavy_workload_matches_oracle(backend, record_property, prefill_mode):
     record_property("block_score_margin", block_margin)
     record_property("router_probability_margin", router_margin)
     record_property("near_ties_adopted", len(ref.adopted))
+    parity_note(f"{name} prompt {prompt} {prefill_mode}: {len(blocks) + len(experts)} routing and block "
+                f"decisions, near-ties adopted {len(ref.adopted)}, mismatches {len(ref.mismatches)}, smallest "
+                f"block-score gap {block_margin:.2e}, smallest router probability gap {router_margin:.2e}")
     assert ref.mismatches == []
     # rare (at most one per thousand decisions), or the two paths are not the same arithmetic
     assert len(ref.adopted) <= max(4, (len(blocks) + len(experts)) // 1000), ref.adopted

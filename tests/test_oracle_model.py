@@ -307,3 +307,34 @@ def test_oracle_follow_adopts_expert_order_and_traces_its_own():
     strict = OracleModel(_FOLLOW, weights, context_length=64, follow=rec)
     np.testing.assert_array_equal(strict.prefill(ids, return_all=True), logits)
     assert [m[:4] for m in strict.mismatches] == [("experts", 0, 25, 1)]
+
+
+def test_oracle_follow_width_moves_only_to_the_other_rounding():
+    """A rounding near-tie of the adaptive width can move it by one, to the
+    other rounding of its raw value; a followed width two away, or one away on
+    the wrong side, is a mismatch even where every value counts as a near-tie."""
+    weights, ids, logits, trace, cfg = _follow_setup()
+    rec = follow_record(trace, cfg, len(ids))
+
+    def plant(at, width):
+        p, l, i = at
+        planted = follow_record(trace, cfg, len(ids))
+        own = planted[p, l, i, 1:1 + planted[p, l, i, 0]].tolist()
+        extra = [e for e in range(16) if e not in own]
+        planted[p, l, i, 0] = width
+        planted[p, l, i, 1:1 + 4] = -1
+        planted[p, l, i, 1:1 + width] = (own + extra)[:width]
+        loose = OracleModel(_FOLLOW, weights, context_length=64, follow=planted)
+        loose.NEAR_TIE = 1e3
+        loose.prefill(ids, return_all=True)
+        return [e[:4] for e in loose.adopted], [e[:4] for e in loose.mismatches]
+
+    # width kmax = 4 (raw >= 1.5): its other rounding is 3 at most, never 2
+    at = tuple(int(v) for v in np.argwhere(rec[:, :, :, 0] == 4)[0])
+    event = [("experts", at[1], at[0], at[2])]
+    assert plant(at, 2) == ([], event)
+    # width 3 (raw in [0.5, 1.5]): exactly one of 2 and 4 is the other rounding
+    at = tuple(int(v) for v in np.argwhere(rec[:, :, :, 0] == 3)[0])
+    event = [("experts", at[1], at[0], at[2])]
+    outcomes = sorted([plant(at, 2), plant(at, 4)])
+    assert outcomes == [([], event), (event, [])]

@@ -126,6 +126,17 @@ def test_native_names_resolve_every_tensor(family):
         adapt_weights(config, native)
 
 
+def test_native_names_equal_the_reference_table(golden_dir):
+    """native_names equals the reference's own table (weights.py:145-208),
+    written by tests/golden/make_golden.py for every family, tied and untied,
+    with and without Q/K norms where the family allows both."""
+    import json
+    cases = json.loads((golden_dir / "native_names.json").read_text())
+    assert {c.rsplit("-", 2)[0] for c in cases} == set(presets.MICRO)
+    for name, case in cases.items():
+        assert native_names(ModelConfig.from_dict(case["bundle"])) == case["names"], name
+
+
 def test_export_native_npz_to_bundle_and_inspect(tmp_path, capsys):
     config, weights = _tiny()
     source, output = tmp_path / "native", tmp_path / "bundle"
