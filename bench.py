@@ -203,6 +203,43 @@ def summarize_trace(path, steps):
     return 0
 
 
+def summarize_traffic(fetch_csv, write_csv, steps, prompt, commit, name=WORKLOAD):
+    """HBM bytes per persistent decode step from two rocprofv3 counter runs of
+    this bench with --traffic-probe (FETCH_SIZE, then WRITE_SIZE, in KiB per
+    dispatch): the last `steps` k_step dispatches (the timed greedy steps, at
+    positions prompt .. prompt + steps - 1), each counter scaled by what it
+    reads for the probe's copy of 268,435,456 bytes (the largest copy
+    dispatch).  Prints the JSON that bench.py reads into roofline.traffic."""
+    import csv
+
+    def read(path, counter):
+        rows = []
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        rows.sort()
+        copy = max(v for _, k, v in rows if "copyBuffer" in k)
+        step = [v for _, k, v in rows if "k_step" in k][-steps:]
+        return copy, float(np.mean(step)), len(step)
+
+    out = {"kernel": "k_step", "workload": name, "step_mode": "persistent", "commit": commit,
+           "positions": [prompt, prompt + steps - 1]}
+    total = 0.0
+    for key, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        copy_kib, step_kib, n = read(path, counter)
+        scale = 268435456 / (copy_kib * 1024)
+        out[f"copy_{key}_kib"] = round(copy_kib, 2)
+        out[f"step_{key}_kib"] = round(step_kib, 2)
+        out[f"{key}_scale"] = round(scale, 6)
+        out[f"{key}_bytes"] = int(step_kib * 1024 * scale)
+        out["dispatches"] = n
+        total += step_kib * 1024 * scale
+    out["traffic_bytes"] = int(total)
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 def trace_summary(model, cfg, steps, dump=None):
     """Per-phase anatomy of `steps` persistent decode steps (mr_model_trace_step)
     from the model's current position, as a markdown table: for each phase kind
@@ -277,6 +314,10 @@ def main():
     ap.add_argument("--trace-steps", type=int, default=0,
                     help="after the prefill, trace this many persistent decode steps phase by phase, print the "
                          "per-phase anatomy (markdown) and exit")
+    ap.add_argument("--summarize-traffic", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "COMMIT"), default=None,
+                    help="print the per-step HBM traffic JSON (profiles/k_step_<workload>_traffic.json) from two "
+                         "rocprofv3 --pmc runs of this bench with --traffic-probe (FETCH_SIZE, WRITE_SIZE) over "
+                         "the last --steps step dispatches; COMMIT names the build measured")
     ap.add_argument("--trace-dump", metavar="NPY", default=None,
                     help="with --trace-steps: also save the raw timestamps [steps, phases, workgroups, 5] in µs: "
                          "GEMV phases (entry, input staged, last stream wave stored, first stream wave stored, "
@@ -285,6 +326,10 @@ def main():
     args = ap.parse_args()
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace, args.steps)
+    if args.summarize_traffic:
+        fetch_csv, write_csv, commit = args.summarize_traffic
+        return summarize_traffic(fetch_csv, write_csv, args.steps, args.prompt or presets.workload(WORKLOAD)["prompt"],
+                                 commit)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this path has no multi-GPU "
               "sharding: bs=1 decode of one sequence runs on one GPU).", file=sys.stderr)
@@ -367,14 +412,16 @@ def main():
         # summary of this kernel and workload (FETCH_SIZE + WRITE_SIZE, scaled
         # by a copy of known size); it is not measured in this run.
         step_ms = device_ms / args.steps
-        traffic = None
+        traffic, measured = None, None
         tf = ROOT / "profiles" / f"k_step_{name}_traffic.json"
         if tf.exists():
-            traffic = json.loads(tf.read_text()).get("traffic_bytes")
+            rec = json.loads(tf.read_text())
+            traffic = rec.get("traffic_bytes")
+            measured = {k: rec.get(k) for k in ("commit", "positions")}
         roof = {"kernel": f"persistent decode step ({cfg.layers} layers + LM head + greedy choice)", "bound": "hbm",
                 "achieved": round(avg_bytes / (step_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(avg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "algorithmic_bytes": int(avg_bytes), "avg_ms": round(step_ms, 5)}
+                "traffic_measured": measured, "algorithmic_bytes": int(avg_bytes), "avg_ms": round(step_ms, 5)}
     elif not gqa:
         # heavy / latent families: the graph-captured step (many small kernels) as one unit
         step_ms = device_ms / args.steps

@@ -304,6 +304,13 @@ MR_API int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float
                                       float *out, int rows, int p0, int heads, int kv_heads, int d, int cap,
                                       int window, int presplit);
 
+/* Test hook: y[i] = 2^x[i] by the hardware exp2 the batched prefill's
+ * softmax uses (which 0; log2 e is folded into its score scale), or
+ * y[i] = e^x[i] by the expf of the token step's softmax (which 1), for device
+ * x and y of n floats.  Synchronizes.  Not a counterpart of any reference
+ * function. */
+MR_API int mr_debug_exp(mr_ctx *ctx, const float *x, float *y, int n, int which);
+
 #ifdef __cplusplus
 }
 #endif

@@ -348,6 +348,13 @@ int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *a
     return MR_OK;
 }
 
+int mr_debug_exp(mr_ctx *ctx, const float *x, float *y, int n, int which) {
+    OP_BEGIN("debug exp");
+    MR_TRY(launch_debug_exp(s, x, y, n, which));
+    MR_HIP(hipStreamSynchronize(s), "debug exp");
+    return MR_OK;
+}
+
 int mr_debug_prefill_attention(mr_ctx *ctx, const float *qkv, const float *ring_k, const float *ring_v, float *out,
                                int rows, int p0, int heads, int kv_heads, int d, int cap, int window, int presplit) {
     OP_BEGIN("debug prefill attention");

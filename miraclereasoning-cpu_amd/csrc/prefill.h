@@ -39,6 +39,9 @@ struct PrefillAttnArgs {
 // p - hole), keys before the chunk read from the ring at slot position % cap;
 // with ext, the extra columns' partial joins the softmax.
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a);
+// y[i] = 2^x[i] by the prefill attention's hardware exp2 (which 0) or
+// e^x[i] by expf (which 1), for measuring their errors.
+int launch_debug_exp(hipStream_t s, const float *x, float *y, int n, int which);
 
 // flashnano-1.6's relay rows (keys pooled from completed chunks) as the
 // attention's extra partial: ext[t][head] = (m, l, 0, 0, o[d]) over the first

@@ -1102,7 +1102,21 @@ __global__ void __launch_bounds__(256) k_relay_partial(RelayPartialArgs a, int r
     }
 }
 
+// y = 2^x by exp2_hw (which 0) or e^x by the library expf (which 1): the
+// softmax exponential of the batched prefill and the token step's.
+__global__ void __launch_bounds__(256) k_debug_exp(const float *x, float *y, int n, int which) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = which == 0 ? exp2_hw(x[i]) : expf(x[i]);
+}
+
 }  // namespace
+
+int launch_debug_exp(hipStream_t s, const float *x, float *y, int n, int which) {
+    MR_REQUIRE(x && y && n > 0 && (which == 0 || which == 1), "debug exp: bad arguments");
+    k_debug_exp<<<ceil_div(n, 256), 256, 0, s>>>(x, y, n, which);
+    MR_LAUNCHED("enqueue debug exp");
+    return MR_OK;
+}
 
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     MR_REQUIRE(a.qkv && a.ring_k && a.ring_v && a.out && a.rows > 0 && a.cap > 0, "prefill attention: bad arguments");

@@ -103,6 +103,7 @@ _SIGNATURES = {
     "mr_debug_step_timeout": [_P],
     "mr_debug_gemm": [_P, _P, _P, _P, _P, _i, _i, _i, _i],
     "mr_debug_prefill_attention": [_P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i, _i],
+    "mr_debug_exp": [_P, _P, _P, _i, _i],
 }
 
 _lib = None
@@ -418,6 +419,14 @@ class HIPBackend:
         out, ws = self.empty((m, n)), self.empty((m,))
         _check(self.lib.mr_debug_gemm(self.ctx, a.handle, weight.handle, out.handle, ws.handle, m, n, k, scheme),
                "debug gemm")
+        return out
+
+    def debug_exp(self, x, which):
+        """2^x by the prefill softmax's hardware exp2 (which 0) or e^x by the
+        token step's expf (which 1), elementwise (test hook)."""
+        self._owns(x)
+        out = self.empty(x.shape)
+        _check(self.lib.mr_debug_exp(self.ctx, x.handle, out.handle, int(np.prod(x.shape)), which), "debug exp")
         return out
 
     def debug_prefill_attention(self, qkv, ring_k, ring_v, *, p0, heads, kv_heads, dim, window=0, presplit=False):

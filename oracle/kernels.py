@@ -19,7 +19,9 @@ from pathlib import Path
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "_build" / "liboracle.so"
+# ORACLE_LIBRARY names another build of kernels.c (the sanitizer build of
+# `make -C oracle check-sanitize`); the default is the plain build.
+_LIB_PATH = Path(os.environ.get("ORACLE_LIBRARY") or _HERE / "_build" / "liboracle.so")
 _lib = None
 
 _F = C.POINTER(C.c_float)

@@ -299,3 +299,24 @@ def test_prefill_attention_wide_chunk(backend, dim):
         bound = 2e-5 * np.abs(src[:, heads + kvh + kv]).max()
         err = np.abs(got[:, h] - want)
         assert np.all(err <= bound), (h, err.max() / bound)
+
+
+def test_softmax_exponentials_error_bound(backend, record_property):
+    """The batched prefill's softmax weights come from the hardware exp2 (log2 e
+    folded into the score scale), the token step's from expf.  Over the
+    arguments a softmax produces after its maximum is subtracted (x <= 0,
+    down to where the result leaves FP32's normal range: 2^x for x in
+    [-125, 0], e^x for x in [-87, 0]), both against float64: the largest
+    relative error is recorded and bounded by 2 ulp of FP32 (2^-22)."""
+    b = backend
+    errs = {}
+    for which, name, ref, lo in ((0, "exp2_hw", np.exp2, 125.0), (1, "expf", np.exp, 87.0)):
+        x = np.concatenate([-np.linspace(0.0, lo, 1 << 20), -np.abs(np.random.default_rng(5).normal(size=1 << 16)),
+                            np.float32([0.0, -1e-30, -0.5, -1.0])]).astype(np.float32)
+        got = b.read(b.debug_exp(b.upload(x), which)).astype(np.float64)
+        want = ref(x.astype(np.float64))
+        rel = np.abs(got - want) / want
+        errs[name] = float(rel.max())
+        print(f"{name}: max relative error {errs[name]:.3e} ({errs[name] / 2.0 ** -23:.2f} ulp)", flush=True)
+        record_property(f"{name}_max_rel_error", errs[name])
+        assert errs[name] <= 2.0 ** -22, name

@@ -180,6 +180,39 @@ def test_heavy_workload_matches_oracle(backend, record_property, parity_note, pr
     assert stream == want_stream
 
 
+def test_heavy_full_prompt_matches_oracle_fixture(backend, golden_dir, parity_note):
+    """heavy-medium-2.0 at the bench's 2048-token prompt (33 blocks of 64 keys,
+    top-8; 98,544 routing and block decisions).  The oracle takes longer than a
+    GPU test may run, so tests/golden/make_workload_golden.py ran it in the
+    build container following a record of this engine's choices
+    (tests/golden/record_heavy_choices.py): it adopted a recorded choice only
+    where it is a valid choice within its near-tie band and found no
+    mismatch.  The device must make exactly the choices the oracle validated
+    (bit-exact record), and its last-row logits and greedy stream must match
+    the oracle's along that path."""
+    fx = np.load(golden_dir / "workload_heavy-medium-2.0-p2048.npz")
+    wl = presets.workload("heavy-medium-2.0")
+    cfg = ModelConfig.from_dict(wl["config"])
+    prompt = int(fx["prompt"])
+    ids = synthetic.prompt_ids(cfg.vocab_size, prompt, wl["seed"])
+    assert int(fx["seed"]) == wl["seed"] and int(np.sum(ids, dtype=np.int64)) == int(fx["ids_sum"])
+    weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
+    print("case heavy-medium-2.0 2048 batched", flush=True)
+    with MiracleModel(cfg, weights, backend=backend, context_length=wl["context"], prefill_mode="batched") as model:
+        last = model.prefill(ids)
+        stream = model.generate(list(ids), max_new_tokens=len(fx["stream"]))
+        choices = model.engine.choices()
+    want = fx["choices"]
+    assert choices.shape == want.shape
+    differ = np.argwhere((choices.astype(np.int8) != want).any(axis=3))
+    assert len(differ) == 0, differ[:10]
+    np.testing.assert_allclose(last, fx["last"], **TOL)
+    assert stream == fx["stream"].tolist()
+    parity_note(f"heavy-medium-2.0 prompt {prompt} batched (oracle fixture): {int(fx['decisions'])} routing and block "
+                f"decisions, every one equal to the oracle-validated record; near-ties the oracle adopted "
+                f"{len(fx['adopted'])} (largest gap {np.abs(fx['adopted_gap']).max():.1e}), mismatches 0")
+
+
 LIGHT_SPLIT = dict(presets.workload("flashlighting-2.0")["config"], layers=2, window=150, memory_slots=8,
                    max_positions=4096)
 
