@@ -74,8 +74,16 @@ class OracleModel:
 
     NEAR_TIE = 1e-4
 
-    def __init__(self, config, weights, context_length=None, trace=None, follow=None):
+    def __init__(self, config, weights, context_length=None, trace=None, follow=None, latent_kv_cache=False):
         cfg = config if isinstance(config, OracleConfig) else OracleConfig.from_bundle(config)
+        # FlashLighting: the reference recomputes every latent row's key and
+        # value at every step (model.py:160-163).  Row r's key and value
+        # depend only on its latent and stored position (every kernel involved
+        # computes each row on its own), so with latent_kv_cache a row keeps
+        # them from the step it was appended (or merged) on: the same bits at
+        # a fraction of the cost, for long prompts; pinned against the
+        # recomputing form by tests/test_oracle_model.py.
+        self.latent_kv_cache = latent_kv_cache
         self.cfg = cfg
         self.ctx = context_length if context_length is not None else min(2048, cfg.max_positions)
         if not 0 < self.ctx <= cfg.max_positions:
@@ -200,14 +208,37 @@ class OracleModel:
         positions = state.get("positions", []) + [self.position]
         counts = state.get("counts", []) + [1.0]
         key_pos = np.asarray(positions, np.float32)
-        key = self._rope(self._rms(K.linear(rows, self.w[p + "k"]), p + "k_norm", c.head_dim), key_pos, c.kv_heads)
-        value = K.linear(rows, self.w[p + "v"])
+
+        def kv(r, at):
+            return (self._rope(self._rms(K.linear(r, self.w[p + "k"]), p + "k_norm", c.head_dim), at, c.kv_heads),
+                    K.linear(r, self.w[p + "v"]))
+
+        if self.latent_kv_cache:
+            # rows [lo, hi) of two buffers hold the cached keys and values in
+            # row order; rows leave at the front and arrive at the back, and the
+            # live rows move to the front when the back is reached
+            if old is None:
+                cap = 2 * (c.window + c.memory_slots + 2)
+                state.update(kbuf=np.zeros((cap, c.kv_heads * c.head_dim), np.float32),
+                             vbuf=np.zeros((cap, c.kv_heads * c.head_dim), np.float32), lo=0, hi=0)
+            kb, vb = state["kbuf"], state["vbuf"]
+            if state["hi"] == kb.shape[0]:
+                n = state["hi"] - state["lo"]
+                kb[:n], vb[:n] = kb[state["lo"]:state["hi"]].copy(), vb[state["lo"]:state["hi"]].copy()
+                state.update(lo=0, hi=n)
+            kb[state["hi"]], vb[state["hi"]] = (a.reshape(-1) for a in kv(latent, key_pos[-1:]))
+            state["hi"] += 1
+            key, value = kb[state["lo"]:state["hi"]], vb[state["lo"]:state["hi"]]
+        else:
+            key, value = kv(rows, key_pos)
         s = K.scores(q, key, None, c.query_heads, c.kv_heads, c.head_dim, n1, 0, n1, 0)
         K.latent_mask(s, key_pos, c.query_heads, n1, state.get("memory_size", 0), self.position - c.window + 1)
         attended = K.mix(K.softmax(s), value, None, c.query_heads, c.kv_heads, c.head_dim, n1, 0, n1, 0)
         overflow = max(0, n1 - c.window)
         if c.memory_slots == 0 and overflow:
             rows, positions, counts, memory = rows[overflow:], positions[overflow:], counts[overflow:], 0
+            if self.latent_kv_cache:
+                state["lo"] += overflow
         elif overflow > c.memory_slots:
             a, b = np.float32(counts[0]), np.float32(counts[1])
             merged = K.merge_rows(rows[:2], c.latent_dim, float(a), float(b))
@@ -216,6 +247,10 @@ class OracleModel:
             positions = [int(np.rint(centre))] + positions[2:]
             counts = [float(a + b)] + counts[2:]
             memory = c.memory_slots
+            if self.latent_kv_cache:   # rows 0 and 1 become the merged row at its rounded position
+                k0, v0 = kv(np.ascontiguousarray(merged[None, :]), np.asarray(positions[:1], np.float32))
+                state["lo"] += 1
+                state["kbuf"][state["lo"]], state["vbuf"][state["lo"]] = k0.reshape(-1), v0.reshape(-1)
         else:
             memory = overflow
         state.update(latent=np.ascontiguousarray(rows), positions=positions, counts=counts, memory_size=memory)

@@ -93,29 +93,42 @@ def test_long_prompt_matches_oracle(backend, name, prompt, mode, prefill_mode):
         assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
-def test_flashnano17_full_prompt_matches_oracle_fixture(backend, golden_dir):
-    """flashnano-1.7 at the bench's own positions: the whole 4096-token prompt,
-    then decoding at 4096..4099 with the 6 global layers attending over ~4100
-    keys in every key split the step runs, against the oracle's fixture
-    (tests/golden/make_workload_golden.py: last prompt row's logits, the next
-    4 positions' logits, an 8-token greedy stream).  Token-loop prefill with
-    the persistent step and with the graph step, and batched prefill then
-    persistent decode (the bench's configuration)."""
-    fx = np.load(golden_dir / "workload_flashnano-1.7-p4096.npz")
-    wl = presets.workload("flashnano-1.7")
-    prompt = int(fx["prompt"])
+FULL_PROMPT_MODES = {
+    # (step mode, prefill mode): batched prefill + persistent decode is the bench's configuration
+    "flashnano-1.7": (("persistent", "batched"), ("persistent", "exact"), ("graph", "exact")),
+    "flashlighting-2.0": ((None, "batched"), (None, "exact")),
+}
+
+
+@pytest.mark.parametrize("name,prompt", [("flashnano-1.7", 4096), ("flashlighting-2.0", 4700)])
+def test_full_prompt_matches_oracle_fixture(backend, golden_dir, name, prompt):
+    """The decode paths at the bench's own row counts against the oracle's
+    fixtures (tests/golden/make_workload_golden.py: last prompt row's logits,
+    the next 4 positions' logits, an 8-token greedy stream).
+    flashnano-1.7: the whole 4096-token prompt, decoding at 4096..4099 with the
+    6 global layers attending over ~4100 keys in every key split the step runs;
+    token-loop prefill with the persistent step and with the graph step, and
+    batched prefill then persistent decode.
+    flashlighting-2.0: a 4700-token prompt, where its latent memory is full as
+    at the bench's positions (4096 window + 512 memory rows + the new row =
+    4609 rows in 73 key splits, a compaction every step); batched prefill and
+    the token loop, each followed by graph-step decoding."""
+    fx = np.load(golden_dir / f"workload_{name}-p{prompt}.npz")
+    wl = presets.workload(name)
+    assert int(fx["prompt"]) == prompt
     ids = synthetic.prompt_ids(wl["config"]["vocab_size"], prompt, wl["seed"])
     assert int(fx["seed"]) == wl["seed"] and int(np.sum(ids, dtype=np.int64)) == int(fx["ids_sum"])
     weights = synthetic.synthetic_weights(wl["config"], wl["seed"], wl["dtype"])
     stream = [int(t) for t in fx["stream"]]
     with MiracleModel(ModelConfig.from_dict(wl["config"]), weights, backend=backend,
                       context_length=wl["context"]) as model:
-        for mode, prefill_mode in (("persistent", "batched"), ("persistent", "exact"), ("graph", "exact")):
-            print("case flashnano-1.7 4096", mode, prefill_mode, flush=True)
+        for mode, prefill_mode in FULL_PROMPT_MODES[name]:
+            print("case", name, prompt, mode, prefill_mode, flush=True)
             model.reset()
             model.prefill_mode = prefill_mode
-            model.engine.set_step_mode(mode)
-            assert model.engine.step_mode() == mode
+            if mode is not None:
+                model.engine.set_step_mode(mode)
+                assert model.engine.step_mode() == mode
             np.testing.assert_allclose(model.prefill(ids), fx["last"], **TOL)
             for i, want in enumerate(fx["decode"]):
                 np.testing.assert_allclose(model.decode(stream[i]), want, **TOL)

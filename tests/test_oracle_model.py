@@ -338,3 +338,23 @@ def test_oracle_follow_width_moves_only_to_the_other_rounding():
     event = [("experts", at[1], at[0], at[2])]
     outcomes = sorted([plant(at, 2), plant(at, 4)])
     assert outcomes == [([], event), (event, [])]
+
+
+@pytest.mark.parametrize("slots", [2, 0])
+def test_oracle_latent_kv_cache_equals_recompute(slots):
+    """The oracle's per-row latent K/V cache (each row's key and value kept
+    from the step it was appended or merged on) gives the same bits as the
+    reference's recompute-every-row form (model.py:160-163), through merges
+    into the memory slots (slots 2) and through drops (slots 0), on BF16 and
+    FP32 weights."""
+    bundle = dict(presets.micro("flashlighting-2.0"), memory_slots=slots)
+    ids = [(7 * i + 3) % 32 for i in range(24)]
+    for weights in (synthetic.micro_weights(bundle),
+                    {k: (v.bits if hasattr(v, "bits") else v)
+                     for k, v in synthetic.synthetic_weights(bundle, 9, "bf16").items()}):
+        plain = OracleModel(bundle, weights, context_length=32)
+        cached = OracleModel(bundle, weights, context_length=32, latent_kv_cache=True)
+        want = plain.prefill(ids, return_all=True)
+        np.testing.assert_array_equal(cached.prefill(ids, return_all=True), want)
+        np.testing.assert_array_equal(cached.decode(5), plain.decode(5))
+        assert [len(s["positions"]) for s in cached.layers] == [len(s["positions"]) for s in plain.layers]
