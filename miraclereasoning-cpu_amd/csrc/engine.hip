@@ -72,14 +72,37 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *logits, int n, int
     float best = -INFINITY;
     int idx = n;
     bool nonfinite = false;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = logits[i];
+    auto consider = [&](float v, int i) {
         if (!isfinite(v)) nonfinite = true;
         if (v > best || (v == best && i < idx)) {
             best = v;
             idx = i;
         }
+    };
+    // 16-byte loads, eight per thread issued together before any compare (a
+    // load at a time made the pass 31 dependent round trips); the choice is
+    // the largest value, lowest index among equals, in any visiting order.
+    constexpr int U = 8;
+    const int n4 = ((uintptr_t)logits & 15) == 0 ? n / 4 : 0;
+    for (int base = threadIdx.x; base < n4; base += blockDim.x * U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i4 = base + u * (int)blockDim.x;
+            v[u] = i4 < n4 ? *(const float4 *)(logits + 4 * i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i4 = base + u * (int)blockDim.x;
+            if (i4 < n4) {
+                consider(v[u].x, 4 * i4);
+                consider(v[u].y, 4 * i4 + 1);
+                consider(v[u].z, 4 * i4 + 2);
+                consider(v[u].w, 4 * i4 + 3);
+            }
+        }
     }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) consider(logits[i], i);
     if (nonfinite) atomicOr(&bad, 1);
     bv[threadIdx.x] = best;
     bi[threadIdx.x] = idx;
