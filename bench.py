@@ -397,6 +397,8 @@ def main():
     decode_s = time.perf_counter() - t0
     device_ms = eng.last_decode_ms()
     assert len(tokens) == args.steps + 1
+    if eng.step_mode() != step_mode:   # a failed persistent step falls back to graph mode
+        raise SystemExit(f"bench: the step mode changed from {step_mode} to {eng.step_mode()} while decoding")
     tok_s = args.steps / decode_s
     positions = range(prompt_len, prompt_len + args.steps)
     avg_bytes = float(np.mean([decode_bytes(cfg, wl["context"], p) for p in positions]))
