@@ -560,6 +560,59 @@ __global__ void __launch_bounds__(256) k_row_split(const float *a, int lda, int 
     }
 }
 
+// k_row_split with the row kept in registers (NV 16-byte vectors per lane,
+// k <= 256 NV): every load of the row in flight at once and the row read
+// once; the same maximum (an exact operation in any order), scale and planes.
+template <int NV>
+__global__ void __launch_bounds__(256) k_row_split_reg(const float *a, int lda, int m, int k, float *scale,
+                                                       _Float16 *hl) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float *r = a + (int64_t)row * lda;
+    float4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = 4 * lane + 4 * kWave * i;
+        v[i] = c < k ? load_f4(r + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = wave_max(mx);
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) {
+        frexpf(mx, &e);                     // mx = f 2^e, f in [0.5, 1)
+        e = min(max(14 - e, -126), 126);    // mx 2^(14 - e) in [2^13, 2^14)
+    }
+    const float sc = ldexpf(1.0f, e);
+    if (lane == 0) scale[row] = sc;
+    _Float16 *hi = hl + (int64_t)row * k, *lo = hl + (int64_t)m * k + (int64_t)row * k;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = 4 * lane + 4 * kWave * i;
+        if (c >= k) break;
+        const float x[4] = {v[i].x * sc, v[i].y * sc, v[i].z * sc, v[i].w * sc};
+        f16x4 h, l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            _Float16 th, tl;
+            split2h(x[j], th, tl);
+            h[j] = th;
+            l[j] = tl;
+        }
+        *(f16x4 *)(hi + c) = h;
+        *(f16x4 *)(lo + c) = l;
+    }
+}
+
+// A's FP16 planes and row scales (k_row_split, or its register form).
+void row_split(hipStream_t s, const float *a, int lda, int m, int k, float *scale, _Float16 *hl) {
+    if (k <= 4 * kWave * 8) k_row_split_reg<8><<<ceil_div(m, 4), 256, 0, s>>>(a, lda, m, k, scale, hl);
+    else if (k <= 4 * kWave * 24) k_row_split_reg<24><<<ceil_div(m, 4), 256, 0, s>>>(a, lda, m, k, scale, hl);
+    else k_row_split<<<ceil_div(m, 4), 256, 0, s>>>(a, lda, m, k, scale, hl);
+}
+
 __global__ void __launch_bounds__(256) k_bf16_to_f16(const uint16_t *w, int64_t count, float scale, _Float16 *dst) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
         dst[i] = (_Float16)(__uint_as_float((unsigned)w[i] << 16) * scale);
@@ -648,7 +701,7 @@ int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroup
                    "grouped gemm: FP16 terms need the rows to split, their workspaces and the weights' scales");
         GemmArgs h = g;
         h.ahl = g.ahl_ws;
-        if (!g.a_split) k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        if (!g.a_split) row_split(s, g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
         const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
                          (int64_t)g.n * g.k * 2 < (1ll << 31);
@@ -688,7 +741,7 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         h.ahl = g.ahl_ws;
         h.w = g.wh;   // 16-bit rows: the BF16 loaders read them as they are
         h.w2 = g.wh2;
-        if (!g.a_split) k_row_split<<<ceil_div(g.m, 4), 256, 0, s>>>(g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
+        if (!g.a_split) row_split(s, g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // 128 x 128 tiles (wider SwiGLU tiles, 192 or 256 columns, measured
         // slower: the accumulators leave one or two waves per SIMD)
         // the buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
@@ -750,7 +803,7 @@ int launch_gemm_split(hipStream_t s, const GemmArgs &g, int slices, float *part)
 
 int launch_row_split(hipStream_t s, const float *a, int lda, int m, int k, float *scale, _Float16 *planes) {
     MR_REQUIRE(a && scale && planes && m > 0 && k > 0 && k % 4 == 0 && lda % 4 == 0, "row split: bad arguments");
-    k_row_split<<<ceil_div(m, 4), 256, 0, s>>>(a, lda, m, k, scale, planes);
+    row_split(s, a, lda, m, k, scale, planes);
     MR_LAUNCHED("enqueue row split");
     return MR_OK;
 }

@@ -1194,12 +1194,77 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
     return MR_OK;
 }
 
+// k_rms_rows_split for rows of at most 2048 values, one wave per row and four
+// rows per workgroup, with no barrier: lane l holds the runs that threads l,
+// l + 64, l + 128 and l + 192 of the one-workgroup-per-row form hold, keeps
+// their sums of squares apart and adds their wave sums in that form's order,
+// so the scale, the planes and the row scales are the same bits.
+__global__ void __launch_bounds__(256) k_rms_rows_split_w(const float *x, int ldx, const float *gain, float eps,
+                                                          int width, float *scale, _Float16 *hl, int rows) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + (int64_t)row * ldx;
+    const int runs = width / 8;   // <= 256
+    float4 v[4][2], g[4][2];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int r = lane + 64 * w;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            v[w][t] = r < runs ? load_f4(xr + 8 * r + 4 * t) : make_float4(0.f, 0.f, 0.f, 0.f);
+            g[w][t] = gain && r < runs ? load_f4(gain + 8 * r + 4 * t) : make_float4(1.f, 1.f, 1.f, 1.f);
+        }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            ss += v[w][t].x * v[w][t].x + v[w][t].y * v[w][t].y + v[w][t].z * v[w][t].z + v[w][t].w * v[w][t].w;
+        total += wave_sum(ss);
+    }
+    const float rs = 1.0f / sqrtf(total / (float)width + eps);
+    float mx = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        if (lane + 64 * w >= runs) continue;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            v[w][t] = make_float4(v[w][t].x * rs * g[w][t].x, v[w][t].y * rs * g[w][t].y, v[w][t].z * rs * g[w][t].z,
+                                  v[w][t].w * rs * g[w][t].w);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[w][t].x), fabsf(v[w][t].y)), fmaxf(fabsf(v[w][t].z), fabsf(v[w][t].w))));
+        }
+    }
+    mx = wave_max(mx);
+    const float sc = f16_range_scale(mx);
+    if (lane == 0) scale[row] = sc;
+    _Float16 *hi = hl + (int64_t)row * width, *lo = hl + (int64_t)rows * width + (int64_t)row * width;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int r = lane + 64 * w;
+        if (r >= runs) continue;
+        const float y[8] = {v[w][0].x, v[w][0].y, v[w][0].z, v[w][0].w, v[w][1].x, v[w][1].y, v[w][1].z, v[w][1].w};
+        f16x8 h, l;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 th, tl;
+            split2h(y[i] * sc, th, tl);
+            h[i] = th;
+            l[i] = tl;
+        }
+        *(f16x8 *)(hi + 8 * r) = h;
+        *(f16x8 *)(lo + 8 * r) = l;
+    }
+}
+
 int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
                           float *scale, _Float16 *planes, int rows) {
     static_assert(256 * 8 * kSplitChunks == 8192, "rms_split_fits");
     MR_REQUIRE(rms_split_fits(width) && ldx % 4 == 0,
                "row RMSNorm into FP16 terms: width must be a multiple of 8 and at most 8192");
-    k_rms_rows_split<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
+    if (width <= 2048) k_rms_rows_split_w<<<ceil_div(rows, 4), 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
+    else k_rms_rows_split<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
     MR_LAUNCHED("enqueue row RMSNorm into FP16 terms");
     return MR_OK;
 }
