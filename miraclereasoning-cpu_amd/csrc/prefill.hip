@@ -764,22 +764,35 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
 // The keys and values of positions first .. first + n - 1 (ring slot p % cap
 // before p0, chunk row p - p0 after): per-KV-head maxima of |K| and |V| into
 // mx[2][kv_heads] (bit patterns of non-negative floats, which order like the
-// values; zeroed before).  A block takes kMaxRows positions, a thread 4 dims;
-// the D / 4 threads of a head combine their maxima before one atomic each.
+// values; zeroed before).  A block takes kMaxRows positions, a thread 4 dims,
+// their loads in flight kMaxBatch positions at a time (positions past the
+// range read the last one again, which leaves a maximum as it is; more blocks
+// with fewer positions measured slower, their atomics queueing on the same
+// words); the D / 4 threads of a head combine their maxima before one atomic
+// each.
 constexpr int kMaxRows = 32;
+constexpr int kMaxBatch = 8;
 
 __global__ void k_kv_max(PrefillAttnArgs a, int first, int n) {
     const int kvw = a.kv_heads * a.d, qd = a.heads * a.d, c4 = 4 * threadIdx.x;
     const bool on = c4 < kvw;
     float mk = 0.0f, mv = 0.0f;
-    for (int i = 0; i < kMaxRows && on; ++i) {
-        const int p = first + blockIdx.x * kMaxRows + i;
-        if (p >= first + n) break;
-        const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
-        const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
-        const float4 x = load_f4(k + c4), y = load_f4(v + c4);
-        mk = fmaxf(mk, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
-        mv = fmaxf(mv, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+    for (int i0 = 0; i0 < kMaxRows && on; i0 += kMaxBatch) {
+        if (first + (int)blockIdx.x * kMaxRows + i0 >= first + n) break;
+        float4 x[kMaxBatch], y[kMaxBatch];
+#pragma unroll
+        for (int i = 0; i < kMaxBatch; ++i) {
+            const int p = min(first + (int)blockIdx.x * kMaxRows + i0 + i, first + n - 1);
+            const float *k = p >= a.p0 ? a.qkv + (int64_t)(p - a.p0) * a.ld + qd : a.ring_k + (int64_t)(p % a.cap) * kvw;
+            const float *v = p >= a.p0 ? k + kvw : a.ring_v + (int64_t)(p % a.cap) * kvw;
+            x[i] = load_f4(k + c4);
+            y[i] = load_f4(v + c4);
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxBatch; ++i) {
+            mk = fmaxf(mk, fmaxf(fmaxf(fabsf(x[i].x), fabsf(x[i].y)), fmaxf(fabsf(x[i].z), fabsf(x[i].w))));
+            mv = fmaxf(mv, fmaxf(fmaxf(fabsf(y[i].x), fabsf(y[i].y)), fmaxf(fabsf(y[i].z), fabsf(y[i].w))));
+        }
     }
     // the head's threads are a run of D / 4 <= 32 lanes starting at a multiple of D / 4
     for (int off = 1; off < a.d / 4; off <<= 1) {
@@ -954,6 +967,59 @@ __global__ void __launch_bounds__(256) k_qk_rows(float *qkv, int ld, int p0, int
         rope_rotate(u, v, cs[2 * i], cs[2 * i + 1]);
         row[j] = u;
         row[k] = v;
+    }
+}
+
+// k_qk_rows for head dims up to 128 with R rows per wave: every load of the
+// R rows (the pair of lane l, the norm's elements l and l + 64, the RoPE row)
+// in flight before any arithmetic, then each row exactly as k_qk_rows takes it.
+template <int R>
+__global__ void __launch_bounds__(256) k_qk_rows_r(float *qkv, int ld, int p0, int heads, int kv_heads, int d,
+                                                   const float *q_gain, const float *k_gain, float eps, int norm,
+                                                   const float *rope, int split_half, const int *positions,
+                                                   int rows) {
+    const int lane = threadIdx.x & 63, hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (hh >= heads + kv_heads) return;
+    const float *gain = hh < heads ? q_gain : k_gain;
+    const int half = d / 2;
+    const bool pair = lane < half;
+    const int j = split_half ? lane : 2 * lane, k = split_half ? lane + half : 2 * lane + 1;
+    float u[R], v[R], c[R], sn[R], x0[R], x1[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = blockIdx.x * R + r;
+        const bool live = row < rows;
+        const float *rp = qkv + (int64_t)(live ? row : 0) * ld + (int64_t)hh * d;
+        const int p = positions ? positions[live ? row : 0] : p0 + row;
+        const float *cs = rope + ((int64_t)p * half + lane) * 2;
+        u[r] = live && pair ? rp[j] : 0.0f;
+        v[r] = live && pair ? rp[k] : 0.0f;
+        c[r] = live && pair ? cs[0] : 1.0f;
+        sn[r] = live && pair ? cs[1] : 0.0f;
+        x0[r] = norm && live && lane < d ? rp[lane] : 0.0f;
+        x1[r] = norm && live && lane + kWave < d ? rp[lane + kWave] : 0.0f;
+    }
+    const float gj = norm && gain && pair ? gain[j] : 1.0f, gk = norm && gain && pair ? gain[k] : 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = blockIdx.x * R + r;
+        float scale = 1.0f;
+        if (norm) {
+            float ss = 0.0f;
+            if (lane < d) ss += x0[r] * x0[r];
+            if (lane + kWave < d) ss += x1[r] * x1[r];
+            scale = 1.0f / sqrtf(wave_sum(ss) / (float)d + eps);
+        }
+        if (row >= rows || !pair) continue;
+        float a = u[r], b = v[r];
+        if (norm) {
+            a = a * scale * gj;
+            b = b * scale * gk;
+        }
+        rope_rotate(a, b, c[r], sn[r]);
+        float *rp = qkv + (int64_t)row * ld + (int64_t)hh * d;
+        rp[j] = a;
+        rp[k] = b;
     }
 }
 
@@ -1271,16 +1337,24 @@ int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *g
 
 int launch_qk_rows(hipStream_t s, float *qkv, int ld, int rows, int p0, int heads, int kv_heads, int d,
                    const float *q_gain, const float *k_gain, float eps, int norm, const float *rope, int split_half) {
-    k_qk_rows<<<dim3(rows, ceil_div(heads + kv_heads, 4)), 256, 0, s>>>(qkv, ld, p0, heads, kv_heads, d, q_gain,
-                                                                       k_gain, eps, norm, rope, split_half, nullptr);
+    if (d <= 128)
+        k_qk_rows_r<8><<<dim3(ceil_div(rows, 8), ceil_div(heads + kv_heads, 4)), 256, 0, s>>>(
+            qkv, ld, p0, heads, kv_heads, d, q_gain, k_gain, eps, norm, rope, split_half, nullptr, rows);
+    else
+        k_qk_rows<<<dim3(rows, ceil_div(heads + kv_heads, 4)), 256, 0, s>>>(qkv, ld, p0, heads, kv_heads, d, q_gain,
+                                                                           k_gain, eps, norm, rope, split_half, nullptr);
     MR_LAUNCHED("enqueue q/k norm and RoPE");
     return MR_OK;
 }
 
 int launch_k_rows_at(hipStream_t s, float *k, int ld, int rows, const int *positions, int kv_heads, int d,
                      const float *k_gain, float eps, const float *rope, int split_half) {
-    k_qk_rows<<<dim3(rows, ceil_div(kv_heads, 4)), 256, 0, s>>>(k, ld, 0, 0, kv_heads, d, nullptr, k_gain, eps, 1,
-                                                               rope, split_half, positions);
+    if (d <= 128)
+        k_qk_rows_r<8><<<dim3(ceil_div(rows, 8), ceil_div(kv_heads, 4)), 256, 0, s>>>(
+            k, ld, 0, 0, kv_heads, d, nullptr, k_gain, eps, 1, rope, split_half, positions, rows);
+    else
+        k_qk_rows<<<dim3(rows, ceil_div(kv_heads, 4)), 256, 0, s>>>(k, ld, 0, 0, kv_heads, d, nullptr, k_gain, eps, 1,
+                                                                   rope, split_half, positions);
     MR_LAUNCHED("enqueue key norm and RoPE at row positions");
     return MR_OK;
 }
