@@ -384,74 +384,23 @@ __device__ __forceinline__ void load_w_h(const GemmArgs &g, int n0, int k0, u32x
     }
 }
 
-// The buffer form of the two loaders, for K a multiple of KB and matrices
-// under 2^31 bytes: a thread's byte offsets into A's planes and the weight
-// rows are computed once per tile, a k-step only moves the scalar offset,
-// and a row past M or N addresses past its buffer's end, where the bounds
-// check returns zeros (no per-load address arithmetic, no 64-bit pointers).
+// Buffer addressing for K a multiple of the k-step and matrices under 2^31
+// bytes: a thread's byte offsets into A's planes and the weight rows are
+// computed once per tile, a k-step only moves the scalar offset, and a row
+// past M or N addresses past its buffer's end, where the bounds check returns
+// zeros (no per-load address arithmetic, no 64-bit pointers).
 constexpr unsigned kPastEnd = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t half_rsrc(const void *p, int64_t halves) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(halves * 2), 0x00020000);
 }
 
-template <int NI, int KB>
-struct TileOffsets {
-    unsigned a[KB / 16];        // the rows of A (chunks t + 256 j)
-    unsigned w[NI * KB / 64];   // the weight rows (chunks t + 256 i)
-};
-
-// Weight load step i of a SwiGLU tile reads up rows (else gate rows): every
-// step covers 256 / (KB / 8) rows, inside one run of 8 NI gate or up rows.
-template <int EPI, int NI, int KB>
-__device__ __forceinline__ constexpr bool w_up(int i) {
-    constexpr int rps = kThreads / (KB / 8);
-    return EPI == GEMM_SWIGLU && (i * rps) % (16 * NI) >= 8 * NI;
-}
-
-template <int EPI, int NI, int KB>
-__device__ __forceinline__ void tile_offsets(const GemmArgs &g, int m0, int n0, TileOffsets<NI, KB> &o) {
-    constexpr int CPR = KB / 8;
-    static_assert(EPI != GEMM_SWIGLU || (8 * NI) % (kThreads / CPR) == 0, "a load step spans gate and up rows");
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < KB / 16; ++j) {
-        const int q = tid + kThreads * j, row = m0 + q / CPR;
-        o.a[j] = row < g.m ? (unsigned)(((int64_t)row * g.k + (q % CPR) * 8) * 2) : kPastEnd;
-    }
-#pragma unroll
-    for (int i = 0; i < NI * KB / 64; ++i) {
-        const int q = tid + kThreads * i, r = q / CPR;
-        int f = n0 + r;
-        if constexpr (EPI == GEMM_SWIGLU) f = n0 + (r / (16 * NI)) * 8 * NI + (r % (16 * NI)) % (8 * NI);
-        o.w[i] = f < g.n ? (unsigned)(((int64_t)f * g.k + (q % CPR) * 8) * 2) : kPastEnd;
-    }
-}
-
-template <int EPI, int NI, int KB>
-__device__ __forceinline__ void load_tile_buf(const GemmArgs &g, const TileOffsets<NI, KB> &o, int k0, AHRegs<KB> &ar,
-                                              u32x4 (&wr)[NI * KB / 64]) {
-    const int64_t mk = (int64_t)g.m * g.k, nk = (int64_t)g.n * g.k;
-    const __amdgpu_buffer_rsrc_t a0 = half_rsrc(g.ahl, mk),
-                                 a1 = half_rsrc(g.ahl + (g.plane_stride ? g.plane_stride : mk), mk);
-    const __amdgpu_buffer_rsrc_t w0 = half_rsrc(g.w, nk), w1 = half_rsrc(EPI == GEMM_SWIGLU ? g.w2 : g.w, nk);
-    const int so = k0 * 2;
-#pragma unroll
-    for (int j = 0; j < KB / 16; ++j) {
-        ar.v[0][j] = __builtin_amdgcn_raw_buffer_load_b128(a0, o.a[j], so, 0);
-        ar.v[1][j] = __builtin_amdgcn_raw_buffer_load_b128(a1, o.a[j], so, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < NI * KB / 64; ++i)
-        wr[i] = __builtin_amdgcn_raw_buffer_load_b128(w_up<EPI, NI, KB>(i) ? w1 : w0, o.w[i], so, 0);
-}
-
 // One 128 x 32 NI output tile in FP16 terms (BF16 weights, g.wscale > 0, A's
 // planes and row scales from k_row_split, the weights' FP16 copy), k-steps
-// of KB halves; each wave owns 64 x 16 NI outputs.  (Two LDS stages with one
-// barrier per k-step measured slower: the LDS per workgroup halves the
-// workgroups per CU.)
-template <int EPI, int NI, int KB, bool BUF>
+// of KB halves; each wave owns 64 x 16 NI outputs.  The operands pass through
+// registers on their way to LDS; gemm_tile_hd below is the form for K a
+// multiple of its k-step.
+template <int EPI, int NI, int KB>
 __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     constexpr int CPR = KB / 8;
     __shared__ __attribute__((aligned(16))) _Float16 as[2][kBM][KB + 8];
@@ -470,14 +419,8 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 
     AHRegs<KB> ar;
     u32x4 wr[NI * KB / 64];
-    TileOffsets<NI, KB> off;
-    if constexpr (BUF) {
-        tile_offsets<EPI, NI, KB>(g, m0, n0, off);
-        load_tile_buf<EPI, NI, KB>(g, off, 0, ar, wr);
-    } else {
-        load_a_h<KB>(g, m0, 0, ar);
-        load_w_h<EPI, NI, KB>(g, n0, 0, wr);
-    }
+    load_a_h<KB>(g, m0, 0, ar);
+    load_w_h<EPI, NI, KB>(g, n0, 0, wr);
     for (int kt = 0; kt < nk; ++kt) {
         if (kt) lds_barrier();   // every wave is done with the previous k-step's LDS
         store_a_h<KB>(as, ar);
@@ -488,12 +431,8 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
         }
         lds_barrier();
         if (kt + 1 < nk) {
-            if constexpr (BUF) {
-                load_tile_buf<EPI, NI, KB>(g, off, (kt + 1) * KB, ar, wr);
-            } else {
-                load_a_h<KB>(g, m0, (kt + 1) * KB, ar);
-                load_w_h<EPI, NI, KB>(g, n0, (kt + 1) * KB, wr);
-            }
+            load_a_h<KB>(g, m0, (kt + 1) * KB, ar);
+            load_w_h<EPI, NI, KB>(g, n0, (kt + 1) * KB, wr);
         }
 #pragma unroll
         for (int kk = 0; kk < KB / 32; ++kk) {
@@ -516,9 +455,159 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
     gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
 }
 
-template <int EPI, int NI, bool BUF>
+// gemm_tile_h with its operands copied into LDS by the buffer unit
+// (buffer_load_dwordx4 ... lds): no register staging and no LDS write
+// instructions.  A stage holds A's hi and lo planes and the weight rows of a
+// k-step of KB halves, rows unpadded (one copy fills 1 KB in lane order) with
+// the 16-byte chunks of a row at swizzled positions, so that the operand reads
+// of 16 consecutive rows fall on distinct banks.  S = 1: the next k-step is
+// copied once every wave has read the stage (other workgroups on the CU cover
+// the copy); S = 2: the copy of k-step kt + 1 runs while the waves compute kt.
+// The same MFMAs in the same order as gemm_tile_h, so the same results.
+// K a multiple of KB, every operand under 2^31 bytes.  The kernels use
+// KB = 64, S = 1 (48 KB of LDS, three workgroups per CU); two stages, or
+// KB = 32 with one or two stages, measured slower on the prefill GEMMs.
+template <int KB>
+__device__ __forceinline__ constexpr int chunk_swizzle(int r) {
+    return KB == 64 ? (r >> 1) & 7 : (r >> 2) & 3;
+}
+
+// One copy: 16 bytes a lane from byte voff + so of the buffer into LDS at
+// dst + 16 lane.  (Outside a lambda: the host pass of hipcc rejects the
+// builtin inside one whose enclosing template is instantiated twice.)
+__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, void *dst, unsigned voff, int so) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, so, 0, 0);
+}
+
+template <int EPI, int NI, int KB, int S>
+__device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) {
+    static_assert(KB == 32 || KB == 64, "k-step");
+    constexpr int CPR = KB / 8;                    // 16-byte chunks per row
+    constexpr int RPB = 1024 / (KB * 2);           // rows per 1 KB copy
+    constexpr int NR = 32 * NI;                    // weight rows of a tile
+    constexpr int BA = kBM / RPB, BW = NR / RPB;   // copies per A plane, for the weights
+    constexpr int NW = kThreads / kWave;
+    constexpr int NB = 2 * BA + BW;                // copies per stage
+    static_assert(NB % NW == 0 && (8 * NI) % RPB == 0, "a copy per wave and row run");
+    constexpr int NQ = NB / NW;                    // copies per wave per stage
+    constexpr int SA = kBM * KB;                   // halves of an A plane in a stage
+    __shared__ __attribute__((aligned(16))) _Float16 st[S][2 * SA + NR * KB];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int nk = g.k / KB;
+    const int64_t mk = (int64_t)g.m * g.k, nkw = (int64_t)g.n * g.k;
+    const __amdgpu_buffer_rsrc_t ra0 = half_rsrc(g.ahl, mk),
+                                 ra1 = half_rsrc(g.ahl + (g.plane_stride ? g.plane_stride : mk), mk);
+
+    // Copy i of this wave fills block b = wave + NW i of a stage: rows
+    // RPB b' .. of A's hi plane (b < BA), lo plane (b < 2 BA) or the weights;
+    // the lane's 16 bytes land at chunk lane % CPR of its row, so it reads the
+    // logical chunk that the swizzle puts there.  Rows past M or N read zeros.
+    unsigned voff[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int b = wave + NW * i;
+        const int rb = (b < 2 * BA ? b % BA : b - 2 * BA) * RPB + lane / CPR;
+        const int c = (lane % CPR) ^ chunk_swizzle<KB>(rb);
+        if (b < 2 * BA) {
+            const int row = m0 + rb;
+            voff[i] = row < g.m ? (unsigned)(((int64_t)row * g.k + c * 8) * 2) : kPastEnd;
+        } else {
+            int f = n0 + rb;
+            if constexpr (EPI == GEMM_SWIGLU) f = n0 + (rb / (16 * NI)) * 8 * NI + (rb % (16 * NI)) % (8 * NI);
+            voff[i] = f < g.n ? (unsigned)(((int64_t)f * g.k + c * 8) * 2) : kPastEnd;
+        }
+    }
+    // Copy i of a wave lies in A's hi plane for i < BA / NW, its lo plane
+    // below 2 BA / NW, the weights above, whatever the wave, so the A buffers
+    // are chosen at compile time; a weight copy builds its buffer from a
+    // wave-uniform base (gate or up rows).  A choice among descriptors at run
+    // time made the compiler loop over its lanes' values for every copy.
+    static_assert(BA % NW == 0, "A copies per wave");
+    const auto uniform = [](const void *p) {
+        const uint64_t v = (uint64_t)p;
+        return (const void *)(((uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)(v >> 32)) << 32) |
+                              (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane((unsigned)v));
+    };
+    const auto issue = [&](int kt, int stage) {
+        const int so = kt * KB * 2;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            const int b = wave + NW * i;
+            void *dst = &st[stage][b * 512];
+            if (i < BA / NW) {
+                copy_to_lds(ra0, dst, voff[i], so);
+            } else if (i < 2 * BA / NW) {
+                copy_to_lds(ra1, dst, voff[i], so);
+            } else {
+                const bool up = EPI == GEMM_SWIGLU && ((b - 2 * BA) * RPB) % (16 * NI) >= 8 * NI;
+                copy_to_lds(half_rsrc(uniform(up ? g.w2 : g.w), nkw), dst, voff[i], so);
+            }
+        }
+    };
+
+    f32x4 acc[4][NI];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    issue(0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int stage = S == 2 ? (kt & 1) : 0;
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's copies of k-step kt are in LDS
+        lds_barrier();                          // every wave's are (S = 2: and stage kt + 1 is read)
+        if (S == 2 && kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+        const _Float16 *ah = &st[stage][0], *al = ah + SA, *ws = ah + 2 * SA;
+#pragma unroll
+        for (int kk = 0; kk < KB / 32; ++kk) {
+            const int c = 4 * kk + lq;
+            f16x8 bf[NI];
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) {
+                const int r = wn * 16 * NI + ni * 16 + lr;
+                bf[ni] = *(const f16x8 *)(ws + r * KB + (c ^ chunk_swizzle<KB>(r)) * 8);
+            }
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int r = wm * 64 + mi * 16 + lr, off = r * KB + (c ^ chunk_swizzle<KB>(r)) * 8;
+                const f16x8 lo = *(const f16x8 *)(al + off);
+                const f16x8 hi = *(const f16x8 *)(ah + off);
+                // the smaller term first
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(lo, bf[ni], acc[mi][ni]);
+#pragma unroll
+                for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma(hi, bf[ni], acc[mi][ni]);
+            }
+        }
+        if (S == 1 && kt + 1 < nk) {
+            lds_barrier();   // every wave has read the stage
+            issue(kt + 1, 0);
+        }
+    }
+    const float inv_w = 1.0f / g.wscale;
+    gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
+}
+
+constexpr int kDmaKB = 64, kDmaStages = 1, kDmaBlocksPerCU = 3;
+
+// The FP16-term GEMMs take the LDS-copy tile when K is a multiple of its
+// k-step and every operand is under 2^31 bytes (the buffer offsets), else
+// the tile that loads through registers.
+__host__ __device__ inline bool dma_tile_fits(const GemmArgs &g) {
+    return g.k % kDmaKB == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) && (int64_t)g.n * g.k * 2 < (1ll << 31);
+}
+
+template <int EPI, int NI>
+__global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_hd(GemmArgs g) {
+    gemm_tile_hd<EPI, NI, kDmaKB, kDmaStages>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+}
+
+template <int EPI, int NI>
 __global__ void __launch_bounds__(kThreads) k_gemm_h(GemmArgs g) {
-    gemm_tile_h<EPI, NI, kKBH, BUF>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    gemm_tile_h<EPI, NI, kKBH>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 // A in FP16 terms, once per GEMM: row r's scale 2^t (max_k |a[r][k]| 2^t in
@@ -676,10 +765,10 @@ __global__ void __launch_bounds__(kThreads) k_gemm_grouped(GemmArgs g, GemmGroup
 
 // The FP16-term form: group z's rows are rows offset[z] .. of the planes and
 // row scales split for all g.m rows.
-template <int EPI, int NI, bool BUF>
-__global__ void __launch_bounds__(kThreads) k_gemm_grouped_h(GemmArgs g, GemmGroups gg) {
-    const int z = blockIdx.z, m0 = blockIdx.y * kBM, rows = gg.count[z];
-    if (m0 >= rows) return;
+template <int EPI>
+__device__ __forceinline__ bool group_args(GemmArgs &g, const GemmGroups &gg, int z, int m0) {
+    const int rows = gg.count[z];
+    if (m0 >= rows) return false;
     const int64_t first = gg.offset[z];
     g.plane_stride = (int64_t)g.m * g.k;
     g.ahl += first * g.k;
@@ -689,7 +778,21 @@ __global__ void __launch_bounds__(kThreads) k_gemm_grouped_h(GemmArgs g, GemmGro
     g.w = gg.wh[z];
     if (EPI == GEMM_SWIGLU) g.w2 = gg.wh2[z];
     g.wscale = gg.wscale[z];
-    gemm_tile_h<EPI, NI, kKBH, BUF>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    return true;
+}
+
+template <int EPI, int NI>
+__global__ void __launch_bounds__(kThreads) k_gemm_grouped_h(GemmArgs g, GemmGroups gg) {
+    const int m0 = blockIdx.y * kBM;
+    if (!group_args<EPI>(g, gg, blockIdx.z, m0)) return;
+    gemm_tile_h<EPI, NI, kKBH>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+}
+
+template <int EPI, int NI>
+__global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_grouped_hd(GemmArgs g, GemmGroups gg) {
+    const int m0 = blockIdx.y * kBM;
+    if (!group_args<EPI>(g, gg, blockIdx.z, m0)) return;
+    gemm_tile_hd<EPI, NI, kDmaKB, kDmaStages>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 template <int DT>
@@ -702,20 +805,18 @@ int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroup
         GemmArgs h = g;
         h.ahl = g.ahl_ws;
         if (!g.a_split) row_split(s, g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
-        // buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
-        const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
-                         (int64_t)g.n * g.k * 2 < (1ll << 31);
+        const bool dma = dma_tile_fits(g);
         switch (epi) {
             case GEMM_STORE: {
                 const dim3 gs(ceil_div(g.n, 32 * 4), ceil_div(gg.max_rows, kBM), gg.groups);
-                if (buf) k_gemm_grouped_h<GEMM_STORE, 4, true><<<gs, kThreads, 0, s>>>(h, gg);
-                else k_gemm_grouped_h<GEMM_STORE, 4, false><<<gs, kThreads, 0, s>>>(h, gg);
+                if (dma) k_gemm_grouped_hd<GEMM_STORE, 4><<<gs, kThreads, 0, s>>>(h, gg);
+                else k_gemm_grouped_h<GEMM_STORE, 4><<<gs, kThreads, 0, s>>>(h, gg);
                 break;
             }
             case GEMM_SWIGLU: {
                 const dim3 gs(ceil_div(g.n, 16 * kSwigluNI), ceil_div(gg.max_rows, kBM), gg.groups);
-                if (buf) k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI, true><<<gs, kThreads, 0, s>>>(h, gg);
-                else k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI, false><<<gs, kThreads, 0, s>>>(h, gg);
+                if (dma) k_gemm_grouped_hd<GEMM_SWIGLU, kSwigluNI><<<gs, kThreads, 0, s>>>(h, gg);
+                else k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI><<<gs, kThreads, 0, s>>>(h, gg);
                 break;
             }
             default: return fail(MR_ERR_INVALID, "grouped gemm: epilogue must be STORE or SWIGLU");
@@ -744,22 +845,20 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         if (!g.a_split) row_split(s, g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         // 128 x 128 tiles (wider SwiGLU tiles, 192 or 256 columns, measured
         // slower: the accumulators leave one or two waves per SIMD)
-        // the buffer loaders: K a multiple of the k-step, every operand under 2^31 bytes
-        const bool buf = g.k % kKBH == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) &&
-                         (int64_t)g.n * g.k * 2 < (1ll << 31);
+        const bool dma = dma_tile_fits(g);
         const dim3 sgrid(ceil_div(g.n, 16 * kSwigluNI), grid.y);
         switch (epi) {
             case GEMM_STORE:
-                if (buf) k_gemm_h<GEMM_STORE, 4, true><<<grid, kThreads, 0, s>>>(h);
-                else k_gemm_h<GEMM_STORE, 4, false><<<grid, kThreads, 0, s>>>(h);
+                if (dma) k_gemm_hd<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_RESIDUAL:
-                if (buf) k_gemm_h<GEMM_RESIDUAL, 4, true><<<grid, kThreads, 0, s>>>(h);
-                else k_gemm_h<GEMM_RESIDUAL, 4, false><<<grid, kThreads, 0, s>>>(h);
+                if (dma) k_gemm_hd<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_SWIGLU:
-                if (buf) k_gemm_h<GEMM_SWIGLU, kSwigluNI, true><<<sgrid, kThreads, 0, s>>>(h);
-                else k_gemm_h<GEMM_SWIGLU, kSwigluNI, false><<<sgrid, kThreads, 0, s>>>(h);
+                if (dma) k_gemm_hd<GEMM_SWIGLU, kSwigluNI><<<sgrid, kThreads, 0, s>>>(h);
+                else k_gemm_h<GEMM_SWIGLU, kSwigluNI><<<sgrid, kThreads, 0, s>>>(h);
                 break;
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
         }
