@@ -465,8 +465,10 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 // the copy); S = 2: the copy of k-step kt + 1 runs while the waves compute kt.
 // The same MFMAs in the same order as gemm_tile_h, so the same results.
 // K a multiple of KB, every operand under 2^31 bytes.  The kernels use
-// KB = 64, S = 1 (48 KB of LDS, three workgroups per CU); two stages, or
-// KB = 32 with one or two stages, measured slower on the prefill GEMMs.
+// KB = 64: S = 1 (48 KB of LDS, three workgroups per CU) where the grid has
+// more tiles than the device has CUs, S = 2 (96 KB, one workgroup per CU)
+// where it has no more; S = 2 on the large grids, and KB = 32 with one or
+// two stages, measured slower.
 template <int KB>
 __device__ __forceinline__ constexpr int chunk_swizzle(int r) {
     return KB == 64 ? (r >> 1) & 7 : (r >> 2) & 3;
@@ -591,7 +593,7 @@ __device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) 
     gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
 }
 
-constexpr int kDmaKB = 64, kDmaStages = 1, kDmaBlocksPerCU = 3;
+constexpr int kDmaKB = 64, kDmaBlocksPerCU = 3;
 
 // The FP16-term GEMMs take the LDS-copy tile when K is a multiple of its
 // k-step and every operand is under 2^31 bytes (the buffer offsets), else
@@ -600,9 +602,21 @@ __host__ __device__ inline bool dma_tile_fits(const GemmArgs &g) {
     return g.k % kDmaKB == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) && (int64_t)g.n * g.k * 2 < (1ll << 31);
 }
 
-template <int EPI, int NI>
-__global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_hd(GemmArgs g) {
-    gemm_tile_hd<EPI, NI, kDmaKB, kDmaStages>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+template <int EPI, int NI, int S>
+__global__ void __launch_bounds__(kThreads, S == 1 ? kDmaBlocksPerCU : 1) k_gemm_hd(GemmArgs g) {
+    gemm_tile_hd<EPI, NI, kDmaKB, S>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+}
+
+// Compute units of the current device, queried once per device.
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
 }
 
 template <int EPI, int NI>
@@ -792,7 +806,7 @@ template <int EPI, int NI>
 __global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_grouped_hd(GemmArgs g, GemmGroups gg) {
     const int m0 = blockIdx.y * kBM;
     if (!group_args<EPI>(g, gg, blockIdx.z, m0)) return;
-    gemm_tile_hd<EPI, NI, kDmaKB, kDmaStages>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    gemm_tile_hd<EPI, NI, kDmaKB, 1>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 template <int DT>
@@ -847,17 +861,24 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         // slower: the accumulators leave one or two waves per SIMD)
         const bool dma = dma_tile_fits(g);
         const dim3 sgrid(ceil_div(g.n, 16 * kSwigluNI), grid.y);
+        // A grid of at most one tile per CU leaves no other workgroup to
+        // cover a k-step's copy: two LDS stages overlap it with the MFMAs.
+        const int64_t tiles = (int64_t)(epi == GEMM_SWIGLU ? sgrid.x : grid.x) * grid.y;
+        const bool two = tiles <= device_cus();
         switch (epi) {
             case GEMM_STORE:
-                if (dma) k_gemm_hd<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h);
+                if (dma && two) k_gemm_hd<GEMM_STORE, 4, 2><<<grid, kThreads, 0, s>>>(h);
+                else if (dma) k_gemm_hd<GEMM_STORE, 4, 1><<<grid, kThreads, 0, s>>>(h);
                 else k_gemm_h<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_RESIDUAL:
-                if (dma) k_gemm_hd<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h);
+                if (dma && two) k_gemm_hd<GEMM_RESIDUAL, 4, 2><<<grid, kThreads, 0, s>>>(h);
+                else if (dma) k_gemm_hd<GEMM_RESIDUAL, 4, 1><<<grid, kThreads, 0, s>>>(h);
                 else k_gemm_h<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_SWIGLU:
-                if (dma) k_gemm_hd<GEMM_SWIGLU, kSwigluNI><<<sgrid, kThreads, 0, s>>>(h);
+                if (dma && two) k_gemm_hd<GEMM_SWIGLU, kSwigluNI, 2><<<sgrid, kThreads, 0, s>>>(h);
+                else if (dma) k_gemm_hd<GEMM_SWIGLU, kSwigluNI, 1><<<sgrid, kThreads, 0, s>>>(h);
                 else k_gemm_h<GEMM_SWIGLU, kSwigluNI><<<sgrid, kThreads, 0, s>>>(h);
                 break;
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");

@@ -190,17 +190,21 @@ def test_copy_bounds_and_ownership(backend):
         b.empty((0, 3))
 
 
-def test_prefill_gemm_term_schemes(backend):
+@pytest.mark.parametrize("k", [1000, 1024])
+def test_prefill_gemm_term_schemes(backend, k):
     """The batched-prefill MFMA GEMM in both term schemes against a float64
     product, on rows that stress FP16's range: ordinary values, a row far above
     FP16's maximum (6.5e4), a row of tiny values (1e-20), a zero row and a row
     mixing magnitudes 1e4 .. 1e-4; BF16 weights of magnitudes 2^-20 .. 8 with
     a few zeros.  Bound per element: 2^-20 * sum_k |a| |w| (FP32 accumulation
-    of k = 1000 products of operands carried to 2^-22 or better); the FP16
-    scheme's row and matrix scales are powers of two, so they add no error."""
+    of about 1000 products of operands carried to 2^-22 or better); the FP16
+    scheme's row and matrix scales are powers of two, so they add no error.
+    K = 1000 takes the FP16-term tile that stages its operands through
+    registers, K = 1024 the one whose operands the buffer unit copies into
+    LDS; 200 rows and 300 columns leave both with partial tiles."""
     from miracle_hip.weights import BF16Array, bf16_bits
     b, rng = backend, np.random.default_rng(21)
-    m, n, k = 200, 300, 1000
+    m, n = 200, 300
     a = rng.normal(size=(m, k)).astype(np.float32)
     a[1] *= 3.0e6
     a[2] *= 1.0e-20
