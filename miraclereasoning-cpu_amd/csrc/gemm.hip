@@ -210,12 +210,13 @@ __device__ __forceinline__ f32x4 mfma(const f16x8 &a, const f16x8 &b, const f32x
 // The epilogue of both schemes: rows m0.., columns n0.. of the tile from the
 // accumulators times `unscale` (per output row; 1 for the BF16 scheme).  A
 // wave holds NI 16-column tiles; with SwiGLU the first NI / 2 are gate
-// columns and the others the up columns of the same FFN columns.
-template <int EPI, int NI = 4, typename Unscale>
+// columns and the others the up columns of the same FFN columns.  The waves
+// of a tile are two rows of WN.
+template <int EPI, int NI = 4, int WN = 2, typename Unscale>
 __device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, const f32x4 (&acc)[4][NI],
                                            Unscale unscale) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1, lr = lane & 15;
+    const int wm = wave / WN, wn = wave % WN, lr = lane & 15;
     // C[4 (lane / 16) + j][lane % 16] of each 16 x 16 tile
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
@@ -464,11 +465,16 @@ __device__ __forceinline__ void gemm_tile_h(const GemmArgs &g, int m0, int n0) {
 // copied once every wave has read the stage (other workgroups on the CU cover
 // the copy); S = 2: the copy of k-step kt + 1 runs while the waves compute kt.
 // The same MFMAs in the same order as gemm_tile_h, so the same results.
-// K a multiple of KB, every operand under 2^31 bytes.  The kernels use
-// KB = 64: S = 1 (48 KB of LDS, three workgroups per CU) where the grid has
-// more tiles than the device has CUs, S = 2 (96 KB, one workgroup per CU)
-// where it has no more; S = 2 on the large grids, and KB = 32 with one or
-// two stages, measured slower.
+// K a multiple of KB, every operand under 2^31 bytes.  The waves are two
+// rows of WN, each with 64 x 16 NI outputs: WN = 2 gives 128 x 32 NI tiles
+// of four waves, WN = 4 128 x 64 NI tiles of eight (fewer copied bytes per
+// MFMA, since A's two planes serve twice the weight rows).  The kernels use
+// KB = 64 with S = 1 where the grid has more tiles than the device has CUs
+// (48 KB of LDS and three workgroups per CU, or 64 KB and two for WN = 4)
+// and S = 2 where it has no more.  Measured slower on the prefill GEMMs:
+// S = 2 on the large grids, KB = 32 with one or two stages, three stages of
+// KB = 32 (two workgroups per CU), and 128 x 64 tiles of four waves (four
+// workgroups per CU).
 template <int KB>
 __device__ __forceinline__ constexpr int chunk_swizzle(int r) {
     return KB == 64 ? (r >> 1) & 7 : (r >> 2) & 3;
@@ -481,14 +487,14 @@ __device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, void *dst,
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, so, 0, 0);
 }
 
-template <int EPI, int NI, int KB, int S>
+template <int EPI, int NI, int KB, int S, int WN = 2>
 __device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) {
     static_assert(KB == 32 || KB == 64, "k-step");
     constexpr int CPR = KB / 8;                    // 16-byte chunks per row
     constexpr int RPB = 1024 / (KB * 2);           // rows per 1 KB copy
-    constexpr int NR = 32 * NI;                    // weight rows of a tile
+    constexpr int NR = 16 * NI * WN;               // weight rows of a tile
     constexpr int BA = kBM / RPB, BW = NR / RPB;   // copies per A plane, for the weights
-    constexpr int NW = kThreads / kWave;
+    constexpr int NW = 2 * WN;                     // waves: two rows of WN
     constexpr int NB = 2 * BA + BW;                // copies per stage
     static_assert(NB % NW == 0 && (8 * NI) % RPB == 0, "a copy per wave and row run");
     constexpr int NQ = NB / NW;                    // copies per wave per stage
@@ -497,7 +503,7 @@ __device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) 
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 15, lq = lane >> 4;
     const int nk = g.k / KB;
     const int64_t mk = (int64_t)g.m * g.k, nkw = (int64_t)g.n * g.k;
@@ -556,12 +562,13 @@ __device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) 
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    static_assert(S == 1 || S == 2, "stages");
     issue(0, 0);
+    int stage = 0;
     for (int kt = 0; kt < nk; ++kt) {
-        const int stage = S == 2 ? (kt & 1) : 0;
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's copies of k-step kt are in LDS
-        lds_barrier();                          // every wave's are (S = 2: and stage kt + 1 is read)
-        if (S == 2 && kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+        lds_barrier();   // every wave's are (S = 2: and every wave is done with the other stage)
+        if (S == 2 && kt + 1 < nk) issue(kt + 1, stage ^ 1);
         const _Float16 *ah = &st[stage][0], *al = ah + SA, *ws = ah + 2 * SA;
 #pragma unroll
         for (int kk = 0; kk < KB / 32; ++kk) {
@@ -588,9 +595,10 @@ __device__ __forceinline__ void gemm_tile_hd(const GemmArgs &g, int m0, int n0) 
             lds_barrier();   // every wave has read the stage
             issue(kt + 1, 0);
         }
+        stage ^= S - 1;
     }
     const float inv_w = 1.0f / g.wscale;
-    gemm_store<EPI, NI>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
+    gemm_store<EPI, NI, WN>(g, m0, n0, acc, [&](int row) { return (1.0f / g.ascale[row]) * inv_w; });
 }
 
 constexpr int kDmaKB = 64, kDmaBlocksPerCU = 3;
@@ -602,9 +610,16 @@ __host__ __device__ inline bool dma_tile_fits(const GemmArgs &g) {
     return g.k % kDmaKB == 0 && (int64_t)g.m * g.k * 2 < (1ll << 31) && (int64_t)g.n * g.k * 2 < (1ll << 31);
 }
 
-template <int EPI, int NI, int S>
-__global__ void __launch_bounds__(kThreads, S == 1 ? kDmaBlocksPerCU : 1) k_gemm_hd(GemmArgs g) {
-    gemm_tile_hd<EPI, NI, kDmaKB, S>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+// Workgroups per CU that S stages of k-steps of KB halves leave room for in
+// the CU's 160 KB of LDS (a stage: 2 x 128 A rows + 64 WN weight rows of KB
+// halves), at most three.
+constexpr int dma_blocks(int kb, int s, int wn) {
+    return 160 * 1024 / (s * kb * 2 * (256 + 64 * wn)) < 3 ? 160 * 1024 / (s * kb * 2 * (256 + 64 * wn)) : 3;
+}
+
+template <int EPI, int NI, int KB, int S, int WN>
+__global__ void __launch_bounds__(128 * WN, dma_blocks(KB, S, WN)) k_gemm_hd(GemmArgs g) {
+    gemm_tile_hd<EPI, NI, KB, S, WN>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 8 : 16) * NI * WN);
 }
 
 // Compute units of the current device, queried once per device.
@@ -806,7 +821,7 @@ template <int EPI, int NI>
 __global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_grouped_hd(GemmArgs g, GemmGroups gg) {
     const int m0 = blockIdx.y * kBM;
     if (!group_args<EPI>(g, gg, blockIdx.z, m0)) return;
-    gemm_tile_hd<EPI, NI, kDmaKB, 1>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+    gemm_tile_hd<EPI, NI, kDmaKB, 1, 2>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
 template <int DT>
@@ -861,26 +876,41 @@ int launch_dt(hipStream_t s, int epi, const GemmArgs &g) {
         // slower: the accumulators leave one or two waves per SIMD)
         const bool dma = dma_tile_fits(g);
         const dim3 sgrid(ceil_div(g.n, 16 * kSwigluNI), grid.y);
+        const int cus = device_cus();
+        // 128 x 256 tiles of eight waves (fewer LDS bytes per MFMA) for the
+        // projections whose grid of them still covers every CU; the SwiGLU
+        // GEMM's large grids keep three 128 x 128 workgroups per CU
+        const bool wide = epi != GEMM_SWIGLU && (int64_t)ceil_div(g.n, 256) * grid.y >= cus;
+        const int wn = wide ? 4 : 2;
+        const dim3 wgrid(ceil_div(g.n, (epi == GEMM_SWIGLU ? 8 : 16) * 4 * wn), grid.y);
         // A grid of at most one tile per CU leaves no other workgroup to
         // cover a k-step's copy: two LDS stages overlap it with the MFMAs.
-        const int64_t tiles = (int64_t)(epi == GEMM_SWIGLU ? sgrid.x : grid.x) * grid.y;
-        const bool two = tiles <= device_cus();
+        const bool two = (int64_t)wgrid.x * wgrid.y <= cus;
+        const int threads = 128 * wn;
+#define MR_HD(E, NI_)                                                                                  \
+    do {                                                                                               \
+        if (wn == 4) {                                                                                 \
+            if (two) k_gemm_hd<E, NI_, 64, 2, 4><<<wgrid, threads, 0, s>>>(h);                         \
+            else k_gemm_hd<E, NI_, 64, 1, 4><<<wgrid, threads, 0, s>>>(h);                             \
+        } else {                                                                                       \
+            if (two) k_gemm_hd<E, NI_, 64, 2, 2><<<wgrid, threads, 0, s>>>(h);                         \
+            else k_gemm_hd<E, NI_, 64, 1, 2><<<wgrid, threads, 0, s>>>(h);                             \
+        }                                                                                              \
+    } while (0)
         switch (epi) {
             case GEMM_STORE:
-                if (dma && two) k_gemm_hd<GEMM_STORE, 4, 2><<<grid, kThreads, 0, s>>>(h);
-                else if (dma) k_gemm_hd<GEMM_STORE, 4, 1><<<grid, kThreads, 0, s>>>(h);
+                if (dma) MR_HD(GEMM_STORE, 4);
                 else k_gemm_h<GEMM_STORE, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_RESIDUAL:
-                if (dma && two) k_gemm_hd<GEMM_RESIDUAL, 4, 2><<<grid, kThreads, 0, s>>>(h);
-                else if (dma) k_gemm_hd<GEMM_RESIDUAL, 4, 1><<<grid, kThreads, 0, s>>>(h);
+                if (dma) MR_HD(GEMM_RESIDUAL, 4);
                 else k_gemm_h<GEMM_RESIDUAL, 4><<<grid, kThreads, 0, s>>>(h);
                 break;
             case GEMM_SWIGLU:
-                if (dma && two) k_gemm_hd<GEMM_SWIGLU, kSwigluNI, 2><<<sgrid, kThreads, 0, s>>>(h);
-                else if (dma) k_gemm_hd<GEMM_SWIGLU, kSwigluNI, 1><<<sgrid, kThreads, 0, s>>>(h);
+                if (dma) MR_HD(GEMM_SWIGLU, kSwigluNI);
                 else k_gemm_h<GEMM_SWIGLU, kSwigluNI><<<sgrid, kThreads, 0, s>>>(h);
                 break;
+#undef MR_HD
             default: return fail(MR_ERR_INVALID, "gemm: unknown epilogue");
         }
         MR_LAUNCHED("enqueue MFMA GEMM (FP16 terms)");
