@@ -617,9 +617,32 @@ constexpr int dma_blocks(int kb, int s, int wn) {
     return 160 * 1024 / (s * kb * 2 * (256 + 64 * wn)) < 3 ? 160 * 1024 / (s * kb * 2 * (256 + 64 * wn)) : 3;
 }
 
+// The tile (row ty, column tx) a workgroup of a k_gemm_hd grid computes.
+// Workgroups go to the 8 XCDs in turn (linear id mod 8), each XCD with its
+// own L2; in launch order an XCD takes every eighth column tile of every
+// row, which, where a grid is resident at once, shares the weight columns
+// but none of A's rows.  Here XCD k takes the k-th contiguous share of an
+// order that walks groups of kTileGroup row tiles column by column, so the
+// workgroups an XCD runs together share a few A row blocks and a few weight
+// column blocks (groups of 4 measured faster than 2, 8 or 16, and than the
+// launch order for the multi-round grids too).
+constexpr int kTileGroup = 4;
+__device__ __forceinline__ void xcd_tile(int &ty, int &tx) {
+    const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
+    const int lin = blockIdx.x + gx * blockIdx.y;
+    const int k = lin % 8, q = total / 8, r = total % 8;
+    const int t = k * q + min(k, r) + lin / 8;   // XCD k: tiles [k q + min(k, r), ...)
+    const int grp = t / (kTileGroup * gx), within = t % (kTileGroup * gx);
+    const int rows = min(kTileGroup, gy - grp * kTileGroup);
+    ty = grp * kTileGroup + within % rows;
+    tx = within / rows;
+}
+
 template <int EPI, int NI, int KB, int S, int WN>
 __global__ void __launch_bounds__(128 * WN, dma_blocks(KB, S, WN)) k_gemm_hd(GemmArgs g) {
-    gemm_tile_hd<EPI, NI, KB, S, WN>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? 8 : 16) * NI * WN);
+    int ty, tx;
+    xcd_tile(ty, tx);
+    gemm_tile_hd<EPI, NI, KB, S, WN>(g, ty * kBM, tx * (EPI == GEMM_SWIGLU ? 8 : 16) * NI * WN);
 }
 
 // Compute units of the current device, queried once per device.
