@@ -190,21 +190,34 @@ def test_copy_bounds_and_ownership(backend):
         b.empty((0, 3))
 
 
-@pytest.mark.parametrize("k", [1000, 1024])
-def test_prefill_gemm_term_schemes(backend, k):
+# (rows, columns, K) and the FP16-term tile each selects on a 256-CU MI355X:
+# K not a multiple of 64 takes the tile that stages its operands through
+# registers; otherwise the buffer unit copies them into LDS, in 128 x 256
+# tiles of eight waves where those still give a tile per CU (else 128 x 128
+# of four), with two LDS stages where the grid has no more tiles than CUs.
+GEMM_TILE_CASES = {
+    "registers": (200, 300, 1000),
+    "lds-128x128-two-stages": (200, 300, 1024),   # 6 tiles
+    "lds-128x128-one-stage": (12700, 300, 512),   # 300 tiles of 128 x 128, 200 of 128 x 256
+    "lds-128x256-two-stages": (4096, 2000, 512),  # 256 tiles
+    "lds-128x256-one-stage": (4100, 3072, 512),   # 396 tiles
+}
+
+
+@pytest.mark.parametrize("case", list(GEMM_TILE_CASES))
+def test_prefill_gemm_term_schemes(backend, case):
     """The batched-prefill MFMA GEMM in both term schemes against a float64
     product, on rows that stress FP16's range: ordinary values, a row far above
     FP16's maximum (6.5e4), a row of tiny values (1e-20), a zero row and a row
     mixing magnitudes 1e4 .. 1e-4; BF16 weights of magnitudes 2^-20 .. 8 with
     a few zeros.  Bound per element: 2^-20 * sum_k |a| |w| (FP32 accumulation
-    of about 1000 products of operands carried to 2^-22 or better); the FP16
-    scheme's row and matrix scales are powers of two, so they add no error.
-    K = 1000 takes the FP16-term tile that stages its operands through
-    registers, K = 1024 the one whose operands the buffer unit copies into
-    LDS; 200 rows and 300 columns leave both with partial tiles."""
+    of up to about 1000 products of operands carried to 2^-22 or better); the
+    FP16 scheme's row and matrix scales are powers of two, so they add no
+    error.  The shapes take each form of the FP16-term tile (GEMM_TILE_CASES),
+    with partial tiles in rows or columns."""
     from miracle_hip.weights import BF16Array, bf16_bits
     b, rng = backend, np.random.default_rng(21)
-    m, n = 200, 300
+    m, n, k = GEMM_TILE_CASES[case]
     a = rng.normal(size=(m, k)).astype(np.float32)
     a[1] *= 3.0e6
     a[2] *= 1.0e-20
