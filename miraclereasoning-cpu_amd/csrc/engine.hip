@@ -1507,6 +1507,7 @@ struct PrefillWs {
     float *lat = nullptr, *sums = nullptr, *ext = nullptr, *router = nullptr, *mw = nullptr, *xg = nullptr,
           *y = nullptr;
     int *ids = nullptr, *active = nullptr, *counts = nullptr, *offsets = nullptr, *fill = nullptr, *map = nullptr;
+    int *tile_start = nullptr;   // [groups + 1] prefix sums of the groups' GEMM row tiles
     float *slot0 = nullptr, *slot0_final = nullptr, *kv0 = nullptr, *obuf = nullptr, *fbuf = nullptr,
           *merge_count = nullptr;
     int *flags = nullptr, *extra_index = nullptr, *merge_row = nullptr, *extra_pos = nullptr;
@@ -1558,6 +1559,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->xn_scale, heavy ? r : 0}, {(void **)&w->xn_planes, heavy ? r * h : 0},
         {(void **)&w->y, heavy ? r * slots * h : 0}, {(void **)&w->ids, r * kmax}, {(void **)&w->active, heavy ? r : 0},
         {(void **)&w->counts, groups}, {(void **)&w->offsets, groups}, {(void **)&w->fill, groups},
+        {(void **)&w->tile_start, heavy ? groups + 1 : 0},
         {(void **)&w->map, r * kmax},
         // flashlighting-2.0
         {(void **)&w->slot0, light ? r * lat : 0}, {(void **)&w->slot0_final, light ? lat : 0},
@@ -1854,6 +1856,7 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         e.shared_scale = d.heavy_shared_scale; e.scale = d.heavy_step_scale;
         mr_.rows = T; mr_.p0 = p0;
         mr_.counts = w.counts; mr_.offsets = w.offsets; mr_.fill = w.fill; mr_.map = w.map; mr_.xg = w.xg;
+        mr_.tile_start = w.tile_start; mr_.tile_rows = kGemmRowTile;
         const bool f16 = L.expert_tab_h != nullptr;   // FP16 terms: the experts' copies and scales
         const int rows = T * (kmax + S);   // the gathered rows' capacity (routed slots, then shared)
         // FP16 terms: the T rows split once and their terms gathered, not the gathered rows split
@@ -1866,6 +1869,8 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         MR_TRY(launch_moe_route_rows(s, mr_));
         GemmGroups gg;
         gg.offset = w.offsets; gg.count = w.counts; gg.groups = groups; gg.max_rows = T;
+        // every gathered row is in one group: at most rows / 128 tiles plus a partial one a group
+        gg.row_tile_start = w.tile_start; gg.row_tiles = ceil_div(T * (kmax + S), kGemmRowTile) + groups;
         gg.w = L.expert_tab; gg.w2 = L.expert_tab + groups;
         if (f16) { gg.wh = L.expert_tab_h; gg.wh2 = L.expert_tab_h + groups; gg.wscale = L.expert_scale; }
         GemmArgs gu;

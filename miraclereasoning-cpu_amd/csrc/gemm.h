@@ -88,7 +88,14 @@ struct GemmGroups {
     const float *wscale = nullptr;   // [groups] their scales
     int groups = 0;
     int max_rows = 0;                // bound on every count (sizes the grid)
+    // Optional: [groups + 1] device prefix sums of the groups' kGemmRowTile-row
+    // tiles, and a bound on the last (total_rows / kGemmRowTile + groups): the
+    // FP16-term kernel then runs only the groups' own row tiles, not
+    // max_rows' worth in every group.
+    const int *row_tile_start = nullptr;
+    int row_tiles = 0;
 };
+constexpr int kGemmRowTile = 128;   // rows of a GEMM tile
 int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const GemmGroups &gg);
 
 }  // namespace mr

@@ -33,6 +33,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
+static_assert(kBM == kGemmRowTile, "the row tiles the grouped GEMM's tile list counts");
 constexpr int kPitch = kBK + 8;   // BF16 elements per LDS row (80 bytes: rows stay 16-byte aligned)
 constexpr int kThreads = 256;
 #ifndef MR_GEMM_SWIGLU_NI
@@ -847,6 +848,31 @@ __global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_grouped_hd(G
     gemm_tile_hd<EPI, NI, kDmaKB, 1, 2>(g, m0, blockIdx.x * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
 }
 
+// The same over the groups' own row tiles only: grid (column tiles,
+// row_tiles); row tile t belongs to the group z with row_tile_start[z] <= t
+// < row_tile_start[z + 1], and those past the last group's end exit.  (The
+// launch order, in which an expert's row tiles are neighbours, measured
+// faster here than the XCD-aware order of the plain GEMMs.)
+constexpr int kMaxTileGroups = 1024;   // groups the tile list's search holds in LDS
+template <int EPI, int NI>
+__global__ void __launch_bounds__(kThreads, kDmaBlocksPerCU) k_gemm_grouped_hd_list(GemmArgs g, GemmGroups gg) {
+    const int ty = blockIdx.y, tx = blockIdx.x;
+    // the prefix sums in LDS with one round of loads, then the search there
+    __shared__ int start[kMaxTileGroups + 1];
+    for (int i = threadIdx.x; i <= gg.groups; i += kThreads) start[i] = gg.row_tile_start[i];
+    __syncthreads();
+    if (ty >= start[gg.groups]) return;
+    int lo = 0, hi = gg.groups - 1;   // the last z with start[z] <= ty
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (start[mid] <= ty) lo = mid;
+        else hi = mid - 1;
+    }
+    const int m0 = (ty - start[lo]) * kBM;
+    if (!group_args<EPI>(g, gg, lo, m0)) return;
+    gemm_tile_hd<EPI, NI, kDmaKB, 1, 2>(g, m0, tx * (EPI == GEMM_SWIGLU ? 16 * NI : 32 * NI));
+}
+
 template <int DT>
 int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroups &gg) {
     const int cols = epi == GEMM_SWIGLU ? kBN / 2 : kBN;
@@ -858,16 +884,23 @@ int launch_grouped_dt(hipStream_t s, int epi, const GemmArgs &g, const GemmGroup
         h.ahl = g.ahl_ws;
         if (!g.a_split) row_split(s, g.a, g.lda, g.m, g.k, g.ascale, g.ahl_ws);
         const bool dma = dma_tile_fits(g);
+        // the groups' own row tiles where their prefix sums are given
+        const bool list = dma && gg.row_tile_start && gg.row_tiles > 0 &&
+                          gg.groups <= kMaxTileGroups;
         switch (epi) {
             case GEMM_STORE: {
                 const dim3 gs(ceil_div(g.n, 32 * 4), ceil_div(gg.max_rows, kBM), gg.groups);
-                if (dma) k_gemm_grouped_hd<GEMM_STORE, 4><<<gs, kThreads, 0, s>>>(h, gg);
+                const dim3 gl(gs.x, gg.row_tiles);
+                if (list) k_gemm_grouped_hd_list<GEMM_STORE, 4><<<gl, kThreads, 0, s>>>(h, gg);
+                else if (dma) k_gemm_grouped_hd<GEMM_STORE, 4><<<gs, kThreads, 0, s>>>(h, gg);
                 else k_gemm_grouped_h<GEMM_STORE, 4><<<gs, kThreads, 0, s>>>(h, gg);
                 break;
             }
             case GEMM_SWIGLU: {
                 const dim3 gs(ceil_div(g.n, 16 * kSwigluNI), ceil_div(gg.max_rows, kBM), gg.groups);
-                if (dma) k_gemm_grouped_hd<GEMM_SWIGLU, kSwigluNI><<<gs, kThreads, 0, s>>>(h, gg);
+                const dim3 gl(gs.x, gg.row_tiles);
+                if (list) k_gemm_grouped_hd_list<GEMM_SWIGLU, kSwigluNI><<<gl, kThreads, 0, s>>>(h, gg);
+                else if (dma) k_gemm_grouped_hd<GEMM_SWIGLU, kSwigluNI><<<gs, kThreads, 0, s>>>(h, gg);
                 else k_gemm_grouped_h<GEMM_SWIGLU, kSwigluNI><<<gs, kThreads, 0, s>>>(h, gg);
                 break;
             }

@@ -111,6 +111,8 @@ struct MoeRowsArgs {
     int rows = 0, p0 = 0;
     int *counts = nullptr, *offsets = nullptr, *fill = nullptr;   // [experts + shared]
     int *map = nullptr;              // [rows][kmax]
+    int *tile_start = nullptr;       // optional [experts + shared + 1]: prefix sums of the groups' row tiles
+    int tile_rows = 128;             // rows of such a tile
     float *xg = nullptr;             // [rows (kmax + shared)][h]
     // FP16 terms (h a multiple of 8): the rows' scales and planes from
     // launch_row_split over `rows` rows, gathered into the grouped GEMM's

@@ -1016,16 +1016,22 @@ __global__ void k_moe_zero(int *counts, int n) {
 }
 
 // one thread: group offsets (routed experts in expert order, then one group
-// of every row per shared expert) and cleared fill cursors
+// of every row per shared expert), cleared fill cursors and, where asked,
+// the prefix sums of the groups' row tiles
 __global__ void k_moe_offsets(MoeRowsArgs m) {
     const int E = m.a.experts, S = m.a.shared;
-    int at = 0;
+    int at = 0, tiles = 0;
     for (int e = 0; e < E + S; ++e) {
         if (e >= E) m.counts[e] = m.rows;
         m.offsets[e] = at;
         at += m.counts[e];
         m.fill[e] = 0;
+        if (m.tile_start) {
+            m.tile_start[e] = tiles;
+            tiles += (m.counts[e] + m.tile_rows - 1) / m.tile_rows;
+        }
     }
+    if (m.tile_start) m.tile_start[E + S] = tiles;
 }
 
 // grid rows, 256 threads: copy the row into each of its groups
