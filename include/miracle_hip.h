@@ -291,6 +291,20 @@ MR_API int mr_debug_step_timeout(mr_model *model);
 MR_API int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *ascale, int m, int n, int k,
                          int scheme);
 
+/* Test hook: the batched prefill's grouped (expert) MFMA GEMM in the FP16-term
+ * scheme.  Group z holds counts[z] (host, >= 0) consecutive rows of a
+ * [rows, k] (device FP32, groups in order, rows = the sum of counts) and its
+ * own weights, rows z n .. z n + n - 1 of w (device BF16 [groups, n, k]);
+ * c [rows, n] receives a . w_z^T for each group's rows, or with swiglu the
+ * SwiGLU of the gate (w) and up (w2, same layout) products (a group's gate
+ * and up copies share one FP16 scale, as the model's do).  tile_list 1 runs
+ * the kernel over the groups' own 128-row tiles (the prefix sums the prefill
+ * takes from its routing), 0 the grid of max(counts) rows in every group.
+ * Synchronizes; k must be a multiple of 8.  Not a counterpart of any
+ * reference function. */
+MR_API int mr_debug_gemm_grouped(mr_ctx *ctx, const float *a, const void *w, const void *w2, float *c,
+                                 const int *counts, int groups, int n, int k, int swiglu, int tile_list);
+
 /* Test hook: the batched-prefill attention over device FP32 buffers.  qkv
  * [rows, heads*d + 2*kv_heads*d] holds each row's (normalized, rotated)
  * query, key and value at positions p0 .. p0 + rows - 1; ring_k/ring_v

@@ -348,6 +348,96 @@ int mr_debug_gemm(mr_ctx *ctx, const float *a, const void *w, float *c, float *a
     return MR_OK;
 }
 
+int mr_debug_gemm_grouped(mr_ctx *ctx, const float *a, const void *w, const void *w2, float *c, const int *counts,
+                          int groups, int n, int k, int swiglu, int tile_list) {
+    OP_BEGIN("debug grouped gemm");
+    MR_REQUIRE(a && w && c && counts && groups > 0 && groups <= 1024 && n > 0 && k > 0 && k % 8 == 0 &&
+                   (!swiglu || w2),
+               "debug grouped gemm: bad arguments");
+    std::vector<int> offset(groups), start(groups + 1);
+    int rows = 0, max_rows = 0;
+    start[0] = 0;
+    for (int z = 0; z < groups; ++z) {
+        MR_REQUIRE(counts[z] >= 0, "debug grouped gemm: negative group size");
+        offset[z] = rows;
+        rows += counts[z];
+        max_rows = std::max(max_rows, counts[z]);
+        start[z + 1] = start[z] + ceil_div(counts[z], kGemmRowTile);
+    }
+    MR_REQUIRE(rows > 0, "debug grouped gemm: no rows");
+    std::vector<void *> owned;   // freed on every return
+    auto alloc = [&](size_t bytes, void **p) {
+        const hipError_t e = hipMalloc(p, bytes);
+        if (e == hipSuccess) owned.push_back(*p);
+        return e;
+    };
+    struct Free {   // after the stream's work on them
+        std::vector<void *> &v;
+        hipStream_t s;
+        ~Free() {
+            (void)hipStreamSynchronize(s);
+            for (void *p : v) (void)hipFree(p);
+        }
+    } release{owned, s};
+    const int mats = swiglu ? 2 : 1;
+    const int64_t nk = (int64_t)n * k;
+    std::vector<void *> tab_w(mats * groups), tab_h(mats * groups);
+    std::vector<float> scale(mats * groups);
+    _Float16 *wh = nullptr;
+    MR_HIP(alloc((size_t)mats * groups * nk * 2, (void **)&wh), "debug grouped gemm workspace");
+    // a scale per matrix; a group's gate and up rows share the smaller, as
+    // the model's expert copies do (the SwiGLU kernel unscales both by one)
+    for (int t = 0; t < mats; ++t)
+        for (int z = 0; z < groups; ++z) {
+            const void *src = (const char *)(t ? w2 : w) + (size_t)z * nk * 2;
+            float sc = 0.0f;
+            MR_TRY(gemm_f16_weight_scale(s, src, MR_BF16, nk, &sc));
+            MR_REQUIRE(sc > 0.0f, "debug grouped gemm: weights not eligible for FP16 terms");
+            tab_w[t * groups + z] = const_cast<void *>(src);
+            scale[t * groups + z] = sc;
+        }
+    for (int z = 0; z < groups && mats == 2; ++z)
+        scale[z] = scale[groups + z] = std::min(scale[z], scale[groups + z]);
+    for (int t = 0; t < mats; ++t)
+        for (int z = 0; z < groups; ++z) {
+            _Float16 *dst = wh + ((size_t)t * groups + z) * nk;
+            MR_TRY(gemm_f16_weight_copy(s, tab_w[t * groups + z], nk, scale[t * groups + z], dst));
+            tab_h[t * groups + z] = dst;
+        }
+    void **d_w = nullptr, **d_h = nullptr;
+    float *d_scale = nullptr, *ascale = nullptr;
+    int *d_off = nullptr, *d_cnt = nullptr, *d_start = nullptr;
+    _Float16 *planes = nullptr;
+    MR_HIP(alloc(tab_w.size() * sizeof(void *), (void **)&d_w), "debug grouped gemm workspace");
+    MR_HIP(alloc(tab_h.size() * sizeof(void *), (void **)&d_h), "debug grouped gemm workspace");
+    MR_HIP(alloc(scale.size() * sizeof(float), (void **)&d_scale), "debug grouped gemm workspace");
+    MR_HIP(alloc((size_t)groups * sizeof(int), (void **)&d_off), "debug grouped gemm workspace");
+    MR_HIP(alloc((size_t)groups * sizeof(int), (void **)&d_cnt), "debug grouped gemm workspace");
+    MR_HIP(alloc((size_t)(groups + 1) * sizeof(int), (void **)&d_start), "debug grouped gemm workspace");
+    MR_HIP(alloc((size_t)rows * sizeof(float), (void **)&ascale), "debug grouped gemm workspace");
+    MR_HIP(alloc((size_t)2 * rows * k * sizeof(_Float16), (void **)&planes), "debug grouped gemm workspace");
+    MR_HIP(hipMemcpy(d_w, tab_w.data(), tab_w.size() * sizeof(void *), hipMemcpyHostToDevice), "debug grouped gemm");
+    MR_HIP(hipMemcpy(d_h, tab_h.data(), tab_h.size() * sizeof(void *), hipMemcpyHostToDevice), "debug grouped gemm");
+    MR_HIP(hipMemcpy(d_scale, scale.data(), scale.size() * sizeof(float), hipMemcpyHostToDevice), "debug grouped gemm");
+    MR_HIP(hipMemcpy(d_off, offset.data(), groups * sizeof(int), hipMemcpyHostToDevice), "debug grouped gemm");
+    MR_HIP(hipMemcpy(d_cnt, counts, groups * sizeof(int), hipMemcpyHostToDevice), "debug grouped gemm");
+    MR_HIP(hipMemcpy(d_start, start.data(), (groups + 1) * sizeof(int), hipMemcpyHostToDevice), "debug grouped gemm");
+    GemmArgs g;
+    g.a = a; g.lda = k; g.dtype = MR_BF16; g.c = c; g.ldc = n; g.m = rows; g.n = n; g.k = k;
+    g.ascale = ascale; g.ahl_ws = planes;
+    GemmGroups gg;
+    gg.offset = d_off; gg.count = d_cnt; gg.groups = groups; gg.max_rows = max_rows;
+    gg.w = d_w; gg.w2 = swiglu ? d_w + groups : nullptr;
+    gg.wh = d_h; gg.wh2 = swiglu ? d_h + groups : nullptr; gg.wscale = d_scale;
+    if (tile_list) {
+        gg.row_tile_start = d_start;
+        gg.row_tiles = start[groups];
+    }
+    MR_TRY(launch_gemm_grouped(s, swiglu ? GEMM_SWIGLU : GEMM_STORE, g, gg));
+    MR_HIP(hipStreamSynchronize(s), "debug grouped gemm");
+    return MR_OK;
+}
+
 int mr_debug_exp(mr_ctx *ctx, const float *x, float *y, int n, int which) {
     OP_BEGIN("debug exp");
     MR_TRY(launch_debug_exp(s, x, y, n, which));

@@ -102,6 +102,7 @@ _SIGNATURES = {
     "mr_debug_fail_next": [_P],
     "mr_debug_step_timeout": [_P],
     "mr_debug_gemm": [_P, _P, _P, _P, _P, _i, _i, _i, _i],
+    "mr_debug_gemm_grouped": [_P, _P, _P, _P, _P, C.POINTER(C.c_int), _i, _i, _i, _i, _i],
     "mr_debug_prefill_attention": [_P, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i, _i],
     "mr_debug_exp": [_P, _P, _P, _i, _i],
 }
@@ -419,6 +420,28 @@ class HIPBackend:
         out, ws = self.empty((m, n)), self.empty((m,))
         _check(self.lib.mr_debug_gemm(self.ctx, a.handle, weight.handle, out.handle, ws.handle, m, n, k, scheme),
                "debug gemm")
+        return out
+
+    def debug_gemm_grouped(self, a, weight, counts, weight2=None, tile_list=True):
+        """The batched prefill's grouped (expert) MFMA GEMM in FP16 terms (test
+        hook): group z is the next counts[z] rows of ``a`` [rows, k] with
+        weight rows z n .. z n + n - 1 of ``weight`` (BF16 [groups n, k]);
+        with ``weight2`` (same layout) the SwiGLU of the two products.  Returns
+        c [rows, n]."""
+        self._owns(a, weight, *([weight2] if weight2 is not None else []))
+        groups = len(counts)
+        if (weight.dtype != "bf16" or len(a.shape) != 2 or len(weight.shape) != 2 or a.shape[1] != weight.shape[1]
+                or groups == 0 or weight.shape[0] % groups or a.shape[0] != sum(counts)
+                or (weight2 is not None and (weight2.dtype != "bf16" or weight2.shape != weight.shape))):
+            raise ValueError("debug_gemm_grouped needs a[sum(counts), k] and BF16 weights[groups n, k]")
+        rows, k = a.shape
+        n = weight.shape[0] // groups
+        out = self.empty((rows, n))
+        c_counts = (C.c_int * groups)(*counts)
+        _check(self.lib.mr_debug_gemm_grouped(self.ctx, a.handle, weight.handle,
+                                              weight2.handle if weight2 is not None else None, out.handle, c_counts,
+                                              groups, n, k, int(weight2 is not None), int(tile_list)),
+               "debug grouped gemm")
         return out
 
     def debug_exp(self, x, which):

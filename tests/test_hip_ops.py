@@ -239,6 +239,69 @@ def test_prefill_gemm_term_schemes(backend, case):
         assert worst <= 1.0, scheme
 
 
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_grouped_gemm_groups_against_float64(backend, swiglu):
+    """The batched prefill's grouped (expert) GEMM in FP16 terms against float64
+    per group: groups of 130, 0, 1, 257, 0 and 64 rows (empty groups, a single
+    row, partial 128-row tiles), each with its own BF16 weights of its own
+    magnitude (so its own power-of-two FP16 scale), K = 1024; 384 output
+    columns (a partial 256-column tile), or 192 SwiGLU columns.  Bound per
+    element as in the plain GEMM's test: 2^-20 sum_k |a| |w| for each product
+    (the SwiGLU of the two products checked against their float64 SwiGLU
+    with the bound carried through its derivative).  The kernel over the
+    groups' own row tiles and the one over max(counts) rows in every group
+    give the same bits."""
+    from miracle_hip.weights import BF16Array, bf16_bits
+    b, rng = backend, np.random.default_rng(33)
+    counts = [130, 0, 1, 257, 0, 64]
+    k, n = 1024, (192 if swiglu else 384)
+    rows = sum(counts)
+    a = rng.normal(size=(rows, k)).astype(np.float32)
+    a[5] *= 3.0e4
+    a[140] = 0.0
+
+    def weights():
+        w = np.concatenate([rng.normal(size=(n, k)) * 2.0 ** rng.integers(-12, 6) for _ in counts])
+        bits = bf16_bits(w.astype(np.float32))
+        return bits, BF16Array(bits)[:].astype(np.float64)
+
+    bits, wf = weights()
+    bits2, wf2 = weights() if swiglu else (None, None)
+    want = np.zeros((rows, n))
+    bound = np.zeros((rows, n))
+    r0 = 0
+    for z, cnt in enumerate(counts):
+        sl = slice(r0, r0 + cnt)
+        wz = wf[z * n:(z + 1) * n]
+        g = a[sl].astype(np.float64) @ wz.T
+        eg = 2.0 ** -20 * (np.abs(a[sl]).astype(np.float64) @ np.abs(wz).T)
+        if swiglu:
+            uz = wf2[z * n:(z + 1) * n]
+            u = a[sl].astype(np.float64) @ uz.T
+            eu = 2.0 ** -20 * (np.abs(a[sl]).astype(np.float64) @ np.abs(uz).T)
+            sig = 1.0 / (1.0 + np.exp(-g))
+            silu = g * sig
+            dsilu = np.abs(sig * (1.0 + g * (1.0 - sig)))
+            want[sl] = silu * u
+            # first-order error of silu(g) u, plus FP32 rounding of the epilogue
+            bound[sl] = dsilu * eg * np.abs(u) + np.abs(silu) * eu + 1e-6 * np.abs(silu * u)
+        else:
+            want[sl] = g
+            bound[sl] = eg
+        r0 += cnt
+    bound += 1e-30
+    dev_a = b.upload(a)
+    dev_w = b.upload_weight(BF16Array(bits))
+    dev_w2 = b.upload_weight(BF16Array(bits2)) if swiglu else None
+    got = b.read(b.debug_gemm_grouped(dev_a, dev_w, counts, weight2=dev_w2, tile_list=True))
+    ref = b.read(b.debug_gemm_grouped(dev_a, dev_w, counts, weight2=dev_w2, tile_list=False))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.all(got[140] == 0.0)
+    worst = np.max(np.abs(got.astype(np.float64) - want) / bound)
+    print("grouped", "swiglu" if swiglu else "store", "worst error / bound", worst, flush=True)
+    assert worst <= 1.0
+
+
 @pytest.mark.parametrize("presplit", [False, True])
 @pytest.mark.parametrize("dim", [32, 64, 128])
 def test_prefill_attention_term_scaling(backend, dim, presplit):
