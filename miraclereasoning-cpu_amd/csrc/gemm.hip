@@ -36,14 +36,8 @@ constexpr int kBM = 128, kBN = 128, kBK = 32;
 static_assert(kBM == kGemmRowTile, "the row tiles the grouped GEMM's tile list counts");
 constexpr int kPitch = kBK + 8;   // BF16 elements per LDS row (80 bytes: rows stay 16-byte aligned)
 constexpr int kThreads = 256;
-#ifndef MR_GEMM_SWIGLU_NI
-#define MR_GEMM_SWIGLU_NI 4
-#endif
-constexpr int kSwigluNI = MR_GEMM_SWIGLU_NI;
-#ifndef MR_GEMM_KBH
-#define MR_GEMM_KBH 64
-#endif
-constexpr int kKBH = MR_GEMM_KBH;   // k-step of the FP16-term GEMM (halves)   // 16-column MFMA tiles per wave in the SwiGLU FP16-term GEMM
+constexpr int kSwigluNI = 4;   // 16-column MFMA tiles per wave in the SwiGLU FP16-term GEMM
+constexpr int kKBH = 64;       // k-step of the register-staged FP16-term GEMM (halves)
 
 template <int DT>
 constexpr int planes() {

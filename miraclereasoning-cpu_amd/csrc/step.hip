@@ -114,14 +114,11 @@ __device__ __forceinline__ void wg_rows(const Phase &ph, int &r0, int &r1) {
 }
 constexpr int kVC = 4;
 constexpr int kDepth = 4;   // jobs in flight per stream wave when a job is one matrix (M = 1)
-#ifndef MR_STEP_ENTRY_DEPTH
-#define MR_STEP_ENTRY_DEPTH 2
-#endif
 // Of them, the jobs issued before the phase's input is staged: the rest go
 // out once it is (a CU returns loads in issue order, so the control waves'
 // polls wait behind whatever the stream waves have in flight; two of four
 // measured fastest, none much slower).
-constexpr int kEntryDepth = MR_STEP_ENTRY_DEPTH;
+constexpr int kEntryDepth = 2;
 
 struct GemvGeo {
     int r0, r1;      // rows of this workgroup
