@@ -488,8 +488,9 @@ __device__ __forceinline__ bool combine_cells(const AttnStepArgs &a, int v, int 
         return (unsigned)(p[0].x >> 32) == io.ep_out && (unsigned)(p[0].y >> 32) == io.ep_out &&
                (unsigned)(p[1].x >> 32) == io.ep_out && (unsigned)(p[1].y >> 32) == io.ep_out;
     };
-    // Round 1: the first chunk of o and this thread's (m, l) pair.  Cells that
-    // arrived are kept: a poll round re-reads only what is still missing.
+    // The first chunk of o and this thread's (m, l) pair, polled until they are
+    // all there.  Cells that arrived are kept: each poll re-reads only what is
+    // still missing.
     {
         const int i = tid < active * G ? tid : active * G;
         ll::u64x2 ml{0ull, 0ull};
