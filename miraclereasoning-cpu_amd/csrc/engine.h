@@ -22,6 +22,7 @@ struct Weight {
     // term scheme is used for this matrix)
     float f16_scale = 0.0f;
     void *f16 = nullptr;   // the matrix times f16_scale in FP16 (owned)
+    float row_norm = 0.0f;  // SwiGLU gate and up: bound on the largest row norm (0: none)
     explicit operator bool() const { return ptr != nullptr; }
     const float *f() const { return (const float *)ptr; }
 };

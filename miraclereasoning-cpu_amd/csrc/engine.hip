@@ -976,6 +976,22 @@ int f16_copies(mr_model *m, std::initializer_list<Weight *> ws, std::initializer
     return MR_OK;
 }
 
+// Bounds on the gate and up rows' norms where the batched prefill writes the
+// SwiGLU output straight into the down projection's FP16 terms (every
+// matrix of the FFN with an FP16 copy).
+int swiglu_row_norms(mr_model *m, Mlp &f) {
+    if (f.gate.f16_scale > 0.0f && f.up.f16_scale > 0.0f && f.down.f16_scale > 0.0f)
+        for (Weight *w : {&f.gate, &f.up})
+            MR_TRY(gemm_row_norm_bound(m->ctx->stream, w->ptr, w->dtype, w->rows, w->cols, &w->row_norm));
+    return MR_OK;
+}
+
+// The SwiGLU output of rows of `h` values straight into the down
+// projection's FP16 terms (the row-norm bounds found at finalize).
+bool act_split_fits(const Mlp &f, int h) {
+    return h <= 2048 && f.down.f16_scale > 0.0f && f.gate.row_norm > 0.0f && f.up.row_norm > 0.0f;
+}
+
 int finalize_heavy_layer(mr_model *m, Layer &L, int i) {
     const mr_model_desc &d = m->d;
     const int hd = d.head_dim, qd = d.query_heads * hd, kvw = L.kv_heads * hd;
@@ -1058,6 +1074,7 @@ int finalize_light_layer(mr_model *m, Layer &L, int i) {
     L.kv_up.rows = 2 * kvw;
     MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
     MR_TRY(f16_copies(m, {&L.qkv, &L.kv_up, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
+    MR_TRY(swiglu_row_norms(m, L.ffn));
     L.light_cap = d.window + d.memory_slots + 1;
     const size_t cap = L.light_cap;
     MR_TRY(device_alloc(m, cap * d.latent_dim * sizeof(float), (void **)&L.arena));
@@ -1319,6 +1336,7 @@ int mr_model_finalize(mr_model *m) {
         MR_TRY(need(L.ffn.down, "ffn.down", i));
         MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
         MR_TRY(f16_copies(m, {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
+        MR_TRY(swiglu_row_norms(m, L.ffn));
         const int kvw = L.kv_heads * hd;
         max_kvw = std::max(max_kvw, kvw);
         max_kvh = std::max(max_kvh, L.kv_heads);
@@ -1516,6 +1534,7 @@ struct PrefillWs {
     float *xn_scale = nullptr;      // heavy-medium-2.0: the normalized rows' FP16 terms, split once
     _Float16 *xn_planes = nullptr;
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
+    float *act_scale = nullptr;  // row scales of the SwiGLU output written in FP16 terms (into act)
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
     int kv16_rows = 0;
@@ -1569,7 +1588,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
         // flashnano-1.6
         {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
-        {(void **)&w->rowscale, split_rows},
+        {(void **)&w->rowscale, split_rows}, {(void **)&w->act_scale, r},
         {(void **)&w->planes, split_rows * std::max({h, qd, (size_t)d.ffn_dim})},
         {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, 2 * kvw}, {(void **)&w->kv16_max, 2 * kvw}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
@@ -1760,14 +1779,25 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     gu.wscale = L.ffn.gate.f16_scale; gu.wh = L.ffn.gate.f16; gu.wh2 = L.ffn.up.f16; gu.ascale = w.rowscale;
     gu.ahl_ws = w.planes;
     gu.a_split = gu.wscale > 0.0f && rms_split_fits(h);
-    if (gu.a_split) MR_TRY(launch_rms_rows_split(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T));
+    // the SwiGLU output straight into the down projection's FP16 terms (act
+    // holds T x ffn floats, the same bytes as its two planes of halves)
+    const bool act_split = gu.a_split && act_split_fits(L.ffn, h);
+    if (act_split) {
+        gu.c_hl = (_Float16 *)w.act;
+        gu.c_scale = w.act_scale;
+    }
+    if (gu.a_split)
+        MR_TRY(launch_rms_rows_split(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T,
+                                     L.ffn.gate.row_norm, L.ffn.up.row_norm, act_split ? w.act_scale : nullptr));
     else MR_TRY(launch_rms_rows(s, w.x, h, L.f_norm.f(), d.norm_eps, h, w.xn, h, T));
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.x; dn.ldc = h;
     dn.m = T; dn.n = h; dn.k = ffn; dn.scale = d.residual_scale; dn.wscale = L.ffn.down.f16_scale;
     dn.wh = L.ffn.down.f16;
-    dn.ascale = w.rowscale; dn.ahl_ws = w.planes;
+    dn.ascale = act_split ? w.act_scale : w.rowscale;
+    dn.ahl_ws = act_split ? (_Float16 *)w.act : w.planes;
+    dn.a_split = act_split;
     return launch_gemm(s, GEMM_RESIDUAL, dn);
 }
 
@@ -1902,7 +1932,16 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     hipStream_t s = m->ctx->stream;
     const int h = d.hidden_size, hd = d.head_dim, qd = d.query_heads * hd, ffn = d.ffn_dim, lat = d.latent_dim;
     const int kvw = L.kv_heads * hd, ld = qd + 2 * kvw;
-    MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    // the normalized rows straight into FP16 terms where the Q/latent and FFN
+    // GEMMs take them (BF16 weights with FP16 copies), with the scales of the
+    // SwiGLU output for the down projection's FP16 terms
+    const bool xn_split = L.qkv.dtype == MR_BF16 && L.qkv.f16_scale > 0.0f && rms_split_fits(h);
+    const bool gu_split = xn_split && L.ffn.gate.dtype == MR_BF16 && L.ffn.gate.f16_scale > 0.0f;
+    const bool act_split = gu_split && act_split_fits(L.ffn, h);
+    if (!gu_split) MR_TRY(launch_rms_rows(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.xn, h, T));
+    if (xn_split)
+        MR_TRY(launch_rms_rows_split(s, w.x, h, L.a_norm.f(), d.norm_eps, h, w.rowscale, w.planes, T,
+                                     L.ffn.gate.row_norm, L.ffn.up.row_norm, act_split ? w.act_scale : nullptr));
     // FP16-term GEMMs where the weights have FP16 copies (BF16 weights)
     auto f16 = [&](GemmArgs &g, const Weight &wt, size_t row0 = 0) {
         g.wscale = wt.f16_scale;
@@ -1914,14 +1953,14 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     q.a = w.xn; q.lda = h; q.w = L.qkv.ptr; q.dtype = L.qkv.dtype; q.c = w.qkv; q.ldc = ld;
     q.m = T; q.n = qd; q.k = h;
     f16(q, L.qkv);
+    q.a_split = xn_split;
     MR_TRY(launch_gemm(s, GEMM_STORE, q));
     GemmArgs lt = q;   // its latent rows, then RMSNorm with latent_norm in place
     lt.w = (const char *)L.qkv.ptr + (size_t)qd * h * dtype_bytes(L.qkv.dtype); lt.c = w.lat; lt.ldc = lat;
     lt.n = lat;
     f16(lt, L.qkv, qd);
-    // the Q projection left the normalized rows' FP16 terms in the workspace when it took them:
-    // the latent rows and the FFN branch (the same input) reuse them before anything else splits
-    const bool xn_split = q.dtype == MR_BF16 && q.wscale > 0.0f;
+    // the latent rows and the FFN branch (the same input) reuse the normalized
+    // rows' FP16 terms before anything else splits
     lt.a_split = xn_split;
     MR_TRY(launch_gemm(s, GEMM_STORE, lt));
     GemmArgs gu;   // the FFN branch reads the same normalized input
@@ -1929,7 +1968,11 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     gu.c = w.act; gu.ldc = ffn; gu.m = T; gu.n = ffn; gu.k = h;
     f16(gu, L.ffn.gate);
     gu.wh2 = L.ffn.up.f16;
-    gu.a_split = xn_split && gu.dtype == MR_BF16 && gu.wscale > 0.0f;
+    gu.a_split = gu_split;
+    if (act_split) {
+        gu.c_hl = (_Float16 *)w.act;
+        gu.c_scale = w.act_scale;
+    }
     MR_TRY(launch_gemm(s, GEMM_SWIGLU, gu));
     MR_TRY(launch_rms_rows(s, w.lat, lat, L.latent_norm.f(), d.norm_eps, lat, w.lat, lat, T));
     GemmArgs kv;   // [Wk; Wv] . latent beside the queries
@@ -1971,6 +2014,11 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.fbuf; dn.ldc = h;
     dn.m = T; dn.n = h; dn.k = ffn;
     f16(dn, L.ffn.down);
+    if (act_split) {
+        dn.ascale = w.act_scale;
+        dn.ahl_ws = (_Float16 *)w.act;
+        dn.a_split = true;
+    }
     MR_TRY(launch_gemm(s, GEMM_STORE, dn));
     MR_TRY(launch_light_residual(s, w.x, w.obuf, w.fbuf, L.attention_gate.f(), L.ffn_gate.f(), d.residual_scale,
                                  T * h, nullptr));

@@ -43,6 +43,12 @@ struct GemmArgs {
     const _Float16 *ahl = nullptr;   // set by launch_gemm for the kernel
     int64_t plane_stride = 0;        // halves from A's hi plane to its lo plane (0: m k)
     int ldw = 0;                     // elements between weight rows (0: k; set by the split GEMM)
+    // GEMM_SWIGLU, FP16 terms: with c_hl the output is written as the next
+    // FP16-term GEMM's A (a_split) instead of into c: row r times c_scale[r]
+    // (a power of two that keeps every value of the row below 2^14) = hi + lo
+    // into planes [hi: m x n | lo: m x n] of c_hl.
+    _Float16 *c_hl = nullptr;
+    const float *c_scale = nullptr;
 };
 
 // STORE:    c = A . W^T
@@ -66,6 +72,11 @@ int launch_gemm_split(hipStream_t s, const GemmArgs &g, int slices, float *part)
 // for every |w| >= 2^-31 max |w|; 0 for a matrix holding a non-finite value or
 // another dtype (the FP16 scheme is then not used).  Synchronizes the stream.
 int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count, float *scale);
+
+// An upper bound on the largest row norm, max_r sqrt(sum_k w[r][k]^2), of a
+// BF16 matrix of `rows` x `cols` values into *norm (0 for another dtype or a
+// non-finite value).  Synchronizes the stream.
+int gemm_row_norm_bound(hipStream_t s, const void *w, int dtype, int64_t rows, int64_t cols, float *norm);
 
 // dst[i] = FP16(w[i] * scale) for `count` BF16 values (exact for a scale from
 // gemm_f16_weight_scale, or a smaller power of two).

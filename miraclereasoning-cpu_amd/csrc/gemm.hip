@@ -222,12 +222,22 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &g, int m0, int n0, co
             const float u = unscale(row);
             float *crow = g.c + (int64_t)row * g.ldc;
             if constexpr (EPI == GEMM_SWIGLU) {
+                const float cs = g.c_hl ? g.c_scale[row] : 1.0f;
+                _Float16 *hrow = g.c_hl + (int64_t)row * g.n;
 #pragma unroll
                 for (int ni = 0; ni < NI / 2; ++ni) {
                     const int f = n0 + wn * 8 * NI + ni * 16 + lr;
                     if (f >= g.n) continue;
                     const float gt = acc[mi][ni][j] * u, up = acc[mi][ni + NI / 2][j] * u;
-                    crow[f] = (gt / (1.0f + expf(-gt))) * up;
+                    const float v = (gt / (1.0f + expf(-gt))) * up;
+                    if (g.c_hl) {
+                        _Float16 th, tl;
+                        split2h(v * cs, th, tl);
+                        hrow[f] = th;
+                        hrow[(int64_t)g.m * g.n + f] = tl;
+                    } else {
+                        crow[f] = v;
+                    }
                 }
             } else {
 #pragma unroll
@@ -764,6 +774,23 @@ __global__ void __launch_bounds__(256) k_abs_max_bf16(const uint16_t *w, int64_t
     if ((threadIdx.x & 63) == 0) atomicMax(out, mx);
 }
 
+// max over rows of the row's L2 norm, one wave per row, as the bits of a
+// non-negative float (atomic max on the bit patterns).
+__global__ void __launch_bounds__(256) k_row_norm_max_bf16(const uint16_t *w, int64_t rows, int64_t cols,
+                                                           unsigned *out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint16_t *r = w + row * cols;
+    float ss = 0.0f;
+    for (int64_t c = lane; c < cols; c += kWave) {
+        const float v = __uint_as_float((unsigned)r[c] << 16);
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) atomicMax(out, __float_as_uint(sqrtf(ss)));
+}
+
 template <int DT, int EPI>
 __global__ void __launch_bounds__(kThreads) k_gemm(GemmArgs g) {
     gemm_tile<DT, EPI>(g, blockIdx.y * kBM, blockIdx.x * (EPI == GEMM_SWIGLU ? kBN / 2 : kBN));
@@ -1012,7 +1039,7 @@ int launch_row_split(hipStream_t s, const float *a, int lda, int m, int k, float
 
 int launch_gemm_grouped(hipStream_t s, int epilogue, const GemmArgs &g, const GemmGroups &gg) {
     MR_REQUIRE(g.a && g.c && g.n > 0 && g.k > 0 && gg.offset && gg.count && gg.w && gg.groups > 0 &&
-                   gg.groups <= 65535 && gg.max_rows > 0 && (epilogue != GEMM_SWIGLU || gg.w2),
+                   gg.groups <= 65535 && gg.max_rows > 0 && (epilogue != GEMM_SWIGLU || gg.w2) && !g.c_hl,
                "grouped gemm: bad arguments");
     MR_REQUIRE(g.k % 8 == 0 && g.lda % 4 == 0 && g.lda >= g.k && g.ldc >= g.n && ((uintptr_t)g.a & 15) == 0,
                "grouped gemm: k must be a multiple of 8 and rows 16-byte aligned");
@@ -1054,6 +1081,31 @@ int gemm_f16_weight_scale(hipStream_t s, const void *w, int dtype, int64_t count
     return MR_OK;
 }
 
+int gemm_row_norm_bound(hipStream_t s, const void *w, int dtype, int64_t rows, int64_t cols, float *norm) {
+    MR_REQUIRE(norm && (w || rows * cols == 0) && rows >= 0 && cols >= 0, "row norm bound: bad arguments");
+    *norm = 0.0f;
+    if (dtype != MR_BF16 || rows == 0 || cols == 0) return MR_OK;
+    MR_REQUIRE(ceil_div(rows, (int64_t)4) <= INT32_MAX, "row norm bound: too many rows");
+    unsigned *dev = nullptr;
+    MR_HIP(hipMalloc((void **)&dev, sizeof(unsigned)), "row norm bound");
+    unsigned bits = 0;
+    hipError_t e = hipMemsetAsync(dev, 0, sizeof(unsigned), s);
+    if (e == hipSuccess) {
+        k_row_norm_max_bf16<<<(int)ceil_div(rows, (int64_t)4), 256, 0, s>>>((const uint16_t *)w, rows, cols, dev);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(&bits, dev, sizeof(unsigned), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(dev);
+    MR_HIP(e, "row norm bound");
+    float mx;
+    memcpy(&mx, &bits, sizeof(mx));
+    if (!(mx <= 1.0e30f)) return MR_OK;   // inf or NaN: no bound
+    // the FP32 sums of squares carry a relative error below cols 2^-24
+    *norm = mx * (1.0f + 1.0e-3f + (float)cols * 0x1p-24f);
+    return MR_OK;
+}
+
 int gemm_f16_weight_copy(hipStream_t s, const void *w, int64_t count, float scale, void *dst) {
     MR_REQUIRE(w && dst && count > 0 && scale > 0.0f, "f16 weight copy: bad arguments");
     const int64_t blocks = std::min<int64_t>(ceil_div(count, (int64_t)256 * 8), 8192);
@@ -1075,6 +1127,8 @@ int launch_gemm(hipStream_t s, int epilogue, const GemmArgs &g) {
                                      ((uintptr_t)g.wh2 & 15) == 0),
                "gemm: FP16 terms need BF16 weights, their FP16 copies and the row-scale and plane workspaces");
     MR_REQUIRE(ceil_div(g.m, kBM) <= 65535, "gemm: too many rows");
+    MR_REQUIRE(!g.c_hl || (epilogue == GEMM_SWIGLU && g.wscale > 0.0f && g.c_scale && ((uintptr_t)g.c_hl & 15) == 0),
+               "gemm: an output in FP16 terms needs the FP16-term SwiGLU GEMM and its row scales");
     switch (g.dtype) {
         case MR_BF16: return launch_dt<MR_BF16>(s, epilogue, g);
         case MR_F16: return launch_dt<MR_F16>(s, epilogue, g);

@@ -58,9 +58,13 @@ int launch_relay_partial(hipStream_t s, const RelayPartialArgs &a);
 
 // y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * gain (gain may be null).
 // k_rms_rows straight into an FP16-term GEMM's A workspace (row scales and
-// hi / lo planes, see gemm.h): the GEMM then runs with a_split.
+// hi / lo planes, see gemm.h): the GEMM then runs with a_split.  With
+// oscale (width <= 2048), also the scales that put the rows' SwiGLU output
+// (gemm.h c_hl) below 2^14, from the gate and up weights' row norm bounds ng
+// and nu (gemm_row_norm_bound).
 int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
-                          float *scale, _Float16 *planes, int rows);
+                          float *scale, _Float16 *planes, int rows, float ng = 0.0f, float nu = 0.0f,
+                          float *oscale = nullptr);
 // The widths launch_rms_rows_split takes: multiples of 8 up to 8192 (wider
 // rows take launch_rms_rows and the GEMM's own split).
 inline bool rms_split_fits(int width) { return width % 8 == 0 && width <= 8192; }

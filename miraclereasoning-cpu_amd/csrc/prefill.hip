@@ -1265,8 +1265,14 @@ int launch_rms_rows(hipStream_t s, const float *x, int ldx, const float *gain, f
 // l + 64, l + 128 and l + 192 of the one-workgroup-per-row form hold, keeps
 // their sums of squares apart and adds their wave sums in that form's order,
 // so the scale, the planes and the row scales are the same bits.
+//
+// With oscale, also the row scale of the SwiGLU output that a GEMM computes
+// from these rows (gemm.h, c_hl): |silu(g)| <= |g| and, by Cauchy-Schwarz,
+// |g| <= |y| ng and |u| <= |y| nu for the gate and up weights' largest row
+// norms ng and nu, so |y|^2 ng nu bounds every value of the output row.
 __global__ void __launch_bounds__(256) k_rms_rows_split_w(const float *x, int ldx, const float *gain, float eps,
-                                                          int width, float *scale, _Float16 *hl, int rows) {
+                                                          int width, float *scale, _Float16 *hl, int rows,
+                                                          float ng, float nu, float *oscale) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *xr = x + (int64_t)row * ldx;
@@ -1305,6 +1311,18 @@ __global__ void __launch_bounds__(256) k_rms_rows_split_w(const float *x, int ld
     mx = wave_max(mx);
     const float sc = f16_range_scale(mx);
     if (lane == 0) scale[row] = sc;
+    if (oscale) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if (lane + 64 * w >= runs) continue;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                ss += v[w][t].x * v[w][t].x + v[w][t].y * v[w][t].y + v[w][t].z * v[w][t].z + v[w][t].w * v[w][t].w;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) oscale[row] = f16_range_scale(ss * 1.001f * ng * nu);
+    }
     _Float16 *hi = hl + (int64_t)row * width, *lo = hl + (int64_t)rows * width + (int64_t)row * width;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -1325,11 +1343,15 @@ __global__ void __launch_bounds__(256) k_rms_rows_split_w(const float *x, int ld
 }
 
 int launch_rms_rows_split(hipStream_t s, const float *x, int ldx, const float *gain, float eps, int width,
-                          float *scale, _Float16 *planes, int rows) {
+                          float *scale, _Float16 *planes, int rows, float ng, float nu, float *oscale) {
     static_assert(256 * 8 * kSplitChunks == 8192, "rms_split_fits");
     MR_REQUIRE(rms_split_fits(width) && ldx % 4 == 0,
                "row RMSNorm into FP16 terms: width must be a multiple of 8 and at most 8192");
-    if (width <= 2048) k_rms_rows_split_w<<<ceil_div(rows, 4), 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
+    MR_REQUIRE(!oscale || (width <= 2048 && ng > 0.0f && nu > 0.0f),
+               "row RMSNorm into FP16 terms: the SwiGLU output scale needs rows of at most 2048 and weight norms");
+    if (width <= 2048)
+        k_rms_rows_split_w<<<ceil_div(rows, 4), 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows, ng, nu,
+                                                             oscale);
     else k_rms_rows_split<<<rows, 256, 0, s>>>(x, ldx, gain, eps, width, scale, planes, rows);
     MR_LAUNCHED("enqueue row RMSNorm into FP16 terms");
     return MR_OK;
