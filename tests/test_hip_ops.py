@@ -279,7 +279,8 @@ def test_grouped_gemm_groups_against_float64(backend, swiglu):
             uz = wf2[z * n:(z + 1) * n]
             u = a[sl].astype(np.float64) @ uz.T
             eu = 2.0 ** -20 * (np.abs(a[sl]).astype(np.float64) @ np.abs(uz).T)
-            sig = 0.5 * (1.0 + np.tanh(0.5 * g))   # the logistic function without overflow
+            e = np.exp(-np.abs(g))   # the logistic function without overflow, accurate in both tails
+            sig = np.where(g >= 0.0, 1.0 / (1.0 + e), e / (1.0 + e))
             silu = g * sig
             dsilu = np.abs(sig * (1.0 + g * (1.0 - sig)))
             want[sl] = silu * u
