@@ -978,11 +978,24 @@ int f16_copies(mr_model *m, std::initializer_list<Weight *> ws, std::initializer
 
 // Bounds on the gate and up rows' norms where the batched prefill writes the
 // SwiGLU output straight into the down projection's FP16 terms (every
-// matrix of the FFN with an FP16 copy).
-int swiglu_row_norms(mr_model *m, Mlp &f) {
-    if (f.gate.f16_scale > 0.0f && f.up.f16_scale > 0.0f && f.down.f16_scale > 0.0f)
-        for (Weight *w : {&f.gate, &f.up})
-            MR_TRY(gemm_row_norm_bound(m->ctx->stream, w->ptr, w->dtype, w->rows, w->cols, &w->row_norm));
+// matrix of the FFN with an FP16 copy).  The FFN's input rows are RMSNorm
+// outputs of `width` values with `gain` (1-D, float32), so |y|^2 <= width
+// max gain^2 and every output of a row is at most width max gain^2 ng nu: the
+// bounds are kept only where that stays finite, so that the row scales are.
+int swiglu_row_norms(mr_model *m, Mlp &f, const Weight &gain, int width) {
+    f.gate.row_norm = f.up.row_norm = 0.0f;
+    if (!(f.gate.f16_scale > 0.0f && f.up.f16_scale > 0.0f && f.down.f16_scale > 0.0f)) return MR_OK;
+    for (Weight *w : {&f.gate, &f.up})
+        MR_TRY(gemm_row_norm_bound(m->ctx->stream, w->ptr, w->dtype, w->rows, w->cols, &w->row_norm));
+    double gmax = 1.0;
+    if (gain.ptr) {
+        std::vector<float> g(width);
+        MR_HIP(hipMemcpy(g.data(), gain.ptr, (size_t)width * sizeof(float), hipMemcpyDeviceToHost), "read norm gain");
+        gmax = 0.0;
+        for (float v : g) gmax = std::isfinite(v) ? std::max(gmax, (double)std::fabs(v)) : INFINITY;
+    }
+    const double bound = (double)width * gmax * gmax * f.gate.row_norm * f.up.row_norm;
+    if (!(bound < 1.0e37)) f.gate.row_norm = f.up.row_norm = 0.0f;
     return MR_OK;
 }
 
@@ -1074,7 +1087,7 @@ int finalize_light_layer(mr_model *m, Layer &L, int i) {
     L.kv_up.rows = 2 * kvw;
     MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
     MR_TRY(f16_copies(m, {&L.qkv, &L.kv_up, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
-    MR_TRY(swiglu_row_norms(m, L.ffn));
+    MR_TRY(swiglu_row_norms(m, L.ffn, L.a_norm, d.hidden_size));   // the FFN branch reads the attention's input
     L.light_cap = d.window + d.memory_slots + 1;
     const size_t cap = L.light_cap;
     MR_TRY(device_alloc(m, cap * d.latent_dim * sizeof(float), (void **)&L.arena));
@@ -1336,7 +1349,7 @@ int mr_model_finalize(mr_model *m) {
         MR_TRY(need(L.ffn.down, "ffn.down", i));
         MR_REQUIRE(L.ffn.gate.dtype == L.ffn.up.dtype, "ffn gate and up must share one dtype");
         MR_TRY(f16_copies(m, {&L.qkv, &L.o, &L.ffn.gate, &L.ffn.up, &L.ffn.down}, {&L.ffn.gate, &L.ffn.up}));
-        MR_TRY(swiglu_row_norms(m, L.ffn));
+        MR_TRY(swiglu_row_norms(m, L.ffn, L.f_norm, h));
         const int kvw = L.kv_heads * hd;
         max_kvw = std::max(max_kvw, kvw);
         max_kvh = std::max(max_kvh, L.kv_heads);
