@@ -1548,6 +1548,7 @@ struct PrefillWs {
     _Float16 *xn_planes = nullptr;
     float *rowscale = nullptr;   // FP16-term GEMMs: scales of the rows of A
     float *act_scale = nullptr;  // row scales of the SwiGLU output written in FP16 terms (into act)
+    float *att_scale = nullptr;  // row scales of the attended values written in FP16 terms (into att)
     _Float16 *planes = nullptr;  // and its hi and lo FP16 planes
     _Float16 *kv16 = nullptr;    // attention: the attended keys and values in FP16 terms
     int kv16_rows = 0;
@@ -1601,7 +1602,7 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->merge_row, light ? r : 0}, {(void **)&w->extra_pos, light ? r : 0},
         // flashnano-1.6
         {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
-        {(void **)&w->rowscale, split_rows}, {(void **)&w->act_scale, r},
+        {(void **)&w->rowscale, split_rows}, {(void **)&w->act_scale, r}, {(void **)&w->att_scale, r},
         {(void **)&w->planes, split_rows * std::max({h, qd, (size_t)d.ffn_dim})},
         {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, 2 * kvw}, {(void **)&w->kv16_max, 2 * kvw}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
@@ -1780,11 +1781,21 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
         MR_TRY(launch_relay_partial(s, r));
         a.ext = w.ext;
     }
+    // the attended values straight into the O projection's FP16 terms (att
+    // holds T x qd floats, the same bytes as its two planes of halves)
+    const bool att_split = !a.ext && L.o.dtype == MR_BF16 && L.o.f16_scale > 0.0f && prefill_attention_presplit(a);
+    if (att_split) {
+        a.out_hl = (_Float16 *)w.att;
+        a.out_scale = w.att_scale;
+    }
     MR_TRY(launch_prefill_attention(s, a));
     MR_TRY(launch_ring_store(s, w.qkv, ld, qd, kvw, L.ring_k, L.ring_v, L.capacity, p0, T));
     GemmArgs o;
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
-    o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale; o.wscale = L.o.f16_scale; o.wh = L.o.f16; o.ascale = w.rowscale; o.ahl_ws = w.planes;
+    o.m = T; o.n = h; o.k = qd; o.scale = d.residual_scale; o.wscale = L.o.f16_scale; o.wh = L.o.f16;
+    o.ascale = att_split ? w.att_scale : w.rowscale;
+    o.ahl_ws = att_split ? (_Float16 *)w.att : w.planes;
+    o.a_split = att_split;
     MR_TRY(launch_gemm(s, GEMM_RESIDUAL, o));
     GemmArgs gu;
     gu.a = w.xn; gu.lda = h; gu.w = L.ffn.gate.ptr; gu.w2 = L.ffn.up.ptr; gu.dtype = L.ffn.gate.dtype;

@@ -32,7 +32,19 @@ struct PrefillAttnArgs {
     int kv16_rows = 0;
     float *kv16_scale = nullptr;
     unsigned *kv16_max = nullptr;
+    // With out_hl (the presplit form above, no ext): the attended values go
+    // out as the O projection's FP16 terms (gemm.h, a_split) instead of into
+    // out.  Every output is a convex combination of values, so the power of
+    // two that maps the largest |v| of every KV head into [2^13, 2^14) serves
+    // as every row's scale: into out_scale[r], and o 2^t = hi + lo into planes
+    // [hi: rows x ldo | lo: rows x ldo] of out_hl.
+    _Float16 *out_hl = nullptr;
+    float *out_scale = nullptr;
 };
+
+// Whether launch_prefill_attention takes the presplit form for a (head dims
+// 32, 64 or 128, with the kv16 workspace and enough rows in it).
+bool prefill_attention_presplit(const PrefillAttnArgs &a);
 
 // out = softmax(q . k / sqrt(d)) . v per query head over the keys at
 // positions max(0, p - window + 1) .. p of each query position p (but

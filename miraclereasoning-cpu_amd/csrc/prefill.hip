@@ -733,6 +733,12 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
         }
     }
     const float vun = 1.0f / sv;
+    float so = 1.0f;   // out_hl: the rows' scale, from every KV head's max |v|
+    if (a.out_hl) {
+        unsigned mb = 0;
+        for (int kh = 0; kh < a.kv_heads; ++kh) mb = max(mb, a.kv16_max[a.kv_heads + kh]);
+        so = f16_range_scale(__uint_as_float(mb));
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (!qvalid[r]) continue;
@@ -756,7 +762,23 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
                 const float4 e = load_f4(ext + 4 + dim);
                 x = make_float4(x.x + e.x * we, x.y + e.y * we, x.z + e.z * we, x.w + e.w * we);
             }
-            *(float4 *)(a.out + (int64_t)tq[r] * a.ldo + h * D + dim) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+            const float y[4] = {x.x * inv, x.y * inv, x.z * inv, x.w * inv};
+            if (a.out_hl) {
+                f16x4 hh, hl;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    _Float16 th, tl;
+                    split2h(y[i] * so, th, tl);
+                    hh[i] = th;
+                    hl[i] = tl;
+                }
+                _Float16 *po = a.out_hl + (int64_t)tq[r] * a.ldo + h * D + dim;
+                *(f16x4 *)po = hh;
+                *(f16x4 *)(po + (int64_t)a.rows * a.ldo) = hl;
+                if (h == 0 && t == 0 && lq == 0) a.out_scale[tq[r]] = so;
+            } else {
+                *(float4 *)(a.out + (int64_t)tq[r] * a.ldo + h * D + dim) = make_float4(y[0], y[1], y[2], y[3]);
+            }
         }
     }
 }
@@ -1184,6 +1206,14 @@ int launch_debug_exp(hipStream_t s, const float *x, float *y, int n, int which) 
     return MR_OK;
 }
 
+bool prefill_attention_presplit(const PrefillAttnArgs &a) {
+    const int win = a.window ? a.window : a.cap;
+    const int first = std::max(0, a.p0 - win + 1), n = a.p0 + a.rows - first;
+    const bool h = a.d == 128 || a.d == 64 || a.d == 32;
+    return h && a.kv16 && a.kv16_scale && a.kv16_max && ceil_div(n, kKeys) * kKeys <= a.kv16_rows &&
+           a.kv_heads * a.d <= 4096 && (int64_t)4 * a.kv16_rows * a.kv_heads * a.d * 2 < ((int64_t)1 << 31);
+}
+
 int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     MR_REQUIRE(a.qkv && a.ring_k && a.ring_v && a.out && a.rows > 0 && a.cap > 0, "prefill attention: bad arguments");
     MR_REQUIRE(a.kv_heads > 0 && a.heads % a.kv_heads == 0, "prefill attention: heads must be a multiple of kv_heads");
@@ -1194,10 +1224,10 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     const dim3 grid(ceil_div(a.rows, 64 / gb), a.kv_heads * (G / gb));
     const int win = a.window ? a.window : a.cap;
     const int first = std::max(0, a.p0 - win + 1), n = a.p0 + a.rows - first;
-    const bool h = a.d == 128 || a.d == 64 || a.d == 32;
     const int n_tiles = ceil_div(n, kKeys);
-    const bool planes = h && a.kv16 && a.kv16_scale && a.kv16_max && n_tiles * kKeys <= a.kv16_rows &&
-                        a.kv_heads * a.d <= 4096 && (int64_t)4 * a.kv16_rows * a.kv_heads * a.d * 2 < ((int64_t)1 << 31);
+    const bool planes = prefill_attention_presplit(a);
+    MR_REQUIRE(!a.out_hl || (planes && !a.ext && a.out_scale && ((uintptr_t)a.out_hl & 7) == 0),
+               "prefill attention: FP16-term output needs the presplit form, no extra partial and row scales");
     if (planes) {   // split the attended keys and values once
         MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
         const int threads = ceil_div(a.kv_heads * a.d / 4, kWave) * kWave;
