@@ -2029,10 +2029,21 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
     a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
+    // without an extra partial, the attended values straight into the O projection's FP16 terms
+    const bool att_split = !a.ext && L.o.dtype == MR_BF16 && L.o.f16_scale > 0.0f && prefill_attention_presplit(a);
+    if (att_split) {
+        a.out_hl = (_Float16 *)w.att;
+        a.out_scale = w.att_scale;
+    }
     MR_TRY(launch_prefill_attention(s, a));
     GemmArgs o;
     o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.obuf; o.ldc = h; o.m = T; o.n = h; o.k = qd;
     f16(o, L.o);
+    if (att_split) {
+        o.ascale = w.att_scale;
+        o.ahl_ws = (_Float16 *)w.att;
+        o.a_split = true;
+    }
     MR_TRY(launch_gemm(s, GEMM_STORE, o));
     GemmArgs dn;
     dn.a = w.act; dn.lda = ffn; dn.w = L.ffn.down.ptr; dn.dtype = L.ffn.down.dtype; dn.c = w.fbuf; dn.ldc = h;
