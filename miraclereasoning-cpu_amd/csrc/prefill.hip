@@ -1048,11 +1048,13 @@ __global__ void __launch_bounds__(256) k_qk_rows_r(float *qkv, int ld, int p0, i
 __global__ void k_ring_store(const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,
                              int first, int p0) {
     const int p = first + blockIdx.x;
-    const float *src = qkv + (int64_t)(p - p0) * ld + qd;
+    const float4 *src = (const float4 *)(qkv + (int64_t)(p - p0) * ld + qd);
     const int64_t slot = p % cap;
-    for (int j = threadIdx.x; j < kvw; j += blockDim.x) {
-        ring_k[slot * kvw + j] = src[j];
-        ring_v[slot * kvw + j] = src[kvw + j];
+    float4 *dk = (float4 *)(ring_k + slot * kvw), *dv = (float4 *)(ring_v + slot * kvw);
+    const int n4 = kvw / 4;   // 16-byte copies (ld, qd and kvw multiples of 4)
+    for (int j = threadIdx.x; j < n4; j += blockDim.x) {
+        dk[j] = src[j];
+        dv[j] = src[n4 + j];
     }
 }
 
@@ -1413,6 +1415,8 @@ int launch_k_rows_at(hipStream_t s, float *k, int ld, int rows, const int *posit
 
 int launch_ring_store(hipStream_t s, const float *qkv, int ld, int qd, int kvw, float *ring_k, float *ring_v, int cap,
                       int p0, int rows) {
+    MR_REQUIRE(ld % 4 == 0 && qd % 4 == 0 && kvw % 4 == 0 && (((uintptr_t)qkv | (uintptr_t)ring_k | (uintptr_t)ring_v) & 15) == 0,
+               "ring fill: rows must be 16-byte aligned");
     const int first = std::max(p0, p0 + rows - cap);
     k_ring_store<<<p0 + rows - first, 256, 0, s>>>(qkv, ld, qd, kvw, ring_k, ring_v, cap, first, p0);
     MR_LAUNCHED("enqueue ring fill");
