@@ -61,6 +61,41 @@ def test_batched_workload_geometry_matches_oracle(backend, name, prompt):
     assert model.generate(list(ids), max_new_tokens=6) == stream
 
 
+def test_batched_fp16_term_inputs_at_extreme_scales(backend):
+    """The down and O projections take the SwiGLU output and the attended
+    values as FP16 terms whose row scales are bounds fixed before those rows
+    exist: |y|^2 ng nu from the FFN input's norm and the gate and up weights'
+    row norms, and the largest |v| of every KV head.  Stretch both on the
+    flashnano-1.5 mid geometry (BF16): layer 0's gate and up rows x 2^10 and
+    its FFN gain x 2^4 (SwiGLU outputs near 10^9, their bound 140-220 times
+    higher), layer 1's values of KV head 0 x 2^12 (every other head's
+    outputs 2^12 below the scale's bound), and one prompt token's embedding
+    row x 2^8.  The batched prefill still matches the exact token loop."""
+    from miracle_hip.weights import BF16Array, bf16_bits
+    wl = presets.workload("flashnano-1.5-mid")
+    cfg = wl["config"]
+    weights = synthetic.synthetic_weights(cfg, 29, "bf16")
+    ids = synthetic.prompt_ids(cfg["vocab_size"], 300, 29)
+
+    def scale(name, factor, rows=slice(None)):   # powers of two: exact in BF16
+        w = weights[name][:]
+        w[rows] *= np.float32(factor)
+        weights[name] = BF16Array(bf16_bits(w))
+
+    scale("layers.0.ffn.gate", 2.0 ** 10)
+    scale("layers.0.ffn.up", 2.0 ** 10)
+    weights["layers.0.f_norm"] = weights["layers.0.f_norm"] * np.float32(16.0)
+    scale("layers.1.v", 2.0 ** 12, slice(0, cfg["head_dim"]))
+    scale("embed", 2.0 ** 8, slice(int(ids[5]), int(ids[5]) + 1))
+    runs = {}
+    for mode in ("exact", "batched"):
+        with MiracleModel(ModelConfig.from_dict(cfg), weights, backend=backend, context_length=1024,
+                          prefill_mode=mode) as model:
+            runs[mode] = model.prefill(ids, return_all=True)
+    assert np.all(np.isfinite(runs["batched"]))
+    np.testing.assert_allclose(runs["batched"], runs["exact"], rtol=1e-3, atol=1e-4)
+
+
 def test_batched_split_prompt_matches_whole(backend):
     """Chunk invariance at tolerance: a prompt appended in three uneven parts
     (each reading the previous parts' keys from the rings, one part shorter
