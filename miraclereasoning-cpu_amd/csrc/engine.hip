@@ -1554,6 +1554,8 @@ struct PrefillWs {
     int kv16_rows = 0;
     float *kv16_scale = nullptr;
     unsigned *kv16_max = nullptr;
+    unsigned *kv_part = nullptr;   // the K/V maxima pass's per-block partials
+    int kv_part_blocks = 0;
 };
 
 int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
@@ -1579,6 +1581,9 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
     // attention sees the window, the others up to the ring
     const int attend = heavy && d.window > 0 ? d.window : max_cap;
     w->kv16_rows = ceil_div(rows + attend, 32) * 32;
+    int max_kvh = 1;
+    for (const Layer &L : m->layers) max_kvh = std::max(max_kvh, L.kv_heads);
+    w->kv_part_blocks = prefill_kv_max_blocks(rows + attend);
     const size_t kv16 = (size_t)w->kv16_rows * kvw * 2;   // 4 planes of halves, in floats
     struct Piece { void **ptr; size_t floats; };
     const Piece pieces[] = {
@@ -1604,7 +1609,8 @@ int prefill_workspace(mr_model *m, int rows, bool all, PrefillWs *w) {
         {(void **)&w->cbr_scores, pr * (cbr ? d.cbr_chunk_size : 0)}, {(void **)&w->cbr_pooled, pr * h}, {(void **)&w->cbr_anchor, pr}, {(void **)&w->cbr_kv, pr * 2 * kvw},
         {(void **)&w->rowscale, split_rows}, {(void **)&w->act_scale, r}, {(void **)&w->att_scale, r},
         {(void **)&w->planes, split_rows * std::max({h, qd, (size_t)d.ffn_dim})},
-        {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, 2 * kvw}, {(void **)&w->kv16_max, 2 * kvw}};
+        {(void **)&w->kv16, kv16}, {(void **)&w->kv16_scale, 2 * kvw}, {(void **)&w->kv16_max, 2 * kvw},
+        {(void **)&w->kv_part, (size_t)w->kv_part_blocks * 2 * max_kvh}};
     auto up = [](size_t floats) { return (floats + 63) & ~(size_t)63; };   // 256-byte slices
     size_t total = 0;
     for (const Piece &pc : pieces) total += up(pc.floats);
@@ -1773,6 +1779,7 @@ int gqa_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, int p0, int T) {
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
     a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
+    a.kv_part = w.kv_part; a.kv_part_blocks = w.kv_part_blocks;
     if (cbr) {   // the relay rows join every row's softmax as its extra partial
         RelayPartialArgs r;
         r.qkv = w.qkv; r.ld = ld; r.relay_k = L.relay_k; r.relay_v = L.relay_v; r.ext = w.ext;
@@ -1884,6 +1891,7 @@ int heavy_layer_rows(mr_model *m, Layer &L, int li, const PrefillWs &w, int p0, 
         a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
         a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
         a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
+        a.kv_part = w.kv_part; a.kv_part_blocks = w.kv_part_blocks;
         MR_TRY(launch_prefill_attention(s, a));
         GemmArgs o;   // hidden += step_scale * Wo . attended
         o.a = w.att; o.lda = qd; o.w = L.o.ptr; o.dtype = L.o.dtype; o.c = w.x; o.ldc = h;
@@ -2029,6 +2037,7 @@ int light_layer_rows(mr_model *m, Layer &L, const PrefillWs &w, const LightPlan 
     a.out = w.att; a.ldo = qd; a.p0 = p0; a.rows = T;
     a.heads = d.query_heads; a.kv_heads = L.kv_heads; a.d = hd; a.inv_root = 1.0f / sqrtf((float)hd);
     a.kv16 = w.kv16; a.kv16_rows = w.kv16_rows; a.kv16_scale = w.kv16_scale; a.kv16_max = w.kv16_max;
+    a.kv_part = w.kv_part; a.kv_part_blocks = w.kv_part_blocks;
     // without an extra partial, the attended values straight into the O projection's FP16 terms
     const bool att_split = !a.ext && L.o.dtype == MR_BF16 && L.o.f16_scale > 0.0f && prefill_attention_presplit(a);
     if (att_split) {

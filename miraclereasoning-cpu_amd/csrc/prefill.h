@@ -32,6 +32,11 @@ struct PrefillAttnArgs {
     int kv16_rows = 0;
     float *kv16_scale = nullptr;
     unsigned *kv16_max = nullptr;
+    // Optional with kv16: room for kv_part_blocks x 2 kv_heads words, the
+    // per-block maxima of the K/V maxima pass, which the split then reduces
+    // per head (no zeroing and no atomics on the same 2 kv_heads words).
+    unsigned *kv_part = nullptr;
+    int kv_part_blocks = 0;
     // With out_hl (the presplit form above, no ext): the attended values go
     // out as the O projection's FP16 terms (gemm.h, a_split) instead of into
     // out.  Every output is a convex combination of values, so the power of
@@ -41,6 +46,11 @@ struct PrefillAttnArgs {
     _Float16 *out_hl = nullptr;
     float *out_scale = nullptr;
 };
+
+// Blocks of the K/V maxima pass over n attended positions (kv_part's rows):
+// kKvMaxRows positions each.
+constexpr int kKvMaxRows = 32;
+__host__ __device__ inline int prefill_kv_max_blocks(int n) { return (n + kKvMaxRows - 1) / kKvMaxRows; }
 
 // Whether launch_prefill_attention takes the presplit form for a (head dims
 // 32, 64 or 128, with the kv16 workspace and enough rows in it).

@@ -792,7 +792,7 @@ __global__ void __launch_bounds__(kAttnThreads) k_attn_prefill_t(PrefillAttnArgs
 // with fewer positions measured slower, their atomics queueing on the same
 // words); the D / 4 threads of a head combine their maxima before one atomic
 // each.
-constexpr int kMaxRows = 32;
+constexpr int kMaxRows = kKvMaxRows;
 constexpr int kMaxBatch = 8;
 
 __global__ void k_kv_max(PrefillAttnArgs a, int first, int n) {
@@ -823,8 +823,14 @@ __global__ void k_kv_max(PrefillAttnArgs a, int first, int n) {
     }
     if (on && c4 % a.d == 0) {
         const int head = c4 / a.d;
-        atomicMax(a.kv16_max + head, __float_as_uint(mk));
-        atomicMax(a.kv16_max + a.kv_heads + head, __float_as_uint(mv));
+        if (a.kv_part) {   // this block's maxima, reduced by k_kv_split_tiles
+            unsigned *part = a.kv_part + (size_t)blockIdx.x * 2 * a.kv_heads;
+            part[head] = __float_as_uint(mk);
+            part[a.kv_heads + head] = __float_as_uint(mv);
+        } else {
+            atomicMax(a.kv16_max + head, __float_as_uint(mk));
+            atomicMax(a.kv16_max + a.kv_heads + head, __float_as_uint(mv));
+        }
     }
 }
 
@@ -841,8 +847,37 @@ __global__ void __launch_bounds__(256) k_kv_split_tiles(PrefillAttnArgs a, int f
     static_assert(PER >= 1 && kKeys * D / 4 % 256 == 0, "tile split");
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * kKeys];
     const int kvw = a.kv_heads * D, qd = a.heads * D, head = blockIdx.y, j = blockIdx.x;
-    const float sk = f16_range_scale(__uint_as_float(a.kv16_max[head]));
-    const float sv = f16_range_scale(__uint_as_float(a.kv16_max[a.kv_heads + head]));
+    unsigned mk, mv;
+    if (a.kv_part) {   // the head's maxima over k_kv_max's blocks (an exact operation in any order)
+        __shared__ unsigned red[2][256 / kWave];
+        mk = 0;
+        mv = 0;
+        const unsigned *part = a.kv_part;
+        for (int b = threadIdx.x, nb = prefill_kv_max_blocks(n); b < nb; b += 256) {
+            mk = max(mk, part[(size_t)b * 2 * a.kv_heads + head]);
+            mv = max(mv, part[(size_t)b * 2 * a.kv_heads + a.kv_heads + head]);
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            mk = max(mk, (unsigned)__shfl_xor((int)mk, off));
+            mv = max(mv, (unsigned)__shfl_xor((int)mv, off));
+        }
+        if ((threadIdx.x & 63) == 0) {
+            red[0][threadIdx.x >> 6] = mk;
+            red[1][threadIdx.x >> 6] = mv;
+        }
+        __syncthreads();
+        mk = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+        mv = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+        if (j == 0 && threadIdx.x == 0) {   // for the attention's FP16-term output
+            a.kv16_max[head] = mk;
+            a.kv16_max[a.kv_heads + head] = mv;
+        }
+    } else {
+        mk = a.kv16_max[head];
+        mv = a.kv16_max[a.kv_heads + head];
+    }
+    const float sk = f16_range_scale(__uint_as_float(mk));
+    const float sv = f16_range_scale(__uint_as_float(mv));
     if (j == 0 && threadIdx.x == 0) {
         a.kv16_scale[head] = sk;
         a.kv16_scale[a.kv_heads + head] = sv;
@@ -1231,13 +1266,17 @@ int launch_prefill_attention(hipStream_t s, const PrefillAttnArgs &a) {
     MR_REQUIRE(!a.out_hl || (planes && !a.ext && a.out_scale && ((uintptr_t)a.out_hl & 7) == 0),
                "prefill attention: FP16-term output needs the presplit form, no extra partial and row scales");
     if (planes) {   // split the attended keys and values once
-        MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
+        PrefillAttnArgs b = a;   // the maxima's per-block partials where they fit, else atomics
+        if (!(b.kv_part && prefill_kv_max_blocks(n) <= b.kv_part_blocks)) {
+            b.kv_part = nullptr;
+            MR_HIP(hipMemsetAsync(a.kv16_max, 0, 2 * a.kv_heads * sizeof(unsigned), s), "prefill attention");
+        }
         const int threads = ceil_div(a.kv_heads * a.d / 4, kWave) * kWave;
-        k_kv_max<<<ceil_div(n, kMaxRows), threads, 0, s>>>(a, first, n);
+        k_kv_max<<<prefill_kv_max_blocks(n), threads, 0, s>>>(b, first, n);
         const dim3 tiles(n_tiles, a.kv_heads);
-        if (a.d == 128) k_kv_split_tiles<128><<<tiles, 256, 0, s>>>(a, first, n);
-        else if (a.d == 64) k_kv_split_tiles<64><<<tiles, 256, 0, s>>>(a, first, n);
-        else k_kv_split_tiles<32><<<tiles, 256, 0, s>>>(a, first, n);
+        if (a.d == 128) k_kv_split_tiles<128><<<tiles, 256, 0, s>>>(b, first, n);
+        else if (a.d == 64) k_kv_split_tiles<64><<<tiles, 256, 0, s>>>(b, first, n);
+        else k_kv_split_tiles<32><<<tiles, 256, 0, s>>>(b, first, n);
     }
     // Two row sets a wave where that still leaves two workgroups per CU and
     // the rows' key counts are about even (at most a quarter of the rows see
